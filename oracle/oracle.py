@@ -1,0 +1,276 @@
+"""CPU oracle for the 4-bit affine group-64 qmv — TEST INFRASTRUCTURE ONLY.
+
+Only `tests/`, `__graft_entry__.smoke()` and the CPU-baseline leg of `bench.py` may
+import this module, and only as the checker (or the timed CPU baseline).  The product
+(`ironmule_amd`) never imports it; the product path fails loudly without its HIP library.
+
+What lives here:
+
+* numpy restatements of the format (low-nibble-first pack/unpack, bf16 widening and
+  round-to-nearest-even) — ironmule/cuda_native.py:43-51, 54-56, 91;
+* ctypes bindings to `imq_oracle.c` (the C restatements: fp32 dequantise-then-matmul,
+  fp64 product with an error bound, the reference CUDA row kernel's exact arithmetic,
+  the reference Metal kernels' arithmetic order — see that file's header);
+* the seeded synthetic inputs of the benchmark configurations (numpy PCG64,
+  seed 20261201 + config index): uniform uint32 words (so every nibble is uniform on
+  0..15), scales U(0.005, 0.02) and biases U(-0.1, 0.1) rounded to bf16, x ~ N(0, 1)
+  rounded to bf16;
+* the parity predicates used by the tests (`check_bf16`, `check_f32`).
+
+Pinning: every function here is checked in tests/test_oracle.py against closed forms,
+exact rational arithmetic on tiny inputs (tests/golden/), torch's own bf16 rounding,
+and the special cases that reduce the product to a textbook sum.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libimq_oracle.so")
+GROUP_SIZE = 64
+SEED_BASE = 20261201
+
+_lib = None
+
+
+def build() -> str:
+    """Compile imq_oracle.c with its Makefile (gcc is enough)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        I64, I32 = ctypes.c_int64, ctypes.c_int32
+        _lib.imo_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        _lib.imo_bf16_to_f32.restype = ctypes.c_float
+        _lib.imo_f32_to_bf16.argtypes = [ctypes.c_float]
+        _lib.imo_f32_to_bf16.restype = ctypes.c_uint16
+        _lib.imo_f32_to_bf16_array.argtypes = [P, P, I64]
+        _lib.imo_bf16_to_f32_array.argtypes = [P, P, I64]
+        _lib.imo_unpack.argtypes = [P, P, I64]
+        _lib.imo_dequant_f32.argtypes = [P, P, P, P, I64, I64, I32]
+        _lib.imo_qmv_dequant_f32.argtypes = [P, P, P, P, P, I64, I64, I64, I32, I32]
+        _lib.imo_qmv_f64.argtypes = [P, P, P, P, P, P, I64, I64, I64, I32, I32]
+        _lib.imo_qmv_rowkernel.argtypes = [P, P, P, P, P, I32, I64, I64, I64, I32, I32]
+        _lib.imo_qmv_mlx.argtypes = [P, P, P, P, P, I32, I64, I64, I64, I32, I32, I32]
+        _lib.imo_max_threads.restype = I32
+    return _lib
+
+
+def _p(a: np.ndarray) -> ctypes.c_void_p:
+    assert a.flags["C_CONTIGUOUS"], "oracle inputs must be C-contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def max_threads() -> int:
+    return int(lib().imo_max_threads())
+
+
+# ------------------------------------------------------------------ bf16 (numpy)
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    """Widen bf16 bit patterns (uint16) to float32 by a 16-bit shift."""
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f: np.ndarray) -> np.ndarray:
+    """Round float32 to bf16 bit patterns, nearest-even; any NaN becomes 0x7fc0."""
+    u = np.ascontiguousarray(f, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = 0x7FC0
+    return r
+
+
+def bf16_ulp(v: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 numbers at |v| (one unit in the last place), for finite v."""
+    a = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    e = np.maximum(e, -126.0)
+    return np.where(a > 0, np.exp2(e - 7), np.exp2(-133.0))
+
+
+# ------------------------------------------------------------ format (numpy)
+
+def unpack(w: np.ndarray) -> np.ndarray:
+    """uint32 words -> uint8 nibbles, low nibble first: element j of u is (u >> 4j) & 0xF."""
+    w = np.asarray(w, dtype=np.uint32)
+    shifts = (4 * np.arange(8, dtype=np.uint32))
+    q = (w[..., None] >> shifts) & 0xF
+    return q.reshape(*w.shape[:-1], w.shape[-1] * 8).astype(np.uint8)
+
+
+def pack(q: np.ndarray) -> np.ndarray:
+    """uint8 nibbles (..., K) -> uint32 words (..., K/8), low nibble first."""
+    q = np.asarray(q, dtype=np.uint32)
+    assert q.shape[-1] % 8 == 0 and int(q.max(initial=0)) < 16
+    q = q.reshape(*q.shape[:-1], q.shape[-1] // 8, 8)
+    shifts = (4 * np.arange(8, dtype=np.uint32))
+    return np.bitwise_or.reduce(q << shifts, axis=-1).astype(np.uint32)
+
+
+def dequant_np(w, s, b, gs: int = GROUP_SIZE) -> np.ndarray:
+    """fl32(s*q + b), computed in float64 and rounded once (s*q + b is exact in
+    float64 for bf16 s, b of ordinary magnitude), an independent route to the C oracle."""
+    q = unpack(w).astype(np.float64)
+    sf = np.repeat(bf16_to_f32(s).astype(np.float64), gs, axis=-1)
+    bf = np.repeat(bf16_to_f32(b).astype(np.float64), gs, axis=-1)
+    return (sf * q + bf).astype(np.float32)
+
+
+# --------------------------------------------------------------- C oracle calls
+
+def dequant_f32(w, s, b, gs: int = GROUP_SIZE) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    n, k = w.shape[0], w.shape[1] * 8
+    out = np.empty((n, k), dtype=np.float32)
+    lib().imo_dequant_f32(_p(w), _p(s), _p(b), _p(out), n, k, gs)
+    return out
+
+
+def qmv_dequant_f32(w, s, b, x, gs: int = GROUP_SIZE, threads: int = 0) -> np.ndarray:
+    w, s, b, x = _prep(w, s, b, x)
+    m, k, n = x.shape[0], x.shape[1], w.shape[0]
+    y = np.empty((m, n), dtype=np.float32)
+    lib().imo_qmv_dequant_f32(_p(w), _p(s), _p(b), _p(x), _p(y), m, n, k, gs,
+                              threads or max_threads())
+    return y
+
+
+def qmv_f64(w, s, b, x, gs: int = GROUP_SIZE, threads: int = 0):
+    """(y, abssum): fp64 product and sum_k |w_k x_k| per output."""
+    w, s, b, x = _prep(w, s, b, x)
+    m, k, n = x.shape[0], x.shape[1], w.shape[0]
+    y = np.empty((m, n), dtype=np.float64)
+    a = np.empty((m, n), dtype=np.float64)
+    lib().imo_qmv_f64(_p(w), _p(s), _p(b), _p(x), _p(y), _p(a), m, n, k, gs,
+                      threads or max_threads())
+    return y, a
+
+
+def qmv_rowkernel(w, s, b, x, out_f32: bool = False, gs: int = GROUP_SIZE,
+                  threads: int = 0) -> np.ndarray:
+    w, s, b, x = _prep(w, s, b, x)
+    m, k, n = x.shape[0], x.shape[1], w.shape[0]
+    y = np.empty((m, n), dtype=np.float32 if out_f32 else np.uint16)
+    lib().imo_qmv_rowkernel(_p(w), _p(s), _p(b), _p(x), _p(y), int(out_f32), m, n, k, gs,
+                            threads or max_threads())
+    return y
+
+
+def qmv_mlx(w, s, b, x, values_per_thread: int = 8, out_f32: bool = False,
+            gs: int = GROUP_SIZE, threads: int = 0) -> np.ndarray:
+    w, s, b, x = _prep(w, s, b, x)
+    m, k, n = x.shape[0], x.shape[1], w.shape[0]
+    y = np.empty((m, n), dtype=np.float32 if out_f32 else np.uint16)
+    lib().imo_qmv_mlx(_p(w), _p(s), _p(b), _p(x), _p(y), int(out_f32), m, n, k, gs,
+                      values_per_thread, threads or max_threads())
+    return y
+
+
+def _prep(w, s, b, x):
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.uint16)
+    assert w.ndim == 2 and x.shape[1] == w.shape[1] * 8, (w.shape, x.shape)
+    assert s.shape == b.shape == (w.shape[0], x.shape[1] // GROUP_SIZE), (s.shape, b.shape)
+    return w, s, b, x
+
+
+# ---------------------------------------------------------------- synthetic data
+
+@dataclass
+class Problem:
+    """One seeded qmv problem: bit patterns only (uint32 words, bf16 as uint16)."""
+    w: np.ndarray
+    s: np.ndarray
+    b: np.ndarray
+    x: np.ndarray
+    seed: int
+
+    @property
+    def n(self) -> int:
+        return self.w.shape[0]
+
+    @property
+    def k(self) -> int:
+        return self.w.shape[1] * 8
+
+
+def synthetic(n: int, k: int, m: int = 1, seed: int = SEED_BASE) -> Problem:
+    """The benchmark configurations' input distribution at any shape."""
+    assert k % GROUP_SIZE == 0
+    rng = np.random.Generator(np.random.PCG64(seed))
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint64).astype(np.uint32)
+    s = f32_to_bf16(rng.uniform(0.005, 0.02, size=(n, k // GROUP_SIZE)).astype(np.float32))
+    b = f32_to_bf16(rng.uniform(-0.1, 0.1, size=(n, k // GROUP_SIZE)).astype(np.float32))
+    x = f32_to_bf16(rng.standard_normal(size=(m, k)).astype(np.float32))
+    return Problem(w, s, b, x, seed)
+
+
+# ---------------------------------------------------------------- parity checks
+
+#: Additive allowance for fp32 summation-order differences, as a fraction of
+#: sum_k |w_k x_k|.  2**-20 is far above what any fp32 order produces in practice
+#: (~2**-24 * sqrt(K) relative to that sum) and only matters where cancellation
+#: makes |y| small; everywhere else the 1-ulp or 1e-3 bound is the binding one.
+SUM_ALLOWANCE = 2.0 ** -20
+#: The north-star bound on max|y - ref| / max|ref| (the reference's own metric,
+#: ironmule/cuda_native.py:267-268).
+MAX_REL = 1e-3
+
+
+@dataclass
+class Verdict:
+    ok: bool
+    max_rel: float
+    worst_ulps: float
+    violations: int
+    detail: str
+
+
+def check_bf16(y_bits: np.ndarray, ref64: np.ndarray, abssum: np.ndarray) -> Verdict:
+    """bf16 outputs: each within 1 bf16 ulp of the exactly-computed product (plus the
+    fp32 summation allowance).  This is stricter than "within 1 ulp of the bf16-rounded
+    reference".  The 1e-3 max-relative bound is reported but not applied: bf16 rounding
+    alone is up to 2**-9 relative, so that bound is the fp32-output criterion."""
+    y = bf16_to_f32(y_bits).astype(np.float64)
+    err = np.abs(y - ref64)
+    ulp = bf16_ulp(ref64)
+    bound = ulp + SUM_ALLOWANCE * abssum
+    bad = ~(err <= bound)
+    scale = max(float(np.max(np.abs(ref64))), 1e-30)
+    max_rel = float(np.max(err)) / scale if err.size else 0.0
+    worst = float(np.max(err / ulp)) if err.size else 0.0
+    ok = not bad.any()
+    detail = "" if ok else f"{int(bad.sum())} outputs outside 1 ulp+allowance; max_rel={max_rel:.3g}"
+    return Verdict(ok, max_rel, worst, int(bad.sum()), detail)
+
+
+def check_f32(y: np.ndarray, ref64: np.ndarray, abssum: np.ndarray) -> Verdict:
+    """fp32 outputs: each within the fp32 summation allowance of the exact product
+    (plus one fp32 rounding), and max|y-ref|/max|ref| <= 1e-3."""
+    y = np.asarray(y, dtype=np.float64)
+    err = np.abs(y - ref64)
+    bound = SUM_ALLOWANCE * abssum + np.abs(ref64) * 2.0 ** -23
+    bad = ~(err <= bound)
+    scale = max(float(np.max(np.abs(ref64))), 1e-30)
+    max_rel = float(np.max(err)) / scale if err.size else 0.0
+    ok = (not bad.any()) and max_rel <= MAX_REL
+    detail = "" if ok else f"{int(bad.sum())} outputs outside allowance; max_rel={max_rel:.3g}"
+    return Verdict(ok, max_rel, 0.0, int(bad.sum()), detail)
