@@ -1,0 +1,318 @@
+"""Benchmark of the 4-bit affine group-64 qmv on one MI355X.
+
+Default workload (the headline): one Qwen3-4B-shaped decoder layer, all seven
+projections as 4-bit qmv at batch 1 (q 2560->4096, k/v 2560->1024, o 4096->2560,
+gate/up 2560->9728, down 9728->2560), seeded random weights, bf16 activations.
+A step is one pass over one layer's seven projections; consecutive steps rotate over
+36 distinct layer copies (2.05 GB, one Qwen3-4B's worth), so every step streams its
+weights from HBM rather than the 256 MB last-level cache.  Launches are captured in a
+HIP graph (as a decode engine would replay them); inputs are resident in HBM.
+
+Prints one JSON line.  `value` = algorithmic bytes moved per step (packed weights +
+bf16 scales/biases + x + y) / wall time per step, in GB/s.  `roofline` is the dominant
+kernel (gate/up projection, 2560->9728) timed with HIP events over back-to-back graph
+replays on its own stream.  `cpu_baseline` times the oracle's restatement of the
+reference row kernel on the host cores (rank 0, N=1 only).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+LAYER = [("q", 4096, 2560), ("k", 1024, 2560), ("v", 1024, 2560), ("o", 2560, 4096),
+         ("gate", 9728, 2560), ("up", 9728, 2560), ("down", 2560, 9728)]
+LAYERS = 36
+SEED = 20261201
+
+
+def qmv_bytes(n: int, k: int, m: int, y_bytes: int = 2) -> int:
+    """Algorithmic bytes of one call: packed w, bf16 scales and biases, x, y."""
+    return n * k // 2 + n * (k // 64) * 4 + m * k * 2 + m * n * y_bytes
+
+
+def weight_bytes(n: int, k: int) -> int:
+    return n * k // 2 + n * (k // 64) * 4
+
+
+def make_weight(torch, n, k, gen, device):
+    w = torch.randint(0, 2**32, (n, k // 8), dtype=torch.int64, device=device,
+                      generator=gen).to(torch.int32)
+    s = torch.empty((n, k // 64), device=device).uniform_(0.005, 0.02, generator=gen)
+    b = torch.empty((n, k // 64), device=device).uniform_(-0.1, 0.1, generator=gen)
+    return w, s.to(torch.bfloat16), b.to(torch.bfloat16)
+
+
+def make_x(torch, m, k, gen, device):
+    return torch.randn((m, k), device=device, generator=gen).to(torch.bfloat16)
+
+
+class GraphRunner:
+    """Captures a list of launch closures into one HIP graph on a side stream."""
+
+    def __init__(self, torch, launches, stream):
+        self.torch = torch
+        self.stream = stream
+        with torch.cuda.stream(stream):
+            for fn in launches:  # eager warm-up (first-use device set-up happens here)
+                fn()
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=stream):
+            for fn in launches:
+                fn()
+        torch.cuda.synchronize()
+
+    def replay(self):
+        with self.torch.cuda.stream(self.stream):
+            self.graph.replay()
+
+
+def time_graph(torch, runner, repeats, stream):
+    """Seconds per replay: events on the graph's own stream around `repeats` replays."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(repeats):
+        runner.replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / repeats
+
+
+# The layer in decode order: launches that read the same activation share one launch.
+LAUNCHES = [("qkv", ["q", "k", "v"], 2560), ("o", ["o"], 4096), ("gate_up", ["gate", "up"], 2560),
+            ("down", ["down"], 9728)]
+
+
+def bench_layer(torch, native, steps, warmup, device, breakdown=True):
+    """The headline: K steps of one layer's seven projections, rotating 36 layers, as
+    four launches in decode order (q/k/v grouped, o, gate/up grouped, down)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(SEED + 1)
+    index = {name: i for i, (name, _, _) in enumerate(LAYER)}
+    layers = [[make_weight(torch, n, k, gen, device) for (_, n, k) in LAYER]
+              for _ in range(LAYERS)]
+    xs = {k: make_x(torch, 1, k, gen, device) for k in {k for (_, _, k) in LAYER}}
+    ys = {name: torch.empty((1, n), dtype=torch.bfloat16, device=device)
+          for (name, n, _) in LAYER}
+    stream = torch.cuda.Stream(device=device)
+
+    def launch(i, names, k):
+        weights = [layers[i][index[nm]] for nm in names]
+        outs = [ys[nm] for nm in names]
+        return lambda: native.qmv_grouped(weights, [xs[k]] * len(names), outs=outs,
+                                          stream=stream)
+
+    def layer_launches(i):
+        return [launch(i, names, k) for (_, names, k) in LAUNCHES]
+
+    full = GraphRunner(torch, [fn for i in range(LAYERS) for fn in layer_launches(i)], stream)
+    part_n = steps % LAYERS
+    part = (GraphRunner(torch, [fn for i in range(part_n) for fn in layer_launches(i)], stream)
+            if part_n else None)
+    for _ in range(warmup // LAYERS + (1 if warmup % LAYERS else 0)):
+        full.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps // LAYERS):
+        full.replay()
+    if part is not None:
+        part.replay()
+    end.record(stream)
+    end.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = start.elapsed_time(end) / 1e3
+    step_bytes = sum(qmv_bytes(n, k, 1) for (_, n, k) in LAYER)
+
+    if not breakdown:
+        del layers
+        torch.cuda.empty_cache()
+        return {"gpu_s": gpu_s, "wall_s": wall, "step_bytes": step_bytes}
+
+    # each launch type alone: 36 back-to-back launches over distinct weights
+    per_launch = {}
+    for (lname, names, k) in LAUNCHES:
+        runner = GraphRunner(torch, [launch(i, names, k) for i in range(LAYERS)], stream)
+        runner.replay()
+        sec = time_graph(torch, runner, 20, stream) / LAYERS
+        nbytes = sum(qmv_bytes(n, kk, 1) for (nm, n, kk) in LAYER if nm in names)
+        per_launch[lname] = {"us": sec * 1e6, "gbs": nbytes / sec / 1e9, "bytes": nbytes}
+        del runner
+
+    # all seven projections of a layer in one launch (they are independent here)
+    runner = GraphRunner(torch, [
+        (lambda i=i: native.qmv_grouped(layers[i], [xs[k] for (_, _, k) in LAYER],
+                                        outs=[ys[nm] for (nm, _, _) in LAYER], stream=stream))
+        for i in range(LAYERS)], stream)
+    runner.replay()
+    sec = time_graph(torch, runner, 20, stream) / LAYERS
+    one_launch = {"us": sec * 1e6, "gbs": step_bytes / sec / 1e9}
+    del runner, layers
+    torch.cuda.empty_cache()
+    return {"gpu_s": gpu_s, "wall_s": wall, "step_bytes": step_bytes, "per_launch": per_launch,
+            "one_launch": one_launch}
+
+
+def bench_config(torch, native, n, k, ms, y_dtype, copies, device, seed, repeats=10):
+    """Rotating copies (>= 1 GiB total) of one (N, K) weight, one graph per M."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    ws = [make_weight(torch, n, k, gen, device) for _ in range(copies)]
+    stream = torch.cuda.Stream(device=device)
+    out = {}
+    ybytes = 4 if y_dtype == torch.float32 else 2
+    for m in ms:
+        x = make_x(torch, m, k, gen, device)
+        y = torch.empty((m, n), dtype=y_dtype, device=device)
+        runner = GraphRunner(torch, [
+            (lambda w=w, s=s, b=b: native.qmv(w, s, b, x, out=y, stream=stream))
+            for (w, s, b) in ws], stream)
+        runner.replay()
+        sec = time_graph(torch, runner, repeats, stream) / copies
+        out[str(m)] = {"us": sec * 1e6, "gbs": qmv_bytes(n, k, m, ybytes) / sec / 1e9,
+                       "weight_gbs": weight_bytes(n, k) / sec / 1e9}
+        del runner
+    del ws
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(seconds: float = 10.0):
+    """The oracle's restatement of the reference CUDA row kernel (ironmule/cuda_native.py:
+    57-128) on the host cores, over the same layer shapes, rotating 4 layer copies."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    threads = orc.max_threads()
+    copies = [[orc.synthetic(n, k, 1, seed=SEED + 7 + c * 10 + i) for i, (_, n, k) in enumerate(LAYER)]
+              for c in range(4)]
+    step_bytes = sum(qmv_bytes(n, k, 1) for (_, n, k) in LAYER)
+
+    def run(nthreads, budget):
+        for pr in copies[0]:  # warm
+            orc.qmv_rowkernel(pr.w, pr.s, pr.b, pr.x, threads=nthreads)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            for pr in copies[done % 4]:
+                orc.qmv_rowkernel(pr.w, pr.s, pr.b, pr.x, threads=nthreads)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return done * step_bytes / el / 1e9, done, el
+
+    gbs, layers_done, el = run(threads, seconds)
+    gbs1, layers1, el1 = run(1, seconds / 2)
+    del np
+    return {
+        "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"{layers_done} passes over one layer's 7 projections at batch 1 "
+                   f"({step_bytes / 1e6:.1f} MB each, 4 rotating copies), {el:.1f} s, "
+                   f"oracle restatement of the reference row kernel, {threads} OpenMP threads"),
+        "single_thread_gbs": round(gbs1, 3),
+        "single_thread_sample": f"{layers1} passes, {el1:.1f} s, 1 thread",
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=360)
+    ap.add_argument("--warmup", type=int, default=36)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-breakdown", action="store_true",
+                    help="time only the headline layer steps (a short program for profilers)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs "
+                          "are not part of this build", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    from ironmule_amd import _native
+
+    device = "cuda:0"
+    torch.cuda.set_device(0)
+    code, arch, cus = _native.device_check()
+    if code != 0:
+        raise SystemExit(f"unsupported device {arch!r}")
+    print(f"[bench] device {arch} with {cus} CUs; layer workload, {args.steps} steps",
+          file=sys.stderr, flush=True)
+    res = bench_layer(torch, _native, args.steps, args.warmup, device,
+                      breakdown=not args.no_breakdown)
+    if args.no_breakdown:
+        value = res["step_bytes"] * args.steps / res["gpu_s"] / 1e9
+        print(json.dumps({"metric": "layer GB/s (profiling run)", "value": round(value, 2),
+                          "unit": "GB/s", "steps": args.steps}), flush=True)
+        return
+    ms_per_step = res["gpu_s"] / args.steps * 1e3
+    value = res["step_bytes"] * args.steps / res["gpu_s"] / 1e9
+    gate = res["per_launch"]["gate_up"]
+    line = {
+        "metric": "4-bit qmv HBM GB/s (% of peak) + synthetic decode tokens/s at batch 1 and 32",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic: seeded random 4-bit weights, bf16 scales/biases, bf16 x ~ N(0,1)",
+        "config": {"workload": "qwen3-4b decoder layer, 7 projections as 4-bit qmv, batch 1",
+                   "projections": {name: [k, n] for (name, n, k) in LAYER},
+                   "group_size": 64, "batch": 1, "rotating_layers": LAYERS,
+                   "launch": "hip graph per 36 layers; per layer 4 launches in decode order: "
+                             "q/k/v grouped, o, gate/up grouped, down"},
+        "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gate["gbs"], 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gate["gbs"] / PEAK_HBM_GBS, 4),
+                     "traffic": None,
+                     "kernel": "qmv_fixed_kernel<1,4,5>: gate+up grouped launch, 2 x (2560->9728), M=1",
+                     "bytes_per_launch": gate["bytes"],
+                     "avg_launch_us": round(gate["us"], 3)},
+        "per_launch": {k: {"us": round(v["us"], 3), "gbs": round(v["gbs"], 1)}
+                       for k, v in res["per_launch"].items()},
+        "layer_one_launch": {"us": round(res["one_launch"]["us"], 3),
+                             "gbs": round(res["one_launch"]["gbs"], 1),
+                             "note": "all 7 independent projections in one grouped launch"},
+        "decode_tokens_per_s": {"batch_1": None, "batch_32": None},
+    }
+    if not args.no_extra:
+        print("[bench] secondary configs", file=sys.stderr, flush=True)
+        line["configs"] = {
+            "c1_2560x2560": bench_config(torch, _native, 2560, 2560, [1], torch.bfloat16, 300,
+                                         device, SEED),
+            "c3_k3840_n15360": bench_config(torch, _native, 15360, 3840, [1, 2, 4, 8, 16, 32],
+                                            torch.bfloat16, 36, device, SEED + 2),
+            "c4_lm_head_fp32": bench_config(torch, _native, 151936, 2560, [1, 32],
+                                            torch.float32, 5, device, SEED + 3, repeats=4),
+        }
+    if not args.no_cpu:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

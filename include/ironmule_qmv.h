@@ -1,0 +1,146 @@
+/*
+ * ironmule_qmv.h — C ABI of the MI355X (gfx950) 4-bit affine group-quantised
+ * matrix-vector product ("qmv") library, libironmule_qmv.so.
+ *
+ * Weight format (the reference's, unchanged, so callers pass their buffers as-is):
+ *   w       uint32 (N, K/8), eight 4-bit values per word, low nibble first
+ *           (element j of word u is (u >> 4j) & 0xF)
+ *   scales  bf16 bit patterns (N, K/64), biases bf16 bit patterns (N, K/64)
+ *   weight  scale * q + bias, q in 0..15, group size 64, bits 4
+ *   x       bf16 (M, K) activation rows; y (M, N) bf16 or fp32
+ *
+ * Contract shared by every entry point:
+ *   - all array pointers are device pointers; the caller allocates them;
+ *   - the library never allocates, frees or synchronises per call; work is queued on
+ *     `stream` (a hipStream_t, NULL for the default stream) and the call returns;
+ *   - every output element is written exactly once (outputs need no initialisation);
+ *   - the library keeps no state between calls and is reentrant; per-device set-up
+ *     (architecture check, kernel attributes) happens once, on first use;
+ *   - errors are returned as codes, never raised; imq_last_error() describes the last
+ *     one on the calling thread.
+ *
+ * Alignment: w and every x row 16-byte aligned, ldx a multiple of 8 elements; scales,
+ * biases 2-byte aligned; y 2-byte (bf16) or 4-byte (fp32) aligned.
+ */
+#ifndef IRONMULE_QMV_H
+#define IRONMULE_QMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IMQ_ABI_VERSION 1
+
+#ifndef IMQ_API
+#define IMQ_API __attribute__((visibility("default")))
+#endif
+
+/* Return codes. */
+#define IMQ_OK 0
+#define IMQ_EINVAL 1       /* bad pointer, shape, stride, alignment or dtype code */
+#define IMQ_EUNSUPPORTED 2 /* well-formed but outside the kernels: bits != 4, gs != 64, M > 32 */
+#define IMQ_EUNAVAILABLE 3 /* no HIP device, or the current device is not gfx950 */
+#define IMQ_ELAUNCH 6      /* the HIP runtime refused the launch */
+
+/* Output dtype codes. */
+#define IMQ_BF16 0
+#define IMQ_F32 1
+#define IMQ_F16 2 /* imq_dequant only */
+
+/* Largest number of activation rows one call serves with a single weight sweep. */
+#define IMQ_MAX_ROWS 32
+
+/* Largest number of weights one imq_qmv_grouped call serves. */
+#define IMQ_MAX_PROBLEMS 8
+
+/* One weight and its activation/output rows, for imq_qmv_grouped. */
+typedef struct imq_problem {
+  const uint32_t* w;       /* (N, K/8) packed words */
+  const uint16_t* scales;  /* (N, K/64) bf16 */
+  const uint16_t* biases;  /* (N, K/64) bf16 */
+  const uint16_t* x;       /* (M, K) bf16, rows ldx elements apart */
+  int64_t ldx;
+  void* y;                 /* (M, N) bf16 or fp32, rows ldy elements apart */
+  int64_t ldy;
+  int32_t N;
+  int32_t K;
+} imq_problem;
+
+/* The ABI version this library implements (IMQ_ABI_VERSION). */
+IMQ_API int32_t imq_abi_version(void);
+
+/* IMQ_OK if the current HIP device is a gfx950 the kernels run on.  Fills `arch`
+ * (NUL-terminated, may be NULL) and `cu_count` (may be NULL). */
+IMQ_API int32_t imq_device_check(char* arch, size_t arch_len, int32_t* cu_count);
+
+/*
+ * y[m][n] = sum_k (scales[n][k/64] * q[n][k] + biases[n][k/64]) * x[m][k]
+ * for m < M (1..32), n < N, with fp32 accumulation; y rounded to bf16 (nearest even)
+ * or stored as fp32 per y_dtype.  The weight is read from memory once for all M rows
+ * (the shared-weight multi-request form).
+ *
+ * Replaces the reference's per-call kernel launches of the 4-bit qmv:
+ *   ironmule/qmv_k3840.py:299-310        run(kernel, w, scales, biases, x, N, K)  (M = 1)
+ *   ironmule/qmv_variant.py:116-129      GatedVariantLinear.__call__ kernel branch (M = 1)
+ *   ironmule/cuda_native.py:155-168      _qmv(x, w, scales, biases)              (M <= 8)
+ *   ironmule/cuda_native.py:171-179      matmul(...) decode branch, LM head via
+ *                                         NativeQuantizedEmbedding.as_linear (227-229)
+ * x rows are `ldx` elements apart, y rows `ldy` elements apart.
+ */
+IMQ_API int32_t imq_qmv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                const uint16_t* x, int64_t ldx, void* y, int64_t ldy, int32_t M, int32_t N,
+                int32_t K, int32_t group_size, int32_t bits, int32_t y_dtype, void* stream);
+
+/*
+ * The same product for `count` separate activation vectors xs[i] (each (1, K)) and
+ * separate outputs ys[i] (each (1, N)), one weight sweep for all of them.
+ *
+ * Replaces:
+ *   ironmule/qmv_shared.py:169-181       run_shared(w, scales, biases, vectors, N)  (K = 3840)
+ *   ironmule/qmv_fast_shared.py:161-172  run_fast(w, scales, biases, vectors, N, K)
+ * `xs` and `ys` are host arrays of `count` device pointers (1 <= count <= 32).
+ */
+IMQ_API int32_t imq_qmv_multi(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                      const uint16_t* const* xs, void* const* ys, int32_t count, int32_t N,
+                      int32_t K, int32_t group_size, int32_t bits, int32_t y_dtype,
+                      void* stream);
+
+/*
+ * imq_qmv for `count` (1..IMQ_MAX_PROBLEMS) weights in one launch, every one with the
+ * same M, group size, bits and output dtype; each weight is read once for its M rows.
+ * Projections that read the same activation (q/k/v, gate/up) take the same x pointer.
+ *
+ * Replaces the reference's fused projection groups, ironmule/fast.py:186-215
+ * (fuse_projections: q/k/v and gate/up concatenated into one quantised linear so one
+ * launch serves them); here the weights stay separate buffers and the launch is shared.
+ */
+IMQ_API int32_t imq_qmv_grouped(const imq_problem* problems, int32_t count, int32_t M,
+                                int32_t group_size, int32_t bits, int32_t y_dtype,
+                                void* stream);
+
+/*
+ * out[n][k] = scales[n][k/64] * q[n][k] + biases[n][k/64] as fp32 (bit-exact:
+ * scale*q is exact in fp32, so only the add rounds), or that fp32 value rounded
+ * to bf16 / fp16 (nearest even) per out_dtype.  out is (N, K) contiguous.
+ *
+ * Replaces mx.dequantize on the path:
+ *   ironmule/cuda_native.py:177-179      prefill: dequantise (fp16) then GEMM
+ *   ironmule/cuda_native.py:265-266      probe reference: dequantise with fp32 scales
+ *   ironmule/numeric_plans.py:462-464    the `dequantize` plan's fp32 weights
+ */
+IMQ_API int32_t imq_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                    void* out, int32_t out_dtype, int32_t N, int32_t K, int32_t group_size,
+                    int32_t bits, void* stream);
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated to
+ * len) and returns the last error code (IMQ_OK if none). */
+IMQ_API int32_t imq_last_error(char* buf, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IRONMULE_QMV_H */

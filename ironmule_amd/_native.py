@@ -1,0 +1,259 @@
+"""The ctypes boundary to libironmule_qmv.so (C ABI: include/ironmule_qmv.h).
+
+Everything above this module passes torch tensors; everything below it is plain device
+pointers, sizes and a HIP stream.  There is no fallback: if the library is missing or
+the device is not a gfx950, calls raise `NativeUnavailable`.
+
+Tensor conventions (the reference's buffers, ironmule/qmv_k3840.py:379-408):
+  w       torch.int32 or torch.uint32 (N, K/8): packed words, low nibble first
+  scales  torch.bfloat16 (N, K/64);  biases torch.bfloat16 (N, K/64)
+  x       torch.bfloat16 (K,) or (M, K), M <= 32
+  y       torch.bfloat16 or torch.float32 (M, N)
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import threading
+
+import torch
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "libironmule_qmv.so")
+HEADER_PATH = os.path.join(ROOT, "include", "ironmule_qmv.h")
+
+GROUP_SIZE = 64
+BITS = 4
+MAX_ROWS = 32
+
+IMQ_OK, IMQ_EINVAL, IMQ_EUNSUPPORTED, IMQ_EUNAVAILABLE, IMQ_ELAUNCH = 0, 1, 2, 3, 6
+IMQ_BF16, IMQ_F32, IMQ_F16 = 0, 1, 2
+_DTYPE_CODE = {torch.bfloat16: IMQ_BF16, torch.float32: IMQ_F32, torch.float16: IMQ_F16}
+
+
+class NativeUnavailable(RuntimeError):
+    """The HIP library is not built, not loadable, or the device is not a gfx950."""
+
+
+class NativeError(RuntimeError):
+    """The C ABI refused a call; `code` is its IMQ_* return code."""
+
+    def __init__(self, code: int, message: str) -> None:
+        super().__init__(f"[imq code {code}] {message}")
+        self.code = code
+
+
+_lib = None
+_lock = threading.Lock()
+
+_P = ctypes.c_void_p
+_I32, _I64 = ctypes.c_int32, ctypes.c_int64
+MAX_PROBLEMS = 8
+
+
+class Problem(ctypes.Structure):
+    """imq_problem: one weight and its activation/output rows for imq_qmv_grouped."""
+
+    _fields_ = [("w", _P), ("scales", _P), ("biases", _P), ("x", _P), ("ldx", _I64),
+                ("y", _P), ("ldy", _I64), ("N", _I32), ("K", _I32)]
+
+
+_SIGNATURES = {
+    "imq_abi_version": ([], _I32),
+    "imq_device_check": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(_I32)], _I32),
+    "imq_qmv": ([_P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P], _I32),
+    "imq_qmv_multi": ([_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P], _I32),
+    "imq_qmv_grouped": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P], _I32),
+    "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
+    "imq_last_error": ([ctypes.c_char_p, ctypes.c_size_t], _I32),
+}
+
+
+def declared_functions() -> list[str]:
+    """Every function the public header declares (what the library must export)."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*IMQ_API\s+int32_t\s+(imq_\w+)\s*\(", text, flags=re.M)
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once.  Raises NativeUnavailable if it is not built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise NativeUnavailable(
+                        f"{LIB_PATH} is not built; run `python -m ironmule_amd.build`")
+                try:
+                    handle = ctypes.CDLL(LIB_PATH)
+                except OSError as exc:
+                    raise NativeUnavailable(f"cannot load {LIB_PATH}: {exc}") from exc
+                for name, (args, res) in _SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.argtypes = args
+                    fn.restype = res
+                _lib = handle
+    return _lib
+
+
+def last_error() -> tuple[int, str]:
+    buf = ctypes.create_string_buffer(512)
+    code = lib().imq_last_error(buf, len(buf))
+    return int(code), buf.value.decode(errors="replace")
+
+
+def _check(code: int) -> None:
+    if code != IMQ_OK:
+        _, msg = last_error()
+        if code == IMQ_EUNAVAILABLE:
+            raise NativeUnavailable(msg)
+        raise NativeError(code, msg)
+
+
+def device_check() -> tuple[int, str, int]:
+    """(code, arch, cu_count) for the current HIP device."""
+    arch = ctypes.create_string_buffer(64)
+    cus = _I32(0)
+    code = lib().imq_device_check(arch, len(arch), ctypes.byref(cus))
+    return int(code), arch.value.decode(), int(cus.value)
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(int(stream.cuda_stream))
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def check_weights(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> tuple[int, int]:
+    """(N, K) of a well-formed 4-bit group-64 weight on a GPU, else ValueError."""
+    if w.dtype not in (torch.int32, torch.uint32):
+        raise ValueError(f"w must be int32/uint32 packed words, got {w.dtype}")
+    if w.dim() != 2:
+        raise ValueError(f"w must be (N, K/8), got {tuple(w.shape)}")
+    n, k = int(w.shape[0]), int(w.shape[1]) * 8
+    if k % GROUP_SIZE:
+        raise ValueError(f"K={k} is not a multiple of {GROUP_SIZE}")
+    for name, t in (("scales", scales), ("biases", biases)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+        if tuple(t.shape) != (n, k // GROUP_SIZE):
+            raise ValueError(f"{name} must be {(n, k // GROUP_SIZE)}, got {tuple(t.shape)}")
+    for name, t in (("w", w), ("scales", scales), ("biases", biases)):
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a GPU")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    return n, k
+
+
+def qmv(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, x: torch.Tensor,
+        out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+        stream=None) -> torch.Tensor:
+    """y = x @ dequantize(w, scales, biases).T for M = x.shape[0] <= 32 rows, one weight
+    sweep.  x is bf16 (K,) or (M, K); y is bf16 (default) or fp32, shape (M, N)."""
+    n, k = check_weights(w, scales, biases)
+    x2 = x.reshape(1, -1) if x.dim() == 1 else x
+    if x2.dim() != 2 or int(x2.shape[1]) != k:
+        raise ValueError(f"x must be (M, {k}), got {tuple(x.shape)}")
+    if x2.dtype != torch.bfloat16:
+        raise ValueError(f"x must be bfloat16, got {x2.dtype}")
+    m = int(x2.shape[0])
+    if not 1 <= m <= MAX_ROWS:
+        raise ValueError(f"the qmv kernels take 1 to {MAX_ROWS} rows, got {m}")
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    dtype = out_dtype or (out.dtype if out is not None else torch.bfloat16)
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"output must be bfloat16 or float32, got {dtype}")
+    if out is None:
+        out = torch.empty((m, n), dtype=dtype, device=w.device)
+    elif tuple(out.shape) != (m, n) or out.dtype != dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous (M, N) tensor of the output dtype")
+    _check(lib().imq_qmv(_ptr(w), _ptr(scales), _ptr(biases), _ptr(x2), k, _ptr(out), n,
+                         m, n, k, GROUP_SIZE, BITS, _DTYPE_CODE[dtype], _stream(stream)))
+    return out
+
+
+def qmv_multi(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+              vectors: list[torch.Tensor], out_dtype: torch.dtype = torch.bfloat16,
+              outs: list[torch.Tensor] | None = None, stream=None) -> list[torch.Tensor]:
+    """One weight sweep, len(vectors) separate results (each (1, N))."""
+    n, k = check_weights(w, scales, biases)
+    count = len(vectors)
+    if not 1 <= count <= MAX_ROWS:
+        raise ValueError(f"1 to {MAX_ROWS} vectors, got {count}")
+    xs = []
+    for v in vectors:
+        if v.dtype != torch.bfloat16 or v.numel() != k:
+            raise ValueError(f"every vector must be bf16 with {k} elements")
+        xs.append(v if v.is_contiguous() else v.contiguous())
+    if outs is None:
+        outs = [torch.empty((1, n), dtype=out_dtype, device=w.device) for _ in range(count)]
+    xa = (ctypes.c_void_p * count)(*[t.data_ptr() for t in xs])
+    ya = (ctypes.c_void_p * count)(*[t.data_ptr() for t in outs])
+    _check(lib().imq_qmv_multi(_ptr(w), _ptr(scales), _ptr(biases), xa, ya, count, n, k,
+                               GROUP_SIZE, BITS, _DTYPE_CODE[out_dtype], _stream(stream)))
+    return outs
+
+
+def qmv_grouped(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
+                xs: list[torch.Tensor], outs: list[torch.Tensor] | None = None,
+                out_dtype: torch.dtype = torch.bfloat16, stream=None) -> list[torch.Tensor]:
+    """One launch for up to 8 weights, each with its own (M, K_i) activation rows (the
+    same tensor may serve several weights, e.g. q/k/v); returns the (M, N_i) outputs."""
+    count = len(weights)
+    if not 1 <= count <= MAX_PROBLEMS or len(xs) != count:
+        raise ValueError(f"1 to {MAX_PROBLEMS} weights with one activation each")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"output must be bfloat16 or float32, got {out_dtype}")
+    probs = (Problem * count)()
+    m = None
+    result = []
+    for i, ((w, s, b), x) in enumerate(zip(weights, xs)):
+        n, k = check_weights(w, s, b)
+        x2 = x.reshape(1, -1) if x.dim() == 1 else x
+        if x2.dtype != torch.bfloat16 or x2.dim() != 2 or int(x2.shape[1]) != k:
+            raise ValueError(f"activation {i} must be bf16 (M, {k})")
+        if not x2.is_contiguous():
+            raise ValueError(f"activation {i} must be contiguous")
+        if m is None:
+            m = int(x2.shape[0])
+        elif int(x2.shape[0]) != m:
+            raise ValueError("every weight of one call takes the same number of rows")
+        if outs is None:
+            y = torch.empty((m, n), dtype=out_dtype, device=w.device)
+        else:
+            y = outs[i]
+            if tuple(y.shape) != (m, n) or y.dtype != out_dtype or not y.is_contiguous():
+                raise ValueError(f"output {i} must be a contiguous ({m}, {n}) {out_dtype} tensor")
+        probs[i] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x2.data_ptr(), k,
+                           y.data_ptr(), n, n, k)
+        result.append(y)
+    if not 1 <= m <= MAX_ROWS:
+        raise ValueError(f"the qmv kernels take 1 to {MAX_ROWS} rows, got {m}")
+    _check(lib().imq_qmv_grouped(probs, count, m, GROUP_SIZE, BITS, _DTYPE_CODE[out_dtype],
+                                 _stream(stream)))
+    return result
+
+
+def dequant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+            out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
+            stream=None) -> torch.Tensor:
+    """The dense (N, K) weight, scale*q + bias, as fp32 (bit-exact) or rounded to
+    bf16/fp16."""
+    n, k = check_weights(w, scales, biases)
+    if out_dtype not in _DTYPE_CODE:
+        raise ValueError(f"out_dtype must be fp32, bf16 or fp16, got {out_dtype}")
+    if out is None:
+        out = torch.empty((n, k), dtype=out_dtype, device=w.device)
+    _check(lib().imq_dequant(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out),
+                             _DTYPE_CODE[out_dtype], n, k, GROUP_SIZE, BITS, _stream(stream)))
+    return out

@@ -1,0 +1,88 @@
+"""The C ABI library without a GPU: it loads, exports every function its header
+declares, and refuses malformed calls with the documented codes before touching a
+device.  (No compute call is made here.)"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import pytest
+
+from ironmule_amd import _native
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_native.LIB_PATH):
+        from ironmule_amd import build
+        build.build()
+    return _native.lib()
+
+
+def test_every_declared_function_is_exported(lib):
+    declared = _native.declared_functions()
+    assert set(declared) == set(_native._SIGNATURES), declared
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.imq_abi_version() == 1
+
+
+def _qmv(lib, **over):
+    args = dict(w=1 << 20, s=1 << 20, b=1 << 20, x=1 << 20, ldx=2560, y=1 << 20, ldy=2560,
+                M=1, N=2560, K=2560, gs=64, bits=4, dtype=0)
+    args.update(over)
+    P = ctypes.c_void_p
+    return lib.imq_qmv(P(args["w"]), P(args["s"]), P(args["b"]), P(args["x"]), args["ldx"],
+                       P(args["y"]), args["ldy"], args["M"], args["N"], args["K"], args["gs"],
+                       args["bits"], args["dtype"], None)
+
+
+@pytest.mark.parametrize("over,code", [
+    ({"bits": 8}, _native.IMQ_EUNSUPPORTED),
+    ({"gs": 128}, _native.IMQ_EUNSUPPORTED),
+    ({"K": 100}, _native.IMQ_EINVAL),
+    ({"K": 0}, _native.IMQ_EINVAL),
+    ({"N": 0}, _native.IMQ_EINVAL),
+    ({"w": 0}, _native.IMQ_EINVAL),
+    ({"w": (1 << 20) + 4}, _native.IMQ_EINVAL),
+    ({"M": 0}, _native.IMQ_EINVAL),
+    ({"M": 33}, _native.IMQ_EUNSUPPORTED),
+    ({"x": 0}, _native.IMQ_EINVAL),
+    ({"x": (1 << 20) + 2}, _native.IMQ_EINVAL),
+    ({"dtype": 7}, _native.IMQ_EINVAL),
+    ({"M": 2, "ldx": 2564}, _native.IMQ_EINVAL),
+    ({"M": 2, "ldy": 100}, _native.IMQ_EINVAL),
+])
+def test_malformed_calls_are_refused_with_codes(lib, over, code):
+    assert _qmv(lib, **over) == code
+    got, msg = _native.last_error()
+    assert got == code and msg
+
+
+def test_dequant_refuses_bad_dtype(lib):
+    P = ctypes.c_void_p
+    assert lib.imq_dequant(P(1 << 20), P(1 << 20), P(1 << 20), P(1 << 20), 9, 64, 64, 64, 4,
+                           None) == _native.IMQ_EINVAL
+
+
+def test_multi_refuses_too_many_vectors(lib):
+    P = ctypes.c_void_p
+    arr = (P * 33)(*([1 << 20] * 33))
+    assert lib.imq_qmv_multi(P(1 << 20), P(1 << 20), P(1 << 20), arr, arr, 33, 64, 64, 64, 4,
+                             0, None) == _native.IMQ_EUNSUPPORTED
+
+
+def test_python_side_validates_before_the_abi():
+    import torch
+    w = torch.zeros((8, 8), dtype=torch.int32)
+    s = torch.zeros((8, 1), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        _native.check_weights(w, s, s)
+    with pytest.raises(ValueError, match="bfloat16"):
+        _native.check_weights(w, s.float(), s)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        _native.check_weights(torch.zeros((8, 3), dtype=torch.int32), s, s)
