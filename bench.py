@@ -239,6 +239,9 @@ def main() -> None:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-breakdown", action="store_true",
                     help="time only the headline layer steps (a short program for profilers)")
+    ap.add_argument("--only", default=None, metavar="N,K,M[,f32]",
+                    help="time one qmv shape over rotating weights (>= 1 GiB) and exit; "
+                         "a short program for profilers")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs "
@@ -254,6 +257,15 @@ def main() -> None:
     code, arch, cus = _native.device_check()
     if code != 0:
         raise SystemExit(f"unsupported device {arch!r}")
+    if args.only:
+        parts = args.only.split(",")
+        n, k, m = (int(v) for v in parts[:3])
+        y_dtype = torch.float32 if len(parts) > 3 and parts[3] == "f32" else torch.bfloat16
+        copies = max(2, -(-(1 << 30) // weight_bytes(n, k)))
+        res = bench_config(torch, _native, n, k, [m], y_dtype, copies, device, SEED + 9)
+        print(json.dumps({"metric": "qmv GB/s (profiling run)", "shape": [n, k, m],
+                          "copies": copies, **res[str(m)]}), flush=True)
+        return
     print(f"[bench] device {arch} with {cus} CUs; layer workload, {args.steps} steps",
           file=sys.stderr, flush=True)
     res = bench_layer(torch, _native, args.steps, args.warmup, device,

@@ -21,6 +21,8 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     # Packed fp32 arithmetic is switched off for device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results straight into VGPRs (no accumulation-register round trips)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"),
     "-Wall",
 ]

@@ -40,6 +40,13 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
 
 constexpr int kThreads = 256;  // 4 wavefronts of 64
 constexpr int kGroup = 64;
@@ -457,49 +464,20 @@ __global__ __launch_bounds__(kThreads) void qmv_fixed_kernel(LaunchArgs a) {
 
 // ------------------------------------------------------- MFMA kernel (more rows)
 //
-// A workgroup owns 16*NT weight rows of one problem; its four wavefronts split K into
-// quarters and add their partial sums through LDS at the end.  In a wavefront, lane
-// (n = lane%16, kg = lane/16) holds, per group of 64 and per 16-row tile, the two words
-// 8g+2kg and 8g+2kg+1 of weight row n (one 8-byte load): as B operands of two
-// v_mfma_f32_16x16x32_bf16 they cover the group's words {0,2,4,6} and {1,3,5,7}.  The
-// A operands are the matching x words of activation row m = lane%16 (+16 per m-tile),
-// read from memory (they stay in L2) and put in pair order.  D[m][n] lands in lane
-// (n, kg) as rows m = 4*kg + r, r < 4.  Per group: acc += s*P + (b - 128 s)*P1, where P1
-// is the same MFMA against a ones operand, i.e. sum x per group.
-
-template <int MT, int NT>
-struct MfmaStage {
-  uint2 w[NT];
-  uint32_t s[NT];
-  uint32_t b[NT];
-  uint4 x0[MT];
-  uint4 x1[MT];
-};
-
-template <int MT, int NT>
-__device__ __forceinline__ void mfma_load(MfmaStage<MT, NT>& st, const uint32_t* const (&wrow)[NT],
-                                          const uint16_t* const (&srow)[NT],
-                                          const uint16_t* const (&brow)[NT],
-                                          const uint16_t* const (&xr)[MT],
-                                          const bool (&has_x)[MT], int g) {
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    st.w[t] = *reinterpret_cast<const uint2*>(wrow[t] + 8 * g);
-    st.s[t] = srow[t][g];
-    st.b[t] = brow[t][g];
-  }
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    if (has_x[mt]) {
-      const uint4* xv = reinterpret_cast<const uint4*>(xr[mt] + 64 * g);
-      st.x0[mt] = xv[0];
-      st.x1[mt] = xv[1];
-    } else {
-      st.x0[mt] = make_uint4(0, 0, 0, 0);
-      st.x1[mt] = make_uint4(0, 0, 0, 0);
-    }
-  }
-}
+// A workgroup owns 16*NT weight rows of one problem; its four wavefronts split the
+// groups of 64 into quarters and add their partial sums through LDS at the end.  In a
+// wavefront, lane (n = lane%16, kg = lane/16) holds, per group g and per 16-row tile,
+// the two words 8g+2kg and 8g+2kg+1 of weight row n (one 8-byte load): as B operands of
+// two v_mfma_f32_16x16x32_bf16 they cover the group's words {0,2,4,6} and {1,3,5,7}.
+// The A operands are the matching x words of activation row m = lane%16 (+16 per
+// m-tile), read from memory (they stay in L2) one group ahead and put in pair order.
+// D[m][n] lands in lane (n, kg) as rows m = 4*kg + r, r < 4.  Per group:
+//     acc += s * P + (b - 128 s) * P1,
+// where P1 is the same MFMA pair against a ones operand, i.e. sum x over the group.
+//
+// Memory-level parallelism: the weight words of GS groups are loaded at once, and the
+// next GS groups are in flight while these compute.  The scales and biases of the
+// workgroup's rows are staged once in LDS as (s | b << 16) words, [row][group].
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   u32x4_t t = {v.x, v.y, v.z, v.w};
@@ -512,87 +490,186 @@ __device__ __forceinline__ bf16x8_t unpack_word(uint32_t u, uint32_t magic) {
   return __builtin_bit_cast(bf16x8_t, t);
 }
 
-template <int MT, int NT>
-__device__ __forceinline__ void mfma_compute(const MfmaStage<MT, NT>& st,
-                                             f32x4_t (&acc)[NT][MT], uint32_t magic) {
-  const u32x4_t ones_u = {kOnes, kOnes, kOnes, kOnes};
-  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  bf16x8_t a0[MT], a1[MT];
-  f32x4_t sumx[MT];
+// One stage: the weight words (per tile) and the x words (per m-tile) of GS groups.
+template <int MT, int NT, int GS>
+struct MfmaStage {
+  uint2 w[GS][NT];
+  uint4 x0[GS][MT];
+  uint4 x1[GS][MT];
+};
+
+// Weight words of groups g .. g+GS-1 as raw buffer loads (one lane offset per tile plus
+// immediate offsets; reads past the matrix return zero, so no group needs a clamp), and
+// the matching x words.  Groups past the wavefront's range are loaded but never used.
+//
+// Every stage is always issued, so the number of loads in flight is the same on every
+// path and the compiler's waits stay exact (a conditional stage would make it wait for
+// everything).  Groups past the range get an offset past the buffer: the hardware
+// returns zero for them without touching memory.
+constexpr uint32_t kPastBuffer = 0x80000000u;
+
+template <int MT, int NT, int GS>
+__device__ __forceinline__ void load_stage(MfmaStage<MT, NT, GS>& st, __amdgpu_buffer_rsrc_t wrsrc,
+                                           const uint32_t (&voff)[NT],
+                                           const uint16_t* const (&xr)[MT], int g, int g1) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    a0[mt] = as_bf16x8(pair_order(st.x0[mt]));
-    a1[mt] = as_bf16x8(pair_order(st.x1[mt]));
-    sumx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mt], ones, zero, 0, 0, 0);
-    sumx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], ones, sumx[mt], 0, 0, 0);
+  for (int i = 0; i < GS; ++i) {
+    const uint32_t goff = g + i < g1 ? 32u * (g + i) : kPastBuffer;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wrsrc, voff[t] + goff, 0, 0);
+      st.w[i][t] = make_uint2(v.x, v.y);
+    }
   }
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const bf16x8_t b0 = unpack_word(st.w[t].x, magic);
-    const bf16x8_t b1 = unpack_word(st.w[t].y, magic);
-    const float sc = bf16_bits_to_f32(st.s[t]);
-    const float bp = fmaf(-128.0f, sc, bf16_bits_to_f32(st.b[t]));
+  for (int i = 0; i < GS; ++i) {
+    const int gg = g + i < g1 ? g + i : g1 - 1;  // x rows end at K: stay inside them
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      f32x4_t p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mt], b0, zero, 0, 0, 0);
-      p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], b1, p, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        acc[t][mt][r] = fmaf(sc, p[r], fmaf(bp, sumx[mt][r], acc[t][mt][r]));
+      const uint4* xv = reinterpret_cast<const uint4*>(xr[mt] + 64 * gg);
+      st.x0[i][mt] = xv[0];
+      st.x1[i][mt] = xv[1];
     }
   }
 }
 
-template <int MT, int NT>
+template <int MT, int NT, int GS>
+__device__ __forceinline__ void compute_stage(const MfmaStage<MT, NT, GS>& st, const uint32_t* sb,
+                                              int G, int g, int g1, f32x4_t (&acc)[NT][MT],
+                                              uint32_t magic) {
+  const u32x4_t ones_u = {kOnes, kOnes, kOnes, kOnes};
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < GS; ++i) {
+    if (g + i >= g1) break;
+    bf16x8_t a0[MT], a1[MT];
+    f32x4_t sumx[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      a0[mt] = as_bf16x8(pair_order(st.x0[i][mt]));
+      a1[mt] = as_bf16x8(pair_order(st.x1[i][mt]));
+      sumx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mt], ones, zero, 0, 0, 0);
+      sumx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], ones, sumx[mt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const bf16x8_t b0 = unpack_word(st.w[i][t].x, magic);
+      const bf16x8_t b1 = unpack_word(st.w[i][t].y, magic);
+      const uint32_t pk = sb[t * 16 * G + g + i];
+      const float sc = bf16_bits_to_f32(pk & 0xffffu);
+      const float bp = fmaf(-128.0f, sc, __uint_as_float(pk & 0xffff0000u));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        f32x4_t p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mt], b0, zero, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], b1, p, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[t][mt][r] = fmaf(sc, p[r], fmaf(bp, sumx[mt][r], acc[t][mt][r]));
+      }
+    }
+  }
+}
+
+template <int MT, int NT, int GS>
 __global__ __launch_bounds__(kThreads) void qmv_mfma_kernel(LaunchArgs a) {
+  extern __shared__ uint32_t sb_lds[];  // (s | b << 16) per [row of the workgroup][group]
   __shared__ f32x4_t red[3][NT][MT][64];
   const Problem& P = a.p[find_problem(a, blockIdx.x)];
   const int K = P.K, N = P.N, M = a.M;
   const int G = K >> 6, W = K >> 3;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // the wave index is uniform across the wavefront: keep it (and the group range and
+  // loop control derived from it) in scalar registers, so branches are scalar
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, kg = lane >> 4;
   const int row0 = (blockIdx.x - P.first) * (16 * NT);
   const uint32_t magic = in_vgpr(kMagic);
 
-  const uint32_t* wrow[NT];
-  const uint16_t* srow[NT];
-  const uint16_t* brow[NT];
+  // Scales and biases of the workgroup's rows (one contiguous span each), loaded first
+  // so they land before the weights: 16-byte loads when aligned and whole, else halves.
+  constexpr int SBV = 4;  // uint4 per thread: spans up to 8192 halves (G <= 8192 / (16 NT))
+  const int span = 16 * NT * G;
+  const uint16_t* s0 = P.s + (size_t)row0 * G;
+  const uint16_t* b0 = P.b + (size_t)row0 * G;
+  const bool vec = ((reinterpret_cast<uintptr_t>(s0) | reinterpret_cast<uintptr_t>(b0)) & 15) == 0 &&
+                   row0 + 16 * NT <= N && span % 8 == 0 && span <= 8 * kThreads * SBV;
+  uint4 sv[SBV], bv[SBV];
+  if (vec) {
+#pragma unroll
+    for (int q = 0; q < SBV; ++q) {
+      const int idx = tid + kThreads * q;
+      if (idx * 8 < span) {
+        sv[q] = reinterpret_cast<const uint4*>(s0)[idx];
+        bv[q] = reinterpret_cast<const uint4*>(b0)[idx];
+      }
+    }
+  }
+
+  // the host guarantees N * K / 2 < 2^31, so byte offsets fit the buffer's 32 bits
+  const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(P.w, (uint32_t)((size_t)N * W * 4));
+  uint32_t voff[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int row = row0 + 16 * t + n;
     const int r = row < N ? row : N - 1;
-    wrow[t] = P.w + (size_t)r * W + 2 * kg;
-    srow[t] = P.s + (size_t)r * G;
-    brow[t] = P.b + (size_t)r * G;
+    voff[t] = ((uint32_t)r * (uint32_t)W + 2u * kg) * 4u;
   }
+  // rows m >= M feed MFMA rows whose results are never stored: read row M-1 for them
   const uint16_t* xr[MT];
-  bool has_x[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = n + 16 * mt;
-    has_x[mt] = m < M;
-    xr[mt] = has_x[mt] ? x_row(a, P, m) + 16 * kg : nullptr;
+    xr[mt] = x_row(a, P, m < M ? m : M - 1) + 16 * kg;
   }
 
-  // this wavefront's quarter of the groups
+  // this wavefront's quarter of the groups, in double-buffered stages of GS groups
   const int g0 = (G * wave) >> 2, g1 = (G * (wave + 1)) >> 2;
+  MfmaStage<MT, NT, GS> sa, sb2;
+  load_stage<MT, NT, GS>(sa, wrsrc, voff, xr, g0, g1 > g0 ? g1 : g0 + 1);
+
+  if (vec) {
+#pragma unroll
+    for (int q = 0; q < SBV; ++q) {
+      const int idx = tid + kThreads * q;
+      if (idx * 8 < span) {
+        const uint32_t ss[4] = {sv[q].x, sv[q].y, sv[q].z, sv[q].w};
+        const uint32_t bb[4] = {bv[q].x, bv[q].y, bv[q].z, bv[q].w};
+        uint4 lo, hi;  // entries idx*8 .. idx*8+7: (s | b << 16)
+        lo.x = (ss[0] & 0xffffu) | (bb[0] << 16);
+        lo.y = (ss[0] >> 16) | (bb[0] & 0xffff0000u);
+        lo.z = (ss[1] & 0xffffu) | (bb[1] << 16);
+        lo.w = (ss[1] >> 16) | (bb[1] & 0xffff0000u);
+        hi.x = (ss[2] & 0xffffu) | (bb[2] << 16);
+        hi.y = (ss[2] >> 16) | (bb[2] & 0xffff0000u);
+        hi.z = (ss[3] & 0xffffu) | (bb[3] << 16);
+        hi.w = (ss[3] >> 16) | (bb[3] & 0xffff0000u);
+        reinterpret_cast<uint4*>(sb_lds)[2 * idx] = lo;
+        reinterpret_cast<uint4*>(sb_lds)[2 * idx + 1] = hi;
+      }
+    }
+  } else {
+    for (int idx = tid; idx < span; idx += kThreads) {  // tail tile or unaligned scales
+      const int rr = idx / G, g = idx - rr * G;
+      const int row = row0 + rr < N ? row0 + rr : N - 1;
+      sb_lds[idx] = (uint32_t)P.s[(size_t)row * G + g] | ((uint32_t)P.b[(size_t)row * G + g] << 16);
+    }
+  }
+  lds_barrier();
+
+  const uint32_t* sbl = sb_lds + n * G;
   f32x4_t acc[NT][MT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  MfmaStage<MT, NT> ping, pong;
-  if (g0 < g1) mfma_load(ping, wrow, srow, brow, xr, has_x, g0);
-  for (int g = g0; g < g1; g += 2) {
-    if (g + 1 < g1) mfma_load(pong, wrow, srow, brow, xr, has_x, g + 1);
-    mfma_compute<MT, NT>(ping, acc, magic);
-    if (g + 1 < g1) {
-      if (g + 2 < g1) mfma_load(ping, wrow, srow, brow, xr, has_x, g + 2);
-      mfma_compute<MT, NT>(pong, acc, magic);
-    }
+  for (int g = g0; g < g1; g += 2 * GS) {
+    load_stage<MT, NT, GS>(sb2, wrsrc, voff, xr, g + GS, g1);
+    compute_stage<MT, NT, GS>(sa, sbl, G, g, g1, acc, magic);
+    if (g + GS >= g1) break;
+    load_stage<MT, NT, GS>(sa, wrsrc, voff, xr, g + 2 * GS, g1);
+    compute_stage<MT, NT, GS>(sb2, sbl, G, g + GS, g1, acc, magic);
   }
 
   // add the four quarters: waves 1..3 park their sums in LDS, wave 0 adds and stores
@@ -764,6 +841,7 @@ int32_t check_rows(const uint16_t* x, int64_t ldx, const void* y, int64_t ldy, i
 constexpr int kValuMaxRows = 2;
 constexpr size_t kValuLdsLimit = 64 * 1024;
 constexpr int kMfmaTiles = 2;  // 16-row tiles per MFMA workgroup
+constexpr size_t kMfmaLdsLimit = 48 * 1024;  // its (scale, bias) table; K up to 24576
 
 // Lanes per weight row for the VALU kernel: the widest of 64/32/16 that still gives
 // each lane at least four 16-byte chunks with at most 10% of the lanes' chunks idle.
@@ -847,9 +925,12 @@ hipError_t launch_rows(const LaunchArgs& a, size_t lds, hipStream_t stream) {
   return hipGetLastError();
 }
 
+constexpr int kMfmaStage = 4;  // groups of weight and x words loaded at once per wavefront
+
 template <int MT>
-hipError_t launch_mfma(const LaunchArgs& a, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((qmv_mfma_kernel<MT, kMfmaTiles>), dim3(grid), dim3(kThreads), 0, stream, a);
+hipError_t launch_mfma(const LaunchArgs& a, int grid, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((qmv_mfma_kernel<MT, kMfmaTiles, kMfmaStage>), dim3(grid), dim3(kThreads),
+                     lds, stream, a);
   return hipGetLastError();
 }
 
@@ -890,7 +971,15 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream) {
       tiles += (a.p[i].N + rows_per_wg - 1) / rows_per_wg;
     }
     if (tiles > 0x7fffffff) return fail(IMQ_EUNSUPPORTED, "too many rows for one launch");
-    e = (M <= 16) ? launch_mfma<1>(a, (int)tiles, stream) : launch_mfma<2>(a, (int)tiles, stream);
+    int kmax = 0;
+    for (int i = 0; i < a.count; ++i) kmax = a.p[i].K > kmax ? a.p[i].K : kmax;
+    const size_t lds = (size_t)rows_per_wg * (kmax / 64) * 4;  // (s, b) per row and group
+    if (lds > kMfmaLdsLimit) return fail(IMQ_EUNSUPPORTED, "K too large for the MFMA kernel");
+    for (int i = 0; i < a.count; ++i)
+      if ((int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31))
+        return fail(IMQ_EUNSUPPORTED, "a weight of 2 GiB or more exceeds the MFMA kernel's offsets");
+    e = (M <= 16) ? launch_mfma<1>(a, (int)tiles, lds, stream)
+                  : launch_mfma<2>(a, (int)tiles, lds, stream);
   }
   if (e != hipSuccess)
     return fail(IMQ_ELAUNCH, std::string("qmv launch failed: ") + hipGetErrorString(e));
