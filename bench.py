@@ -229,6 +229,115 @@ def cpu_baseline(seconds: float = 10.0):
     }
 
 
+COPY_READ = 1 << 30   # the calibration copy: 2^27 int64 values read ...
+COPY_WRITTEN = 1 << 29  # ... and written back as int32
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmv_layer_m1_hbm_traffic.md")
+# the dominant kernel of the layer step: the gate+up launch, 2 x 9728 rows at 16 rows per
+# workgroup (16 lanes per row, 4 wavefronts)
+DOMINANT = ("qmv_fixed_kernel<1, 4, 5>", 1216)
+
+
+def copy_calibration(torch, device) -> None:
+    """One plain elementwise copy of known size (int64 -> int32, COPY_READ bytes in,
+    COPY_WRITTEN out): the yardstick that scales a profiling pass's FETCH_SIZE /
+    WRITE_SIZE counters to bytes."""
+    src = torch.ones(COPY_READ // 8, dtype=torch.int64, device=device)
+    dst = src.to(torch.int32)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
+def _short(name: str) -> str:
+    for marker in ("qmv_fixed_kernel", "qmv_rows_kernel", "qmv_mfma_kernel", "dequant_kernel"):
+        if marker in name:
+            return name[name.index(marker):].split("(")[0]
+    if "direct_copy_kernel" in name:
+        return "torch copy kernel"
+    return name.split("(")[0][:60]
+
+
+def profile_summary(directories: list[str]) -> str:
+    """Reduces rocprofv3 CSV output (kernel trace and --pmc passes) under `directories` to
+    short text tables per (kernel, workgroups): dispatch count and mean duration from the
+    trace; mean counters per dispatch from each pass.  FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch) are scaled to bytes by the calibration copy found in the same pass (the
+    largest torch copy kernel, COPY_READ bytes read and COPY_WRITTEN written)."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    lines, traffic = [], defaultdict(dict)
+    paths = lambda pattern: sorted(p for d in directories
+                                   for p in glob.glob(os.path.join(d, "**", pattern), recursive=True))
+    for path in paths("*kernel_trace.csv"):
+        agg = defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            key = (_short(r["Kernel_Name"]), int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]),
+                   r.get("VGPR_Count", "?"), r.get("LDS_Block_Size", "?"))
+            agg[key].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        lines += [f"kernel trace ({os.path.basename(path)}), qmv kernels:", "",
+                  "| kernel | workgroups | vgpr | lds bytes | dispatches | mean us | median us |",
+                  "|---|---|---|---|---|---|---|"]
+        for key, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+            if "kernel<" not in key[0]:
+                continue
+            v.sort()
+            lines.append(f"| {key[0]} | {key[1]} | {key[2]} | {key[3]} | {len(v)} | "
+                         f"{sum(v) / len(v) / 1e3:.3f} | {v[len(v) // 2] / 1e3:.3f} |")
+        lines.append("")
+    for path in paths("*counter_collection.csv"):
+        agg = defaultdict(lambda: defaultdict(list))
+        for r in csv.DictReader(open(path)):
+            grid = int(r.get("Grid_Size", r.get("Grid_Size_X", 0)))
+            wg = int(r.get("Workgroup_Size", r.get("Workgroup_Size_X", 1)) or 1)
+            agg[(_short(r["Kernel_Name"]), grid // wg)][r["Counter_Name"]].append(float(r["Counter_Value"]))
+        copies = [k for k in agg if k[0] == "torch copy kernel"]
+        copy = agg[max(copies, key=lambda k: k[1])] if copies else None
+        lines += [f"counters ({os.path.basename(path)}), mean per dispatch:", ""]
+        for key, cs in sorted(agg.items()):
+            if "kernel<" not in key[0]:
+                continue
+            vals = ", ".join(f"{c}={sum(v) / len(v):.1f}" for c, v in sorted(cs.items()))
+            lines.append(f"* {key[0]}, {key[1]} workgroups, {len(next(iter(cs.values())))} "
+                         f"dispatches: {vals}")
+        if copy is not None:
+            for c, known in (("FETCH_SIZE", COPY_READ), ("WRITE_SIZE", COPY_WRITTEN)):
+                if c not in copy:
+                    continue
+                kib = sum(copy[c]) / len(copy[c])
+                factor = known / 1024 / kib
+                lines.append(f"* calibration: the copy moves {known} B; {c} reads {kib:.1f} KiB "
+                             f"-> factor {factor:.4f}")
+                for key, cs in agg.items():
+                    if "kernel<" in key[0] and c in cs:
+                        traffic[key][c] = sum(cs[c]) / len(cs[c]) * 1024 * factor
+        lines.append("")
+    if traffic:
+        lines += ["HBM traffic per dispatch (calibrated bytes):", "",
+                  "| kernel | workgroups | fetch bytes | write bytes | traffic bytes |",
+                  "|---|---|---|---|---|"]
+        for key, t in sorted(traffic.items()):
+            if "FETCH_SIZE" in t and "WRITE_SIZE" in t:
+                lines.append(f"| {key[0]} | {key[1]} | {t['FETCH_SIZE']:.0f} | "
+                             f"{t['WRITE_SIZE']:.0f} | {t['FETCH_SIZE'] + t['WRITE_SIZE']:.0f} |")
+    return "\n".join(lines)
+
+
+def profiled_traffic(kernel: str, workgroups: int):
+    """Calibrated HBM bytes per dispatch of (kernel, workgroups) from the committed
+    counter summary, or None when it holds no such row."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    for row in text.splitlines():
+        cells = [c.strip() for c in row.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == kernel and cells[1] == str(workgroups):
+            return int(cells[4])
+    return None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -239,10 +348,17 @@ def main() -> None:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-breakdown", action="store_true",
                     help="time only the headline layer steps (a short program for profilers)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 1 GiB device copies (the yardstick for --pmc byte counters)")
+    ap.add_argument("--profile-summary", nargs="+", default=None, metavar="DIR",
+                    help="print a text summary of rocprofv3 CSV output under DIR... and exit")
     ap.add_argument("--only", default=None, metavar="N,K,M[,f32]",
                     help="time one qmv shape over rotating weights (>= 1 GiB) and exit; "
                          "a short program for profilers")
     args = ap.parse_args()
+    if args.profile_summary:
+        print(profile_summary(args.profile_summary))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs "
                           "are not part of this build", "n_gpus": args.gpus}))
@@ -257,6 +373,8 @@ def main() -> None:
     code, arch, cus = _native.device_check()
     if code != 0:
         raise SystemExit(f"unsupported device {arch!r}")
+    if args.copy_calibration:
+        copy_calibration(torch, device)
     if args.only:
         parts = args.only.split(",")
         n, k, m = (int(v) for v in parts[:3])
@@ -299,8 +417,10 @@ def main() -> None:
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gate["gbs"], 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gate["gbs"] / PEAK_HBM_GBS, 4),
-                     "traffic": None,
-                     "kernel": "qmv_fixed_kernel<1,4,5>: gate+up grouped launch, 2 x (2560->9728), M=1",
+                     "traffic": profiled_traffic(*DOMINANT),
+                     "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
+                     "kernel": f"{DOMINANT[0]} x {DOMINANT[1]} workgroups: gate+up grouped "
+                               "launch, 2 x (2560->9728), M=1",
                      "bytes_per_launch": gate["bytes"],
                      "avg_launch_us": round(gate["us"], 3)},
         "per_launch": {k: {"us": round(v["us"], 3), "gbs": round(v["gbs"], 1)}

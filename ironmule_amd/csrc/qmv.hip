@@ -13,9 +13,10 @@
 // (x3,x7) of each word.  The offset is removed with the group's sum of x:
 //     s * sum (128+q) x  +  (b - 128 s) * sum x.
 //
-// Two kernels share that arithmetic:
-//   * qmv_valu_kernel (few activation rows): v_dot2_f32_bf16 chains, x staged once per
-//     workgroup in LDS already in pair order, chain started at -128 * sum(x);
+// Kernels sharing that arithmetic:
+//   * qmv_fixed_kernel / qmv_rows_kernel (one or two activation rows): v_dot2_f32_bf16
+//     chains, x staged once per workgroup in LDS already in pair order, each chain
+//     started at -128 * sum(x);
 //   * qmv_mfma_kernel (more rows): v_mfma_f32_16x16x32_bf16 with the activation rows as
 //     the A operand and 16 weight rows as the B operand, one MFMA pair per group of 64,
 //     and a second MFMA pair against a ones operand that yields sum(x) per group.
@@ -470,7 +471,8 @@ __global__ __launch_bounds__(kThreads) void qmv_fixed_kernel(LaunchArgs a) {
 // the two words 8g+2kg and 8g+2kg+1 of weight row n (one 8-byte load): as B operands of
 // two v_mfma_f32_16x16x32_bf16 they cover the group's words {0,2,4,6} and {1,3,5,7}.
 // The A operands are the matching x words of activation row m = lane%16 (+16 per
-// m-tile), read from memory (they stay in L2) one group ahead and put in pair order.
+// m-tile), read from memory with the weights of the same stage (x stays in L2) and put
+// in pair order.
 // D[m][n] lands in lane (n, kg) as rows m = 4*kg + r, r < 4.  Per group:
 //     acc += s * P + (b - 128 s) * P1,
 // where P1 is the same MFMA pair against a ones operand, i.e. sum x over the group.
