@@ -143,8 +143,8 @@ struct Problem {
   int64_t ldy;
   int32_t N;
   int32_t K;
-  int32_t first;      // first workgroup of this problem
-  int32_t lpr_shift;  // VALU kernel: log2 of the lanes that share one weight row
+  int32_t nch;        // one-row VALU kernel: 16-byte weight chunks per lane
+  int32_t lpr_shift;  // VALU kernels: log2 of the lanes that share one weight row
   int32_t pad0;
   int32_t pad1;
 };
@@ -157,18 +157,13 @@ struct LaunchArgs {
   int32_t M;
   int32_t y_f32;
   int32_t table;
-  int32_t items;  // VALU kernel: workgroups over all problems
-  int32_t pad;
+  int32_t pad[2];
 };
 
-// The problem that owns workgroup `idx`; `first` increases with i.
-__device__ __forceinline__ int find_problem(const LaunchArgs& a, int idx) {
-  int pi = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxProblems; ++i)
-    if (i < a.count && idx >= a.p[i].first) pi = i;
-  return pi;
-}
+// Every kernel runs on a (tiles, problems) grid: blockIdx.y names the problem, so a
+// workgroup reads its problem's arguments in one round trip, and blockIdx.x the tile.
+// The grid is as wide as the problem with the most tiles; the surplus workgroups of the
+// other problems return at once.
 
 __device__ __forceinline__ const uint16_t* x_row(const LaunchArgs& a, const Problem& P, int m) {
   return a.table ? a.xt[m] : P.x + (size_t)m * P.ldx;
@@ -265,14 +260,15 @@ __device__ __forceinline__ void compute_batch(const Batch<B>& t, float (&acc)[M]
 template <int M, int B>
 __global__ __launch_bounds__(kThreads) void qmv_rows_kernel(LaunchArgs a) {
   extern __shared__ uint4 smem[];
-  const Problem& P = a.p[find_problem(a, blockIdx.x)];
+  const Problem& P = a.p[blockIdx.y];
   const int K = P.K, N = P.N, sh = P.lpr_shift;
+  if ((int)(blockIdx.x * (kThreads >> sh)) >= N) return;  // past this problem's tiles
   const int C = K >> 5;  // 32-value chunks per row
   const int G = K >> 6;  // groups per row
   const int W = K >> 3;  // words per row
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int j = lane & ((1 << sh) - 1);
-  const int row = (((blockIdx.x - P.first) * 4 + wave) << (6 - sh)) + (lane >> sh);
+  const int row = ((blockIdx.x * 4 + wave) << (6 - sh)) + (lane >> sh);
   const int r = row < N ? row : N - 1;  // clamp loads; the store is guarded
   const uint32_t* wrow = P.w + (size_t)r * W;
   const uint16_t* srow = P.s + (size_t)r * G;
@@ -348,14 +344,21 @@ __global__ __launch_bounds__(kThreads) void qmv_rows_kernel(LaunchArgs a) {
   }
 }
 
-// ------------------------------------- VALU kernel, lanes and chunks fixed at compile time
+// ---------------------------------------------------- VALU kernel, one activation row
 //
-// The same arithmetic and LDS layout as qmv_rows_kernel, for launches whose problems
-// all share the lanes per row (LPR = 1 << SH) and the chunks per lane (NCH).  Every
-// chunk of a lane's row is loaded at once (no second buffer), addresses are one base
-// plus immediate offsets, and only the last chunk can fall past the row (when
-// NCH * LPR > K / 32), so only it is guarded.  Fewer registers let more wavefronts share
-// each SIMD, so one launch's workgroups are resident together instead of in two rounds.
+// One workgroup per tile of 256/LPR weight rows of one problem; LPR = 1 << lpr_shift
+// lanes share a row and lane j takes the 16-byte chunks kc = j, j+LPR, ... (at most NCH,
+// nch for this problem).  The lane shape is a per-problem runtime value, so one launch
+// serves projections of different K (all seven of a decoder layer, for example).
+//
+// Every load of the workgroup is issued at the start, in the order it is consumed: x
+// (XR 16-byte pieces per thread), the tile's scales and biases (one contiguous span of
+// each, read as dwords by consecutive threads), then the weight chunks.  They are raw
+// buffer loads issued unconditionally: a piece that is not needed gets an offset past
+// its buffer, for which the hardware returns zero without touching memory, so the
+// outstanding-load count is the same on every path and each wait is exact.  x goes to
+// LDS in pair order with its per-chunk sums, the (scale, bias) pairs as one dword per
+// (row, group); then each chunk is consumed as it arrives.
 
 __device__ __forceinline__ float chunk_dot(uint4 wv, uint4 x0, uint4 x1, uint4 x2, uint4 x3,
                                            float d, uint32_t magic) {
@@ -378,89 +381,194 @@ __device__ __forceinline__ float chunk_dot(uint4 wv, uint4 x0, uint4 x1, uint4 x
   return d;
 }
 
-template <int M, int SH, int NCH>
-__global__ __launch_bounds__(kThreads) void qmv_fixed_kernel(LaunchArgs a) {
-  constexpr int LPR = 1 << SH;
-  constexpr int XR = (NCH * LPR + 63) / 64;  // x words per thread: W <= NCH * LPR * 4
+constexpr uint32_t kPastBuffer = 0x80000000u;  // a buffer offset that reads as zero
+
+__device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// LDS layout of the one-row kernel, sized by its template so that every staging write
+// is unconditional (pieces past the data are written as zeros): x in pair order as four
+// planes of XR * 64 chunks, their chunk sums, and 2 * SBR * 256 (scale, bias) dwords.
+template <int NCH, int XR>
+struct M1Lds {
+  static constexpr int kChunks = XR * 64;                        // per plane, >= K / 32
+  static constexpr int kSbr = (64 * NCH + kThreads - 1) / kThreads;  // dwords per thread
+  static constexpr size_t kBytes = (size_t)kChunks * (64 + 4) + (size_t)kSbr * kThreads * 8;
+};
+
+// One tile of the one-row kernel, its problem's arguments already in scalar registers.
+template <int NCH, int XR>
+__device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, const uint16_t* bp,
+                                        const uint16_t* xp, void* yp, int K, int N, int sh,
+                                        int nch, int yf32, int row0) {
+  using L = M1Lds<NCH, XR>;
+  constexpr int CP = L::kChunks, SBR = L::kSbr;
   extern __shared__ uint4 smem[];
-  const Problem& P = a.p[find_problem(a, blockIdx.x)];
-  const int K = P.K, N = P.N;
   const int C = K >> 5, G = K >> 6, W = K >> 3;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int j = lane & (LPR - 1);
-  const int row = (((blockIdx.x - P.first) * 4 + wave) << (6 - SH)) + (lane >> SH);
-  const int r = row < N ? row : N - 1;  // clamp loads; the store is guarded
-  const bool last_ok = j + (NCH - 1) * LPR < C;
-  const int kc_last = last_ok ? j + (NCH - 1) * LPR : 0;
-  const uint32_t* wp = P.w + (size_t)r * W;
-  const uint16_t* sp = P.s + (size_t)r * G;
-  const uint16_t* bp = P.b + (size_t)r * G;
-  uint4* xq = smem;
-  float* sx = reinterpret_cast<float*>(smem + M * 4 * C);
+  const int tid = threadIdx.x;
+  const int j = tid & ((1 << sh) - 1);
+  const int rl = tid >> sh;  // the lane's row within the tile
+  const int row = row0 + rl;
+  uint4* xq = smem;                                     // [4][CP]
+  float* sx = reinterpret_cast<float*>(smem + 4 * CP);  // [CP]
+  uint32_t* sbl = reinterpret_cast<uint32_t*>(sx + CP); // [rows][G], padded
   const uint32_t magic = in_vgpr(kMagic);
 
-  // x first (its loads then complete before the weights'), then every weight chunk.
-  uint4 xs[M][XR];
+  // x: XR pieces of 8 values per thread
+  const __amdgpu_buffer_rsrc_t xrsrc = buffer_rsrc(xp, (uint32_t)K * 2u);
+  uint4 xs[XR];
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const uint4* xv = reinterpret_cast<const uint4*>(x_row(a, P, m));
-#pragma unroll
-    for (int t = 0; t < XR; ++t) {
-      const int i = tid + kThreads * t;
-      if (i < W) xs[m][t] = xv[i];
-    }
+  for (int t = 0; t < XR; ++t) {
+    const int i = tid + kThreads * t;
+    xs[t] = load_b128(xrsrc, i < W ? 16u * i : kPastBuffer);
   }
+  // the tile's scales and biases: rows * G halves from row0 * G on, as dwords (rows is
+  // even, so the span starts 4-byte aligned); rows past N read as zero.  The range is
+  // rounded up to whole dwords (an odd N * G ends mid-dword, and a dword that crosses the
+  // range would read as zero); the extra half lies in the same aligned dword as the last
+  // one, so it is mapped, and it belongs to no row.
+  const int D = ((kThreads >> sh) * G) >> 1;
+  const uint32_t sb_bytes = ((uint32_t)N * (uint32_t)G * 2u + 3u) & ~3u;
+  const __amdgpu_buffer_rsrc_t srsrc = buffer_rsrc(sp, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc = buffer_rsrc(bp, sb_bytes);
+  const uint32_t sb0 = (uint32_t)row0 * (uint32_t)G * 2u;
+  uint32_t sv[SBR], bv[SBR];
+#pragma unroll
+  for (int q = 0; q < SBR; ++q) {
+    const int d = tid + kThreads * q;
+    const uint32_t off = d < D ? sb0 + 4u * d : kPastBuffer;
+    sv[q] = __builtin_amdgcn_raw_buffer_load_b32(srsrc, off, 0, 0);
+    bv[q] = __builtin_amdgcn_raw_buffer_load_b32(brsrc, off, 0, 0);
+  }
+  // the weight chunks (rows past N read as zero and are never stored)
+  const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(wp, (uint32_t)N * (uint32_t)W * 4u);
+  const uint32_t wrow = (uint32_t)row * (uint32_t)W * 4u;
   uint4 wv[NCH];
-  uint32_t s16[NCH], b16[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    const int kc = i + 1 < NCH ? j + i * LPR : kc_last;
-    wv[i] = *reinterpret_cast<const uint4*>(wp + kc * 4);
-    s16[i] = sp[kc >> 1];
-    b16[i] = bp[kc >> 1];
+    const int kc = j + (i << sh);
+    wv[i] = load_b128(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
+  }
+
+  // staging, unconditionally (pieces past x and past the span are zeros)
+#pragma unroll
+  for (int t = 0; t < XR; ++t) {
+    const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
+    xq[(i & 3) * CP + (i >> 2)] = pair_order(xs[t]);
+    float part = sum8(xs[t]);
+    part += __shfl_xor(part, 1);
+    part += __shfl_xor(part, 2);
+    if ((i & 3) == 0) sx[i >> 2] = part;
   }
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-#pragma unroll
-    for (int t = 0; t < XR; ++t) {
-      const int i = tid + kThreads * t;
-      if (i < W) {  // the four words of a chunk are four aligned lanes (W % 4 == 0)
-        xq[(m * 4 + (i & 3)) * C + (i >> 2)] = pair_order(xs[m][t]);
-        float part = sum8(xs[m][t]);
-        part += __shfl_xor(part, 1);
-        part += __shfl_xor(part, 2);
-        if ((i & 3) == 0) sx[m * C + (i >> 2)] = part;
-      }
-    }
+  for (int q = 0; q < SBR; ++q) {
+    const int d = tid + kThreads * q;
+    *reinterpret_cast<uint2*>(sbl + 2 * d) =
+        make_uint2((sv[q] & 0xffffu) | (bv[q] << 16), (sv[q] >> 16) | (bv[q] & 0xffff0000u));
   }
   lds_barrier();
 
-  float acc[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+  float acc = 0.0f;
+  const uint32_t* sbr = sbl + rl * G;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    const int kc = i + 1 < NCH ? j + i * LPR : kc_last;
-    const float sc = bf16_bits_to_f32(s16[i]);
-    const float bi = bf16_bits_to_f32(b16[i]);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float sxm = sx[m * C + kc];
-      const float d = chunk_dot(wv[i], xq[(m * 4 + 0) * C + kc], xq[(m * 4 + 1) * C + kc],
-                                xq[(m * 4 + 2) * C + kc], xq[(m * 4 + 3) * C + kc],
+    if (i < nch) {  // uniform over the workgroup's problem
+      const int kc = j + (i << sh);
+      const bool valid = kc < C;
+      const int kk = valid ? kc : 0;
+      const uint32_t sb = sbr[kk >> 1];
+      const float sc = __uint_as_float(sb << 16);
+      const float bi = __uint_as_float(sb & 0xffff0000u);
+      const float sxm = sx[kk];
+      const float d = chunk_dot(wv[i], xq[kk], xq[CP + kk], xq[2 * CP + kk], xq[3 * CP + kk],
                                 -128.0f * sxm, magic);
-      const float v = fmaf(sc, d, fmaf(bi, sxm, acc[m]));
-      acc[m] = (i + 1 < NCH || last_ok) ? v : acc[m];
+      const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
+      acc = valid ? v : acc;
     }
   }
-
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    float v = row16_sum(acc[m]);
-    if (SH >= 5) v += __shfl_xor(v, 16);
-    if (SH >= 6) v += __shfl_xor(v, 32);
-    if (j == 0 && row < N) store_y(a, P, m, row, v);
+  float v = row16_sum(acc);
+  if (sh >= 5) v += __shfl_xor(v, 16);
+  if (sh >= 6) v += __shfl_xor(v, 32);
+  if (j == 0 && row < N) {
+    if (yf32)
+      static_cast<float*>(yp)[row] = v;
+    else
+      static_cast<uint16_t*>(yp)[row] = f32_to_bf16_bits(v);
   }
+}
+
+// Any number of problems: blockIdx.y is the problem, blockIdx.x its tile.
+template <int NCH, int XR>
+__global__ __launch_bounds__(kThreads) void qmv_m1_kernel(LaunchArgs a) {
+  const Problem& P = a.p[blockIdx.y];
+  const uint32_t* wp = P.w;
+  const uint16_t* sp = P.s;
+  const uint16_t* bp = P.b;
+  const uint16_t *x0 = P.x, *x1 = a.xt[0];
+  void *y0 = P.y, *y1 = a.yt[0];
+  const int K = P.K, N = P.N, sh = P.lpr_shift, nch = P.nch, yf32 = a.y_f32, table = a.table;
+  // every argument in one round trip: without this the exit test below would fetch N
+  // and the lane shape first, and the rest only after that answer arrived
+  asm volatile("" ::"s"(wp), "s"(sp), "s"(bp), "s"(x0), "s"(x1), "s"(y0), "s"(y1), "s"(K),
+               "s"(N), "s"(sh), "s"(nch), "s"(yf32), "s"(table));
+  const int row0 = blockIdx.x * (kThreads >> sh);
+  if (row0 >= N) return;  // past this problem's tiles
+  m1_tile<NCH, XR>(wp, sp, bp, table ? x1 : x0, table ? y1 : y0, K, N, sh, nch, yf32, row0);
+}
+
+// Up to kM1Compact problems on a linear grid with no idle workgroups: all their
+// arguments arrive in the first round trip and the workgroup picks its problem with
+// scalar selects (an indexed read would cost a second, dependent round trip).
+constexpr int kM1Compact = 4;
+
+struct M1Args {
+  int32_t count;
+  int32_t y_f32;
+  int32_t pad[2];
+  int32_t tile_end[kM1Compact];  // one past the last workgroup of each problem
+  int32_t N[kM1Compact];
+  int32_t K[kM1Compact];
+  int32_t sh[kM1Compact];
+  int32_t nch[kM1Compact];
+  const uint32_t* w[kM1Compact];
+  const uint16_t* s[kM1Compact];
+  const uint16_t* b[kM1Compact];
+  const uint16_t* x[kM1Compact];
+  void* y[kM1Compact];
+};
+
+template <typename T>
+__device__ __forceinline__ T pick4(int i, T v0, T v1, T v2, T v3) {
+  return i == 0 ? v0 : i == 1 ? v1 : i == 2 ? v2 : v3;
+}
+
+template <int NCH, int XR>
+__global__ __launch_bounds__(kThreads) void qmv_m1c_kernel(M1Args a) {
+  asm volatile("" ::"s"(a.count), "s"(a.y_f32), "s"(a.tile_end[0]), "s"(a.tile_end[1]),
+               "s"(a.tile_end[2]), "s"(a.N[0]), "s"(a.N[1]), "s"(a.N[2]), "s"(a.N[3]),
+               "s"(a.K[0]), "s"(a.K[1]), "s"(a.K[2]), "s"(a.K[3]), "s"(a.sh[0]), "s"(a.sh[1]),
+               "s"(a.sh[2]), "s"(a.sh[3]), "s"(a.nch[0]), "s"(a.nch[1]), "s"(a.nch[2]),
+               "s"(a.nch[3]));
+  asm volatile("" ::"s"(a.w[0]), "s"(a.w[1]), "s"(a.w[2]), "s"(a.w[3]), "s"(a.s[0]), "s"(a.s[1]),
+               "s"(a.s[2]), "s"(a.s[3]), "s"(a.b[0]), "s"(a.b[1]), "s"(a.b[2]), "s"(a.b[3]));
+  asm volatile("" ::"s"(a.x[0]), "s"(a.x[1]), "s"(a.x[2]), "s"(a.x[3]), "s"(a.y[0]), "s"(a.y[1]),
+               "s"(a.y[2]), "s"(a.y[3]));
+  const int bx = blockIdx.x;
+  const int pi = (a.count > 1 && bx >= a.tile_end[0]) + (a.count > 2 && bx >= a.tile_end[1]) +
+                 (a.count > 3 && bx >= a.tile_end[2]);
+  const int first = pick4(pi, 0, a.tile_end[0], a.tile_end[1], a.tile_end[2]);
+  const int sh = pick4(pi, a.sh[0], a.sh[1], a.sh[2], a.sh[3]);
+  m1_tile<NCH, XR>(pick4(pi, a.w[0], a.w[1], a.w[2], a.w[3]),
+                   pick4(pi, a.s[0], a.s[1], a.s[2], a.s[3]),
+                   pick4(pi, a.b[0], a.b[1], a.b[2], a.b[3]),
+                   pick4(pi, a.x[0], a.x[1], a.x[2], a.x[3]),
+                   pick4(pi, a.y[0], a.y[1], a.y[2], a.y[3]),
+                   pick4(pi, a.K[0], a.K[1], a.K[2], a.K[3]),
+                   pick4(pi, a.N[0], a.N[1], a.N[2], a.N[3]), sh,
+                   pick4(pi, a.nch[0], a.nch[1], a.nch[2], a.nch[3]), a.y_f32,
+                   (bx - first) * (kThreads >> sh));
 }
 
 // ------------------------------------------------------- MFMA kernel (more rows)
@@ -508,7 +616,6 @@ struct MfmaStage {
 // path and the compiler's waits stay exact (a conditional stage would make it wait for
 // everything).  Groups past the range get an offset past the buffer: the hardware
 // returns zero for them without touching memory.
-constexpr uint32_t kPastBuffer = 0x80000000u;
 
 template <int MT, int NT, int GS>
 __device__ __forceinline__ void load_stage(MfmaStage<MT, NT, GS>& st, __amdgpu_buffer_rsrc_t wrsrc,
@@ -577,15 +684,16 @@ template <int MT, int NT, int GS>
 __global__ __launch_bounds__(kThreads) void qmv_mfma_kernel(LaunchArgs a) {
   extern __shared__ uint32_t sb_lds[];  // (s | b << 16) per [row of the workgroup][group]
   __shared__ f32x4_t red[3][NT][MT][64];
-  const Problem& P = a.p[find_problem(a, blockIdx.x)];
+  const Problem& P = a.p[blockIdx.y];
   const int K = P.K, N = P.N, M = a.M;
+  if ((int)(blockIdx.x * (16 * NT)) >= N) return;  // past this problem's tiles
   const int G = K >> 6, W = K >> 3;
   const int tid = threadIdx.x;
   // the wave index is uniform across the wavefront: keep it (and the group range and
   // loop control derived from it) in scalar registers, so branches are scalar
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, kg = lane >> 4;
-  const int row0 = (blockIdx.x - P.first) * (16 * NT);
+  const int row0 = blockIdx.x * (16 * NT);
   const uint32_t magic = in_vgpr(kMagic);
 
   // Scales and biases of the workgroup's rows (one contiguous span each), loaded first
@@ -845,7 +953,7 @@ constexpr size_t kValuLdsLimit = 64 * 1024;
 constexpr int kMfmaTiles = 2;  // 16-row tiles per MFMA workgroup
 constexpr size_t kMfmaLdsLimit = 48 * 1024;  // its (scale, bias) table; K up to 24576
 
-// Lanes per weight row for the VALU kernel: the widest of 64/32/16 that still gives
+// Lanes per weight row for the VALU kernels: the widest of 64/32/16 that still gives
 // each lane at least four 16-byte chunks with at most 10% of the lanes' chunks idle.
 int choose_lpr_shift(int K) {
   const int C = K / 32;
@@ -857,22 +965,22 @@ int choose_lpr_shift(int K) {
   return 4;
 }
 
-// Tiles of the VALU kernel: 4 wavefronts x 64/LPR rows.  Returns the LDS bytes for the
-// largest x of the launch, or 0 if some x does not fit.
-size_t plan_rows(LaunchArgs& a) {
+// Tiles of the generic VALU kernel: 4 wavefronts x 64/LPR rows.  Returns the LDS bytes
+// for the largest x of the launch (0 if some x does not fit) and the grid width.
+size_t plan_rows(LaunchArgs& a, int* grid_x) {
   size_t lds = 0;
-  int64_t tiles = 0;
+  int tiles = 0;
   for (int i = 0; i < a.count; ++i) {
     Problem& P = a.p[i];
     P.lpr_shift = choose_lpr_shift(P.K);
-    const int rows = 256 >> P.lpr_shift;
-    P.first = (int32_t)tiles;
-    tiles += (P.N + rows - 1) / rows;
+    const int rows = kThreads >> P.lpr_shift;
+    const int t = (P.N + rows - 1) / rows;
+    tiles = t > tiles ? t : tiles;
     const size_t need = (size_t)a.M * (P.K / 32) * (64 + 4);
     lds = need > lds ? need : lds;
   }
-  if (lds > kValuLdsLimit || tiles > 0x7fffffff) return 0;
-  a.items = (int32_t)tiles;
+  if (lds > kValuLdsLimit) return 0;
+  *grid_x = tiles;
   return lds;
 }
 
@@ -899,40 +1007,99 @@ int choose_batch(const LaunchArgs& a, const int* options, int n_options) {
   return best;
 }
 
-template <int M, int SH, int NCH>
-hipError_t launch_fixed(const LaunchArgs& a, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((qmv_fixed_kernel<M, SH, NCH>), dim3(a.items), dim3(kThreads), lds, stream,
-                     a);
+// The one-row kernel's plan: per problem the narrowest row (16, 32 or 64 lanes) whose
+// chunks fit kM1MaxChunks per lane (more rows per tile share one staged x), then the
+// launch's chunk and x-piece bounds.  Returns false when some problem does not qualify
+// (K over 16384, scales/biases not 4-byte aligned, weights of 2 GiB or more).
+constexpr int kM1MaxChunks = 8;
+
+struct M1Plan {
+  int nch = 0;  // chunks per lane, largest over the problems
+  int xr = 0;   // x pieces per thread, largest over the problems
+  int grid_x = 0;
+};
+
+bool plan_m1(LaunchArgs& a, M1Plan* plan) {
+  M1Plan pl;
+  for (int i = 0; i < a.count; ++i) {
+    Problem& P = a.p[i];
+    const int C = P.K / 32;
+    int sh = 4;
+    while (sh <= 6 && (C + (1 << sh) - 1) >> sh > kM1MaxChunks) ++sh;
+    if (sh > 6) return false;
+    if (!aligned(P.s, 4) || !aligned(P.b, 4)) return false;
+    if ((int64_t)P.N * (P.K / 2) >= ((int64_t)1 << 31)) return false;
+    P.lpr_shift = sh;
+    P.nch = (C + (1 << sh) - 1) >> sh;
+    const int rows = kThreads >> sh;
+    const int tiles = (P.N + rows - 1) / rows;
+    const int xr = (P.K / 8 + kThreads - 1) / kThreads;
+    pl.nch = P.nch > pl.nch ? P.nch : pl.nch;
+    pl.xr = xr > pl.xr ? xr : pl.xr;
+    pl.grid_x = tiles > pl.grid_x ? tiles : pl.grid_x;
+  }
+  if (pl.xr > 8) return false;
+  *plan = pl;
+  return true;
+}
+
+template <int NCH, int XR>
+hipError_t launch_m1(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream) {
+  constexpr size_t lds = M1Lds<NCH, XR>::kBytes;
+  if (a.count <= kM1Compact) {
+    M1Args c;
+    memset(&c, 0, sizeof(c));
+    c.count = a.count;
+    c.y_f32 = a.y_f32;
+    int tiles = 0;
+    for (int i = 0; i < a.count; ++i) {
+      const Problem& P = a.p[i];
+      tiles += (P.N + (kThreads >> P.lpr_shift) - 1) / (kThreads >> P.lpr_shift);
+      c.tile_end[i] = tiles;
+      c.N[i] = P.N;
+      c.K[i] = P.K;
+      c.sh[i] = P.lpr_shift;
+      c.nch[i] = P.nch;
+      c.w[i] = P.w;
+      c.s[i] = P.s;
+      c.b[i] = P.b;
+      c.x[i] = a.table ? a.xt[0] : P.x;
+      c.y[i] = a.table ? a.yt[0] : P.y;
+    }
+    hipLaunchKernelGGL((qmv_m1c_kernel<NCH, XR>), dim3(tiles), dim3(kThreads), lds, stream, c);
+  } else {
+    hipLaunchKernelGGL((qmv_m1_kernel<NCH, XR>), dim3(pl.grid_x, a.count), dim3(kThreads), lds,
+                       stream, a);
+  }
   return hipGetLastError();
 }
 
-// The compile-time kernel for (M, SH, NCH) if one is built: SH 4 with 1..8 chunks per
-// lane, SH 5 and 6 with 4..8.  Returns false when none matches.
-template <int M>
-bool launch_fixed_for(const LaunchArgs& a, int sh, int nch, size_t lds, hipStream_t stream,
-                      hipError_t* e) {
-#define IMQ_FIXED(S, NC) \
-  if (sh == S && nch == NC) { *e = launch_fixed<M, S, NC>(a, lds, stream); return true; }
-  IMQ_FIXED(4, 1) IMQ_FIXED(4, 2) IMQ_FIXED(4, 3) IMQ_FIXED(4, 4)
-  IMQ_FIXED(4, 5) IMQ_FIXED(4, 6) IMQ_FIXED(4, 7) IMQ_FIXED(4, 8)
-  IMQ_FIXED(5, 4) IMQ_FIXED(5, 5) IMQ_FIXED(5, 6) IMQ_FIXED(5, 7) IMQ_FIXED(5, 8)
-  IMQ_FIXED(6, 4) IMQ_FIXED(6, 5) IMQ_FIXED(6, 6) IMQ_FIXED(6, 7) IMQ_FIXED(6, 8)
-#undef IMQ_FIXED
-  return false;
+// The instantiation that covers the plan with the fewest idle loads: 2, 5 or 8 chunks
+// per lane, 2, 5 or 8 x pieces per thread (NCH <= 2 means K <= 1024, so XR = 2 there).
+hipError_t launch_m1_for(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream) {
+  if (pl.nch <= 2 && pl.xr <= 2) return launch_m1<2, 2>(a, pl, stream);
+  if (pl.nch <= 5) {
+    if (pl.xr <= 2) return launch_m1<5, 2>(a, pl, stream);
+    if (pl.xr <= 5) return launch_m1<5, 5>(a, pl, stream);
+  }
+  if (pl.xr <= 2) return launch_m1<8, 2>(a, pl, stream);
+  if (pl.xr <= 5) return launch_m1<8, 5>(a, pl, stream);
+  return launch_m1<8, 8>(a, pl, stream);
 }
 
 template <int M, int B>
-hipError_t launch_rows(const LaunchArgs& a, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((qmv_rows_kernel<M, B>), dim3(a.items), dim3(kThreads), lds, stream, a);
+hipError_t launch_rows(const LaunchArgs& a, int grid_x, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((qmv_rows_kernel<M, B>), dim3(grid_x, a.count), dim3(kThreads), lds, stream,
+                     a);
   return hipGetLastError();
 }
 
 constexpr int kMfmaStage = 4;  // groups of weight and x words loaded at once per wavefront
 
 template <int MT>
-hipError_t launch_mfma(const LaunchArgs& a, int grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((qmv_mfma_kernel<MT, kMfmaTiles, kMfmaStage>), dim3(grid), dim3(kThreads),
-                     lds, stream, a);
+hipError_t launch_mfma(const LaunchArgs& a, int grid_x, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((qmv_mfma_kernel<MT, kMfmaTiles, kMfmaStage>), dim3(grid_x, a.count),
+                     dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
 
@@ -941,47 +1108,34 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream) {
   (void)dev;
   const int M = a.M;
   hipError_t e;
-  const size_t lds = M <= kValuMaxRows ? plan_rows(a) : 0;
-  if (lds > 0) {
-    // one (lanes per row, chunks per lane) shape for every problem: the fixed kernel
-    int sh = a.p[0].lpr_shift, nch = -1;
-    for (int i = 0; i < a.count; ++i) {
-      const int lpr = 1 << a.p[i].lpr_shift;
-      const int n = (a.p[i].K / 32 + lpr - 1) / lpr;
-      if (a.p[i].lpr_shift != sh || (nch >= 0 && n != nch)) sh = -1;
-      nch = n;
-    }
-    if (sh >= 0 && M == 1) {  // at M = 2 the fixed kernel needs too many registers
-      if (launch_fixed_for<1>(a, sh, nch, lds, stream, &e)) {
-        if (e != hipSuccess)
-          return fail(IMQ_ELAUNCH, std::string("qmv launch failed: ") + hipGetErrorString(e));
-        return ok();
-      }
-    }
+  M1Plan m1;
+  int grid_x = 0;
+  size_t lds = 0;
+  if (M == 1 && plan_m1(a, &m1)) {
+    e = launch_m1_for(a, m1, stream);
+  } else if (M <= kValuMaxRows && (lds = plan_rows(a, &grid_x)) > 0) {
     if (M == 1) {
       static const int opts[] = {4, 5};
-      e = choose_batch(a, opts, 2) == 4 ? launch_rows<1, 4>(a, lds, stream)
-                                        : launch_rows<1, 5>(a, lds, stream);
+      e = choose_batch(a, opts, 2) == 4 ? launch_rows<1, 4>(a, grid_x, lds, stream)
+                                        : launch_rows<1, 5>(a, grid_x, lds, stream);
     } else {
-      e = launch_rows<2, 2>(a, lds, stream);
+      e = launch_rows<2, 2>(a, grid_x, lds, stream);
     }
   } else {
     const int rows_per_wg = 16 * kMfmaTiles;
-    int64_t tiles = 0;
-    for (int i = 0; i < a.count; ++i) {
-      a.p[i].first = (int32_t)tiles;
-      tiles += (a.p[i].N + rows_per_wg - 1) / rows_per_wg;
-    }
-    if (tiles > 0x7fffffff) return fail(IMQ_EUNSUPPORTED, "too many rows for one launch");
     int kmax = 0;
-    for (int i = 0; i < a.count; ++i) kmax = a.p[i].K > kmax ? a.p[i].K : kmax;
-    const size_t lds = (size_t)rows_per_wg * (kmax / 64) * 4;  // (s, b) per row and group
+    for (int i = 0; i < a.count; ++i) {
+      const int t = (a.p[i].N + rows_per_wg - 1) / rows_per_wg;
+      grid_x = t > grid_x ? t : grid_x;
+      kmax = a.p[i].K > kmax ? a.p[i].K : kmax;
+    }
+    lds = (size_t)rows_per_wg * (kmax / 64) * 4;  // (s, b) per row and group
     if (lds > kMfmaLdsLimit) return fail(IMQ_EUNSUPPORTED, "K too large for the MFMA kernel");
     for (int i = 0; i < a.count; ++i)
       if ((int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31))
         return fail(IMQ_EUNSUPPORTED, "a weight of 2 GiB or more exceeds the MFMA kernel's offsets");
-    e = (M <= 16) ? launch_mfma<1>(a, (int)tiles, lds, stream)
-                  : launch_mfma<2>(a, (int)tiles, lds, stream);
+    e = (M <= 16) ? launch_mfma<1>(a, grid_x, lds, stream)
+                  : launch_mfma<2>(a, grid_x, lds, stream);
   }
   if (e != hipSuccess)
     return fail(IMQ_ELAUNCH, std::string("qmv launch failed: ") + hipGetErrorString(e));
