@@ -1,0 +1,98 @@
+/*
+ * ironmule_decode.h — C ABI of the decode-step kernels that sit between the 4-bit qmv
+ * launches of a Qwen3-style decoder on MI355X (gfx950), in libironmule_qmv.so.
+ *
+ * One decode step of B requests (each its own KV slot and position), as the reference
+ * composes it (ironmule/dense_plan.py:351-376, ironmule/dense_cpu.py:188-220):
+ *   h = embed(tokens)
+ *   per layer: x = rms_norm(h) ; q,k,v = qmv(x) ; q,k = rope(rms_norm_head(q,k)) ;
+ *              KV[slot][pos] = k,v ; o = attention(q, KV[slot][:pos+1]) ;
+ *              h += qmv_o(o) ; x = rms_norm(h) ; h += qmv_down(silu(qmv_gate(x)) * qmv_up(x))
+ *   logits = qmv_head(rms_norm(h))
+ * The projections are imq_qmv / imq_qmv_grouped (ironmule_qmv.h); these entry points are
+ * the rest.
+ *
+ * Contract (as for ironmule_qmv.h): device pointers allocated by the caller, work queued
+ * on `stream`, no allocation or synchronisation per call, int32 return codes (IMQ_*
+ * values of ironmule_qmv.h) with imq_last_error() for the message.
+ *
+ * Layouts:
+ *   h         fp32 (B, dim): the residual stream
+ *   bf16      activations (B, dim) and heads (B, H, 128)
+ *   KV pool   bf16 (slots, kv_heads, capacity, 128) per layer, the reference's pool layout
+ *             (dense_plan.py:294-299, rows = (slot * kv_heads + head) * capacity + position)
+ */
+#ifndef IRONMULE_DECODE_H
+#define IRONMULE_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ironmule_qmv.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IMQ_HEAD_DIM 128
+
+/* h[b][:] = dequantised embedding row tokens[b] (4-bit, group 64, bf16 scales/biases, the
+ * qmv weight format), as fp32.  Tokens outside [0, vocab) are refused by the kernel:
+ * their rows are written as NaN.
+ * Replaces trunk.embed_tokens(tokens) (ironmule/dense_plan.py:357; dense_cpu.py:200). */
+IMQ_API int32_t imq_embed(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                          const int32_t* tokens, float* h, int32_t B, int32_t vocab, int32_t dim,
+                          void* stream);
+
+/* If delta is non-NULL, h += delta (bf16) first; then out = bf16(h * rsqrt(mean(h^2) + eps)
+ * * weight), per row of dim values (dim <= 8192).
+ * Replaces mx.fast.rms_norm(h, weight, eps) and the residual adds `h = h + ...`
+ * (ironmule/dense_plan.py:362, 373-376). */
+IMQ_API int32_t imq_add_rmsnorm(float* h, const uint16_t* delta, const uint16_t* weight,
+                                uint16_t* out, int32_t B, int32_t dim, float eps, void* stream);
+
+/* Per request b and head: q heads and k heads get the per-head RMSNorm (q_norm / k_norm
+ * weights, rounded to bf16 as the reference's module output) and the non-interleaved
+ * rotary embedding at positions[b] with base `theta`; q goes to q_out (B, Hq, 128); k and
+ * the untouched v go to the KV pools (num_slots slots of `capacity` positions) at
+ * (slots[b], head, positions[b]).  A request whose position is not in [0, capacity) or
+ * whose slot is not in [0, num_slots) is refused: nothing is written for it.
+ * Replaces q_norm/k_norm + _rope + the KV write (ironmule/dense_plan.py:363-372, 378-383). */
+IMQ_API int32_t imq_qk_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 const uint16_t* q_norm, const uint16_t* k_norm,
+                                 const int32_t* positions, const int32_t* slots, uint16_t* q_out,
+                                 uint16_t* k_pool, uint16_t* v_pool, int32_t B, int32_t Hq,
+                                 int32_t Hkv, int32_t capacity, int32_t num_slots, float theta,
+                                 float eps, void* stream);
+
+/* Bytes of fp32 workspace imq_attention_decode needs for B requests, Hq query heads and
+ * keys up to max_len (a partial result per 64-key chunk), and the number of uint32
+ * counters it needs (B * Hkv).  The counters must be zero before the first call; every
+ * call leaves them zero again. */
+IMQ_API size_t imq_attention_workspace(int32_t B, int32_t Hq, int32_t max_len);
+
+/* out[b][h] = softmax(scale * q[b][h] . K[slot][h/G][:len]) V[slot][h/G][:len] with
+ * slot = slots[b], len = lengths[b] (clamped to max_len and capacity), G = Hq / Hkv <= 8
+ * query heads per KV head (grouped-query attention).  A request with len <= 0 or a slot
+ * outside [0, num_slots) gets zeros.  Keys are processed in 64-key chunks by separate
+ * workgroups; the last workgroup of each (request, KV head) combines the chunks in chunk
+ * order, so the result does not depend on scheduling.  Calls that share
+ * `workspace`/`counters` must not overlap.
+ * Replaces fa2 (ironmule/dense_plan.py:250-278): FA2_PARTIAL and FA2_COMBINE in one launch. */
+IMQ_API int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool,
+                                     const uint16_t* v_pool, const int32_t* lengths,
+                                     const int32_t* slots, uint16_t* out, int32_t B, int32_t Hq,
+                                     int32_t Hkv, int32_t capacity, int32_t num_slots,
+                                     int32_t max_len, float scale, float* workspace,
+                                     uint32_t* counters, void* stream);
+
+/* out = bf16(silu(gate) * up), silu(g) = g / (1 + exp(-g)), n elements.
+ * Replaces swiglu(gate, up) (ironmule/dense_plan.py:374-375; nn.silu in dense_cpu.py:216). */
+IMQ_API int32_t imq_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IRONMULE_DECODE_H */

@@ -24,6 +24,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 LIB_PATH = os.path.join(PKG, "libironmule_qmv.so")
 HEADER_PATH = os.path.join(ROOT, "include", "ironmule_qmv.h")
+HEADER_PATHS = [HEADER_PATH, os.path.join(ROOT, "include", "ironmule_decode.h")]
 
 GROUP_SIZE = 64
 BITS = 4
@@ -69,14 +70,25 @@ _SIGNATURES = {
     "imq_qmv_grouped": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_last_error": ([ctypes.c_char_p, ctypes.c_size_t], _I32),
+    # decode-step kernels (include/ironmule_decode.h)
+    "imq_embed": ([_P, _P, _P, _P, _P, _I32, _I32, _I32, _P], _I32),
+    "imq_add_rmsnorm": ([_P, _P, _P, _P, _I32, _I32, ctypes.c_float, _P], _I32),
+    "imq_qk_norm_rope": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
+                          ctypes.c_float, ctypes.c_float, _P], _I32),
+    "imq_attention_workspace": ([_I32, _I32, _I32], ctypes.c_size_t),
+    "imq_attention_decode": ([_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
+                              ctypes.c_float, _P, _P, _P], _I32),
+    "imq_silu_mul": ([_P, _P, _P, _I64, _P], _I32),
 }
 
 
 def declared_functions() -> list[str]:
-    """Every function the public header declares (what the library must export)."""
-    text = open(HEADER_PATH).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"^\s*IMQ_API\s+int32_t\s+(imq_\w+)\s*\(", text, flags=re.M)
+    """Every function the public headers declare (what the library must export)."""
+    names = []
+    for path in HEADER_PATHS:
+        text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
+        names += re.findall(r"^\s*IMQ_API\s+\w+\s+(imq_\w+)\s*\(", text, flags=re.M)
+    return names
 
 
 def lib() -> ctypes.CDLL:
@@ -256,4 +268,102 @@ def dequant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
         out = torch.empty((n, k), dtype=out_dtype, device=w.device)
     _check(lib().imq_dequant(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out),
                              _DTYPE_CODE[out_dtype], n, k, GROUP_SIZE, BITS, _stream(stream)))
+    return out
+
+
+# --------------------------------------------------------------- decode-step kernels
+
+def _require(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def embed(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, tokens: torch.Tensor,
+          out: torch.Tensor, stream=None) -> torch.Tensor:
+    """out (B, dim) fp32 = dequantised rows tokens[b] of a 4-bit embedding."""
+    vocab, dim = check_weights(w, scales, biases)
+    _require(tokens, torch.int32, "tokens")
+    _require(out, torch.float32, "out")
+    b = int(tokens.numel())
+    if tuple(out.shape) != (b, dim):
+        raise ValueError(f"out must be ({b}, {dim})")
+    _check(lib().imq_embed(_ptr(w), _ptr(scales), _ptr(biases), _ptr(tokens), _ptr(out), b, vocab,
+                           dim, _stream(stream)))
+    return out
+
+
+def add_rmsnorm(h: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, eps: float,
+                delta: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """h += delta (if given); out = bf16 rms_norm(h) * weight, per row."""
+    _require(h, torch.float32, "h")
+    _require(weight, torch.bfloat16, "weight")
+    _require(out, torch.bfloat16, "out")
+    b, dim = h.shape
+    if delta is not None:
+        _require(delta, torch.bfloat16, "delta")
+        if delta.numel() != h.numel():
+            raise ValueError("delta must match h")
+    if out.numel() != h.numel() or weight.numel() != dim:
+        raise ValueError("out must match h and weight its row length")
+    _check(lib().imq_add_rmsnorm(_ptr(h), _ptr(delta) if delta is not None else None, _ptr(weight),
+                                 _ptr(out), b, dim, float(eps), _stream(stream)))
+    return out
+
+
+def qk_norm_rope(q, k, v, q_norm, k_norm, positions, slots, q_out, k_pool, v_pool, theta: float,
+                 eps: float, stream=None) -> None:
+    """Per-head RMSNorm + rotary embedding of q and k; q to q_out, k and v into the pools
+    (slots, kv_heads, capacity, 128)."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_norm", q_norm), ("k_norm", k_norm),
+                    ("q_out", q_out), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _require(t, torch.bfloat16, name)
+    _require(positions, torch.int32, "positions")
+    _require(slots, torch.int32, "slots")
+    num_slots, hkv, capacity, d = k_pool.shape
+    b = int(positions.numel())
+    hq = q.numel() // (b * d)
+    if d != 128 or v_pool.shape != k_pool.shape or k.numel() != b * hkv * d or q_out.numel() != q.numel():
+        raise ValueError("inconsistent q/k/v/pool shapes (head dim 128)")
+    _check(lib().imq_qk_norm_rope(_ptr(q), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm),
+                                  _ptr(positions), _ptr(slots), _ptr(q_out), _ptr(k_pool),
+                                  _ptr(v_pool), b, hq, hkv, capacity, num_slots, float(theta),
+                                  float(eps), _stream(stream)))
+
+
+def attention_workspace(b: int, hq: int, max_len: int) -> int:
+    """fp32 elements of workspace imq_attention_decode needs."""
+    return int(lib().imq_attention_workspace(b, hq, max_len)) // 4
+
+
+def attention_decode(q, k_pool, v_pool, lengths, slots, out, max_len: int, scale: float,
+                     workspace: torch.Tensor, counters: torch.Tensor, stream=None) -> torch.Tensor:
+    """out (B, Hq, 128) bf16 = grouped-query attention of each request over its slot."""
+    for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool), ("out", out)):
+        _require(t, torch.bfloat16, name)
+    _require(lengths, torch.int32, "lengths")
+    _require(slots, torch.int32, "slots")
+    _require(workspace, torch.float32, "workspace")
+    if counters.dtype not in (torch.int32, torch.uint32) or not counters.is_contiguous():
+        raise ValueError("counters must be contiguous 32-bit integers")
+    num_slots, hkv, capacity, d = k_pool.shape
+    b = int(lengths.numel())
+    hq = q.numel() // (b * d)
+    if workspace.numel() < attention_workspace(b, hq, max_len) or counters.numel() < b * hkv:
+        raise ValueError("workspace or counters too small")
+    _check(lib().imq_attention_decode(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(lengths),
+                                      _ptr(slots), _ptr(out), b, hq, hkv, capacity, num_slots,
+                                      int(max_len), float(scale), _ptr(workspace), _ptr(counters),
+                                      _stream(stream)))
+    return out
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor, stream=None) -> torch.Tensor:
+    """out = bf16(silu(gate) * up)."""
+    for name, t in (("gate", gate), ("up", up), ("out", out)):
+        _require(t, torch.bfloat16, name)
+    if not gate.numel() == up.numel() == out.numel():
+        raise ValueError("gate, up and out must have the same size")
+    _check(lib().imq_silu_mul(_ptr(gate), _ptr(up), _ptr(out), int(gate.numel()), _stream(stream)))
     return out

@@ -1,0 +1,438 @@
+// MI355X (gfx950) kernels for the decode step around the 4-bit projections, and their C
+// ABI (include/ironmule_decode.h): embedding rows, residual add + RMSNorm, per-head
+// q/k norm + rotary embedding + KV write, grouped-query decode attention, SiLU * up.
+//
+// All of them are small next to the weight stream; they are written to keep every
+// launch to one pass over its data with coalesced 16-byte accesses where the data is
+// large (the KV chunks), and to be deterministic (fixed reduction orders).
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/ironmule_decode.h"
+#include "runtime.h"
+
+namespace {
+
+using imq_rt::aligned;
+using imq_rt::current_device;
+using imq_rt::fail;
+using imq_rt::ok;
+
+constexpr int kThreads = 256;
+constexpr int kD = IMQ_HEAD_DIM;  // head dimension
+constexpr int kChunk = 64;        // keys per attention workgroup
+constexpr int kMaxNormDim = 8192;
+constexpr int kNormVpt = kMaxNormDim / kThreads;  // values per thread of the row norm
+
+__device__ __forceinline__ float bf(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Round to nearest even; NaN becomes the quiet NaN 0x7fc0.
+__device__ __forceinline__ uint16_t to_bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// ------------------------------------------------------------------ embedding rows
+
+// One thread per packed word (8 values) of row tokens[b]: fp32 s * q + b.
+__global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ s,
+                                                         const uint16_t* __restrict__ b,
+                                                         const int32_t* __restrict__ tokens,
+                                                         float* __restrict__ h, int vocab, int dim) {
+  const int row = blockIdx.y;
+  const int W = dim >> 3;
+  const int word = blockIdx.x * kThreads + threadIdx.x;
+  if (word >= W) return;
+  const int t = tokens[row];
+  float* out = h + (size_t)row * dim + (size_t)word * 8;
+  if (t < 0 || t >= vocab) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = __uint_as_float(0x7fc00000u);
+    return;
+  }
+  const uint32_t u = w[(size_t)t * W + word];
+  const size_t g = (size_t)t * (dim >> 6) + ((word * 8) >> 6);
+  const float sc = bf(s[g]), bi = bf(b[g]);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = fmaf(sc, (float)((u >> (4 * e)) & 0xFu), bi);
+  reinterpret_cast<float4*>(out)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4*>(out)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// ------------------------------------------------------- residual add + RMSNorm
+
+// One workgroup per row.  Thread t holds values t, t + 256, ...; the sum of squares is
+// added per thread, then over each wavefront (butterfly), then over the four wavefronts in
+// order, so the result does not depend on scheduling.
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(float* __restrict__ h,
+                                                               const uint16_t* __restrict__ delta,
+                                                               const uint16_t* __restrict__ weight,
+                                                               uint16_t* __restrict__ out, int dim,
+                                                               float eps) {
+  __shared__ float red[kThreads / 64];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  float* hr = h + (size_t)row * dim;
+  const uint16_t* dr = delta ? delta + (size_t)row * dim : nullptr;
+  float v[kNormVpt];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormVpt; ++i) {
+    const int idx = tid + kThreads * i;
+    v[i] = 0.0f;
+    if (idx < dim) {
+      float x = hr[idx];
+      if (dr) {
+        x += bf(dr[idx]);
+        hr[idx] = x;
+      }
+      v[i] = x;
+      ss = fmaf(x, x, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / sqrtf(total / (float)dim + eps);
+  uint16_t* orow = out + (size_t)row * dim;
+#pragma unroll
+  for (int i = 0; i < kNormVpt; ++i) {
+    const int idx = tid + kThreads * i;
+    if (idx < dim) orow[idx] = to_bf(v[i] * inv * bf(weight[idx]));
+  }
+}
+
+// ------------------------------------------- q/k norm + rotary embedding + KV write
+
+// One wavefront per (request, head) of q, k or v.  Lane i holds dimensions i and i + 64:
+// exactly the pair the non-interleaved rotary embedding mixes.
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ slots,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    int Hq, int Hkv, int capacity, int num_slots, float log2_theta, float eps) {
+  const int b = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
+  const int pos = positions[b], slot = slots[b];
+  if (pos < 0 || pos >= capacity || slot < 0 || slot >= num_slots) return;  // refused
+  const bool is_q = hh < Hq, is_k = !is_q && hh < Hq + Hkv;
+  const int head = is_q ? hh : (is_k ? hh - Hq : hh - Hq - Hkv);
+  const uint16_t* src = is_q ? q + ((size_t)b * Hq + head) * kD
+                             : (is_k ? k : v) + ((size_t)b * Hkv + head) * kD;
+  float x0 = bf(src[lane]), x1 = bf(src[lane + 64]);
+  if (is_q || is_k) {
+    const uint16_t* nw = is_q ? q_norm : k_norm;
+    const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+    const float inv = 1.0f / sqrtf(ss / (float)kD + eps);
+    // the norm module's output is bf16 in the reference, and the rotation reads it
+    x0 = bf(to_bf(x0 * inv * bf(nw[lane])));
+    x1 = bf(to_bf(x1 * inv * bf(nw[lane + 64])));
+    // angle = pos * theta^(-i / 64) for the pair (i, i + 64)
+    const float inv_freq = exp2f(-(float)lane * (log2_theta / 64.0f));
+    float sn, cs;
+    sincosf((float)pos * inv_freq, &sn, &cs);
+    const float r0 = x0 * cs - x1 * sn;
+    const float r1 = x0 * sn + x1 * cs;
+    x0 = r0;
+    x1 = r1;
+  }
+  uint16_t* dst = is_q ? q_out + ((size_t)b * Hq + head) * kD
+                       : (is_k ? k_pool : v_pool) +
+                             (((size_t)slot * Hkv + head) * capacity + pos) * kD;
+  dst[lane] = to_bf(x0);
+  dst[lane + 64] = to_bf(x1);
+}
+
+// ------------------------------------------------------------ decode attention
+//
+// Workgroup (chunk c, KV head, request b) reads keys and values [64c, 64c + 64) of its
+// request's slot once into LDS and serves the G query heads that share them (one
+// wavefront per head, G <= 8).  In a wavefront lane t scores key t (64 bf16 dot2 against
+// the head's q), the chunk's max and sum come from butterflies, and lane i then
+// accumulates dimensions 2i, 2i+1 of p . V.  The partial (acc, max, sum) goes to the
+// workspace; the last workgroup of the (request, KV head) to finish, counted with one
+// device-scope atomic, combines the chunks in chunk order and writes bf16 heads.
+
+struct AttnLds {
+  uint4 k[kChunk][17];        // a key row is 16 uint4; one of padding keeps lanes on
+                              // distinct banks when lane t reads row t
+  uint32_t v[kChunk][kD / 2];  // lane i reads dword i of a row: conflict-free
+  float p[4][kChunk];
+  int last;
+};
+
+__global__ __launch_bounds__(kThreads) void attention_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ lengths,
+    const int32_t* __restrict__ slots, uint16_t* __restrict__ out, int Hq, int Hkv, int capacity,
+    int max_len, int num_slots, float scale, float* __restrict__ part, float* __restrict__ ml,
+    uint32_t* __restrict__ counters, int NC) {
+  __shared__ AttnLds L;
+  const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int G = Hq / Hkv;
+  const int slot = slots[b];
+  int len = lengths[b];
+  len = len < max_len ? len : max_len;
+  len = len < capacity ? len : capacity;
+  if (len <= 0 || slot < 0 || slot >= num_slots) {  // nothing to attend to: zeros
+    if (c == 0)
+      for (int g = wave; g < G; g += 4) {
+        uint16_t* o = out + ((size_t)b * Hq + kvh * G + g) * kD;
+        o[2 * lane] = 0;
+        o[2 * lane + 1] = 0;
+      }
+    return;
+  }
+  const int start = c * kChunk;
+  if (start >= len) return;
+  const int count = min(kChunk, len - start);
+  const int nch = (len + kChunk - 1) / kChunk;
+  const size_t base = (((size_t)slot * Hkv + kvh) * capacity + start) * kD;
+
+  // the chunk's keys and values: 64 rows x 16 pieces of 16 bytes each
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = tid + kThreads * i;
+    const int row = p >> 4, col = p & 15;
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    if (row < count) {
+      kv = *reinterpret_cast<const uint4*>(k_pool + base + (size_t)row * kD + col * 8);
+      vv = *reinterpret_cast<const uint4*>(v_pool + base + (size_t)row * kD + col * 8);
+    }
+    L.k[row][col] = kv;
+    *reinterpret_cast<uint4*>(&L.v[row][col * 4]) = vv;
+  }
+  __syncthreads();
+
+  for (int g = wave; g < G; g += 4) {
+    const int h = kvh * G + g;
+    const uint4* qv = reinterpret_cast<const uint4*>(q + ((size_t)b * Hq + h) * kD);
+    float s = -INFINITY;
+    if (lane < count) {
+      float d = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint4 a = qv[j], kk = L.k[lane][j];
+        d = dot2(a.x, kk.x, d);
+        d = dot2(a.y, kk.y, d);
+        d = dot2(a.z, kk.z, d);
+        d = dot2(a.w, kk.w, d);
+      }
+      s = d * scale;
+    }
+    const float m = wave_max(s);
+    const float p = lane < count ? expf(s - m) : 0.0f;
+    const float l = wave_sum(p);
+    L.p[wave][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int t = 0; t < count; ++t) {
+      const float pt = L.p[wave][t];
+      const uint32_t vd = L.v[t][lane];
+      a0 = fmaf(pt, bf(vd & 0xffffu), a0);
+      a1 = fmaf(pt, bf(vd >> 16), a1);
+    }
+    const size_t po = ((size_t)b * Hq + h) * NC + c;
+    reinterpret_cast<float2*>(part + po * kD)[lane] = make_float2(a0, a1);
+    if (lane == 0) reinterpret_cast<float2*>(ml)[po] = make_float2(m, l);
+    __builtin_amdgcn_wave_barrier();  // L.p is rewritten by the next head of this wave
+  }
+
+  // the last workgroup of this (request, KV head) combines the chunks
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t done = atomicAdd(&counters[b * Hkv + kvh], 1u);
+    L.last = done == (uint32_t)(nch - 1);
+  }
+  __syncthreads();
+  if (!L.last) return;
+  __threadfence();
+  for (int g = wave; g < G; g += 4) {
+    const int h = kvh * G + g;
+    const size_t p0 = ((size_t)b * Hq + h) * NC;
+    float M = -INFINITY;
+    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, ml[2 * (p0 + cc)]);
+    float Ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
+    for (int cc = 0; cc < nch; ++cc) {
+      const float e = expf(ml[2 * (p0 + cc)] - M);
+      Ls = fmaf(ml[2 * (p0 + cc) + 1], e, Ls);
+      const float2 pa = reinterpret_cast<const float2*>(part + (p0 + cc) * kD)[lane];
+      a0 = fmaf(pa.x, e, a0);
+      a1 = fmaf(pa.y, e, a1);
+    }
+    uint16_t* o = out + ((size_t)b * Hq + h) * kD;
+    o[2 * lane] = to_bf(a0 / Ls);
+    o[2 * lane + 1] = to_bf(a1 / Ls);
+  }
+  if (tid == 0) counters[b * Hkv + kvh] = 0;  // ready for the next call
+}
+
+// ------------------------------------------------------------------ SiLU * up
+
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gate,
+                                                            const uint16_t* __restrict__ up,
+                                                            uint16_t* __restrict__ out, int64_t n) {
+  const int64_t i8 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 8;
+  if (i8 >= n) return;
+  if (i8 + 8 <= n) {
+    const uint4 g = *reinterpret_cast<const uint4*>(gate + i8);
+    const uint4 u = *reinterpret_cast<const uint4*>(up + i8);
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+    uint32_t r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g0 = bf(gw[e] & 0xffffu), g1 = bf(gw[e] >> 16);
+      const float o0 = g0 / (1.0f + expf(-g0)) * bf(uw[e] & 0xffffu);
+      const float o1 = g1 / (1.0f + expf(-g1)) * bf(uw[e] >> 16);
+      r[e] = (uint32_t)to_bf(o0) | ((uint32_t)to_bf(o1) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + i8) = make_uint4(r[0], r[1], r[2], r[3]);
+  } else {
+    for (int64_t i = i8; i < n; ++i) {
+      const float g0 = bf(gate[i]);
+      out[i] = to_bf(g0 / (1.0f + expf(-g0)) * bf(up[i]));
+    }
+  }
+}
+
+int32_t launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string(what) + " launch failed: " + hipGetErrorString(e));
+  return ok();
+}
+
+size_t attention_parts(int32_t B, int32_t Hq, int32_t max_len) {
+  const size_t nc = (size_t)((max_len + kChunk - 1) / kChunk);
+  return (size_t)B * Hq * nc;
+}
+
+}  // namespace
+
+// ==================================================================== C ABI
+
+extern "C" {
+
+int32_t imq_embed(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                  const int32_t* tokens, float* h, int32_t B, int32_t vocab, int32_t dim,
+                  void* stream) {
+  if (!w || !scales || !biases || !tokens || !h) return fail(IMQ_EINVAL, "null pointer");
+  if (B < 1 || vocab < 1) return fail(IMQ_EINVAL, "B and vocab must be >= 1");
+  if (dim < 64 || dim % 64) return fail(IMQ_EINVAL, "dim must be a positive multiple of 64");
+  if (!aligned(w, 4) || !aligned(h, 16)) return fail(IMQ_EINVAL, "w or h is misaligned");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  const int W = dim / 8;
+  hipLaunchKernelGGL(embed_kernel, dim3((W + kThreads - 1) / kThreads, B), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), w, scales, biases, tokens, h, vocab, dim);
+  return launched("embed");
+}
+
+int32_t imq_add_rmsnorm(float* h, const uint16_t* delta, const uint16_t* weight, uint16_t* out,
+                        int32_t B, int32_t dim, float eps, void* stream) {
+  if (!h || !weight || !out) return fail(IMQ_EINVAL, "null pointer");
+  if (B < 1 || dim < 1 || dim > kMaxNormDim) return fail(IMQ_EINVAL, "B >= 1 and 1 <= dim <= 8192");
+  if (!(eps >= 0.0f)) return fail(IMQ_EINVAL, "eps must be >= 0");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(B), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     h, delta, weight, out, dim, eps);
+  return launched("add_rmsnorm");
+}
+
+int32_t imq_qk_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const uint16_t* q_norm, const uint16_t* k_norm, const int32_t* positions,
+                         const int32_t* slots, uint16_t* q_out, uint16_t* k_pool, uint16_t* v_pool,
+                         int32_t B, int32_t Hq, int32_t Hkv, int32_t capacity, int32_t num_slots,
+                         float theta, float eps, void* stream) {
+  if (!q || !k || !v || !q_norm || !k_norm || !positions || !slots || !q_out || !k_pool || !v_pool)
+    return fail(IMQ_EINVAL, "null pointer");
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv) return fail(IMQ_EINVAL, "need B, Hkv >= 1 and Hkv | Hq");
+  if (capacity < 1 || num_slots < 1) return fail(IMQ_EINVAL, "capacity and num_slots must be >= 1");
+  if (!(theta > 1.0f)) return fail(IMQ_EINVAL, "theta must be > 1");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(B, Hq + 2 * Hkv), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), q, k, v, q_norm, k_norm, positions, slots,
+                     q_out, k_pool, v_pool, Hq, Hkv, capacity, num_slots, log2f(theta), eps);
+  return launched("qk_norm_rope");
+}
+
+size_t imq_attention_workspace(int32_t B, int32_t Hq, int32_t max_len) {
+  if (B < 1 || Hq < 1 || max_len < 1) return 0;
+  return attention_parts(B, Hq, max_len) * (kD + 2) * sizeof(float);
+}
+
+int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                             const int32_t* lengths, const int32_t* slots, uint16_t* out, int32_t B,
+                             int32_t Hq, int32_t Hkv, int32_t capacity, int32_t num_slots,
+                             int32_t max_len, float scale, float* workspace, uint32_t* counters,
+                             void* stream) {
+  if (!q || !k_pool || !v_pool || !lengths || !slots || !out || !workspace || !counters)
+    return fail(IMQ_EINVAL, "null pointer");
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || Hq / Hkv > 8)
+    return fail(IMQ_EINVAL, "need Hkv | Hq with at most 8 query heads per KV head");
+  if (capacity < 1 || num_slots < 1 || max_len < 1) return fail(IMQ_EINVAL, "capacity, num_slots, max_len >= 1");
+  if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(workspace, 16))
+    return fail(IMQ_EINVAL, "q, pools and workspace must be 16-byte aligned");
+  const int32_t span = max_len < capacity ? max_len : capacity;
+  const int NC = (span + kChunk - 1) / kChunk;
+  if (B > 65535 || Hkv > 65535) return fail(IMQ_EINVAL, "B and Hkv must be <= 65535");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  const size_t parts = attention_parts(B, Hq, span);
+  float* part = workspace;
+  float* mlp = workspace + parts * kD;
+  hipLaunchKernelGGL(attention_kernel, dim3(NC, Hkv, B), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), q, k_pool, v_pool, lengths, slots, out, Hq,
+                     Hkv, capacity, span, num_slots, scale, part, mlp, counters, NC);
+  return launched("attention");
+}
+
+int32_t imq_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                     void* stream) {
+  if (!gate || !up || !out) return fail(IMQ_EINVAL, "null pointer");
+  if (n < 1) return fail(IMQ_EINVAL, "n must be >= 1");
+  if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(out, 16))
+    return fail(IMQ_EINVAL, "gate, up and out must be 16-byte aligned");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  const int64_t threads = (n + 7) / 8;
+  const int64_t blocks = (threads + kThreads - 1) / kThreads;
+  if (blocks > 0x7fffffff) return fail(IMQ_EINVAL, "n too large");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), gate, up, out, n);
+  return launched("silu_mul");
+}
+
+}  // extern "C"

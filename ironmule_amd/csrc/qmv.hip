@@ -34,6 +34,7 @@
 #include <string>
 
 #include "../../include/ironmule_qmv.h"
+#include "runtime.h"
 
 namespace {
 
@@ -857,62 +858,12 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t* __res
 
 // ================================================================== host side
 
-thread_local int32_t g_last_code = IMQ_OK;
-thread_local std::string g_last_msg;
+using imq_rt::aligned;
+using imq_rt::current_device;
+using imq_rt::DeviceInfo;
+using imq_rt::fail;
+using imq_rt::ok;
 
-int32_t fail(int32_t code, const std::string& msg) {
-  g_last_code = code;
-  g_last_msg = msg;
-  return code;
-}
-
-int32_t ok() {
-  g_last_code = IMQ_OK;
-  g_last_msg.clear();
-  return IMQ_OK;
-}
-
-struct DeviceInfo {
-  int state = 0;  // 0 unknown, 1 gfx950, -1 unsupported
-  int cu_count = 0;
-  char arch[64] = {0};
-};
-
-constexpr int kMaxDevices = 64;
-DeviceInfo g_devices[kMaxDevices];
-std::mutex g_device_mutex;
-
-// Checks once per device that it is a gfx950; returns its info or nullptr.
-const DeviceInfo* current_device(int32_t* code) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    *code = fail(IMQ_EUNAVAILABLE, "no HIP device is available");
-    return nullptr;
-  }
-  DeviceInfo& info = g_devices[dev];
-  if (__atomic_load_n(&info.state, __ATOMIC_ACQUIRE) == 0) {
-    std::lock_guard<std::mutex> lock(g_device_mutex);
-    if (info.state == 0) {
-      hipDeviceProp_t prop;
-      if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
-        *code = fail(IMQ_EUNAVAILABLE, "hipGetDeviceProperties failed");
-        return nullptr;
-      }
-      strncpy(info.arch, prop.gcnArchName, sizeof(info.arch) - 1);
-      info.cu_count = prop.multiProcessorCount;
-      const bool is950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-      __atomic_store_n(&info.state, is950 ? 1 : -1, __ATOMIC_RELEASE);
-    }
-  }
-  if (info.state != 1) {
-    *code = fail(IMQ_EUNAVAILABLE,
-                 std::string("device architecture ") + info.arch + " is not gfx950");
-    return nullptr;
-  }
-  return &info;
-}
-
-bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int32_t check_format(int32_t N, int32_t K, int32_t group_size, int32_t bits) {
   if (bits != 4) return fail(IMQ_EUNSUPPORTED, "only 4-bit weights are supported");
@@ -1153,13 +1104,14 @@ int32_t imq_abi_version(void) { return IMQ_ABI_VERSION; }
 int32_t imq_device_check(char* arch, size_t arch_len, int32_t* cu_count) {
   int32_t code = IMQ_OK;
   int dev = -1;
-  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < imq_rt::kMaxDevices) {
     current_device(&code);
+    const imq_rt::DeviceInfo& info = imq_rt::device_info(dev);
     if (arch && arch_len) {
-      strncpy(arch, g_devices[dev].arch, arch_len - 1);
+      strncpy(arch, info.arch, arch_len - 1);
       arch[arch_len - 1] = 0;
     }
-    if (cu_count) *cu_count = g_devices[dev].cu_count;
+    if (cu_count) *cu_count = info.cu_count;
     return code == IMQ_OK ? ok() : code;
   }
   return fail(IMQ_EUNAVAILABLE, "no HIP device is available");
@@ -1278,12 +1230,6 @@ int32_t imq_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* b
   return ok();
 }
 
-int32_t imq_last_error(char* buf, size_t len) {
-  if (buf && len) {
-    strncpy(buf, g_last_msg.c_str(), len - 1);
-    buf[len - 1] = 0;
-  }
-  return g_last_code;
-}
+int32_t imq_last_error(char* buf, size_t len) { return imq_rt::last_error(buf, len); }
 
 }  // extern "C"

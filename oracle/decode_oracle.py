@@ -1,0 +1,144 @@
+"""CPU oracle for the decode step around the 4-bit projections — TEST INFRASTRUCTURE ONLY.
+
+Only `tests/`, `__graft_entry__.smoke()` and the CPU-baseline leg of `bench.py` may use
+this module, and only as the checker.  It restates, in numpy float64, the reference's
+decode step for a Qwen3-style decoder (ironmule/dense_cpu.py:188-220, `CpuDensePlan.
+forward`; ironmule/dense_plan.py:351-383, `DensePlan.forward` and `_rope`):
+
+    h = embed(tokens)                                         (fp32 residual stream)
+    per layer:
+        x = rms_norm(h, input_layernorm)                      -> bf16 (qmv input)
+        q, k, v = x @ Wq.T, x @ Wk.T, x @ Wv.T                 -> bf16
+        q, k = q_norm(q), k_norm(k)                           -> bf16 (module outputs)
+        q, k = rope(q, pos), rope(k, pos)                     -> bf16
+        KV[slot][:, pos] = k, v
+        o = softmax(scale * q . K[:pos+1]) V[:pos+1]          -> bf16 (GQA)
+        h = h + o @ Wo.T                                      (o_proj output bf16)
+        x = rms_norm(h, post_attention_layernorm)             -> bf16
+        h = h + (silu(x @ Wg.T) * (x @ Wu.T)) @ Wd.T          (bf16 at each output)
+    logits = rms_norm(h, norm) @ Whead.T                      (fp32)
+
+The "-> bf16" marks are where this build's GPU step rounds to bf16 (the projections'
+inputs and outputs are bf16, as in the reference's GPU plans); `round_bf16=False` drops
+them, giving the all-fp32 composition of the CPU plan.  Each helper names the reference
+lines it restates; tests/test_decode_oracle.py pins every helper against an independent
+implementation (torch's rms_norm / scaled_dot_product_attention / silu on the CPU) or a
+closed form (rotations compose and preserve length, position 0 is the identity, one key
+returns its value).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import oracle as qmv_oracle
+
+HEAD_DIM = 128
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round to bf16 (nearest even) and back to float64."""
+    f = np.asarray(x, dtype=np.float32)
+    return qmv_oracle.bf16_to_f32(qmv_oracle.f32_to_bf16(f)).astype(np.float64)
+
+
+def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """x * rsqrt(mean(x^2) + eps) * weight over the last axis (mx.fast.rms_norm,
+    ironmule/dense_plan.py:362, 364-367)."""
+    x = np.asarray(x, dtype=np.float64)
+    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * inv * np.asarray(weight, dtype=np.float64)
+
+
+def rope(x: np.ndarray, positions: np.ndarray, theta: float) -> np.ndarray:
+    """Non-interleaved rotary embedding over the last axis (D = 128): pair (i, i + D/2)
+    turns by pos * theta^(-2i / D) (mx.fast.rope(..., traditional=False, base=theta,
+    scale=1.0, offset=pos), ironmule/dense_plan.py:378-383).  x is (B, H, D), positions (B,)."""
+    x = np.asarray(x, dtype=np.float64)
+    half = x.shape[-1] // 2
+    inv_freq = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / x.shape[-1])
+    ang = np.asarray(positions, dtype=np.float64)[:, None, None] * inv_freq[None, None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=-1)
+
+
+def attention(q: np.ndarray, keys: np.ndarray, values: np.ndarray, scale: float) -> np.ndarray:
+    """Grouped-query attention of one request: q (Hq, D) against keys/values (Hkv, L, D);
+    query head h reads KV head h // (Hq / Hkv) (ironmule/dense_cpu.py:180-185, `_attend`)."""
+    hq, d = q.shape
+    hkv = keys.shape[0]
+    grouped = np.asarray(q, np.float64).reshape(hkv, hq // hkv, d)
+    scores = grouped @ np.asarray(keys, np.float64).transpose(0, 2, 1) * scale  # (Hkv, G, L)
+    scores -= scores.max(axis=-1, keepdims=True)
+    p = np.exp(scores)
+    p /= p.sum(axis=-1, keepdims=True)
+    return (p @ np.asarray(values, np.float64)).reshape(hq, d)
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """silu(gate) * up, silu(g) = g / (1 + exp(-g)) (swiglu, ironmule/dense_plan.py:374-375)."""
+    g = np.asarray(gate, np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(up, np.float64)
+
+
+@dataclass
+class Layer:
+    """One decoder layer's dequantised weights (float64) and norm weights."""
+    wq: np.ndarray
+    wk: np.ndarray
+    wv: np.ndarray
+    wo: np.ndarray
+    wg: np.ndarray
+    wu: np.ndarray
+    wd: np.ndarray
+    input_norm: np.ndarray
+    post_norm: np.ndarray
+    q_norm: np.ndarray
+    k_norm: np.ndarray
+
+
+@dataclass
+class Model:
+    layers: list
+    embed: np.ndarray   # (vocab, dim) dequantised, also the tied head
+    norm: np.ndarray
+    heads: int
+    kv_heads: int
+    eps: float
+    theta: float
+
+
+def decode_step(model: Model, keys: list, values: list, tokens, slots, positions,
+                round_bf16: bool = True):
+    """One decode step of B requests; keys/values[layer] are (slots, Hkv, C, D) float64
+    pools, updated in place at (slot, :, pos).  Returns float64 logits (B, vocab)."""
+    r = bf16_round if round_bf16 else (lambda a: np.asarray(a, np.float64))
+    d = HEAD_DIM
+    tokens = np.asarray(tokens)
+    slots = np.asarray(slots)
+    positions = np.asarray(positions)
+    b = tokens.shape[0]
+    h = model.embed[tokens].astype(np.float64)
+    scale = d ** -0.5
+    for i, lay in enumerate(model.layers):
+        x = r(rms_norm(h, lay.input_norm, model.eps))
+        q = r(x @ lay.wq.T).reshape(b, model.heads, d)
+        k = r(x @ lay.wk.T).reshape(b, model.kv_heads, d)
+        v = r(x @ lay.wv.T).reshape(b, model.kv_heads, d)
+        q = r(rope(r(rms_norm(q, lay.q_norm, model.eps)), positions, model.theta))
+        k = r(rope(r(rms_norm(k, lay.k_norm, model.eps)), positions, model.theta))
+        for row in range(b):
+            keys[i][slots[row], :, positions[row]] = k[row]
+            values[i][slots[row], :, positions[row]] = v[row]
+        o = np.stack([r(attention(q[row], keys[i][slots[row], :, :positions[row] + 1],
+                                  values[i][slots[row], :, :positions[row] + 1], scale))
+                      for row in range(b)]).reshape(b, model.heads * d)
+        h = h + r(o @ lay.wo.T)
+        x = r(rms_norm(h, lay.post_norm, model.eps))
+        act = r(silu_mul(r(x @ lay.wg.T), r(x @ lay.wu.T)))
+        h = h + r(act @ lay.wd.T)
+    x = r(rms_norm(h, model.norm, model.eps))
+    return x @ model.embed.T

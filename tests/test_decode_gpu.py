@@ -1,0 +1,282 @@
+"""GPU parity of the decode-step kernels (include/ironmule_decode.h) and of a whole
+decode step, against the decode oracle, through the C ABI.
+
+Bars: embedding rows and the residual add bit-exact (fp32); RMSNorm, SiLU * up and
+attention outputs within one bf16 ulp of the float64 reference plus a small absolute
+allowance for cancellation; q/k after norm + rotation within two bf16 ulps of their
+pair's length (the rotation mixes two values that each carry one rounding); v and the
+KV placement exact.  The whole step (a small decoder: 2 layers, hidden 256, 4/2 heads)
+within max|logit - ref| / max|ref| <= 1e-2 of the oracle step with the same bf16
+rounding points (the reference's own probe tolerance, ironmule/cuda_native.py:253-268).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from tests.conftest import gpu_available
+from tests.gpu_util import announce, bf16_bits
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+
+RNG = np.random.default_rng(20261207)
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+
+    from ironmule_amd import _native
+    from oracle import decode_oracle as do
+    from oracle import oracle as orc
+    code, arch, _ = _native.device_check()
+    assert code == 0, f"device {arch} is not supported"
+    orc.lib()
+    return torch, _native, do, orc
+
+
+def _bf16(torch, a, device="cuda"):
+    """float array -> bf16 device tensor (round to nearest even) and its exact values."""
+    t = torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16)
+    return t.to(device), t.float().numpy().astype(np.float64)
+
+
+def _vals(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def _ulp(v):
+    from oracle import oracle as orc
+    return orc.bf16_ulp(np.asarray(v, np.float32)).astype(np.float64)
+
+
+def test_embed_rows_are_bit_exact(env):
+    torch, n, do, orc = env
+    announce("embed 1000 x 512")
+    pr = orc.synthetic(1000, 512, 1, seed=11)
+    w = torch.from_numpy(pr.w.view(np.int32)).cuda()
+    s = torch.from_numpy(pr.s).view(torch.bfloat16).cuda()
+    b = torch.from_numpy(pr.b).view(torch.bfloat16).cuda()
+    tokens = torch.tensor([0, 999, 17, 17, 500], dtype=torch.int32, device="cuda")
+    h = torch.empty((5, 512), dtype=torch.float32, device="cuda")
+    n.embed(w, s, b, tokens, h)
+    want = orc.dequant_f32(pr.w, pr.s, pr.b)[[0, 999, 17, 17, 500]]
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    bad = torch.tensor([1000, -1], dtype=torch.int32, device="cuda")
+    h2 = torch.zeros((2, 512), dtype=torch.float32, device="cuda")
+    n.embed(w, s, b, bad, h2)
+    assert torch.isnan(h2).all()
+
+
+@pytest.mark.parametrize("rows,dim,with_delta", [(1, 2560, True), (32, 2560, True), (3, 100, False),
+                                                 (2, 8192, True)])
+def test_add_rmsnorm(env, rows, dim, with_delta):
+    torch, n, do, orc = env
+    announce("add_rmsnorm", rows, dim, with_delta)
+    h0 = RNG.standard_normal((rows, dim)).astype(np.float32) * 3
+    h = torch.from_numpy(h0.copy()).cuda()
+    w, wv = _bf16(torch, RNG.uniform(0.5, 1.5, dim))
+    delta, dv = _bf16(torch, RNG.standard_normal((rows, dim)))
+    out = torch.empty((rows, dim), dtype=torch.bfloat16, device="cuda")
+    n.add_rmsnorm(h, w, out, 1e-6, delta=delta if with_delta else None)
+    h_new = h0 + (dv.astype(np.float32) if with_delta else 0)
+    assert np.array_equal(h.cpu().numpy(), h_new.astype(np.float32))  # the add is exact fp32
+    ref = do.rms_norm(h_new.astype(np.float64), wv, 1e-6)
+    err = np.abs(_vals(out) - ref)
+    assert (err <= _ulp(ref) + 1e-6 * np.abs(ref).max()).all(), err.max()
+
+
+@pytest.mark.parametrize("B,hq,hkv", [(1, 32, 8), (32, 32, 8), (3, 8, 8)])
+def test_qk_norm_rope_and_kv_write(env, B, hq, hkv):
+    torch, n, do, orc = env
+    announce("qk_norm_rope", B, hq, hkv)
+    slots_n, cap, theta, eps = max(B, 4), 700, 1e6, 1e-6
+    q, qv = _bf16(torch, RNG.standard_normal((B, hq * 128)))
+    k, kv = _bf16(torch, RNG.standard_normal((B, hkv * 128)))
+    v, vv = _bf16(torch, RNG.standard_normal((B, hkv * 128)))
+    qn, qnv = _bf16(torch, RNG.uniform(0.8, 1.2, 128))
+    kn, knv = _bf16(torch, RNG.uniform(0.8, 1.2, 128))
+    slots = RNG.permutation(slots_n)[:B].astype(np.int32)
+    pos = RNG.integers(0, cap, B).astype(np.int32)
+    pos[0] = cap - 1
+    kp = torch.zeros((slots_n, hkv, cap, 128), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    q_out = torch.empty((B, hq * 128), dtype=torch.bfloat16, device="cuda")
+    n.qk_norm_rope(q, k, v, qn, kn, torch.from_numpy(pos).cuda(), torch.from_numpy(slots).cuda(),
+                   q_out, kp, vp, theta, eps)
+
+    def reference(x, nw, heads):
+        x = x.reshape(B, heads, 128)
+        normed = do.bf16_round(do.rms_norm(x, nw, eps))
+        return do.rope(normed, pos, theta), normed
+
+    for got, (ref, normed) in ((_vals(q_out).reshape(B, hq, 128), reference(qv, qnv, hq)),
+                               (_vals(kp)[slots, :, pos], reference(kv, knv, hkv))):
+        pair = np.sqrt(normed[..., :64] ** 2 + normed[..., 64:] ** 2)
+        bound = 2.0 ** -7 * np.concatenate([pair, pair], axis=-1) + 1e-30
+        err = np.abs(got - ref)
+        assert (err <= bound).all(), (err / bound).max()
+    assert np.array_equal(bf16_bits(vp)[slots, :, pos], bf16_bits(v).reshape(B, hkv, 128))
+    # nothing else was written
+    mask = np.zeros((slots_n, cap), bool)
+    mask[slots, pos] = True
+    assert not bf16_bits(kp).transpose(0, 2, 1, 3)[~mask].any()
+    assert not bf16_bits(vp).transpose(0, 2, 1, 3)[~mask].any()
+
+
+def test_qk_norm_rope_refuses_out_of_range_requests(env):
+    torch, n, do, orc = env
+    announce("qk_norm_rope refusals")
+    q = torch.ones((2, 8 * 128), dtype=torch.bfloat16, device="cuda")
+    k = torch.ones((2, 2 * 128), dtype=torch.bfloat16, device="cuda")
+    kp = torch.zeros((2, 2, 16, 128), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    q_out = torch.zeros_like(q)
+    norm = torch.ones(128, dtype=torch.bfloat16, device="cuda")
+    n.qk_norm_rope(q, k, k, norm, norm, torch.tensor([16, 3], dtype=torch.int32, device="cuda"),
+                   torch.tensor([0, 2], dtype=torch.int32, device="cuda"), q_out, kp, vp, 1e6, 1e-6)
+    assert not kp.any() and not vp.any() and not q_out.any()
+
+
+def _attention_case(torch, n, do, B, hq, hkv, lengths, cap=600, slots_n=None, max_len=None):
+    slots_n = slots_n or B + 1
+    kp, kpv = _bf16(torch, RNG.standard_normal((slots_n, hkv, cap, 128)))
+    vp, vpv = _bf16(torch, RNG.standard_normal((slots_n, hkv, cap, 128)))
+    q, qv = _bf16(torch, RNG.standard_normal((B, hq, 128)))
+    slots = RNG.permutation(slots_n)[:B].astype(np.int32)
+    lengths = np.asarray(lengths, np.int32)
+    max_len = max_len or max(1, int(lengths.max()))
+    out = torch.empty((B, hq, 128), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(n.attention_workspace(B, hq, max_len), dtype=torch.float32, device="cuda")
+    counters = torch.zeros(B * hkv, dtype=torch.int32, device="cuda")
+    args = (q, kp, vp, torch.from_numpy(lengths).cuda(), torch.from_numpy(slots).cuda(), out,
+            max_len, 128 ** -0.5, ws, counters)
+    n.attention_decode(*args)
+    return args, out, counters, (qv, kpv, vpv, slots, lengths)
+
+
+@pytest.mark.parametrize("B,hq,hkv,lengths", [
+    (1, 32, 8, [513]), (5, 32, 8, [1, 63, 64, 65, 513]), (32, 32, 8, None),
+    (3, 8, 8, [7, 128, 300]), (2, 16, 2, [200, 129]), (2, 8, 1, [64, 1])])
+def test_attention_matches_oracle(env, B, hq, hkv, lengths):
+    torch, n, do, orc = env
+    lengths = lengths if lengths is not None else [513] * B
+    announce("attention", B, hq, hkv, lengths[:4])
+    args, out, counters, (qv, kpv, vpv, slots, lens) = _attention_case(torch, n, do, B, hq, hkv,
+                                                                       lengths)
+    got = _vals(out)
+    for b in range(B):
+        L = int(lens[b])
+        ref = do.attention(qv[b], kpv[slots[b], :, :L], vpv[slots[b], :, :L], 128 ** -0.5)
+        err = np.abs(got[b] - ref)
+        bound = _ulp(ref) + 1e-5 * np.abs(vpv[slots[b], :, :L]).max()
+        assert (err <= bound).all(), (b, (err - bound).max())
+    assert not counters.any()  # every call leaves its counters at zero
+    first = bf16_bits(out).copy()
+    n.attention_decode(*args)  # deterministic: the same bits again
+    assert np.array_equal(bf16_bits(out), first)
+
+
+def test_attention_edge_requests_get_zeros(env):
+    torch, n, do, orc = env
+    announce("attention edges")
+    args, out, counters, _ = _attention_case(torch, n, do, 3, 8, 2, [0, 5, -3], slots_n=4,
+                                             max_len=16)
+    got = _vals(out)
+    assert not got[0].any() and not got[2].any() and np.isfinite(got[1]).all()
+    q, kp, vp, lengths, slots, out, max_len, scale, ws, c = args
+    bad_slots = torch.tensor([9, 0, 1], dtype=torch.int32, device="cuda")
+    n.attention_decode(q, kp, vp, torch.tensor([5, 5, 5], dtype=torch.int32, device="cuda"),
+                       bad_slots, out, max_len, scale, ws, c)
+    assert not _vals(out)[0].any() and not c.any()
+
+
+@pytest.mark.parametrize("count", [8, 311296, 13])
+def test_silu_mul(env, count):
+    torch, n, do, orc = env
+    announce("silu_mul", count)
+    g, gv = _bf16(torch, RNG.standard_normal(count) * 4)
+    u, uv = _bf16(torch, RNG.standard_normal(count))
+    out = torch.empty(count, dtype=torch.bfloat16, device="cuda")
+    n.silu_mul(g, u, out)
+    ref = do.silu_mul(gv, uv)
+    err = np.abs(_vals(out) - ref)
+    assert (err <= _ulp(ref) + 1e-30).all(), err.max()
+
+
+def _tiny():
+    from ironmule_amd.decode import DecoderConfig
+    return DecoderConfig(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128,
+                         intermediate=512, vocab=512, eps=1e-6, theta=1e6)
+
+
+def _oracle_model(torch, do, orc, weights):
+    def deq(q):
+        w, s, b = (t.cpu() for t in q)
+        return orc.dequant_f32(w.numpy().view(np.uint32), s.view(torch.int16).numpy().view(np.uint16),
+                               b.view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+    c = weights.config
+    layers = [do.Layer(wq=deq(L["q"]), wk=deq(L["k"]), wv=deq(L["v"]), wo=deq(L["o"]),
+                       wg=deq(L["gate"]), wu=deq(L["up"]), wd=deq(L["down"]),
+                       input_norm=_vals(L["input_norm"]), post_norm=_vals(L["post_norm"]),
+                       q_norm=_vals(L["q_norm"]), k_norm=_vals(L["k_norm"]))
+              for L in weights.layers]
+    return do.Model(layers=layers, embed=deq(weights.embed), norm=_vals(weights.norm),
+                    heads=c.heads, kv_heads=c.kv_heads, eps=c.eps, theta=c.theta)
+
+
+def test_decode_step_matches_oracle(env):
+    torch, n, do, orc = env
+    from ironmule_amd.decode import DecodeState, decode_step, random_weights
+    announce("decode step, small decoder, B=3")
+    cfg = _tiny()
+    weights = random_weights(cfg, "cuda", seed=5)
+    state = DecodeState(cfg, batch=3, slots=4, capacity=80, max_len=80, device="cuda")
+    for kp, vp in zip(state.k_pool, state.v_pool):  # a synthetic context in every slot
+        kp.copy_(torch.randn(kp.shape, device="cuda").to(torch.bfloat16))
+        vp.copy_(torch.randn(vp.shape, device="cuda").to(torch.bfloat16))
+    keys = [_vals(kp) for kp in state.k_pool]
+    values = [_vals(vp) for vp in state.v_pool]
+    model = _oracle_model(torch, do, orc, weights)
+    tokens, slots, positions = [5, 511, 200], [3, 0, 1], [64, 0, 79]
+    for step in range(2):  # a second step reads the keys the first one wrote
+        state.set_requests(tokens, slots, positions)
+        logits = decode_step(weights, state)
+        torch.cuda.synchronize()
+        ref = do.decode_step(model, keys, values, tokens, slots, positions, round_bf16=True)
+        got = logits.cpu().numpy().astype(np.float64)
+        rel = np.abs(got - ref).max() / np.abs(ref).max()
+        assert rel <= 1e-2, (step, rel)
+        for i in range(cfg.layers):
+            for r in range(3):
+                kg = _vals(state.k_pool[i])[slots[r], :, positions[r]]
+                kr = keys[i][slots[r], :, positions[r]]
+                assert np.abs(kg - kr).max() <= 0.05 * np.abs(kr).max(), (step, i, r)
+        tokens = [int(t) for t in np.argmax(got, axis=1)]
+        positions = [p + 1 if p + 1 < 80 else p for p in positions]
+
+
+def test_decode_step_at_qwen3_4b_shapes_is_deterministic(env):
+    """Real Qwen3-4B layer shapes (2 of the 36 layers, full vocabulary head), B = 32 and
+    B = 1: the step runs, its logits are finite, and a replay gives the same bits."""
+    torch, n, do, orc = env
+    from ironmule_amd.decode import DecodeState, DecoderConfig, decode_step, random_weights
+    cfg = DecoderConfig(layers=2)
+    weights = random_weights(cfg, "cuda", seed=9)
+    for batch in (32, 1):
+        announce("decode step qwen3-4b shapes", batch)
+        state = DecodeState(cfg, batch=batch, slots=batch, capacity=520, max_len=520, device="cuda")
+        for kp in state.k_pool + state.v_pool:
+            kp.copy_(torch.randn(kp.shape, device="cuda").to(torch.bfloat16))
+        state.set_requests(list(range(batch)), list(range(batch)), [512] * batch)
+        first = decode_step(weights, state).clone()
+        torch.cuda.synchronize()
+        assert torch.isfinite(first).all()
+        again = decode_step(weights, state)
+        torch.cuda.synchronize()
+        assert torch.equal(first, again)
+        assert math.isfinite(float(first.abs().max()))
