@@ -192,6 +192,45 @@ def bench_config(torch, native, n, k, ms, y_dtype, copies, device, seed, repeats
     return out
 
 
+CONTEXT = 512  # tokens already in every request's KV slot
+
+
+def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, device="cuda:0",
+                 seed: int = SEED + 4):
+    """Full synthetic Qwen3-4B decode step (36 layers of 4-bit projections + the 151,936-
+    token tied head, GQA attention over a 512-token KV context per request), as one HIP
+    graph per batch size; returns tokens/s and the weight + KV bytes per step."""
+    from ironmule_amd.decode import DecodeState, DecoderConfig, decode_step, random_weights
+
+    cfg = DecoderConfig()
+    weights = random_weights(cfg, device, seed=seed)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed + 1)
+    out = {}
+    for b in batches:
+        state = DecodeState(cfg, batch=b, slots=b, capacity=CONTEXT + 8, max_len=CONTEXT + 8,
+                            device=device)
+        for pool in state.k_pool + state.v_pool:
+            pool.copy_(torch.randn(pool.shape, device=device, generator=gen).to(torch.bfloat16))
+        state.set_requests(torch.randint(0, cfg.vocab, (b,), generator=gen, device=device).tolist(),
+                           list(range(b)), [CONTEXT] * b)
+        stream = torch.cuda.Stream(device=device)
+        runner = GraphRunner(torch, [lambda: decode_step(weights, state, stream=stream)], stream)
+        for _ in range(warmup):
+            runner.replay()
+        sec = time_graph(torch, runner, steps, stream)
+        kv_bytes = cfg.layers * b * cfg.kv_heads * (CONTEXT + 1) * cfg.head_dim * 2 * 2
+        out[str(b)] = {"ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(b / sec, 1),
+                       "weight_gbs": round(cfg.weight_bytes() / sec / 1e9, 1),
+                       "weight_plus_kv_gbs": round((cfg.weight_bytes() + kv_bytes) / sec / 1e9, 1),
+                       "launches_per_step": 2 + cfg.layers * 9}
+        del runner, state
+        torch.cuda.empty_cache()
+    del weights
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds: float = 10.0):
     """The oracle's restatement of the reference CUDA row kernel (ironmule/cuda_native.py:
     57-128) on the host cores, over the same layer shapes, rotating 4 layer copies."""
@@ -249,7 +288,10 @@ def copy_calibration(torch, device) -> None:
 
 
 def _short(name: str) -> str:
-    for marker in ("qmv_fixed_kernel", "qmv_rows_kernel", "qmv_mfma_kernel", "dequant_kernel"):
+    for marker in ("qmv_m1c_kernel", "qmv_m1_kernel", "qmv_rows_kernel", "qmv_mfma_kernel",
+                   "qmv_mma_kernel", "qmv_reduce_kernel",
+                   "dequant_kernel", "embed_kernel", "add_rmsnorm_kernel", "qk_norm_rope_kernel",
+                   "attention_partial_kernel", "attention_combine_kernel", "silu_mul_kernel"):
         if marker in name:
             return name[name.index(marker):].split("(")[0]
     if "direct_copy_kernel" in name:
@@ -276,11 +318,11 @@ def profile_summary(directories: list[str]) -> str:
             key = (_short(r["Kernel_Name"]), int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]),
                    r.get("VGPR_Count", "?"), r.get("LDS_Block_Size", "?"))
             agg[key].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
-        lines += [f"kernel trace ({os.path.basename(path)}), qmv kernels:", "",
+        lines += [f"kernel trace ({os.path.basename(path)}), this library's kernels:", "",
                   "| kernel | workgroups | vgpr | lds bytes | dispatches | mean us | median us |",
                   "|---|---|---|---|---|---|---|"]
         for key, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
-            if "kernel<" not in key[0]:
+            if "at::native" in key[0] or "rocclr" in key[0]:
                 continue
             v.sort()
             lines.append(f"| {key[0]} | {key[1]} | {key[2]} | {key[3]} | {len(v)} | "
@@ -296,7 +338,7 @@ def profile_summary(directories: list[str]) -> str:
         copy = agg[max(copies, key=lambda k: k[1])] if copies else None
         lines += [f"counters ({os.path.basename(path)}), mean per dispatch:", ""]
         for key, cs in sorted(agg.items()):
-            if "kernel<" not in key[0]:
+            if "at::native" in key[0] or "rocclr" in key[0] or key[0] == "torch copy kernel":
                 continue
             vals = ", ".join(f"{c}={sum(v) / len(v):.1f}" for c, v in sorted(cs.items()))
             lines.append(f"* {key[0]}, {key[1]} workgroups, {len(next(iter(cs.values())))} "
@@ -310,7 +352,7 @@ def profile_summary(directories: list[str]) -> str:
                 lines.append(f"* calibration: the copy moves {known} B; {c} reads {kib:.1f} KiB "
                              f"-> factor {factor:.4f}")
                 for key, cs in agg.items():
-                    if "kernel<" in key[0] and c in cs:
+                    if "at::native" not in key[0] and key[0] != "torch copy kernel" and c in cs:
                         traffic[key][c] = sum(cs[c]) / len(cs[c]) * 1024 * factor
         lines.append("")
     if traffic:
@@ -346,6 +388,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the full decode step")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the full decode step and exit (a short program for profilers)")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="time only the headline layer steps (a short program for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -375,6 +420,10 @@ def main() -> None:
         raise SystemExit(f"unsupported device {arch!r}")
     if args.copy_calibration:
         copy_calibration(torch, device)
+    if args.decode_only:
+        print(json.dumps({"metric": "decode tokens/s (profiling run)", **bench_decode(torch, device=device)}),
+              flush=True)
+        return
     if args.only:
         parts = args.only.split(",")
         n, k, m = (int(v) for v in parts[:3])
@@ -428,8 +477,16 @@ def main() -> None:
         "layer_one_launch": {"us": round(res["one_launch"]["us"], 3),
                              "gbs": round(res["one_launch"]["gbs"], 1),
                              "note": "all 7 independent projections in one grouped launch"},
-        "decode_tokens_per_s": {"batch_1": None, "batch_32": None},
     }
+    if not args.no_decode:
+        print("[bench] decode step", file=sys.stderr, flush=True)
+        dec = bench_decode(torch, device=device)
+        line["decode_tokens_per_s"] = {"batch_1": dec["1"]["tokens_per_s"],
+                                       "batch_32": dec["32"]["tokens_per_s"]}
+        line["decode"] = {"workload": "synthetic qwen3-4b decode step: 36 layers + tied "
+                                      "151936-token head, 4-bit group-64 weights, GQA 32/8 "
+                                      f"heads, {CONTEXT}-token KV context per request, one "
+                                      "hip graph per step", **dec}
     if not args.no_extra:
         print("[bench] secondary configs", file=sys.stderr, flush=True)
         line["configs"] = {

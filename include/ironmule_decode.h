@@ -66,25 +66,23 @@ IMQ_API int32_t imq_qk_norm_rope(const uint16_t* q, const uint16_t* k, const uin
                                  float eps, void* stream);
 
 /* Bytes of fp32 workspace imq_attention_decode needs for B requests, Hq query heads and
- * keys up to max_len (a partial result per 64-key chunk), and the number of uint32
- * counters it needs (B * Hkv).  The counters must be zero before the first call; every
- * call leaves them zero again. */
+ * keys up to max_len (at most one partial result per 64-key chunk). */
 IMQ_API size_t imq_attention_workspace(int32_t B, int32_t Hq, int32_t max_len);
 
 /* out[b][h] = softmax(scale * q[b][h] . K[slot][h/G][:len]) V[slot][h/G][:len] with
  * slot = slots[b], len = lengths[b] (clamped to max_len and capacity), G = Hq / Hkv <= 8
  * query heads per KV head (grouped-query attention).  A request with len <= 0 or a slot
- * outside [0, num_slots) gets zeros.  Keys are processed in 64-key chunks by separate
- * workgroups; the last workgroup of each (request, KV head) combines the chunks in chunk
- * order, so the result does not depend on scheduling.  Calls that share
- * `workspace`/`counters` must not overlap.
- * Replaces fa2 (ironmule/dense_plan.py:250-278): FA2_PARTIAL and FA2_COMBINE in one launch. */
+ * outside [0, num_slots) gets zeros.  The keys of each (request, KV head) are split over
+ * several workgroups (whole 64-key chunks each, enough splits to fill the GPU); a second
+ * launch merges the splits in split order, so the result does not depend on scheduling.
+ * Calls that share `workspace` must not overlap.
+ * Replaces fa2 (ironmule/dense_plan.py:250-278): the FA2_PARTIAL / FA2_COMBINE pair. */
 IMQ_API int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool,
                                      const uint16_t* v_pool, const int32_t* lengths,
                                      const int32_t* slots, uint16_t* out, int32_t B, int32_t Hq,
                                      int32_t Hkv, int32_t capacity, int32_t num_slots,
                                      int32_t max_len, float scale, float* workspace,
-                                     uint32_t* counters, void* stream);
+                                     void* stream);
 
 /* out = bf16(silu(gate) * up), silu(g) = g / (1 + exp(-g)), n elements.
  * Replaces swiglu(gate, up) (ironmule/dense_plan.py:374-375; nn.silu in dense_cpu.py:216). */

@@ -121,6 +121,20 @@ IMQ_API int32_t imq_qmv_grouped(const imq_problem* problems, int32_t count, int3
                                 int32_t group_size, int32_t bits, int32_t y_dtype,
                                 void* stream);
 
+/* Bytes of workspace imq_qmv_grouped_ws can use for these problems at M rows: with it the
+ * groups of small-N weights are split over more workgroups (fp32 partials, added in a
+ * fixed order by a second launch).  0 when no split helps (M < 3 or enough rows). */
+IMQ_API size_t imq_qmv_grouped_workspace(const imq_problem* problems, int32_t count, int32_t M);
+
+/* imq_qmv_grouped with a caller-provided fp32 workspace of workspace_bytes (16-byte
+ * aligned; may be 0 bytes, then no split).  Same results as imq_qmv_grouped up to the
+ * fp32 summation order of the splits; calls that share a workspace must not overlap.
+ * Replaces the same reference calls as imq_qmv_grouped, and imq_qmv at M >= 3 (the
+ * shared-weight form, ironmule/cuda_native.py:155-168 for M <= 8, up to 32 here). */
+IMQ_API int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, int32_t M,
+                                   int32_t group_size, int32_t bits, int32_t y_dtype,
+                                   float* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * out[n][k] = scales[n][k/64] * q[n][k] + biases[n][k/64] as fp32 (bit-exact:
  * scale*q is exact in fp32, so only the add rounds), or that fp32 value rounded

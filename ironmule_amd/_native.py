@@ -68,6 +68,9 @@ _SIGNATURES = {
     "imq_qmv": ([_P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_qmv_multi": ([_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_qmv_grouped": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P], _I32),
+    "imq_qmv_grouped_workspace": ([ctypes.POINTER(Problem), _I32, _I32], ctypes.c_size_t),
+    "imq_qmv_grouped_ws": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P,
+                            ctypes.c_size_t, _P], _I32),
     "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_last_error": ([ctypes.c_char_p, ctypes.c_size_t], _I32),
     # decode-step kernels (include/ironmule_decode.h)
@@ -77,7 +80,7 @@ _SIGNATURES = {
                           ctypes.c_float, ctypes.c_float, _P], _I32),
     "imq_attention_workspace": ([_I32, _I32, _I32], ctypes.c_size_t),
     "imq_attention_decode": ([_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
-                              ctypes.c_float, _P, _P, _P], _I32),
+                              ctypes.c_float, _P, _P], _I32),
     "imq_silu_mul": ([_P, _P, _P, _I64, _P], _I32),
 }
 
@@ -189,9 +192,30 @@ def qmv(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, x: torch.Te
         out = torch.empty((m, n), dtype=dtype, device=w.device)
     elif tuple(out.shape) != (m, n) or out.dtype != dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous (M, N) tensor of the output dtype")
+    if m >= 3:  # the shared-weight MFMA path, with a workspace for split groups
+        probs = (Problem * 1)()
+        probs[0] = Problem(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), x2.data_ptr(), k,
+                           out.data_ptr(), n, n, k)
+        _grouped_launch(probs, 1, m, dtype, w.device, stream)
+        return out
     _check(lib().imq_qmv(_ptr(w), _ptr(scales), _ptr(biases), _ptr(x2), k, _ptr(out), n,
                          m, n, k, GROUP_SIZE, BITS, _DTYPE_CODE[dtype], _stream(stream)))
     return out
+
+
+def _grouped_launch(probs, count: int, m: int, dtype: torch.dtype, device, stream) -> None:
+    """imq_qmv_grouped, through imq_qmv_grouped_ws with a fresh workspace when the library
+    wants one (M >= 3 and small N)."""
+    nbytes = int(lib().imq_qmv_grouped_workspace(probs, count, m)) if m >= 3 else 0
+    if nbytes == 0:
+        _check(lib().imq_qmv_grouped(probs, count, m, GROUP_SIZE, BITS, _DTYPE_CODE[dtype],
+                                     _stream(stream)))
+        return
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+    if stream is not None:
+        ws.record_stream(stream)  # keep it from reuse until that stream's work is done
+    _check(lib().imq_qmv_grouped_ws(probs, count, m, GROUP_SIZE, BITS, _DTYPE_CODE[dtype],
+                                    _ptr(ws), nbytes, _stream(stream)))
 
 
 def qmv_multi(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
@@ -251,8 +275,7 @@ def qmv_grouped(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
         result.append(y)
     if not 1 <= m <= MAX_ROWS:
         raise ValueError(f"the qmv kernels take 1 to {MAX_ROWS} rows, got {m}")
-    _check(lib().imq_qmv_grouped(probs, count, m, GROUP_SIZE, BITS, _DTYPE_CODE[out_dtype],
-                                 _stream(stream)))
+    _grouped_launch(probs, count, m, out_dtype, weights[0][0].device, stream)
     return result
 
 
@@ -338,23 +361,21 @@ def attention_workspace(b: int, hq: int, max_len: int) -> int:
 
 
 def attention_decode(q, k_pool, v_pool, lengths, slots, out, max_len: int, scale: float,
-                     workspace: torch.Tensor, counters: torch.Tensor, stream=None) -> torch.Tensor:
+                     workspace: torch.Tensor, stream=None) -> torch.Tensor:
     """out (B, Hq, 128) bf16 = grouped-query attention of each request over its slot."""
     for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool), ("out", out)):
         _require(t, torch.bfloat16, name)
     _require(lengths, torch.int32, "lengths")
     _require(slots, torch.int32, "slots")
     _require(workspace, torch.float32, "workspace")
-    if counters.dtype not in (torch.int32, torch.uint32) or not counters.is_contiguous():
-        raise ValueError("counters must be contiguous 32-bit integers")
     num_slots, hkv, capacity, d = k_pool.shape
     b = int(lengths.numel())
     hq = q.numel() // (b * d)
-    if workspace.numel() < attention_workspace(b, hq, max_len) or counters.numel() < b * hkv:
-        raise ValueError("workspace or counters too small")
+    if workspace.numel() < attention_workspace(b, hq, max_len):
+        raise ValueError("workspace too small")
     _check(lib().imq_attention_decode(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(lengths),
                                       _ptr(slots), _ptr(out), b, hq, hkv, capacity, num_slots,
-                                      int(max_len), float(scale), _ptr(workspace), _ptr(counters),
+                                      int(max_len), float(scale), _ptr(workspace),
                                       _stream(stream)))
     return out
 

@@ -88,9 +88,12 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t* __restr
 
 // ------------------------------------------------------- residual add + RMSNorm
 
-// One workgroup per row.  Thread t holds values t, t + 256, ...; the sum of squares is
-// added per thread, then over each wavefront (butterfly), then over the four wavefronts in
+// One workgroup per row.  Thread t holds values t, t + 256, ... (VPT of them).  Every
+// load is issued before the first is used (indices past the row are clamped to its last
+// value and masked), so the row costs one memory round trip.  The sum of squares is added
+// per thread, then over each wavefront (butterfly), then over the four wavefronts in
 // order, so the result does not depend on scheduling.
+template <int VPT>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(float* __restrict__ h,
                                                                const uint16_t* __restrict__ delta,
                                                                const uint16_t* __restrict__ weight,
@@ -100,20 +103,23 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(float* __restrict
   const int row = blockIdx.x, tid = threadIdx.x;
   float* hr = h + (size_t)row * dim;
   const uint16_t* dr = delta ? delta + (size_t)row * dim : nullptr;
-  float v[kNormVpt];
+  float v[VPT];
+  uint32_t d[VPT], wv[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int idx = min(tid + kThreads * i, dim - 1);
+    v[i] = hr[idx];
+    d[i] = dr ? dr[idx] : 0u;
+    wv[i] = weight[idx];
+  }
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kNormVpt; ++i) {
+  for (int i = 0; i < VPT; ++i) {
     const int idx = tid + kThreads * i;
-    v[i] = 0.0f;
+    if (dr) v[i] += bf(d[i]);
     if (idx < dim) {
-      float x = hr[idx];
-      if (dr) {
-        x += bf(dr[idx]);
-        hr[idx] = x;
-      }
-      v[i] = x;
-      ss = fmaf(x, x, ss);
+      if (dr) hr[idx] = v[i];
+      ss = fmaf(v[i], v[i], ss);
     }
   }
   ss = wave_sum(ss);
@@ -123,9 +129,9 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(float* __restrict
   const float inv = 1.0f / sqrtf(total / (float)dim + eps);
   uint16_t* orow = out + (size_t)row * dim;
 #pragma unroll
-  for (int i = 0; i < kNormVpt; ++i) {
+  for (int i = 0; i < VPT; ++i) {
     const int idx = tid + kThreads * i;
-    if (idx < dim) orow[idx] = to_bf(v[i] * inv * bf(weight[idx]));
+    if (idx < dim) orow[idx] = to_bf(v[i] * inv * bf(wv[i]));
   }
 }
 
@@ -172,130 +178,167 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
 
 // ------------------------------------------------------------ decode attention
 //
-// Workgroup (chunk c, KV head, request b) reads keys and values [64c, 64c + 64) of its
-// request's slot once into LDS and serves the G query heads that share them (one
-// wavefront per head, G <= 8).  In a wavefront lane t scores key t (64 bf16 dot2 against
-// the head's q), the chunk's max and sum come from butterflies, and lane i then
-// accumulates dimensions 2i, 2i+1 of p . V.  The partial (acc, max, sum) goes to the
-// workspace; the last workgroup of the (request, KV head) to finish, counted with one
-// device-scope atomic, combines the chunks in chunk order and writes bf16 heads.
+// Two launches, no communication between workgroups inside either.
+//
+// attention_partial_kernel: workgroup (split s, KV head, request b) walks its share of
+// the request's keys in 64-key chunks (the next chunk's loads in flight while one
+// computes) and serves the G query heads that read that KV head (one wavefront per head,
+// G <= 8).  Per chunk, lane t scores key t (64 bf16 dot2 against the head's q), the chunk
+// max and sum come from butterflies, lane i accumulates dimensions 2i, 2i+1 of p . V, and
+// the chunk is merged into the running (max, sum, acc) of the split.  The split's partial
+// goes to the workspace.
+//
+// attention_combine_kernel: one wavefront per (request, query head) merges the splits in
+// split order and writes the bf16 head.  Both orders are fixed, so results do not depend
+// on scheduling.
 
 struct AttnLds {
   uint4 k[kChunk][17];        // a key row is 16 uint4; one of padding keeps lanes on
                               // distinct banks when lane t reads row t
   uint32_t v[kChunk][kD / 2];  // lane i reads dword i of a row: conflict-free
   float p[4][kChunk];
-  int last;
 };
 
-__global__ __launch_bounds__(kThreads) void attention_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
-    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ lengths,
-    const int32_t* __restrict__ slots, uint16_t* __restrict__ out, int Hq, int Hkv, int capacity,
-    int max_len, int num_slots, float scale, float* __restrict__ part, float* __restrict__ ml,
-    uint32_t* __restrict__ counters, int NC) {
-  __shared__ AttnLds L;
-  const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int G = Hq / Hkv;
-  const int slot = slots[b];
+struct AttnGeometry {
+  int len;    // keys to attend over (0: none)
+  int slot;
+};
+
+__device__ __forceinline__ AttnGeometry attn_geometry(const int32_t* lengths, const int32_t* slots,
+                                                      int b, int max_len, int capacity,
+                                                      int num_slots) {
+  AttnGeometry g;
+  g.slot = slots[b];
   int len = lengths[b];
   len = len < max_len ? len : max_len;
   len = len < capacity ? len : capacity;
-  if (len <= 0 || slot < 0 || slot >= num_slots) {  // nothing to attend to: zeros
-    if (c == 0)
-      for (int g = wave; g < G; g += 4) {
-        uint16_t* o = out + ((size_t)b * Hq + kvh * G + g) * kD;
-        o[2 * lane] = 0;
-        o[2 * lane + 1] = 0;
+  g.len = (g.slot < 0 || g.slot >= num_slots || len < 0) ? 0 : len;
+  return g;
+}
+
+__global__ __launch_bounds__(kThreads) void attention_partial_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ lengths,
+    const int32_t* __restrict__ slots, int Hq, int Hkv, int capacity, int max_len, int num_slots,
+    float scale, int chunks_per_split, int splits, float* __restrict__ part,
+    float* __restrict__ ml) {
+  __shared__ AttnLds L;
+  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int G = Hq / Hkv;
+  const AttnGeometry geo = attn_geometry(lengths, slots, b, max_len, capacity, num_slots);
+  const int first = s * chunks_per_split * kChunk;
+  if (first >= geo.len) return;  // the combine skips this split
+  const int last = min(geo.len, first + chunks_per_split * kChunk);
+  const size_t base = (((size_t)geo.slot * Hkv + kvh) * capacity) * kD;
+
+  // q of this wavefront's heads, as bf16 pairs (uniform across the wavefront)
+  float M[2] = {-INFINITY, -INFINITY}, Ls[2] = {0.0f, 0.0f};
+  float a0[2] = {0.0f, 0.0f}, a1[2] = {0.0f, 0.0f};
+
+  auto load = [&](int start, uint4 (&kr)[4], uint4 (&vr)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + kThreads * i;
+      const int row = p >> 4, col = p & 15;
+      const int t = start + row < last ? start + row : last - 1;  // stays in the slot
+      kr[i] = *reinterpret_cast<const uint4*>(k_pool + base + (size_t)t * kD + col * 8);
+      vr[i] = *reinterpret_cast<const uint4*>(v_pool + base + (size_t)t * kD + col * 8);
+    }
+  };
+  uint4 kr[4], vr[4];
+  load(first, kr, vr);
+  for (int start = first; start < last; start += kChunk) {
+    const int count = min(kChunk, last - start);
+    __syncthreads();  // the previous chunk's readers are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + kThreads * i;
+      const int row = p >> 4, col = p & 15;
+      L.k[row][col] = kr[i];
+      *reinterpret_cast<uint4*>(&L.v[row][col * 4]) = vr[i];
+    }
+    __syncthreads();
+    if (start + kChunk < last) load(start + kChunk, kr, vr);  // next chunk in flight
+
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int g = wave + 4 * r;
+      if (g >= G) break;
+      const uint4* qv = reinterpret_cast<const uint4*>(q + ((size_t)b * Hq + kvh * G + g) * kD);
+      float sc = -INFINITY;
+      if (lane < count) {
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const uint4 a = qv[j], kk = L.k[lane][j];
+          d = dot2(a.x, kk.x, d);
+          d = dot2(a.y, kk.y, d);
+          d = dot2(a.z, kk.z, d);
+          d = dot2(a.w, kk.w, d);
+        }
+        sc = d * scale;
       }
+      const float mc = wave_max(sc);
+      const float p = lane < count ? expf(sc - mc) : 0.0f;
+      const float lc = wave_sum(p);
+      L.p[wave][lane] = p;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float c0 = 0.0f, c1 = 0.0f;
+      for (int t = 0; t < count; ++t) {
+        const float pt = L.p[wave][t];
+        const uint32_t vd = L.v[t][lane];
+        c0 = fmaf(pt, bf(vd & 0xffffu), c0);
+        c1 = fmaf(pt, bf(vd >> 16), c1);
+      }
+      __builtin_amdgcn_wave_barrier();  // L.p is rewritten by this wave's next head
+      // merge the chunk into the split's running result
+      const float mn = fmaxf(M[r], mc);
+      const float eo = expf(M[r] - mn), ec = expf(mc - mn);
+      Ls[r] = fmaf(Ls[r], eo, lc * ec);
+      a0[r] = fmaf(a0[r], eo, c0 * ec);
+      a1[r] = fmaf(a1[r], eo, c1 * ec);
+      M[r] = mn;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int g = wave + 4 * r;
+    if (g >= G) break;
+    const size_t po = ((size_t)b * Hq + kvh * G + g) * splits + s;
+    reinterpret_cast<float2*>(part + po * kD)[lane] = make_float2(a0[r], a1[r]);
+    if (lane == 0) reinterpret_cast<float2*>(ml)[po] = make_float2(M[r], Ls[r]);
+  }
+}
+
+__global__ __launch_bounds__(64) void attention_combine_kernel(
+    const int32_t* __restrict__ lengths, const int32_t* __restrict__ slots,
+    uint16_t* __restrict__ out, int Hq, int capacity, int max_len, int num_slots,
+    int chunks_per_split, int splits, const float* __restrict__ part, const float* __restrict__ ml) {
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const AttnGeometry geo = attn_geometry(lengths, slots, b, max_len, capacity, num_slots);
+  uint16_t* o = out + ((size_t)b * Hq + h) * kD;
+  const int used = (geo.len + chunks_per_split * kChunk - 1) / (chunks_per_split * kChunk);
+  if (used == 0) {  // nothing to attend to: zeros
+    o[2 * lane] = 0;
+    o[2 * lane + 1] = 0;
     return;
   }
-  const int start = c * kChunk;
-  if (start >= len) return;
-  const int count = min(kChunk, len - start);
-  const int nch = (len + kChunk - 1) / kChunk;
-  const size_t base = (((size_t)slot * Hkv + kvh) * capacity + start) * kD;
-
-  // the chunk's keys and values: 64 rows x 16 pieces of 16 bytes each
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = tid + kThreads * i;
-    const int row = p >> 4, col = p & 15;
-    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-    if (row < count) {
-      kv = *reinterpret_cast<const uint4*>(k_pool + base + (size_t)row * kD + col * 8);
-      vv = *reinterpret_cast<const uint4*>(v_pool + base + (size_t)row * kD + col * 8);
-    }
-    L.k[row][col] = kv;
-    *reinterpret_cast<uint4*>(&L.v[row][col * 4]) = vv;
+  const size_t p0 = ((size_t)b * Hq + h) * splits;
+  float M = -INFINITY;
+  for (int s = 0; s < used; ++s) M = fmaxf(M, ml[2 * (p0 + s)]);
+  float Ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
+  for (int s = 0; s < used; ++s) {
+    const float e = expf(ml[2 * (p0 + s)] - M);
+    Ls = fmaf(ml[2 * (p0 + s) + 1], e, Ls);
+    const float2 pa = reinterpret_cast<const float2*>(part + (p0 + s) * kD)[lane];
+    a0 = fmaf(pa.x, e, a0);
+    a1 = fmaf(pa.y, e, a1);
   }
-  __syncthreads();
-
-  for (int g = wave; g < G; g += 4) {
-    const int h = kvh * G + g;
-    const uint4* qv = reinterpret_cast<const uint4*>(q + ((size_t)b * Hq + h) * kD);
-    float s = -INFINITY;
-    if (lane < count) {
-      float d = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint4 a = qv[j], kk = L.k[lane][j];
-        d = dot2(a.x, kk.x, d);
-        d = dot2(a.y, kk.y, d);
-        d = dot2(a.z, kk.z, d);
-        d = dot2(a.w, kk.w, d);
-      }
-      s = d * scale;
-    }
-    const float m = wave_max(s);
-    const float p = lane < count ? expf(s - m) : 0.0f;
-    const float l = wave_sum(p);
-    L.p[wave][lane] = p;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float a0 = 0.0f, a1 = 0.0f;
-    for (int t = 0; t < count; ++t) {
-      const float pt = L.p[wave][t];
-      const uint32_t vd = L.v[t][lane];
-      a0 = fmaf(pt, bf(vd & 0xffffu), a0);
-      a1 = fmaf(pt, bf(vd >> 16), a1);
-    }
-    const size_t po = ((size_t)b * Hq + h) * NC + c;
-    reinterpret_cast<float2*>(part + po * kD)[lane] = make_float2(a0, a1);
-    if (lane == 0) reinterpret_cast<float2*>(ml)[po] = make_float2(m, l);
-    __builtin_amdgcn_wave_barrier();  // L.p is rewritten by the next head of this wave
-  }
-
-  // the last workgroup of this (request, KV head) combines the chunks
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t done = atomicAdd(&counters[b * Hkv + kvh], 1u);
-    L.last = done == (uint32_t)(nch - 1);
-  }
-  __syncthreads();
-  if (!L.last) return;
-  __threadfence();
-  for (int g = wave; g < G; g += 4) {
-    const int h = kvh * G + g;
-    const size_t p0 = ((size_t)b * Hq + h) * NC;
-    float M = -INFINITY;
-    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, ml[2 * (p0 + cc)]);
-    float Ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
-    for (int cc = 0; cc < nch; ++cc) {
-      const float e = expf(ml[2 * (p0 + cc)] - M);
-      Ls = fmaf(ml[2 * (p0 + cc) + 1], e, Ls);
-      const float2 pa = reinterpret_cast<const float2*>(part + (p0 + cc) * kD)[lane];
-      a0 = fmaf(pa.x, e, a0);
-      a1 = fmaf(pa.y, e, a1);
-    }
-    uint16_t* o = out + ((size_t)b * Hq + h) * kD;
-    o[2 * lane] = to_bf(a0 / Ls);
-    o[2 * lane + 1] = to_bf(a1 / Ls);
-  }
-  if (tid == 0) counters[b * Hkv + kvh] = 0;  // ready for the next call
+  o[2 * lane] = to_bf(a0 / Ls);
+  o[2 * lane + 1] = to_bf(a1 / Ls);
 }
 
 // ------------------------------------------------------------------ SiLU * up
@@ -332,9 +375,21 @@ int32_t launched(const char* what) {
   return ok();
 }
 
-size_t attention_parts(int32_t B, int32_t Hq, int32_t max_len) {
-  const size_t nc = (size_t)((max_len + kChunk - 1) / kChunk);
-  return (size_t)B * Hq * nc;
+// Splits per (request, KV head): enough workgroups to cover the chip about twice, each
+// split a whole number of 64-key chunks.
+struct AttnPlan {
+  int splits;
+  int chunks_per_split;
+};
+
+AttnPlan attention_plan(int32_t B, int32_t Hkv, int32_t span) {
+  const int chunks = (span + kChunk - 1) / kChunk;
+  const int pairs = B * Hkv;
+  int splits = (512 + pairs - 1) / pairs;
+  splits = splits < chunks ? splits : chunks;
+  splits = splits > 1 ? splits : 1;
+  const int cps = (chunks + splits - 1) / splits;
+  return AttnPlan{(chunks + cps - 1) / cps, cps};
 }
 
 }  // namespace
@@ -365,8 +420,16 @@ int32_t imq_add_rmsnorm(float* h, const uint16_t* delta, const uint16_t* weight,
   if (!(eps >= 0.0f)) return fail(IMQ_EINVAL, "eps must be >= 0");
   int32_t code;
   if (!current_device(&code)) return code;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(B), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     h, delta, weight, out, dim, eps);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int vpt = (dim + kThreads - 1) / kThreads;
+  if (vpt <= 4)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<4>, dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, eps);
+  else if (vpt <= 10)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<10>, dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, eps);
+  else if (vpt <= 16)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<16>, dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, eps);
+  else
+    hipLaunchKernelGGL(add_rmsnorm_kernel<kNormVpt>, dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, eps);
   return launched("add_rmsnorm");
 }
 
@@ -390,33 +453,36 @@ int32_t imq_qk_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v
 
 size_t imq_attention_workspace(int32_t B, int32_t Hq, int32_t max_len) {
   if (B < 1 || Hq < 1 || max_len < 1) return 0;
-  return attention_parts(B, Hq, max_len) * (kD + 2) * sizeof(float);
+  const size_t chunks = (size_t)((max_len + kChunk - 1) / kChunk);  // splits <= chunks
+  return (size_t)B * Hq * chunks * (kD + 2) * sizeof(float);
 }
 
 int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                              const int32_t* lengths, const int32_t* slots, uint16_t* out, int32_t B,
                              int32_t Hq, int32_t Hkv, int32_t capacity, int32_t num_slots,
-                             int32_t max_len, float scale, float* workspace, uint32_t* counters,
-                             void* stream) {
-  if (!q || !k_pool || !v_pool || !lengths || !slots || !out || !workspace || !counters)
+                             int32_t max_len, float scale, float* workspace, void* stream) {
+  if (!q || !k_pool || !v_pool || !lengths || !slots || !out || !workspace)
     return fail(IMQ_EINVAL, "null pointer");
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || Hq / Hkv > 8)
     return fail(IMQ_EINVAL, "need Hkv | Hq with at most 8 query heads per KV head");
   if (capacity < 1 || num_slots < 1 || max_len < 1) return fail(IMQ_EINVAL, "capacity, num_slots, max_len >= 1");
   if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(workspace, 16))
     return fail(IMQ_EINVAL, "q, pools and workspace must be 16-byte aligned");
-  const int32_t span = max_len < capacity ? max_len : capacity;
-  const int NC = (span + kChunk - 1) / kChunk;
-  if (B > 65535 || Hkv > 65535) return fail(IMQ_EINVAL, "B and Hkv must be <= 65535");
+  if (B > 65535 || Hkv > 65535 || Hq > 65535) return fail(IMQ_EINVAL, "B and the head counts must be <= 65535");
   int32_t code;
   if (!current_device(&code)) return code;
-  const size_t parts = attention_parts(B, Hq, span);
+  const int32_t span = max_len < capacity ? max_len : capacity;
+  const AttnPlan pl = attention_plan(B, Hkv, span);
   float* part = workspace;
-  float* mlp = workspace + parts * kD;
-  hipLaunchKernelGGL(attention_kernel, dim3(NC, Hkv, B), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), q, k_pool, v_pool, lengths, slots, out, Hq,
-                     Hkv, capacity, span, num_slots, scale, part, mlp, counters, NC);
-  return launched("attention");
+  float* mlp = workspace + (size_t)B * Hq * pl.splits * kD;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(attention_partial_kernel, dim3(pl.splits, Hkv, B), dim3(kThreads), 0, st, q,
+                     k_pool, v_pool, lengths, slots, Hq, Hkv, capacity, span, num_slots, scale,
+                     pl.chunks_per_split, pl.splits, part, mlp);
+  if ((code = launched("attention")) != IMQ_OK) return code;
+  hipLaunchKernelGGL(attention_combine_kernel, dim3(Hq, B), dim3(64), 0, st, lengths, slots, out,
+                     Hq, capacity, span, num_slots, pl.chunks_per_split, pl.splits, part, mlp);
+  return launched("attention combine");
 }
 
 int32_t imq_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,

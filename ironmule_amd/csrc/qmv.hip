@@ -810,6 +810,187 @@ __global__ __launch_bounds__(kThreads) void qmv_mfma_kernel(LaunchArgs a) {
   }
 }
 
+// ------------------------------------------------ MFMA kernel, 32 x 32 tiles (M >= 3)
+//
+// A wavefront computes a 32 (activation rows) x 32 (weight rows) tile of y over its share
+// of the groups with v_mfma_f32_32x32x16_bf16, x as the A operand and the weights as the
+// B operand.  For a group of 64 values, lane (r = lane % 32, h = lane / 32) holds
+//   * 16 bytes of weight row r, words 4h .. 4h+3: word 4h+s (as nibble_pair bf16 pairs)
+//     is the lane's B operand of k-step s;
+//   * 64 bytes of activation row r, x[32h .. 32h+32): its piece s in pair order is the
+//     lane's A operand of k-step s.
+// So both operands come from one contiguous load each.  The output lane (n = lane % 32,
+// h) holds rows m = 8(i/4) + 4h + i%4 (i < 16) of column n, so a lane's scale and bias are
+// scalars.  Per group
+//     acc += s * P + (b - 128 s) * P1,
+// P1 being the four k-steps against a ones operand (the row sums of x over the group).
+// Rows m >= M read row M-1 and are never stored.
+//
+// A workgroup's four wavefronts split its groups in quarters and add through LDS in a
+// fixed order.  A weight's groups may also be split over SPLITS workgroups (more
+// workgroups when N is small); each split then writes an fp32 partial (M, N) and
+// qmv_reduce_kernel adds the splits in order.  Loads are issued a stage of MS groups
+// ahead, unconditionally (past the range: offsets past the buffer, zero, no traffic).
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kMmaStage = 1;
+#ifndef IMQ_MMA
+#define IMQ_MMA 1
+#endif
+constexpr bool kUseMma = IMQ_MMA;
+
+// One stage: GS groups of NT weight tiles (32 rows each), the matching x pieces and the
+// tiles' scales and biases.
+template <int NT, int GS>
+struct MmaStage {
+  uint4 w[GS][NT];
+  uint4 x[GS][4];
+  uint32_t s[GS][NT], b[GS][NT];
+};
+
+template <int NT, int GS>
+__device__ __forceinline__ void mma_load(MmaStage<NT, GS>& st, __amdgpu_buffer_rsrc_t wrsrc,
+                                         __amdgpu_buffer_rsrc_t srsrc, __amdgpu_buffer_rsrc_t brsrc,
+                                         const uint32_t (&woff)[NT], const uint32_t (&sboff)[NT],
+                                         const uint16_t* xr, int g, int g1) {
+#pragma unroll
+  for (int i = 0; i < GS; ++i) {
+    const bool in = g + i < g1;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      st.w[i][t] = load_b128(wrsrc, in ? woff[t] + 32u * (g + i) : kPastBuffer);
+      st.s[i][t] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, in ? sboff[t] + 2u * (g + i) : kPastBuffer, 0, 0);
+      st.b[i][t] = __builtin_amdgcn_raw_buffer_load_b16(brsrc, in ? sboff[t] + 2u * (g + i) : kPastBuffer, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < GS; ++i) {
+    const int gg = g + i < g1 ? g + i : g1 - 1;  // x rows end at K: stay inside them
+    const uint4* xv = reinterpret_cast<const uint4*>(xr + 64 * gg);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) st.x[i][q] = xv[q];
+  }
+}
+
+template <int NT, int GS>
+__device__ __forceinline__ void mma_compute(const MmaStage<NT, GS>& st, int g, int g1,
+                                            f32x16_t (&acc)[NT], uint32_t magic) {
+  const u32x4_t ones_u = {kOnes, kOnes, kOnes, kOnes};
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
+  const f32x16_t zero = {};
+#pragma unroll
+  for (int i = 0; i < GS; ++i) {
+    if (g + i >= g1) break;
+    bf16x8_t a[4];
+    f32x16_t p1 = zero;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      a[s] = as_bf16x8(pair_order(st.x[i][s]));
+      p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], ones, p1, 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const uint32_t wd[4] = {st.w[i][t].x, st.w[i][t].y, st.w[i][t].z, st.w[i][t].w};
+      f32x16_t p = zero;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], unpack_word(wd[s], magic), p, 0, 0, 0);
+      const float sc = bf16_bits_to_f32(st.s[i][t]);
+      const float c = fmaf(-128.0f, sc, bf16_bits_to_f32(st.b[i][t]));
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(sc, p[e], fmaf(c, p1[e], acc[t][e]));
+    }
+  }
+}
+
+// NT weight tiles of 32 rows per wavefront (x, its pair order and the row sums shared by
+// them), four wavefronts splitting the groups of a workgroup's 32 * NT rows.
+template <int NT, bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int splits,
+                                                           float* __restrict__ partial,
+                                                           int64_t pstride) {
+  __shared__ f32x16_t red[3][NT][64];
+  const int pi = blockIdx.y / splits, split = blockIdx.y - pi * splits;
+  const Problem& P = a.p[pi];
+  const int K = P.K, N = P.N, M = a.M;
+  const int row0 = blockIdx.x * 32 * NT;
+  if (row0 >= N) return;  // past this problem's tiles
+  const int G = K >> 6, W = K >> 3;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int r = lane & 31, h = lane >> 5;
+  const uint32_t magic = in_vgpr(kMagic);
+
+  // this workgroup's groups, and this wavefront's quarter of them
+  const int gs0 = (G * split) / splits, gs1 = (G * (split + 1)) / splits;
+  const int g0 = gs0 + ((gs1 - gs0) * wave >> 2), g1 = gs0 + ((gs1 - gs0) * (wave + 1) >> 2);
+
+  const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(P.w, (uint32_t)N * (uint32_t)W * 4u);
+  const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
+  const __amdgpu_buffer_rsrc_t srsrc = buffer_rsrc(P.s, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc = buffer_rsrc(P.b, sb_bytes);
+  uint32_t woff[NT], sboff[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int row = row0 + 32 * t + r < N ? row0 + 32 * t + r : N - 1;
+    woff[t] = (uint32_t)row * (uint32_t)W * 4u + 16u * h;
+    sboff[t] = (uint32_t)row * (uint32_t)G * 2u;
+  }
+  const uint16_t* xr = x_row(a, P, r < M ? r : M - 1) + 32 * h;
+
+  f32x16_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x16_t{};
+  MmaStage<NT, kMmaStage> sa, sb;
+  mma_load<NT, kMmaStage>(sa, wrsrc, srsrc, brsrc, woff, sboff, xr, g0, g1 > g0 ? g1 : g0 + 1);
+  for (int g = g0; g < g1; g += 2 * kMmaStage) {
+    mma_load<NT, kMmaStage>(sb, wrsrc, srsrc, brsrc, woff, sboff, xr, g + kMmaStage, g1);
+    mma_compute<NT, kMmaStage>(sa, g, g1, acc, magic);
+    if (g + kMmaStage >= g1) break;
+    mma_load<NT, kMmaStage>(sa, wrsrc, srsrc, brsrc, woff, sboff, xr, g + 2 * kMmaStage, g1);
+    mma_compute<NT, kMmaStage>(sb, g + kMmaStage, g1, acc, magic);
+  }
+
+  // add the four quarters in order: waves 1..3 park theirs, wave 0 adds and stores
+  if (wave > 0)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) acc[t] += red[q][t][lane];
+    const int n = row0 + 32 * t + r;
+    if (n >= N) continue;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+      if (m >= M) continue;
+      if (PARTIAL)
+        partial[pi * pstride + ((int64_t)split * M + m) * N + n] = acc[t][e];
+      else
+        store_y(a, P, m, n, acc[t][e]);
+    }
+  }
+}
+
+// y[m][n] = sum over the splits (in split order) of the fp32 partials of one problem.
+__global__ __launch_bounds__(kThreads) void qmv_reduce_kernel(LaunchArgs a, int splits,
+                                                              const float* __restrict__ partial,
+                                                              int64_t pstride) {
+  const Problem& P = a.p[blockIdx.y];
+  const int N = P.N, M = a.M;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const float* src = partial + pstride * blockIdx.y;
+  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  float v = 0.0f;
+  for (int s = 0; s < splits; ++s) v += src[((size_t)s * M + m) * N + n];
+  store_y(a, P, m, n, v);
+}
+
 // ------------------------------------------------------------------ dequantise
 //
 // One thread per packed word: eight outputs.  fp32 output is fl32(s*q + b), which is
@@ -1054,9 +1235,77 @@ hipError_t launch_mfma(const LaunchArgs& a, int grid_x, size_t lds, hipStream_t 
   return hipGetLastError();
 }
 
-// Plans the work of every problem and launches one kernel for all of them.
-int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream) {
-  (void)dev;
+// The 32 x 32 MFMA kernel's plan: tiles of 32 rows and, when a workspace is given,
+// enough splits of the groups that the launch has about two workgroups per CU, each
+// split keeping at least 8 groups (2 per wavefront) and the partials' traffic small next
+// to the weights' (8 * splits * M * N bytes against N * K / 2).
+struct MmaPlan {
+  int nt = 1;      // 32-row weight tiles per wavefront
+  int grid_x = 0;
+  int splits = 1;
+  int64_t pstride = 0;  // floats per problem in the workspace
+};
+
+#ifndef IMQ_MMA_NT_ROWS
+#define IMQ_MMA_NT_ROWS 8192
+#endif
+
+MmaPlan plan_mma(const LaunchArgs& a, size_t ws_bytes, int cu_count) {
+  MmaPlan pl;
+  int ntotal = 0;
+  for (int i = 0; i < a.count; ++i) ntotal += a.p[i].N;
+  pl.nt = ntotal >= IMQ_MMA_NT_ROWS ? 2 : 1;  // wide launches share x over two tiles
+  int tiles = 0, gmin = 1 << 30, kmin = 1 << 30, nmax = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const int t = (a.p[i].N + 32 * pl.nt - 1) / (32 * pl.nt);
+    pl.grid_x = t > pl.grid_x ? t : pl.grid_x;
+    tiles += t;
+    gmin = a.p[i].K / 64 < gmin ? a.p[i].K / 64 : gmin;
+    kmin = a.p[i].K < kmin ? a.p[i].K : kmin;
+    nmax = a.p[i].N > nmax ? a.p[i].N : nmax;
+  }
+  if (ws_bytes == 0) return pl;
+  int sp = (2 * cu_count + tiles - 1) / tiles;
+  sp = sp < gmin / 8 ? sp : gmin / 8;
+  sp = sp < kmin / (16 * a.M) ? sp : kmin / (16 * a.M);
+  while (sp > 1 && (size_t)a.count * sp * a.M * nmax * sizeof(float) > ws_bytes) --sp;
+  if (sp > 1) {
+    pl.splits = sp;
+    pl.pstride = (int64_t)sp * a.M * nmax;
+  }
+  return pl;
+}
+
+template <int NT>
+void launch_mma_nt(const LaunchArgs& a, const MmaPlan& pl, float* ws, hipStream_t stream) {
+  if (pl.splits == 1)
+    hipLaunchKernelGGL((qmv_mma_kernel<NT, false>), dim3(pl.grid_x, a.count), dim3(kThreads), 0,
+                       stream, a, 1, nullptr, (int64_t)0);
+  else
+    hipLaunchKernelGGL((qmv_mma_kernel<NT, true>), dim3(pl.grid_x, a.count * pl.splits),
+                       dim3(kThreads), 0, stream, a, pl.splits, ws, pl.pstride);
+}
+
+hipError_t launch_mma(const LaunchArgs& a, const MmaPlan& pl, float* ws, hipStream_t stream) {
+  if (pl.nt == 2)
+    launch_mma_nt<2>(a, pl, ws, stream);
+  else
+    launch_mma_nt<1>(a, pl, ws, stream);
+  if (pl.splits == 1) return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  int nmax = 0;
+  for (int i = 0; i < a.count; ++i) nmax = a.p[i].N > nmax ? a.p[i].N : nmax;
+  const int64_t elems = (int64_t)a.M * nmax;
+  hipLaunchKernelGGL(qmv_reduce_kernel, dim3((uint32_t)((elems + kThreads - 1) / kThreads), a.count),
+                     dim3(kThreads), 0, stream, a, pl.splits, ws, pl.pstride);
+  return hipGetLastError();
+}
+
+// Plans the work of every problem and launches one kernel for all of them (two when the
+// MFMA kernel splits the groups over a workspace).
+int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, float* ws = nullptr,
+               size_t ws_bytes = 0) {
   const int M = a.M;
   hipError_t e;
   M1Plan m1;
@@ -1072,6 +1321,12 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream) {
     } else {
       e = launch_rows<2, 2>(a, grid_x, lds, stream);
     }
+  } else if (kUseMma) {
+    for (int i = 0; i < a.count; ++i)
+      if ((int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31))
+        return fail(IMQ_EUNSUPPORTED, "a weight of 2 GiB or more exceeds the MFMA kernel's offsets");
+    const MmaPlan pl = plan_mma(a, ws ? ws_bytes : 0, dev->cu_count);
+    e = launch_mma(a, pl, ws, stream);
   } else {
     const int rows_per_wg = 16 * kMfmaTiles;
     int kmax = 0;
@@ -1168,15 +1423,19 @@ int32_t imq_qmv_multi(const uint32_t* w, const uint16_t* scales, const uint16_t*
   return launch(a, dev, static_cast<hipStream_t>(stream));
 }
 
-int32_t imq_qmv_grouped(const imq_problem* problems, int32_t count, int32_t M,
-                        int32_t group_size, int32_t bits, int32_t y_dtype, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Validates `problems` into `a`; IMQ_OK or the error code.
+int32_t build_grouped(LaunchArgs& a, const imq_problem* problems, int32_t count, int32_t M,
+                      int32_t group_size, int32_t bits, int32_t y_dtype) {
   if (!problems) return fail(IMQ_EINVAL, "problems must be non-null");
   if (count < 1) return fail(IMQ_EINVAL, "count must be >= 1");
   if (count > IMQ_MAX_PROBLEMS)
     return fail(IMQ_EUNSUPPORTED, "at most IMQ_MAX_PROBLEMS problems per call");
   int32_t code = check_dtype(y_dtype);
   if (code != IMQ_OK) return code;
-  LaunchArgs a;
   memset(&a, 0, sizeof(a));
   for (int i = 0; i < count; ++i) {
     const imq_problem& q = problems[i];
@@ -1186,12 +1445,55 @@ int32_t imq_qmv_grouped(const imq_problem* problems, int32_t count, int32_t M,
     a.p[i] = Problem{q.w, q.scales, q.biases, q.x, q.y, M > 1 ? q.ldx : q.K,
                      M > 1 ? q.ldy : q.N, q.N, q.K, 0, 0, 0, 0};
   }
-  const DeviceInfo* dev = current_device(&code);
-  if (!dev) return code;
   a.count = count;
   a.M = M;
   a.y_f32 = (y_dtype == IMQ_F32);
+  return IMQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t imq_qmv_grouped(const imq_problem* problems, int32_t count, int32_t M,
+                        int32_t group_size, int32_t bits, int32_t y_dtype, void* stream) {
+  LaunchArgs a;
+  int32_t code = build_grouped(a, problems, count, M, group_size, bits, y_dtype);
+  if (code != IMQ_OK) return code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
   return launch(a, dev, static_cast<hipStream_t>(stream));
+}
+
+size_t imq_qmv_grouped_workspace(const imq_problem* problems, int32_t count, int32_t M) {
+  if (!problems || count < 1 || count > IMQ_MAX_PROBLEMS || M < 3 || M > IMQ_MAX_ROWS) return 0;
+  int32_t code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return 0;
+  LaunchArgs a;
+  memset(&a, 0, sizeof(a));
+  for (int i = 0; i < count; ++i) {
+    if (problems[i].N < 1 || problems[i].K < 64 || problems[i].K % 64) return 0;
+    a.p[i].N = problems[i].N;
+    a.p[i].K = problems[i].K;
+  }
+  a.count = count;
+  a.M = M;
+  const MmaPlan pl = plan_mma(a, (size_t)1 << 40, dev->cu_count);
+  return pl.splits > 1 ? (size_t)count * pl.pstride * sizeof(float) : 0;
+}
+
+int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, int32_t M,
+                           int32_t group_size, int32_t bits, int32_t y_dtype, float* workspace,
+                           size_t workspace_bytes, void* stream) {
+  LaunchArgs a;
+  int32_t code = build_grouped(a, problems, count, M, group_size, bits, y_dtype);
+  if (code != IMQ_OK) return code;
+  if (workspace_bytes > 0 && (!workspace || !aligned(workspace, 16)))
+    return fail(IMQ_EINVAL, "workspace must be non-null and 16-byte aligned");
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
+  return launch(a, dev, static_cast<hipStream_t>(stream), workspace, workspace_bytes);
 }
 
 int32_t imq_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

@@ -131,7 +131,6 @@ class DecodeState:
         self.logits = torch.empty((batch, c.vocab), dtype=torch.float32, device=device)
         self.workspace = torch.empty(_native.attention_workspace(batch, c.heads, self.max_len),
                                      dtype=torch.float32, device=device)
-        self.counters = torch.zeros(batch * c.kv_heads, dtype=torch.int32, device=device)
         self.tokens = torch.zeros(batch, dtype=torch.int32, device=device)
         self.slot_ids = torch.arange(batch, dtype=torch.int32, device=device) % slots
         self.positions = torch.zeros(batch, dtype=torch.int32, device=device)
@@ -163,7 +162,7 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
         n.qk_norm_rope(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions, s.slot_ids,
                        s.q_rot, s.k_pool[i], s.v_pool[i], c.theta, c.eps, stream=stream)
         n.attention_decode(s.q_rot, s.k_pool[i], s.v_pool[i], s.lengths, s.slot_ids, s.attn,
-                           s.max_len, scale, s.workspace, s.counters, stream=stream)
+                           s.max_len, scale, s.workspace, stream=stream)
         n.qmv(*layer["o"], s.attn, out=s.delta, stream=stream)
         n.add_rmsnorm(s.h, layer["post_norm"], s.x, c.eps, delta=s.delta, stream=stream)
         n.qmv_grouped([layer["gate"], layer["up"]], [s.x, s.x], outs=[s.gate, s.up], stream=stream)
