@@ -24,7 +24,8 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 LIB_PATH = os.path.join(PKG, "libironmule_qmv.so")
 HEADER_PATH = os.path.join(ROOT, "include", "ironmule_qmv.h")
-HEADER_PATHS = [HEADER_PATH, os.path.join(ROOT, "include", "ironmule_decode.h")]
+HEADER_PATHS = [HEADER_PATH, os.path.join(ROOT, "include", "ironmule_decode.h"),
+                os.path.join(ROOT, "include", "ironmule_step.h")]
 
 GROUP_SIZE = 64
 BITS = 4
@@ -62,6 +63,37 @@ class Problem(ctypes.Structure):
                 ("y", _P), ("ldy", _I64), ("N", _I32), ("K", _I32)]
 
 
+class QWeight(ctypes.Structure):
+    """imq_qweight: packed words, bf16 scales, bf16 biases."""
+
+    _fields_ = [("w", _P), ("scales", _P), ("biases", _P)]
+
+
+class StepLayer(ctypes.Structure):
+    """imq_step_layer: one decoder layer's tensors for the persistent decode program."""
+
+    _fields_ = [("q", QWeight), ("k", QWeight), ("v", QWeight), ("o", QWeight), ("gate", QWeight),
+                ("up", QWeight), ("down", QWeight), ("input_norm", _P), ("post_norm", _P),
+                ("q_norm", _P), ("k_norm", _P), ("k_pool", _P), ("v_pool", _P)]
+
+
+class StepDesc(ctypes.Structure):
+    """imq_step_desc: shapes and device tensors of a decode step."""
+
+    _fields_ = [("layers", _I32), ("batch", _I32), ("hidden", _I32), ("heads", _I32),
+                ("kv_heads", _I32), ("intermediate", _I32), ("vocab", _I32), ("capacity", _I32),
+                ("num_slots", _I32), ("max_len", _I32), ("eps", ctypes.c_float),
+                ("theta", ctypes.c_float), ("layer", ctypes.POINTER(StepLayer)),
+                ("final_norm", _P), ("head", QWeight), ("positions", _P), ("slots", _P), ("h", _P),
+                ("logits", _P)]
+
+
+class QmvStage(ctypes.Structure):
+    """imq_qmv_stage: 1-3 one-row qmv problems sharing x, optionally after the previous stage."""
+
+    _fields_ = [("count", _I32), ("wait_previous", _I32), ("problems", Problem * 3)]
+
+
 _SIGNATURES = {
     "imq_abi_version": ([], _I32),
     "imq_device_check": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(_I32)], _I32),
@@ -82,6 +114,14 @@ _SIGNATURES = {
     "imq_attention_decode": ([_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                               ctypes.c_float, _P, _P], _I32),
     "imq_silu_mul": ([_P, _P, _P, _I64, _P], _I32),
+    # persistent programs (include/ironmule_step.h)
+    "imq_decode_program_create": ([ctypes.POINTER(StepDesc), ctypes.POINTER(_P)], _I32),
+    "imq_qmv_program_create": ([ctypes.POINTER(QmvStage), _I32, ctypes.POINTER(_P)], _I32),
+    "imq_program_launch": ([_P, _P], _I32),
+    "imq_program_status": ([_P, ctypes.POINTER(_I32)], _I32),
+    "imq_program_info": ([_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32), ctypes.POINTER(_I32),
+                          ctypes.POINTER(_I32)], _I32),
+    "imq_program_destroy": ([_P], None),
 }
 
 
@@ -388,3 +428,122 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor, stream=Non
         raise ValueError("gate, up and out must have the same size")
     _check(lib().imq_silu_mul(_ptr(gate), _ptr(up), _ptr(out), int(gate.numel()), _stream(stream)))
     return out
+
+
+# ------------------------------------------------------------ persistent programs
+
+
+class Program:
+    """A program of the persistent engine (include/ironmule_step.h): one launch runs all of
+    its stages.  Holds references to every tensor the program points at, so they outlive
+    it; `close()` (or garbage collection) frees the device tables."""
+
+    def __init__(self, handle: ctypes.c_void_p, keep: list) -> None:
+        self._handle = handle
+        self._keep = keep
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._handle is None:
+            raise ValueError("the program is closed")
+        return self._handle
+
+    def launch(self, stream=None) -> None:
+        """Enqueue one run on `stream` (capturable in a HIP graph)."""
+        _check(lib().imq_program_launch(self.handle, _stream(stream)))
+
+    def failed(self) -> bool:
+        """Synchronises the device; True if a run since the last call stopped on a bounded
+        wait (the flag is then cleared)."""
+        flag = _I32(0)
+        _check(lib().imq_program_status(self.handle, ctypes.byref(flag)))
+        return bool(flag.value)
+
+    def info(self) -> dict:
+        vals = [_I32(0) for _ in range(4)]
+        _check(lib().imq_program_info(self.handle, *[ctypes.byref(v) for v in vals]))
+        return dict(zip(("tasks", "stages", "workgroups", "lds_bytes"), (v.value for v in vals)))
+
+    def close(self) -> None:
+        if self._handle is not None and _lib is not None:
+            _lib.imq_program_destroy(self._handle)
+        self._handle = None
+        self._keep = []
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _qweight(w, s, b) -> QWeight:
+    check_weights(w, s, b)
+    return QWeight(w.data_ptr(), s.data_ptr(), b.data_ptr())
+
+
+def qmv_program(stages: list[tuple[list, torch.Tensor, list, bool]]) -> Program:
+    """A chain of one-row qmv stages, each (weights, x, outs, wait_previous): `weights`
+    1-3 (w, scales, biases) triples sharing the bf16 row `x` (K,), `outs` their bf16 (N,)
+    outputs; a stage with wait_previous starts after the previous one has finished."""
+    if not stages:
+        raise ValueError("a program needs at least one stage")
+    arr = (QmvStage * len(stages))()
+    keep = []
+    for i, (weights, x, outs, wait_previous) in enumerate(stages):
+        if not 1 <= len(weights) <= 3 or len(outs) != len(weights):
+            raise ValueError("a stage has 1 to 3 weights and one output per weight")
+        if x.dtype != torch.bfloat16 or not x.is_contiguous():
+            raise ValueError("x must be a contiguous bf16 row")
+        arr[i].count = len(weights)
+        arr[i].wait_previous = int(bool(wait_previous))
+        for k, ((w, s, b), y) in enumerate(zip(weights, outs)):
+            n, kk = check_weights(w, s, b)
+            if x.numel() != kk:
+                raise ValueError(f"stage {i}: x has {x.numel()} values, the weight takes {kk}")
+            if y.dtype != torch.bfloat16 or y.numel() != n or not y.is_contiguous():
+                raise ValueError(f"stage {i}: output {k} must be a contiguous bf16 tensor of {n}")
+            arr[i].problems[k] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(),
+                                         kk, y.data_ptr(), n, n, kk)
+            keep += [w, s, b, y]
+        keep.append(x)
+    handle = _P()
+    _check(lib().imq_qmv_program_create(arr, len(stages), ctypes.byref(handle)))
+    return Program(handle, keep)
+
+
+def decode_program(config, layers: list[dict], final_norm: torch.Tensor, head: tuple,
+                   k_pools: list, v_pools: list, positions: torch.Tensor, slots: torch.Tensor,
+                   h: torch.Tensor, logits: torch.Tensor, max_len: int) -> Program:
+    """The persistent decode step of a Qwen3-style decoder at batch 1 (imq_step_desc):
+    `layers` are dicts of (w, scales, biases) for q k v o gate up down plus bf16
+    input_norm, post_norm, q_norm, k_norm; the pools are (slots, kv_heads, capacity, 128)
+    bf16; positions/slots int32 (1,); h fp32 (1, hidden) holds the embedded token and is
+    updated; logits fp32 (1, vocab) are written."""
+    c = config
+    for name, t, dt in (("positions", positions, torch.int32), ("slots", slots, torch.int32),
+                        ("h", h, torch.float32), ("logits", logits, torch.float32),
+                        ("final_norm", final_norm, torch.bfloat16)):
+        _require(t, dt, name)
+    arr = (StepLayer * len(layers))()
+    keep = [positions, slots, h, logits, final_norm, *head]
+    for i, L in enumerate(layers):
+        for name in ("input_norm", "post_norm", "q_norm", "k_norm"):
+            _require(L[name], torch.bfloat16, name)
+        _require(k_pools[i], torch.bfloat16, "k_pool")
+        _require(v_pools[i], torch.bfloat16, "v_pool")
+        arr[i] = StepLayer(*[_qweight(*L[nm]) for nm in ("q", "k", "v", "o", "gate", "up", "down")],
+                           L["input_norm"].data_ptr(), L["post_norm"].data_ptr(),
+                           L["q_norm"].data_ptr(), L["k_norm"].data_ptr(),
+                           k_pools[i].data_ptr(), v_pools[i].data_ptr())
+        keep += [t for nm in ("q", "k", "v", "o", "gate", "up", "down") for t in L[nm]]
+        keep += [L[nm] for nm in ("input_norm", "post_norm", "q_norm", "k_norm")]
+        keep += [k_pools[i], v_pools[i]]
+    num_slots, _, capacity, _ = k_pools[0].shape
+    desc = StepDesc(len(layers), int(h.shape[0]), c.hidden, c.heads, c.kv_heads, c.intermediate,
+                    c.vocab, int(capacity), int(num_slots), int(max_len), float(c.eps),
+                    float(c.theta), arr, final_norm.data_ptr(), _qweight(*head),
+                    positions.data_ptr(), slots.data_ptr(), h.data_ptr(), logits.data_ptr())
+    handle = _P()
+    _check(lib().imq_decode_program_create(ctypes.byref(desc), ctypes.byref(handle)))
+    return Program(handle, keep + [arr])

@@ -14,9 +14,12 @@
 #include <string>
 
 #include "../../include/ironmule_decode.h"
+#include "common.h"
 #include "runtime.h"
 
 namespace {
+
+using namespace imq_dev;
 
 using imq_rt::aligned;
 using imq_rt::current_device;
@@ -29,33 +32,8 @@ constexpr int kChunk = 64;        // keys per attention workgroup
 constexpr int kMaxNormDim = 8192;
 constexpr int kNormVpt = kMaxNormDim / kThreads;  // values per thread of the row norm
 
-__device__ __forceinline__ float bf(uint32_t h) { return __uint_as_float(h << 16); }
-
-// Round to nearest even; NaN becomes the quiet NaN 0x7fc0.
-__device__ __forceinline__ uint16_t to_bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
+__device__ __forceinline__ float bf(uint32_t h) { return bf16_bits_to_f32(h); }
+__device__ __forceinline__ uint16_t to_bf(float f) { return f32_to_bf16_bits(f); }
 
 // ------------------------------------------------------------------ embedding rows
 

@@ -34,103 +34,16 @@
 #include <string>
 
 #include "../../include/ironmule_qmv.h"
+#include "common.h"
 #include "runtime.h"
 
 namespace {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-
-// Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data format).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
+using namespace imq_dev;
 
 constexpr int kThreads = 256;  // 4 wavefronts of 64
 constexpr int kGroup = 64;
 constexpr int kMaxProblems = IMQ_MAX_PROBLEMS;
-
-// ------------------------------------------------------------------ bf16 helpers
-
-__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
-  return __uint_as_float(h << 16);
-}
-
-// Round to nearest even; NaN becomes the quiet NaN 0x7fc0 (ironmule/cuda_native.py:46-51).
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-// A constant held in a VGPR.  gfx9 VOP3 instructions take no literal operand and at
-// most one SGPR, so (u & mask) | magic becomes one v_and_or_b32 only when `magic` is
-// already in a vector register (the mask then comes from an SGPR).
-__device__ __forceinline__ uint32_t in_vgpr(uint32_t c) {
-  uint32_t r;
-  asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
-  return r;
-}
-
-constexpr uint32_t kMagic = 0x43004300u;  // bf16 pair (128.0, 128.0)
-constexpr uint32_t kOnes = 0x3f803f80u;   // bf16 pair (1.0, 1.0)
-
-// Nibbles p and p+4 of word u as the bf16 pair (128 + q_p, 128 + q_{p+4}).
-// `magic` must be in_vgpr(kMagic).
-__device__ __forceinline__ uint32_t nibble_pair(uint32_t u, int p, uint32_t magic) {
-  return ((u >> (4 * p)) & 0x000F000Fu) | magic;
-}
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-// Eight natural-order bf16 values (x0..x7 in d.x..d.w) -> the pair order of nibble_pair.
-__device__ __forceinline__ uint4 pair_order(uint4 d) {
-  uint4 p;
-  p.x = (d.x & 0xffffu) | (d.z << 16);      // (x0, x4)
-  p.y = (d.x >> 16) | (d.z & 0xffff0000u);  // (x1, x5)
-  p.z = (d.y & 0xffffu) | (d.w << 16);      // (x2, x6)
-  p.w = (d.y >> 16) | (d.w & 0xffff0000u);  // (x3, x7)
-  return p;
-}
-
-__device__ __forceinline__ float sum8(uint4 d) {
-  const float a = bf16_bits_to_f32(d.x & 0xffffu) + bf16_bits_to_f32(d.x >> 16);
-  const float b = bf16_bits_to_f32(d.y & 0xffffu) + bf16_bits_to_f32(d.y >> 16);
-  const float c = bf16_bits_to_f32(d.z & 0xffffu) + bf16_bits_to_f32(d.z >> 16);
-  const float e = bf16_bits_to_f32(d.w & 0xffffu) + bf16_bits_to_f32(d.w >> 16);
-  return (a + b) + (c + e);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over each aligned row of 16 lanes; every lane of the row receives the sum.
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp<0x141>(v);  // row_half_mirror
-  v += dpp<0x140>(v);  // row_mirror
-  return v;
-}
-
-// LDS-only barrier: waits for this wave's LDS traffic, not for its outstanding global
-// loads (a full __syncthreads() would also drain the weight loads issued before it).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // ------------------------------------------------------------------ kernel args
 
@@ -360,34 +273,6 @@ __global__ __launch_bounds__(kThreads) void qmv_rows_kernel(LaunchArgs a) {
 // outstanding-load count is the same on every path and each wait is exact.  x goes to
 // LDS in pair order with its per-chunk sums, the (scale, bias) pairs as one dword per
 // (row, group); then each chunk is consumed as it arrives.
-
-__device__ __forceinline__ float chunk_dot(uint4 wv, uint4 x0, uint4 x1, uint4 x2, uint4 x3,
-                                           float d, uint32_t magic) {
-  d = dot2(nibble_pair(wv.x, 0, magic), x0.x, d);
-  d = dot2(nibble_pair(wv.x, 1, magic), x0.y, d);
-  d = dot2(nibble_pair(wv.x, 2, magic), x0.z, d);
-  d = dot2(nibble_pair(wv.x, 3, magic), x0.w, d);
-  d = dot2(nibble_pair(wv.y, 0, magic), x1.x, d);
-  d = dot2(nibble_pair(wv.y, 1, magic), x1.y, d);
-  d = dot2(nibble_pair(wv.y, 2, magic), x1.z, d);
-  d = dot2(nibble_pair(wv.y, 3, magic), x1.w, d);
-  d = dot2(nibble_pair(wv.z, 0, magic), x2.x, d);
-  d = dot2(nibble_pair(wv.z, 1, magic), x2.y, d);
-  d = dot2(nibble_pair(wv.z, 2, magic), x2.z, d);
-  d = dot2(nibble_pair(wv.z, 3, magic), x2.w, d);
-  d = dot2(nibble_pair(wv.w, 0, magic), x3.x, d);
-  d = dot2(nibble_pair(wv.w, 1, magic), x3.y, d);
-  d = dot2(nibble_pair(wv.w, 2, magic), x3.z, d);
-  d = dot2(nibble_pair(wv.w, 3, magic), x3.w, d);
-  return d;
-}
-
-constexpr uint32_t kPastBuffer = 0x80000000u;  // a buffer offset that reads as zero
-
-__device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 // LDS layout of the one-row kernel, sized by its template so that every staging write
 // is unconditional (pieces past the data are written as zeros): x in pair order as four

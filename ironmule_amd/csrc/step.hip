@@ -1,0 +1,1113 @@
+// Persistent decode-step engine for MI355X (gfx950): one kernel launch runs a whole
+// program of stages (C ABI: include/ironmule_step.h).
+//
+// Scheduling.  The tasks of all stages form one list in stage order.  The grid holds as
+// many workgroups as the device keeps resident at once, and workgroup w runs tasks
+// w, w + G, w + 2G, ... in order.  A task first issues its weight loads, then waits
+// until every task of its input stage has finished, then reads its activations, computes
+// and publishes its outputs.  Because every workgroup is resident and runs its tasks in
+// increasing order, the smallest unfinished task can always run, so the program always
+// completes; the waits are bounded anyway (a stalled run stops and reports it).
+//
+// Completion.  Each stage has kSub counters, each on its own cache line and the lines of
+// one stage's counters 4 KiB apart: one atomic counter serialises its increments (about
+// 11 ns each on MI355X), so a stage's tasks spread theirs over kSub of them.  A waiting
+// workgroup sums the kSub counters with one round of loads per poll.
+//
+// Coherence inside a launch.  Activations produced by one task and read by another
+// (the residual stream h, q/k/v, the attention partials and output, SiLU*up) are
+// written with sc1 stores and read with sc1 loads (common.h), and a producer waits for
+// its stores before it bumps a counter.  No cache write-back or invalidate is used: an
+// agent-scope acquire (a full L2 invalidate) costs tens of microseconds when thousands of
+// workgroups issue it.
+//
+// Arithmetic.  A qmv tile is the one-row VALU tile of qmv.hip (the same lane shape, chunk
+// order, dot2 chains and cross-lane sums); the fused RMSNorm, the residual add, SiLU*up,
+// q/k norm + rotary embedding and attention use the expressions and reduction orders of
+// the decode.hip kernels.  A program's results therefore equal the per-kernel path's bit
+// for bit.
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/ironmule_step.h"
+#include "common.h"
+#include "runtime.h"
+
+namespace {
+
+using namespace imq_dev;
+using imq_rt::aligned;
+using imq_rt::current_device;
+using imq_rt::DeviceInfo;
+using imq_rt::fail;
+using imq_rt::ok;
+
+constexpr int kThreads = 256;
+constexpr int kD = 128;           // attention head dimension
+constexpr int kChunk = 64;        // keys per attention chunk
+constexpr int kSub = 16;          // completion counters per stage
+constexpr int kLineWords = 32;    // one 128-byte line per counter
+constexpr int kMaxPolls = 1 << 22;
+constexpr int kMaxStageProblems = 3;
+constexpr int kMaxHidden = 4096;  // the fused RMSNorm stages one row of h whole
+constexpr int kNormVpt = kMaxHidden / kThreads;
+
+enum : int32_t { kKindQmv = 0, kKindAttention = 1 };
+enum : int32_t { kXVector = 0, kXNorm = 1 };
+enum : int32_t { kEpiBf16 = 0, kEpiF32 = 1, kEpiResidual = 2, kEpiSiluPair = 3 };
+// (chunks per lane, x pieces per thread) of the qmv tile instantiations
+enum : int32_t { kShape22 = 0, kShape52 = 1, kShape82 = 2, kShape55 = 3 };
+
+struct QProb {
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  void* y;
+  int32_t N, K, sh, nch;
+  int32_t tile_end;  // one past the problem's last tile, counted within the stage
+  int32_t pad[3];
+};
+
+struct Stage {
+  int32_t kind, first, count, wait;  // wait: stage index, or -1
+  int32_t wait_count, shape, xsrc, epi;
+  int32_t nprob, pad0, pad1, pad2a;
+  float eps, log2_theta, scale, pad2;
+  const uint16_t* x;       // bf16 activation row (kXVector)
+  float* h;                // residual stream (kXNorm source, kEpiResidual target)
+  const uint16_t* norm_w;  // kXNorm weight
+  uint16_t* act;           // kEpiSiluPair output
+  QProb p[kMaxStageProblems];
+  // attention
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  uint16_t* k_pool;
+  uint16_t* v_pool;
+  uint16_t* attn_out;
+  const int32_t* positions;
+  const int32_t* slots;
+  float* part;
+  float* ml;
+  uint32_t* combine;  // one counter per (request, KV head)
+  int32_t Hq, Hkv, capacity, num_slots, max_len, splits, cps, pad3;
+};
+
+struct StepArgs {
+  uint32_t* done;
+  uint32_t* status;
+  int32_t ntasks;
+  int32_t sub_stride;  // counters between the same sub-counter of consecutive stages
+};
+
+__device__ __forceinline__ float bf(uint32_t h) { return bf16_bits_to_f32(h); }
+__device__ __forceinline__ uint16_t to_bf(float f) { return f32_to_bf16_bits(f); }
+
+// A value the whole workgroup agrees on, kept in a scalar register (a vector load of a
+// uniform address would otherwise make everything derived from it look divergent).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// threadIdx.x made opaque at the start of each task, so that values derived from it are
+// computed inside the task loop rather than hoisted and kept live across every task.
+__device__ __forceinline__ int task_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+// A stage descriptor seen through the global address space: loads of its fields are then
+// known to be the same for every lane (flat loads might reach per-lane scratch).
+typedef const struct Stage __attribute__((address_space(1)))& StageRef;
+__device__ __forceinline__ StageRef global_stage(const Stage* p);
+
+template <typename T>
+__device__ __forceinline__ T* uni(T* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<T*>((hi << 32) | lo);
+}
+
+__device__ __forceinline__ StageRef global_stage(const Stage* p) {
+  return *reinterpret_cast<const Stage __attribute__((address_space(1)))*>(
+      reinterpret_cast<uint64_t>(uni(p)));
+}
+
+__device__ __forceinline__ uint32_t* counter(const StepArgs& a, int stage, int sub) {
+  return a.done + ((size_t)sub * a.sub_stride + stage) * kLineWords;
+}
+
+// Waits until the kSub counters of `stage` add up to `count`.  Wavefront 0 polls (lane i
+// reads counter i), with a short sleep between polls.  Returns false (and raises the
+// status word) if the wait times out or another workgroup raised it.
+__device__ bool wait_stage(const StepArgs& a, int stage, uint32_t count) {
+  __shared__ int s_ok;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const uint32_t* c = counter(a, stage, lane < kSub ? lane : 0);
+    int polls = 0, good = 1;
+    for (;;) {
+      uint32_t v = lane < kSub ? ld_sc1(c) : 0u;
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      v = __shfl(v, 0);
+      if (v >= count) break;
+      if (++polls >= kMaxPolls || ((polls & 63) == 0 && ld_sc1(a.status) != 0)) {
+        good = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) {
+      if (!good) st_sc1(a.status, 1u);
+      s_ok = good;
+    }
+  }
+  __syncthreads();
+  return s_ok != 0;
+}
+
+// After the task's sc1 stores: every thread waits for its own, then one atomic.
+__device__ __forceinline__ void signal(uint32_t* c) {
+  wait_vmem();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------------ qmv tile
+//
+// LDS of a qmv task: x in pair order as four planes of CP chunks, their chunk sums, the
+// tile's (scale, bias) dwords, then (fused RMSNorm) the normalised row as bf16 and the
+// block sums, and the SiLU*up exchange.
+template <int NCH, int XR>
+struct QLds {
+  static constexpr int kChunks = XR * 64;
+  static constexpr int kSbr = (64 * NCH + kThreads - 1) / kThreads;
+  static constexpr size_t kX = 0;
+  static constexpr size_t kSx = kX + (size_t)4 * kChunks * 16;
+  static constexpr size_t kSb = kSx + (size_t)kChunks * 4;
+  static constexpr size_t kPair = kSb + (size_t)kSbr * kThreads * 8;  // 8 floats
+  static constexpr size_t kBytes = kPair + 8 * 4;
+};
+
+// The fused RMSNorm holds the fp32 row of h at the start of LDS (it is consumed before
+// the x planes are written over it) and its block sums after the largest row.
+constexpr size_t kNormRed = (size_t)kMaxHidden * 4;
+constexpr size_t kNormBytes = kNormRed + 16;
+
+// x for the tile from a bf16 row (sc1: it may have been written in this launch).  Pieces
+// past the row lie past the buffer and read as zero.
+template <int XR>
+__device__ __forceinline__ void fetch_x(const uint16_t* x, int K, int tid, uint4 (&xs)[XR]) {
+  const __amdgpu_buffer_rsrc_t r = buffer_rsrc(x, (uint32_t)K * 2u);
+#pragma unroll
+  for (int t = 0; t < XR; ++t) xs[t] = load_b128_sc1(r, 16u * (tid + kThreads * t));
+}
+
+// x = bf16(rms_norm(h) * w) for the tile, in the order of add_rmsnorm_kernel (thread t
+// sums the squares of h[t + 256 i] in increasing i, then the wavefront butterfly, then
+// the four wavefronts as (w0 + w1) + (w2 + w3)).  The row of h goes through LDS so that
+// each thread can then form its own 8-value pieces; values past the row read as zero.
+template <int XR>
+__device__ __forceinline__ void norm_x(const float* h, const uint16_t* nw, int K, float eps,
+                                       int tid, float* hl, float* red, uint4 (&xs)[XR]) {
+  const __amdgpu_buffer_rsrc_t hr = buffer_rsrc(h, (uint32_t)K * 4u);
+  float ss = 0.0f;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    float v[kNormVpt / 2];
+#pragma unroll
+    for (int i = 0; i < kNormVpt / 2; ++i)
+      v[i] = __uint_as_float(load_b32_sc1(hr, 4u * (tid + kThreads * (i + half * kNormVpt / 2))));
+#pragma unroll
+    for (int i = 0; i < kNormVpt / 2; ++i) {
+      const int idx = tid + kThreads * (i + half * kNormVpt / 2);
+      if (idx < K) ss = fmaf(v[i], v[i], ss);
+      hl[idx] = v[i];
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  lds_barrier();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / sqrtf(total / (float)K + eps);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(nw, (uint32_t)K * 2u);
+#pragma unroll
+  for (int t = 0; t < XR; ++t) {
+    const int i = tid + kThreads * t;  // piece i: values 8i .. 8i+7 (zeros past the row)
+    const uint4 w8 = load_b128(wr, 16u * i);
+    const uint32_t ww[4] = {w8.x, w8.y, w8.z, w8.w};
+    const float4 h0 = reinterpret_cast<const float4*>(hl)[2 * i];
+    const float4 h1 = reinterpret_cast<const float4*>(hl)[2 * i + 1];
+    const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = (uint32_t)to_bf(hv[2 * e] * inv * bf(ww[e] & 0xffffu)) |
+             ((uint32_t)to_bf(hv[2 * e + 1] * inv * bf(ww[e] >> 16)) << 16);
+    xs[t] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  lds_barrier();  // the x planes are written over the row
+}
+
+// One qmv task: one tile of one problem (tiles are numbered across the stage's
+// problems), or for a SiLU*up pair stage one tile of the gate/up pair, whose rows 0-7
+// are gate rows and rows 8-15 the same up rows (wavefronts 0-1 and 2-3).
+template <int NCH, int XR, int XSRC, int EPI>
+__device__ __forceinline__ bool qmv_task(StageRef S, int task, const StepArgs& a, uint4* smem) {
+  using L = QLds<NCH, XR>;
+  constexpr int CP = L::kChunks, SBR = L::kSbr;
+  constexpr bool kPair = EPI == kEpiSiluPair;
+  const int tid = task_tid();
+  const int wave = uni(tid >> 6);
+  int pi = 0, tile = task;
+  if (!kPair) {
+    if (S.nprob > 1 && task >= S.p[0].tile_end) pi = 1;
+    if (S.nprob > 2 && task >= S.p[1].tile_end) pi = 2;
+    if (pi > 0) tile = task - S.p[pi - 1].tile_end;
+  }
+  const int qi = kPair ? (wave >= 2 ? 1 : 0) : pi;  // this wavefront's problem
+  const uint32_t* wp = S.p[qi].w;
+  const uint16_t* sp = S.p[qi].s;
+  const uint16_t* bp = S.p[qi].b;
+  const int K = S.p[0].K, N = S.p[qi].N, sh = S.p[0].sh, nch = S.p[0].nch;
+  const int C = K >> 5, G = K >> 6, W = K >> 3;
+  const int j = tid & ((1 << sh) - 1);
+  const int rl = tid >> sh;  // the lane's row within the tile
+  const int rows = kPair ? 8 : (kThreads >> sh);
+  const int row0 = tile * rows;
+  const int row = row0 + (kPair ? (rl & 7) : rl);
+  uint4* xq = smem;
+  float* sx = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kSx);
+  uint32_t* sbl = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(smem) + L::kSb);
+  const uint32_t magic = in_vgpr(kMagic);
+
+  // the tile's (scale, bias) span (a pair tile: threads 0-127 the 8 gate rows, 128-255
+  // the 8 up rows), rounded up to whole dwords (the extra half lies in the same aligned
+  // dword as the last one and belongs to no row)
+  const uint32_t sb_bytes = ((uint32_t)N * (uint32_t)G * 2u + 3u) & ~3u;
+  const __amdgpu_buffer_rsrc_t srsrc = buffer_rsrc(sp, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc = buffer_rsrc(bp, sb_bytes);
+  const int st = kPair ? (tid & 127) : tid;
+  const int D = (rows * G) >> 1;
+  const uint32_t sb0 = (uint32_t)row0 * (uint32_t)G * 2u;
+  uint32_t sv[SBR], bv[SBR];
+#pragma unroll
+  for (int q = 0; q < SBR; ++q) {
+    const int d = st + (kPair ? kThreads / 2 : kThreads) * q;
+    const uint32_t off = d < D ? sb0 + 4u * d : kPastBuffer;
+    sv[q] = __builtin_amdgcn_raw_buffer_load_b32(srsrc, off, 0, 0);
+    bv[q] = __builtin_amdgcn_raw_buffer_load_b32(brsrc, off, 0, 0);
+  }
+  // the weight chunks (rows past N read as zero and are never stored)
+  const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(wp, (uint32_t)N * (uint32_t)W * 4u);
+  const uint32_t wrow = (uint32_t)row * (uint32_t)W * 4u;
+  uint4 wv[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int kc = j + (i << sh);
+    wv[i] = load_b128(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
+  }
+
+  if (S.wait >= 0 && !wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
+
+  uint4 xs[XR];
+  if (XSRC == kXNorm)
+    norm_x<XR>(S.h, S.norm_w, K, S.eps, tid, reinterpret_cast<float*>(smem),
+               reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + kNormRed), xs);
+  else
+    fetch_x<XR>(S.x, K, tid, xs);
+#pragma unroll
+  for (int t = 0; t < XR; ++t) {
+    const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
+    xq[(i & 3) * CP + (i >> 2)] = pair_order(xs[t]);
+    float part = sum8(xs[t]);
+    part += __shfl_xor(part, 1);
+    part += __shfl_xor(part, 2);
+    if ((i & 3) == 0) sx[i >> 2] = part;
+  }
+  const int sbase = kPair && tid >= 128 ? 4 * G : 0;  // dword offset of the up rows' span
+#pragma unroll
+  for (int q = 0; q < SBR; ++q) {
+    const int d = st + (kPair ? kThreads / 2 : kThreads) * q;
+    if (d < D)
+      *reinterpret_cast<uint2*>(sbl + 2 * (sbase + d)) =
+          make_uint2((sv[q] & 0xffffu) | (bv[q] << 16), (sv[q] >> 16) | (bv[q] & 0xffff0000u));
+  }
+  lds_barrier();
+
+  float acc = 0.0f;
+  const uint32_t* sbr = sbl + rl * G;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    if (i < nch) {
+      const int kc = j + (i << sh);
+      const bool valid = kc < C;
+      const int kk = valid ? kc : 0;
+      const uint32_t sb = sbr[kk >> 1];
+      const float sc = __uint_as_float(sb << 16);
+      const float bi = __uint_as_float(sb & 0xffff0000u);
+      const float sxm = sx[kk];
+      const float d = chunk_dot(wv[i], xq[kk], xq[CP + kk], xq[2 * CP + kk], xq[3 * CP + kk],
+                                -128.0f * sxm, magic);
+      const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
+      acc = valid ? v : acc;
+    }
+  }
+  float v = row16_sum(acc);
+  if (sh >= 5) v += __shfl_xor(v, 16);
+  if (sh >= 6) v += __shfl_xor(v, 32);
+
+  const bool owner = j == 0 && row < N;
+  if (EPI == kEpiBf16) {
+    if (owner) store_b16_sc1(buffer_rsrc(S.p[qi].y, (uint32_t)N * 2u), 2u * row, to_bf(v));
+  } else if (EPI == kEpiF32) {
+    if (owner) static_cast<float*>(S.p[qi].y)[row] = v;
+  } else if (EPI == kEpiResidual) {
+    if (owner) stf_sc1(S.h + row, ldf_sc1(S.h + row) + bf(to_bf(v)));
+  } else {  // SiLU * up: the up rows hand their values to the gate rows
+    float* pairx = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kPair);
+    if (j == 0 && rl >= 8) pairx[rl - 8] = v;
+    lds_barrier();
+    if (owner && rl < 8) {
+      const float g0 = bf(to_bf(v));
+      const float u = bf(to_bf(pairx[rl]));
+      store_b16_sc1(buffer_rsrc(S.act, (uint32_t)N * 2u), 2u * row,
+                    to_bf(g0 / (1.0f + expf(-g0)) * u));
+    }
+  }
+  return true;
+}
+
+// ------------------------------------------------------------------ attention
+//
+// Task (request b, KV head, split s) over keys [s * cps * 64, ...) of the request's
+// length pos + 1.  The task rotates its G query heads and the new key itself (the
+// arithmetic of qk_norm_rope_kernel), takes the new key and value from registers at
+// row pos (the split that holds pos also writes them into the pools), and runs the
+// chunk loop of attention_partial_kernel with q in LDS and K then V of a chunk sharing
+// one LDS region.  The last split of a (request, KV head) to finish merges the partials
+// in split order (attention_combine_kernel's arithmetic) into the bf16 output.
+
+struct AttnLds {
+  uint4 kv[kChunk][17];  // K rows (padded), or V as uint32 [64][64]
+  float p[4][2][kChunk];
+  uint32_t qs[8][kD / 2];  // rotated q of the task's heads, bf16 pairs
+  uint32_t knew[kD / 2];
+  uint32_t vnew[kD / 2];
+  int last;
+};
+
+// a if m is all ones, b if m is zero (a value select the compiler keeps in registers)
+__device__ __forceinline__ uint4 select4(uint32_t m, uint4 a, uint4 b) {
+  return make_uint4((a.x & m) | (b.x & ~m), (a.y & m) | (b.y & ~m), (a.z & m) | (b.z & ~m),
+                    (a.w & m) | (b.w & ~m));
+}
+
+__device__ __forceinline__ uint16_t ld16_sc1(const uint16_t* base, uint32_t bytes, uint32_t off) {
+  return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(base, bytes), off, 0, kSc1);
+}
+
+__device__ __forceinline__ bool attention_task(StageRef S, int task, const StepArgs& a, uint4* smem) {
+  AttnLds& L = *reinterpret_cast<AttnLds*>(smem);
+  const int splits = S.splits, Hkv = S.Hkv, Hq = S.Hq, G = Hq / Hkv;
+  const int s = task % splits, kvh = (task / splits) % Hkv, b = task / (splits * Hkv);
+  const int tid = task_tid(), wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int pos = uni(S.positions[b]), slot = uni(S.slots[b]);
+  const bool slot_ok = slot >= 0 && slot < S.num_slots;
+  const bool write_ok = slot_ok && pos >= 0 && pos < S.capacity;
+  int len = pos + 1;
+  len = len < S.max_len ? len : S.max_len;
+  len = len < S.capacity ? len : S.capacity;
+  if (!write_ok || len < 0) len = 0;
+  const int span = S.cps * kChunk;
+  const int first = s * span;
+  const int last = min(len, first + span);
+  const int used = (len + span - 1) / span;
+  const int newrow = write_ok && pos < len ? pos : -1;
+  const int writer = write_ok ? min(pos / span, splits - 1) : -1;
+  const size_t base = (((size_t)(slot_ok ? slot : 0) * Hkv + kvh) * S.capacity) * kD;
+  uint32_t(*vt)[kD / 2] = reinterpret_cast<uint32_t(*)[kD / 2]>(&L.kv[0][0]);
+
+  // Chunk rows as raw buffer loads: rows past `last` read row last-1 (in the slot; never
+  // used), a split with nothing to do reads past the buffer (zeros, no traffic).  The
+  // row of the new key is read too (whatever the pool holds there) and replaced by the
+  // new key when staged.
+  const uint32_t pool_bytes = (uint32_t)(((size_t)(slot_ok ? slot : 0) * Hkv + kvh + 1) * S.capacity * kD * 2);
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(S.k_pool, pool_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(S.v_pool, pool_bytes);
+  // row p >> 4, 16-byte column p & 15 of the chunk starting at `start`, p = tid + 256 i
+  auto chunk_off = [&](int start, int i) -> uint32_t {
+    const int p = tid + kThreads * i;
+    const int t = start + (p >> 4) < last ? start + (p >> 4) : last - 1;
+    return first < last ? (uint32_t)((base + (size_t)t * kD) * 2) + 16u * (p & 15) : kPastBuffer;
+  };
+  uint4 k0 = load_b128(krs, chunk_off(first, 0)), k1 = load_b128(krs, chunk_off(first, 1));
+  uint4 k2 = load_b128(krs, chunk_off(first, 2)), k3 = load_b128(krs, chunk_off(first, 3));
+  uint4 v0 = load_b128(vrs, chunk_off(first, 0)), v1 = load_b128(vrs, chunk_off(first, 1));
+  uint4 v2 = load_b128(vrs, chunk_off(first, 2)), v3 = load_b128(vrs, chunk_off(first, 3));
+  if (!wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
+
+  // rotated q heads (wavefront per head) and, on wavefront 0, the new key and value
+  const float eps = S.eps;
+  auto rotate = [&](const uint16_t* src, uint32_t bytes, uint32_t off, const uint16_t* nw,
+                    uint16_t* dst) {
+    float x0 = bf(ld16_sc1(src, bytes, off + 2u * lane));
+    float x1 = bf(ld16_sc1(src, bytes, off + 2u * (lane + 64)));
+    const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+    const float inv = 1.0f / sqrtf(ss / (float)kD + eps);
+    x0 = bf(to_bf(x0 * inv * bf(nw[lane])));
+    x1 = bf(to_bf(x1 * inv * bf(nw[lane + 64])));
+    const float inv_freq = exp2f(-(float)lane * (S.log2_theta / 64.0f));
+    float sn, cs;
+    sincosf((float)pos * inv_freq, &sn, &cs);
+    const float r0 = x0 * cs - x1 * sn;
+    const float r1 = x0 * sn + x1 * cs;
+    dst[lane] = to_bf(r0);
+    dst[lane + 64] = to_bf(r1);
+  };
+  const uint32_t qbytes = (uint32_t)(b + 1) * Hq * kD * 2u;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int g = wave + 4 * r;
+    if (g < G)
+      rotate(S.q, qbytes, (uint32_t)((b * Hq + kvh * G + g) * kD) * 2u, S.q_norm,
+             reinterpret_cast<uint16_t*>(L.qs[g]));
+  }
+  if (wave == 0) {
+    const uint32_t kvbytes = (uint32_t)(b + 1) * Hkv * kD * 2u;
+    const uint32_t off = (uint32_t)((b * Hkv + kvh) * kD) * 2u;
+    uint16_t* kn = reinterpret_cast<uint16_t*>(L.knew);
+    uint16_t* vn = reinterpret_cast<uint16_t*>(L.vnew);
+    rotate(S.k, kvbytes, off, S.k_norm, kn);
+    vn[lane] = ld16_sc1(S.v, kvbytes, off + 2u * lane);
+    vn[lane + 64] = ld16_sc1(S.v, kvbytes, off + 2u * (lane + 64));
+    if (s == writer) {  // this step's key and value into the pools (read by later launches)
+      uint16_t* kd = S.k_pool + base + (size_t)pos * kD;
+      uint16_t* vd = S.v_pool + base + (size_t)pos * kD;
+      kd[lane] = kn[lane];
+      kd[lane + 64] = kn[lane + 64];
+      vd[lane] = vn[lane];
+      vd[lane + 64] = vn[lane + 64];
+    }
+  }
+  __syncthreads();
+
+  uint16_t* out = S.attn_out;
+  const uint32_t out_bytes = (uint32_t)(b + 1) * Hq * kD * 2u;
+  if (first >= last) {
+    if (used == 0 && s == 0) {  // nothing to attend to: zeros
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int g = wave + 4 * r;
+        if (g < G)
+          store_b32_sc1(buffer_rsrc(out, out_bytes),
+                        (uint32_t)((b * Hq + kvh * G + g) * kD + 2 * lane) * 2u, 0u);
+      }
+    }
+    return true;
+  }
+
+  float M[2] = {-INFINITY, -INFINITY}, Ls[2] = {0.0f, 0.0f};
+  float a0[2] = {0.0f, 0.0f}, a1[2] = {0.0f, 0.0f};
+  float mc[2], lc[2];
+  const uint4* kn4 = reinterpret_cast<const uint4*>(L.knew);
+  const uint4* vn4 = reinterpret_cast<const uint4*>(L.vnew);
+  for (int start = first; start < last; start += kChunk) {
+    const int count = min(kChunk, last - start);
+    __syncthreads();  // the previous chunk's V readers are done
+    {
+      const uint4 kr[4] = {k0, k1, k2, k3};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = tid + kThreads * i;
+        const int row = p >> 4, col = p & 15;
+        L.kv[row][col] = select4(start + row == newrow ? ~0u : 0u, kn4[col], kr[i]);
+      }
+    }
+    __syncthreads();
+    if (start + kChunk < last) {
+      k0 = load_b128(krs, chunk_off(start + kChunk, 0));
+      k1 = load_b128(krs, chunk_off(start + kChunk, 1));
+      k2 = load_b128(krs, chunk_off(start + kChunk, 2));
+      k3 = load_b128(krs, chunk_off(start + kChunk, 3));
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int g = wave + 4 * r;
+      if (g < G) {
+        const uint4* qv = reinterpret_cast<const uint4*>(L.qs[g]);
+        float sc = -INFINITY;
+        if (lane < count) {
+          float d = 0.0f;
+#pragma unroll
+          for (int jj = 0; jj < 16; ++jj) {
+            const uint4 qa = qv[jj], kk = L.kv[lane][jj];
+            d = dot2(qa.x, kk.x, d);
+            d = dot2(qa.y, kk.y, d);
+            d = dot2(qa.z, kk.z, d);
+            d = dot2(qa.w, kk.w, d);
+          }
+          sc = d * S.scale;
+        }
+        mc[r] = wave_max(sc);
+        const float p = lane < count ? expf(sc - mc[r]) : 0.0f;
+        lc[r] = wave_sum(p);
+        L.p[wave][r][lane] = p;
+      }
+    }
+    __syncthreads();  // the K readers are done: V takes the region
+    {
+      const uint4 vr[4] = {v0, v1, v2, v3};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = tid + kThreads * i;
+        const int row = p >> 4, col = p & 15;
+        *reinterpret_cast<uint4*>(&vt[row][col * 4]) =
+            select4(start + row == newrow ? ~0u : 0u, vn4[col], vr[i]);
+      }
+    }
+    __syncthreads();
+    if (start + kChunk < last) {
+      v0 = load_b128(vrs, chunk_off(start + kChunk, 0));
+      v1 = load_b128(vrs, chunk_off(start + kChunk, 1));
+      v2 = load_b128(vrs, chunk_off(start + kChunk, 2));
+      v3 = load_b128(vrs, chunk_off(start + kChunk, 3));
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int g = wave + 4 * r;
+      if (g < G) {
+        float c0 = 0.0f, c1 = 0.0f;
+        for (int t = 0; t < count; ++t) {
+          const float pt = L.p[wave][r][t];
+          const uint32_t vd = vt[t][lane];
+          c0 = fmaf(pt, bf(vd & 0xffffu), c0);
+          c1 = fmaf(pt, bf(vd >> 16), c1);
+        }
+        const float mn = fmaxf(M[r], mc[r]);
+        const float eo = expf(M[r] - mn), ec = expf(mc[r] - mn);
+        Ls[r] = fmaf(Ls[r], eo, lc[r] * ec);
+        a0[r] = fmaf(a0[r], eo, c0 * ec);
+        a1[r] = fmaf(a1[r], eo, c1 * ec);
+        M[r] = mn;
+      }
+    }
+  }
+
+  // this split's partial, then the last split of (b, kvh) merges them in split order
+  const uint32_t part_bytes = (uint32_t)((b + 1) * Hq * splits) * kD * 4u;
+  const uint32_t ml_bytes = (uint32_t)((b + 1) * Hq * splits) * 8u;
+  const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(S.part, part_bytes);
+  const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(S.ml, ml_bytes);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int g = wave + 4 * r;
+    if (g < G) {
+      const uint32_t po = (uint32_t)((b * Hq + kvh * G + g) * splits + s);
+      store_b32_sc1(prs, (po * kD + 2 * lane) * 4u, __float_as_uint(a0[r]));
+      store_b32_sc1(prs, (po * kD + 2 * lane + 1) * 4u, __float_as_uint(a1[r]));
+      if (lane == 0) {
+        store_b32_sc1(mrs, po * 8u, __float_as_uint(M[r]));
+        store_b32_sc1(mrs, po * 8u + 4u, __float_as_uint(Ls[r]));
+      }
+    }
+  }
+  wait_vmem();
+  __syncthreads();
+  if (tid == 0)
+    L.last = __hip_atomic_fetch_add(S.combine + b * Hkv + kvh, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(used - 1);
+  __syncthreads();
+  if (!L.last) return true;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int g = wave + 4 * r;
+    if (g < G) {
+      const int hh = kvh * G + g;
+      const uint32_t p0 = (uint32_t)((b * Hq + hh) * splits);
+      float Mx = -INFINITY;
+      for (int s2 = 0; s2 < used; ++s2)
+        Mx = fmaxf(Mx, __uint_as_float(load_b32_sc1(mrs, (p0 + s2) * 8u)));
+      float Lx = 0.0f, c0 = 0.0f, c1 = 0.0f;
+      for (int s2 = 0; s2 < used; ++s2) {
+        const float e = expf(__uint_as_float(load_b32_sc1(mrs, (p0 + s2) * 8u)) - Mx);
+        Lx = fmaf(__uint_as_float(load_b32_sc1(mrs, (p0 + s2) * 8u + 4u)), e, Lx);
+        const float px = __uint_as_float(load_b32_sc1(prs, ((p0 + s2) * kD + 2 * lane) * 4u));
+        const float py = __uint_as_float(load_b32_sc1(prs, ((p0 + s2) * kD + 2 * lane + 1) * 4u));
+        c0 = fmaf(px, e, c0);
+        c1 = fmaf(py, e, c1);
+      }
+      const uint32_t o = (uint32_t)to_bf(c0 / Lx) | ((uint32_t)to_bf(c1 / Lx) << 16);
+      store_b32_sc1(buffer_rsrc(out, out_bytes), (uint32_t)((b * Hq + hh) * kD + 2 * lane) * 2u, o);
+    }
+  }
+  return true;
+}
+
+// ------------------------------------------------------------------ the kernels
+
+// One qmv instantiation per (x source, epilogue, tile shape) that a program can hold.
+#define IMQ_QMV_CASE(NCH, XR, XSRC, EPI, SHAPE)                   \
+  case (XSRC) * 16 + (EPI) * 4 + (SHAPE):                          \
+    good = qmv_task<NCH, XR, XSRC, EPI>(S, task, a, smem);         \
+    break;
+#define IMQ_QMV_SHAPES_X2(XSRC, EPI)         \
+  IMQ_QMV_CASE(2, 2, XSRC, EPI, kShape22)    \
+  IMQ_QMV_CASE(5, 2, XSRC, EPI, kShape52)    \
+  IMQ_QMV_CASE(8, 2, XSRC, EPI, kShape82)
+
+__global__ __launch_bounds__(kThreads) void step_kernel(const Stage* __restrict__ stages,
+                                                        StepArgs a) {
+  extern __shared__ uint4 smem[];
+  int si = 0;
+  for (int t = blockIdx.x; t < a.ntasks; t += gridDim.x) {
+    while (t >= stages[si].first + stages[si].count) ++si;
+    StageRef S = global_stage(stages + si);
+    const int task = t - S.first;
+    bool good = false;
+    if (S.kind == kKindAttention) {
+      good = attention_task(S, task, a, smem);
+    } else {
+      switch (S.xsrc * 16 + S.epi * 4 + S.shape) {
+        IMQ_QMV_SHAPES_X2(kXVector, kEpiBf16)
+        IMQ_QMV_CASE(5, 5, kXVector, kEpiBf16, kShape55)
+        IMQ_QMV_SHAPES_X2(kXVector, kEpiResidual)
+        IMQ_QMV_CASE(5, 5, kXVector, kEpiResidual, kShape55)
+        IMQ_QMV_SHAPES_X2(kXNorm, kEpiBf16)
+        IMQ_QMV_SHAPES_X2(kXNorm, kEpiSiluPair)
+        IMQ_QMV_SHAPES_X2(kXNorm, kEpiF32)
+        default: break;  // the host plans only the cases above
+      }
+    }
+    if (!good) return;
+    signal(counter(a, si, task % kSub));
+  }
+}
+
+#undef IMQ_QMV_SHAPES_X2
+#undef IMQ_QMV_CASE
+
+__global__ __launch_bounds__(kThreads) void reset_kernel(uint32_t* words, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) words[i] = 0u;
+}
+
+// ------------------------------------------------------------------ host side
+
+size_t lds_bytes_for(int shape) {
+  switch (shape) {
+    case kShape22: return QLds<2, 2>::kBytes;
+    case kShape52: return QLds<5, 2>::kBytes;
+    case kShape82: return QLds<8, 2>::kBytes;
+    default: return QLds<5, 5>::kBytes;
+  }
+}
+
+// The one-row tile's lane shape of qmv.hip's plan_m1 (16, 32 or 64 lanes per row, at
+// most 8 chunks per lane), and the instantiation that covers it.  -1: not served.
+struct TileShape {
+  int sh, nch, xr, shape;
+};
+
+TileShape tile_shape(int K) {
+  TileShape t{-1, 0, 0, -1};
+  const int C = K / 32;
+  int sh = 4;
+  while (sh <= 6 && (C + (1 << sh) - 1) >> sh > 8) ++sh;
+  if (sh > 6) return t;
+  t.sh = sh;
+  t.nch = (C + (1 << sh) - 1) >> sh;
+  t.xr = (K / 8 + kThreads - 1) / kThreads;
+  if (t.nch <= 2 && t.xr <= 2) t.shape = kShape22;
+  else if (t.nch <= 5 && t.xr <= 2) t.shape = kShape52;
+  else if (t.nch <= 8 && t.xr <= 2) t.shape = kShape82;
+  else if (t.nch <= 5 && t.xr <= 5) t.shape = kShape55;
+  return t;
+}
+
+int32_t check_qweight(const imq_qweight& q, int64_t N, int64_t K, const char* what) {
+  if (!q.w || !q.scales || !q.biases) return fail(IMQ_EINVAL, std::string(what) + ": null weight pointer");
+  if (!aligned(q.w, 16) || !aligned(q.scales, 4) || !aligned(q.biases, 4))
+    return fail(IMQ_EINVAL, std::string(what) + ": w must be 16-byte and scales/biases 4-byte aligned");
+  if (N < 1 || K < 64 || K % 64) return fail(IMQ_EINVAL, std::string(what) + ": bad shape");
+  if (N * (K / 2) >= ((int64_t)1 << 31))
+    return fail(IMQ_EUNSUPPORTED, std::string(what) + ": weights of 2 GiB or more");
+  return IMQ_OK;
+}
+
+}  // namespace
+
+struct imq_program {
+  int device = -1;
+  std::vector<Stage> stages;
+  Stage* d_stages = nullptr;
+  uint32_t* d_words = nullptr;  // completion counters, then combine counters, then status
+  int64_t reset_words = 0;      // words zeroed before each run (all but the status word)
+  uint32_t* d_status = nullptr;
+  void* d_scratch = nullptr;    // activations and attention partials
+  int ntasks = 0;
+  int sub_stride = 0;
+  int grid = 0;
+  size_t lds = 0;
+};
+
+namespace {
+
+void free_program(imq_program* p) {
+  if (!p) return;
+  if (p->d_stages) (void)hipFree(p->d_stages);
+  if (p->d_words) (void)hipFree(p->d_words);
+  if (p->d_scratch) (void)hipFree(p->d_scratch);
+  delete p;
+}
+
+// Adds a qmv stage of one-row tiles over `probs` (same K); pair: a gate/up pair.
+int32_t add_qmv_stage(imq_program* prog, const std::vector<QProb>& probs, int xsrc, int epi,
+                      int wait, const uint16_t* x, float* h,
+                      const uint16_t* norm_w, float eps, uint16_t* act) {
+  Stage S;
+  memset(&S, 0, sizeof(S));
+  S.kind = kKindQmv;
+  S.wait = wait;
+  S.xsrc = xsrc;
+  S.epi = epi;
+  S.nprob = (int)probs.size();
+  S.eps = eps;
+  S.x = x;
+  S.h = h;
+  S.norm_w = norm_w;
+  S.act = act;
+  const TileShape ts = tile_shape(probs[0].K);
+  if (ts.shape < 0) return fail(IMQ_EUNSUPPORTED, "K outside the persistent qmv tiles (K <= 16384 with 2/5/8 chunks per lane)");
+  if (xsrc == kXNorm && (ts.xr > 2 || probs[0].K > kMaxHidden))
+    return fail(IMQ_EUNSUPPORTED, "a fused RMSNorm row is limited to 4096 values");
+  if (epi == kEpiSiluPair && ts.sh != 4)
+    return fail(IMQ_EUNSUPPORTED, "the gate/up pair tile needs 16 lanes per row (K <= 4096)");
+  S.shape = ts.shape;
+  int tiles = 0;
+  for (size_t i = 0; i < probs.size(); ++i) {
+    QProb q = probs[i];
+    if (q.K != probs[0].K) return fail(IMQ_EINVAL, "every problem of a stage has the same K");
+    q.sh = ts.sh;
+    q.nch = ts.nch;
+    const int rows = epi == kEpiSiluPair ? 8 : (kThreads >> ts.sh);
+    const int t = (q.N + rows - 1) / rows;
+    tiles = epi == kEpiSiluPair ? t : tiles + t;
+    q.tile_end = tiles;
+    S.p[i] = q;
+  }
+  S.count = tiles;
+  S.first = prog->ntasks;
+  if (wait >= 0) S.wait_count = prog->stages[wait].count;
+  prog->ntasks += S.count;
+  prog->stages.push_back(S);
+  return IMQ_OK;
+}
+
+// Device tables, counters and the launch geometry of a planned program.
+int32_t finish_program(imq_program* prog) {
+  const int nstages = (int)prog->stages.size();
+  if (nstages == 0 || prog->ntasks == 0) return fail(IMQ_EINVAL, "empty program");
+  size_t lds = sizeof(AttnLds);
+  for (const Stage& S : prog->stages)
+    if (S.kind == kKindQmv)
+      lds = std::max(lds, std::max(lds_bytes_for(S.shape), S.xsrc == kXNorm ? kNormBytes : 0));
+  prog->lds = (lds + 15) & ~(size_t)15;
+  // counters: kSub lines per stage; the same sub-counter of consecutive stages are
+  // neighbours, and consecutive sub-counters of one stage >= 4 KiB apart
+  prog->sub_stride = std::max(nstages, 32);
+  const int64_t counter_words = (int64_t)kSub * prog->sub_stride * kLineWords;
+  int64_t combine_total = 0;
+  for (Stage& S : prog->stages)
+    if (S.kind == kKindAttention) combine_total += (int64_t)S.count / S.splits;
+  prog->reset_words = counter_words + combine_total;
+  const int64_t words = prog->reset_words + 1;
+  if (hipMalloc(&prog->d_words, (size_t)words * 4) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "hipMalloc of the program counters failed");
+  if (hipMemset(prog->d_words, 0, (size_t)words * 4) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "hipMemset of the program counters failed");
+  prog->d_status = prog->d_words + prog->reset_words;
+  int64_t cw = counter_words;
+  for (Stage& S : prog->stages)
+    if (S.kind == kKindAttention) {
+      S.combine = prog->d_words + cw;
+      cw += S.count / S.splits;
+    }
+  if (hipMalloc(&prog->d_stages, sizeof(Stage) * nstages) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "hipMalloc of the stage table failed");
+  if (hipMemcpy(prog->d_stages, prog->stages.data(), sizeof(Stage) * nstages,
+                hipMemcpyHostToDevice) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "copying the stage table failed");
+  int32_t code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(step_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)prog->lds) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "cannot give the persistent kernel its LDS");
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_kernel, kThreads, prog->lds) !=
+          hipSuccess ||
+      per_cu < 1)
+    return fail(IMQ_ELAUNCH, "the persistent kernel does not fit on a CU");
+  prog->grid = std::min(per_cu * dev->cu_count, prog->ntasks);
+  return ok();
+}
+
+// Attention splits: the per-kernel path's plan (decode.hip attention_plan), so both
+// paths merge the same partials in the same order.
+void attention_split(int B, int Hkv, int span, int* splits, int* cps) {
+  const int chunks = (span + kChunk - 1) / kChunk;
+  const int pairs = B * Hkv;
+  int sp = (512 + pairs - 1) / pairs;
+  sp = sp < chunks ? sp : chunks;
+  sp = sp > 1 ? sp : 1;
+  const int c = (chunks + sp - 1) / sp;
+  *cps = c;
+  *splits = (chunks + c - 1) / c;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t imq_qmv_program_create(const imq_qmv_stage* stages, int32_t count, imq_program** out) {
+  if (!out) return fail(IMQ_EINVAL, "out must be non-null");
+  *out = nullptr;
+  if (!stages || count < 1) return fail(IMQ_EINVAL, "need at least one stage");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  imq_program* prog = new imq_program();
+  hipGetDevice(&prog->device);
+  for (int i = 0; i < count; ++i) {
+    const imq_qmv_stage& st = stages[i];
+    if (st.count < 1 || st.count > kMaxStageProblems) {
+      free_program(prog);
+      return fail(IMQ_EINVAL, "a stage has 1 to 3 problems");
+    }
+    std::vector<QProb> probs;
+    for (int k = 0; k < st.count; ++k) {
+      const imq_problem& q = st.problems[k];
+      const imq_qweight qw{q.w, q.scales, q.biases};
+      code = check_qweight(qw, q.N, q.K, "qmv stage");
+      if (code == IMQ_OK && (!q.x || !q.y || !aligned(q.x, 16) || !aligned(q.y, 2)))
+        code = fail(IMQ_EINVAL, "x must be 16-byte aligned and y 2-byte aligned");
+      if (code == IMQ_OK && q.x != st.problems[0].x)
+        code = fail(IMQ_EINVAL, "the problems of a stage share one x");
+      if (code != IMQ_OK) {
+        free_program(prog);
+        return code;
+      }
+      QProb p;
+      memset(&p, 0, sizeof(p));
+      p.w = q.w;
+      p.s = q.scales;
+      p.b = q.biases;
+      p.y = q.y;
+      p.N = q.N;
+      p.K = q.K;
+      probs.push_back(p);
+    }
+    const int wait = st.wait_previous && i > 0 ? i - 1 : -1;
+    if ((code = add_qmv_stage(prog, probs, kXVector, kEpiBf16, wait, st.problems[0].x, nullptr,
+                              nullptr, 0.0f, nullptr)) != IMQ_OK) {
+      free_program(prog);
+      return code;
+    }
+  }
+  if ((code = finish_program(prog)) != IMQ_OK) {
+    free_program(prog);
+    return code;
+  }
+  *out = prog;
+  return IMQ_OK;
+}
+
+int32_t imq_decode_program_create(const imq_step_desc* d, imq_program** out) {
+  if (!out) return fail(IMQ_EINVAL, "out must be non-null");
+  *out = nullptr;
+  if (!d || !d->layer || !d->final_norm || !d->positions || !d->slots || !d->h || !d->logits)
+    return fail(IMQ_EINVAL, "null pointer in the step description");
+  if (d->batch != 1) return fail(IMQ_EUNSUPPORTED, "the persistent decode step runs batch 1");
+  if (d->layers < 1 || d->hidden < 64 || d->hidden % 64 || d->hidden > kMaxHidden)
+    return fail(IMQ_EINVAL, "need layers >= 1 and hidden a multiple of 64 up to 4096");
+  if (d->heads < 1 || d->kv_heads < 1 || d->heads % d->kv_heads || d->heads / d->kv_heads > 8)
+    return fail(IMQ_EINVAL, "need kv_heads | heads with at most 8 query heads per KV head");
+  if (d->intermediate < 64 || d->intermediate % 64 || d->vocab < 1)
+    return fail(IMQ_EINVAL, "bad intermediate size or vocabulary");
+  if (d->capacity < 1 || d->num_slots < 1 || d->max_len < 1)
+    return fail(IMQ_EINVAL, "capacity, num_slots and max_len must be >= 1");
+  if (!(d->theta > 1.0f) || !(d->eps >= 0.0f)) return fail(IMQ_EINVAL, "bad theta or eps");
+  if (!aligned(d->h, 16)) return fail(IMQ_EINVAL, "h must be 16-byte aligned");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  const int B = d->batch, D = d->hidden, Hq = d->heads, Hkv = d->kv_heads, I = d->intermediate;
+  const int qd = Hq * kD, kvd = Hkv * kD;
+  for (int i = 0; i < d->layers; ++i) {
+    const imq_step_layer& Ly = d->layer[i];
+    if ((code = check_qweight(Ly.q, qd, D, "q")) || (code = check_qweight(Ly.k, kvd, D, "k")) ||
+        (code = check_qweight(Ly.v, kvd, D, "v")) || (code = check_qweight(Ly.o, D, qd, "o")) ||
+        (code = check_qweight(Ly.gate, I, D, "gate")) || (code = check_qweight(Ly.up, I, D, "up")) ||
+        (code = check_qweight(Ly.down, D, I, "down")))
+      return code;
+    if (!Ly.input_norm || !Ly.post_norm || !Ly.q_norm || !Ly.k_norm || !Ly.k_pool || !Ly.v_pool)
+      return fail(IMQ_EINVAL, "null norm weight or KV pool");
+    if (!aligned(Ly.k_pool, 16) || !aligned(Ly.v_pool, 16))
+      return fail(IMQ_EINVAL, "the KV pools must be 16-byte aligned");
+  }
+  if ((code = check_qweight(d->head, d->vocab, D, "head")) != IMQ_OK) return code;
+  if ((int64_t)d->num_slots * Hkv * d->capacity * kD * 2 >= ((int64_t)1 << 31))
+    return fail(IMQ_EUNSUPPORTED, "a KV pool of 2 GiB or more exceeds the attention's offsets");
+
+  imq_program* prog = new imq_program();
+  hipGetDevice(&prog->device);
+  const int span = std::min(d->max_len, d->capacity);
+  int splits, cps;
+  attention_split(B, Hkv, span, &splits, &cps);
+  // activations: q, k, v, attention output, SiLU*up (bf16), then the partials (fp32)
+  const size_t off_q = 0, off_k = off_q + (size_t)B * qd * 2, off_v = off_k + (size_t)B * kvd * 2;
+  const size_t off_attn = off_v + (size_t)B * kvd * 2, off_act = off_attn + (size_t)B * qd * 2;
+  const size_t off_part = (off_act + (size_t)B * I * 2 + 255) & ~(size_t)255;
+  const size_t off_ml = off_part + (size_t)B * Hq * splits * kD * 4;
+  const size_t scratch = off_ml + (size_t)B * Hq * splits * 8;
+  if (hipMalloc(&prog->d_scratch, scratch) != hipSuccess) {
+    free_program(prog);
+    return fail(IMQ_ELAUNCH, "hipMalloc of the program activations failed");
+  }
+  char* sc = static_cast<char*>(prog->d_scratch);
+  uint16_t* q = reinterpret_cast<uint16_t*>(sc + off_q);
+  uint16_t* k = reinterpret_cast<uint16_t*>(sc + off_k);
+  uint16_t* v = reinterpret_cast<uint16_t*>(sc + off_v);
+  uint16_t* attn = reinterpret_cast<uint16_t*>(sc + off_attn);
+  uint16_t* act = reinterpret_cast<uint16_t*>(sc + off_act);
+  float* part = reinterpret_cast<float*>(sc + off_part);
+  float* ml = reinterpret_cast<float*>(sc + off_ml);
+  auto qp = [](const imq_qweight& w, void* y, int N, int K) {
+    QProb p;
+    memset(&p, 0, sizeof(p));
+    p.w = w.w;
+    p.s = w.scales;
+    p.b = w.biases;
+    p.y = y;
+    p.N = N;
+    p.K = K;
+    return p;
+  };
+  int prev = -1;
+  for (int i = 0; i < d->layers && code == IMQ_OK; ++i) {
+    const imq_step_layer& Ly = d->layer[i];
+    code = add_qmv_stage(prog, {qp(Ly.q, q, qd, D), qp(Ly.k, k, kvd, D), qp(Ly.v, v, kvd, D)},
+                         kXNorm, kEpiBf16, prev, nullptr, d->h, Ly.input_norm, d->eps, nullptr);
+    if (code) break;
+    const int s_qkv = (int)prog->stages.size() - 1;
+    Stage A;
+    memset(&A, 0, sizeof(A));
+    A.kind = kKindAttention;
+    A.wait = s_qkv;
+    A.wait_count = prog->stages[s_qkv].count;
+    A.count = B * Hkv * splits;
+    A.first = prog->ntasks;
+    A.eps = d->eps;
+    A.log2_theta = log2f(d->theta);
+    A.scale = 1.0f / sqrtf((float)kD);
+    A.q = q;
+    A.k = k;
+    A.v = v;
+    A.q_norm = Ly.q_norm;
+    A.k_norm = Ly.k_norm;
+    A.k_pool = Ly.k_pool;
+    A.v_pool = Ly.v_pool;
+    A.attn_out = attn;
+    A.positions = d->positions;
+    A.slots = d->slots;
+    A.part = part;
+    A.ml = ml;
+    A.Hq = Hq;
+    A.Hkv = Hkv;
+    A.capacity = d->capacity;
+    A.num_slots = d->num_slots;
+    A.max_len = span;
+    A.splits = splits;
+    A.cps = cps;
+    prog->ntasks += A.count;
+    prog->stages.push_back(A);
+    const int s_attn = (int)prog->stages.size() - 1;
+    code = add_qmv_stage(prog, {qp(Ly.o, nullptr, D, qd)}, kXVector, kEpiResidual, s_attn, attn,
+                         d->h, nullptr, d->eps, nullptr);
+    if (code) break;
+    const int s_o = (int)prog->stages.size() - 1;
+    code = add_qmv_stage(prog, {qp(Ly.gate, nullptr, I, D), qp(Ly.up, nullptr, I, D)}, kXNorm,
+                         kEpiSiluPair, s_o, nullptr, d->h, Ly.post_norm, d->eps, act);
+    if (code) break;
+    const int s_gu = (int)prog->stages.size() - 1;
+    code = add_qmv_stage(prog, {qp(Ly.down, nullptr, D, I)}, kXVector, kEpiResidual, s_gu, act,
+                         d->h, nullptr, d->eps, nullptr);
+    prev = (int)prog->stages.size() - 1;
+  }
+  if (code == IMQ_OK)
+    code = add_qmv_stage(prog, {qp(d->head, d->logits, d->vocab, D)}, kXNorm, kEpiF32, prev,
+                         nullptr, d->h, d->final_norm, d->eps, nullptr);
+  if (code == IMQ_OK) code = finish_program(prog);
+  if (code != IMQ_OK) {
+    free_program(prog);
+    return code;
+  }
+  *out = prog;
+  return IMQ_OK;
+}
+
+int32_t imq_program_launch(imq_program* p, void* stream) {
+  if (!p) return fail(IMQ_EINVAL, "null program");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
+    return fail(IMQ_EINVAL, "the program was created on another device");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = p->reset_words;
+  hipLaunchKernelGGL(reset_kernel, dim3((uint32_t)((n + kThreads - 1) / kThreads)), dim3(kThreads),
+                     0, st, p->d_words, n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("reset launch failed: ") + hipGetErrorString(e));
+  StepArgs a;
+  a.done = p->d_words;
+  a.status = p->d_status;
+  a.ntasks = p->ntasks;
+  a.sub_stride = p->sub_stride;
+  hipLaunchKernelGGL(step_kernel, dim3(p->grid), dim3(kThreads), p->lds, st,
+                     static_cast<const Stage*>(p->d_stages), a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("persistent launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+int32_t imq_program_status(imq_program* p, int32_t* failed) {
+  if (!p || !failed) return fail(IMQ_EINVAL, "null argument");
+  if (hipDeviceSynchronize() != hipSuccess) return fail(IMQ_ELAUNCH, "device synchronisation failed");
+  uint32_t s = 0;
+  if (hipMemcpy(&s, p->d_status, 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "reading the status word failed");
+  *failed = s != 0;
+  if (s && hipMemset(p->d_status, 0, 4) != hipSuccess) return fail(IMQ_ELAUNCH, "clearing the status word failed");
+  return ok();
+}
+
+int32_t imq_program_info(const imq_program* p, int32_t* tasks, int32_t* stages, int32_t* workgroups,
+                         int32_t* lds_bytes) {
+  if (!p) return fail(IMQ_EINVAL, "null program");
+  if (tasks) *tasks = p->ntasks;
+  if (stages) *stages = (int32_t)p->stages.size();
+  if (workgroups) *workgroups = p->grid;
+  if (lds_bytes) *lds_bytes = (int32_t)p->lds;
+  return ok();
+}
+
+void imq_program_destroy(imq_program* p) { free_program(p); }
+
+}  // extern "C"

@@ -19,6 +19,10 @@ continuous-batched requests, each with its own KV slot and position:
 All buffers are allocated once per (model, batch size) in `DecodeState`; a step only
 launches kernels, so it can be captured in a HIP graph and replayed.  Every launch goes
 through the C ABI; there is no host fallback.
+
+`PersistentDecode` runs the same step at batch 1 as one persistent-kernel program
+(include/ironmule_step.h): the embedding launch, then one launch for all layers and the
+head, with bit-identical results.
 """
 
 from __future__ import annotations
@@ -172,3 +176,26 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
     n.add_rmsnorm(s.h, weights.norm, s.x, c.eps, delta=delta, stream=stream)
     n.qmv(*weights.embed, s.x, out=s.logits, stream=stream)
     return s.logits
+
+
+class PersistentDecode:
+    """The batch-1 decode step as a persistent program: `step()` launches the embedding and
+    the program (imq_decode_program_create) and returns state.logits.  Same inputs, same
+    bits as `decode_step`."""
+
+    def __init__(self, weights: DecoderWeights, state: DecodeState) -> None:
+        if state.batch != 1:
+            raise ValueError("the persistent decode step runs batch 1")
+        self.weights, self.state = weights, state
+        self.program = _native.decode_program(
+            weights.config, weights.layers, weights.norm, weights.embed, state.k_pool,
+            state.v_pool, state.positions, state.slot_ids, state.h, state.logits, state.max_len)
+
+    def step(self, stream=None) -> torch.Tensor:
+        w, s = self.weights, self.state
+        _native.embed(*w.embed, s.tokens, s.h, stream=stream)
+        self.program.launch(stream)
+        return s.logits
+
+    def failed(self) -> bool:
+        return self.program.failed()

@@ -86,3 +86,38 @@ def test_python_side_validates_before_the_abi():
         _native.check_weights(w, s.float(), s)
     with pytest.raises(ValueError, match="multiple of 64"):
         _native.check_weights(torch.zeros((8, 3), dtype=torch.int32), s, s)
+
+
+def _c_layout(structs: dict[str, list[str]]) -> dict[str, int]:
+    """sizeof and offsetof of the header's structures, as a C compiler lays them out."""
+    import subprocess
+    import tempfile
+
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "ironmule_step.h"',
+             "int main(void) {"]
+    for name, fields in structs.items():
+        lines.append(f'  printf("{name} %zu\\n", sizeof({name}));')
+        for f in fields:
+            lines.append(f'  printf("{name}.{f} %zu\\n", offsetof({name}, {f}));')
+    lines += ["  return 0;", "}"]
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "layout.c"), os.path.join(d, "layout")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-I", os.path.join(_native.ROOT, "include"), src, "-o", exe],
+                       check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    return {k: int(v) for k, v in (ln.split() for ln in out.splitlines())}
+
+
+def test_ctypes_structures_match_the_header():
+    """The ctypes mirrors of imq_problem, imq_qweight, imq_step_layer, imq_step_desc and
+    imq_qmv_stage have the C compiler's sizes and field offsets."""
+    mirrors = {"imq_problem": _native.Problem, "imq_qweight": _native.QWeight,
+               "imq_step_layer": _native.StepLayer, "imq_step_desc": _native.StepDesc,
+               "imq_qmv_stage": _native.QmvStage}
+    structs = {name: [f for f, _ in cls._fields_] for name, cls in mirrors.items()}
+    got = _c_layout(structs)
+    for name, cls in mirrors.items():
+        assert got[name] == ctypes.sizeof(cls), name
+        for f, _ in cls._fields_:
+            assert got[f"{name}.{f}"] == getattr(cls, f).offset, (name, f)

@@ -1,0 +1,220 @@
+"""GPU parity of the persistent engine (include/ironmule_step.h), through the C ABI.
+
+The bar is bit-identity with the per-kernel path on the same inputs: every output of a
+qmv program equals imq_qmv / imq_qmv_grouped's, and the persistent decode step's logits,
+residual stream and KV pools equal `decode_step`'s, over several consecutive steps (the
+per-kernel step is itself checked against the decode oracle in test_decode_gpu.py, and
+the tiny decoder's persistent logits are checked against the oracle here as well).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.conftest import gpu_available
+from tests.gpu_util import announce, to_device
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+
+    from ironmule_amd import _native
+    from oracle import oracle as orc
+    code, arch, _ = _native.device_check()
+    assert code == 0, f"device {arch} is not supported"
+    orc.lib()
+    return torch, _native, orc
+
+
+def _weight(orc, n, k, seed):
+    w, s, b, _ = to_device(orc.synthetic(n, k, 1, seed=seed))
+    return w, s, b
+
+
+def _row(torch, k, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return torch.randn(k, device="cuda", generator=g).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("shapes", [
+    # (K of stage 0 = K of the q/k/v-like stage, N's), then a dependent stage per entry
+    dict(k0=2560, n0=(4096, 1024, 1024), dep=(2560,), k1=2560, n1=(9728, 9728), dep1=(2560,)),
+    dict(k0=64, n0=(128, 17), dep=(100,), k1=192, n1=(64, 8, 24), dep1=(7,)),
+    dict(k0=256, n0=(320,), dep=(77, 5), k1=1024, n1=(1024, 1000), dep1=(64,)),
+])
+def test_qmv_program_chain_matches_per_kernel_calls(env, shapes):
+    """Stage A (1-3 weights on x0), stage B (waits; reads A's first output), stage C (no
+    wait, its own x1), stage D (waits; reads C's first output): every output equals the
+    per-kernel call on the same inputs, bit for bit, on two runs."""
+    torch, n, orc = env
+    announce("qmv program", shapes)
+    seed = 100
+    wa = [_weight(orc, nn, shapes["k0"], seed + i) for i, nn in enumerate(shapes["n0"])]
+    ya = [torch.empty(nn, dtype=torch.bfloat16, device="cuda") for nn in shapes["n0"]]
+    kb = shapes["n0"][0]
+    wb = [_weight(orc, nn, kb, seed + 10 + i) for i, nn in enumerate(shapes["dep"])]
+    yb = [torch.empty(nn, dtype=torch.bfloat16, device="cuda") for nn in shapes["dep"]]
+    wc = [_weight(orc, nn, shapes["k1"], seed + 20 + i) for i, nn in enumerate(shapes["n1"])]
+    yc = [torch.empty(nn, dtype=torch.bfloat16, device="cuda") for nn in shapes["n1"]]
+    kd = shapes["n1"][0]
+    wd = [_weight(orc, nn, kd, seed + 30 + i) for i, nn in enumerate(shapes["dep1"])]
+    yd = [torch.empty(nn, dtype=torch.bfloat16, device="cuda") for nn in shapes["dep1"]]
+    x0, x1 = _row(torch, shapes["k0"], 1), _row(torch, shapes["k1"], 2)
+    prog = n.qmv_program([(wa, x0, ya, False), (wb, ya[0], yb, True), (wc, x1, yc, False),
+                          (wd, yc[0], yd, True)])
+    for run in range(2):
+        prog.launch()
+        torch.cuda.synchronize()
+        assert not prog.failed()
+        for ws, x, ys in ((wa, x0, ya), (wb, ya[0], yb), (wc, x1, yc), (wd, yc[0], yd)):
+            want = n.qmv_grouped(ws, [x.reshape(1, -1)] * len(ws))
+            for y, yw in zip(ys, want):
+                assert torch.equal(y.view(torch.int16), yw.reshape(-1).view(torch.int16)), run
+    info = prog.info()
+    assert info["stages"] == 4 and info["workgroups"] >= 1
+    prog.close()
+
+
+def _tiny():
+    from ironmule_amd.decode import DecoderConfig
+    return DecoderConfig(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128,
+                         intermediate=512, vocab=512, eps=1e-6, theta=1e6)
+
+
+def _twin_states(torch, cfg, capacity, seed):
+    from ironmule_amd.decode import DecodeState
+    a = DecodeState(cfg, batch=1, slots=3, capacity=capacity, max_len=capacity, device="cuda")
+    b = DecodeState(cfg, batch=1, slots=3, capacity=capacity, max_len=capacity, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    for pa, pb in zip(a.k_pool + a.v_pool, b.k_pool + b.v_pool):
+        pa.copy_(torch.randn(pa.shape, device="cuda", generator=g).to(torch.bfloat16))
+        pb.copy_(pa)
+    return a, b
+
+
+def _compare_steps(torch, weights, cfg, capacity, requests, seed):
+    """Runs decode_step on one state and the persistent step on a twin for each request
+    (token, slot, position) in turn; logits, h and every KV pool must agree bit for bit."""
+    from ironmule_amd.decode import PersistentDecode, decode_step
+    ref, per = _twin_states(torch, cfg, capacity, seed)
+    engine = PersistentDecode(weights, per)
+    for step, (tok, slot, pos) in enumerate(requests):
+        ref.set_requests([tok], [slot], [pos])
+        per.set_requests([tok], [slot], [pos])
+        want = decode_step(weights, ref)
+        got = engine.step()
+        torch.cuda.synchronize()
+        assert not engine.failed(), step
+        assert torch.equal(got, want), (step, (got - want).abs().max().item())
+        assert torch.equal(per.h, ref.h), step
+        for i in range(cfg.layers):
+            assert torch.equal(per.k_pool[i], ref.k_pool[i]), (step, i)
+            assert torch.equal(per.v_pool[i], ref.v_pool[i]), (step, i)
+    return engine, per
+
+
+def test_decode_program_matches_decode_step_tiny(env):
+    torch, n, orc = env
+    from ironmule_amd.decode import random_weights
+    announce("persistent decode, tiny decoder")
+    cfg = _tiny()
+    weights = random_weights(cfg, "cuda", seed=5)
+    # first token of a slot, a chunk boundary, the last position, then a continuing request
+    _compare_steps(torch, weights, cfg, 80, [(5, 1, 0), (17, 0, 63), (300, 2, 64), (511, 2, 79),
+                                             (42, 1, 1)], seed=11)
+
+
+def test_decode_program_tiny_against_the_oracle(env):
+    """The persistent logits against the float64 decode oracle with the same rounding
+    points (the bar of test_decode_gpu.py's step test)."""
+    torch, n, orc = env
+    from ironmule_amd.decode import DecodeState, PersistentDecode, random_weights
+    from oracle import decode_oracle as do
+    from tests.test_decode_gpu import _oracle_model, _vals
+    announce("persistent decode vs oracle, tiny decoder")
+    cfg = _tiny()
+    weights = random_weights(cfg, "cuda", seed=6)
+    state = DecodeState(cfg, batch=1, slots=2, capacity=70, max_len=70, device="cuda")
+    for kp, vp in zip(state.k_pool, state.v_pool):
+        kp.copy_(torch.randn(kp.shape, device="cuda").to(torch.bfloat16))
+        vp.copy_(torch.randn(vp.shape, device="cuda").to(torch.bfloat16))
+    keys = [_vals(kp) for kp in state.k_pool]
+    values = [_vals(vp) for vp in state.v_pool]
+    model = _oracle_model(torch, do, orc, weights)
+    engine = PersistentDecode(weights, state)
+    tok, slot, pos = 77, 1, 66
+    for step in range(2):
+        state.set_requests([tok], [slot], [pos])
+        got = engine.step().cpu().numpy().astype(np.float64)
+        assert not engine.failed()
+        ref = do.decode_step(model, keys, values, [tok], [slot], [pos], round_bf16=True)
+        rel = np.abs(got - ref).max() / np.abs(ref).max()
+        assert rel <= 1e-2, (step, rel)
+        tok, pos = int(np.argmax(got[0])), pos + 1
+
+
+def test_decode_program_matches_decode_step_qwen3_4b_shapes(env):
+    """Two Qwen3-4B-shaped layers with the full 151,936-token head and a 512-token
+    context, at the first and a later position."""
+    torch, n, orc = env
+    from ironmule_amd.decode import DecoderConfig, random_weights
+    announce("persistent decode, qwen3-4b shapes, 2 layers")
+    cfg = DecoderConfig(layers=2)
+    weights = random_weights(cfg, "cuda", seed=9)
+    engine, state = _compare_steps(torch, weights, cfg, 520,
+                                   [(11, 0, 512), (151935, 0, 513), (7, 2, 0)], seed=3)
+    info = engine.program.info()
+    assert info["stages"] == 2 * 5 + 1 and info["workgroups"] >= 256
+
+
+def test_decode_program_replays_in_a_graph(env):
+    """Captured in a HIP graph (embedding, counter reset, persistent kernel) and replayed:
+    every replay gives the eager result's bits, with eager work between replays."""
+    torch, n, orc = env
+    from ironmule_amd.decode import PersistentDecode, random_weights
+    announce("persistent decode in a graph")
+    cfg = _tiny()
+    weights = random_weights(cfg, "cuda", seed=12)
+    ref, per = _twin_states(torch, cfg, 80, seed=4)
+    engine = PersistentDecode(weights, per)
+    per.set_requests([9], [0], [40])
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        first = engine.step(stream=stream).clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        engine.step(stream=stream)
+    for _ in range(3):
+        per.logits.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(per.logits, first)
+        assert not engine.failed()
+
+
+def test_decode_program_refuses_unsupported_descriptions(env):
+    torch, n, orc = env
+    from dataclasses import replace
+
+    from ironmule_amd.decode import DecodeState, PersistentDecode, random_weights
+    announce("persistent decode refusals")
+    cfg = _tiny()
+    weights = random_weights(cfg, "cuda", seed=1)
+    with pytest.raises(ValueError, match="batch 1"):
+        PersistentDecode(weights, DecodeState(cfg, batch=2, slots=2, capacity=16, max_len=16,
+                                              device="cuda"))
+    state = DecodeState(cfg, batch=1, slots=1, capacity=16, max_len=16, device="cuda")
+    for bad in (replace(cfg, hidden=100), replace(cfg, kv_heads=3), replace(cfg, heads=40)):
+        with pytest.raises(n.NativeError) as err:
+            n.decode_program(bad, weights.layers, weights.norm, weights.embed, state.k_pool,
+                             state.v_pool, state.positions, state.slot_ids, state.h,
+                             state.logits, 16)
+        assert err.value.code == n.IMQ_EINVAL
