@@ -101,8 +101,13 @@ typedef struct {
 IMQ_API int32_t imq_qmv_program_create(const imq_qmv_stage* stages, int32_t count,
                                        imq_program** out);
 
-/* Enqueues one run of the program on `stream`. */
+/* Enqueues one run of the program on `stream`: every stage in one persistent launch. */
 IMQ_API int32_t imq_program_launch(imq_program* program, void* stream);
+
+/* Enqueues one run of the program on `stream` as one launch per stage (each workgroup
+ * runs one task, the stream order replaces the waits); the same results as
+ * imq_program_launch, bit for bit. */
+IMQ_API int32_t imq_program_launch_staged(imq_program* program, void* stream);
 
 /* Waits for the device, then sets *failed to 1 if a run since the last call stopped on
  * a bounded wait (0 otherwise) and clears the flag. */

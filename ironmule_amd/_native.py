@@ -118,6 +118,7 @@ _SIGNATURES = {
     "imq_decode_program_create": ([ctypes.POINTER(StepDesc), ctypes.POINTER(_P)], _I32),
     "imq_qmv_program_create": ([ctypes.POINTER(QmvStage), _I32, ctypes.POINTER(_P)], _I32),
     "imq_program_launch": ([_P, _P], _I32),
+    "imq_program_launch_staged": ([_P, _P], _I32),
     "imq_program_status": ([_P, ctypes.POINTER(_I32)], _I32),
     "imq_program_info": ([_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32), ctypes.POINTER(_I32),
                           ctypes.POINTER(_I32)], _I32),
@@ -448,9 +449,11 @@ class Program:
             raise ValueError("the program is closed")
         return self._handle
 
-    def launch(self, stream=None) -> None:
-        """Enqueue one run on `stream` (capturable in a HIP graph)."""
-        _check(lib().imq_program_launch(self.handle, _stream(stream)))
+    def launch(self, stream=None, staged: bool = False) -> None:
+        """Enqueue one run on `stream` (capturable in a HIP graph): one persistent launch,
+        or with `staged` one launch per stage."""
+        fn = lib().imq_program_launch_staged if staged else lib().imq_program_launch
+        _check(fn(self.handle, _stream(stream)))
 
     def failed(self) -> bool:
         """Synchronises the device; True if a run since the last call stopped on a bounded

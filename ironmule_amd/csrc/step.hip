@@ -107,6 +107,8 @@ struct StepArgs {
   uint32_t* status;
   int32_t ntasks;
   int32_t sub_stride;  // counters between the same sub-counter of consecutive stages
+  int32_t staged;      // 1: one launch per stage (stream order replaces the waits)
+  int32_t pad;
 };
 
 __device__ __forceinline__ float bf(uint32_t h) { return bf16_bits_to_f32(h); }
@@ -203,51 +205,69 @@ struct QLds {
 constexpr size_t kNormRed = (size_t)kMaxHidden * 4;
 constexpr size_t kNormBytes = kNormRed + 16;
 
-// x for the tile from a bf16 row (sc1: it may have been written in this launch).  Pieces
-// past the row lie past the buffer and read as zero.
-template <int XR>
-__device__ __forceinline__ void fetch_x(const uint16_t* x, int K, int tid, uint4 (&xs)[XR]) {
-  const __amdgpu_buffer_rsrc_t r = buffer_rsrc(x, (uint32_t)K * 2u);
-#pragma unroll
-  for (int t = 0; t < XR; ++t) xs[t] = load_b128_sc1(r, 16u * (tid + kThreads * t));
+// Loads that may see data written earlier in the same launch use sc1 (`kSc1` true);
+// in a staged launch the previous stage ended with its kernel, and plain loads do.
+template <bool kSc1Load>
+__device__ __forceinline__ uint4 load_act(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return kSc1Load ? load_b128_sc1(r, off) : load_b128(r, off);
 }
 
-// x = bf16(rms_norm(h) * w) for the tile, in the order of add_rmsnorm_kernel (thread t
-// sums the squares of h[t + 256 i] in increasing i, then the wavefront butterfly, then
-// the four wavefronts as (w0 + w1) + (w2 + w3)).  The row of h goes through LDS so that
-// each thread can then form its own 8-value pieces; values past the row read as zero.
-template <int XR>
-__device__ __forceinline__ void norm_x(const float* h, const uint16_t* nw, int K, float eps,
-                                       int tid, float* hl, float* red, uint4 (&xs)[XR]) {
+// x for the tile from a bf16 row.  Pieces past the row lie past the buffer and read as
+// zero.
+template <int XR, bool kSc1Load>
+__device__ __forceinline__ void load_x(const uint16_t* x, int K, int tid, uint4 (&xs)[XR]) {
+  const __amdgpu_buffer_rsrc_t r = buffer_rsrc(x, (uint32_t)K * 2u);
+#pragma unroll
+  for (int t = 0; t < XR; ++t) xs[t] = load_act<kSc1Load>(r, 16u * (tid + kThreads * t));
+}
+
+// The fp32 row of h as each thread's own 8-value pieces (values 8i .. 8i+7 of piece
+// i = tid + 256 t; zeros past the row).
+template <int XR, bool kSc1Load>
+__device__ __forceinline__ void load_h(const float* h, int K, int tid, uint4 (&h0)[XR],
+                                       uint4 (&h1)[XR]) {
   const __amdgpu_buffer_rsrc_t hr = buffer_rsrc(h, (uint32_t)K * 4u);
+#pragma unroll
+  for (int t = 0; t < XR; ++t) {
+    const uint32_t off = 32u * (tid + kThreads * t);
+    h0[t] = load_act<kSc1Load>(hr, off);
+    h1[t] = load_act<kSc1Load>(hr, off + 16u);
+  }
+}
+
+// x = bf16(rms_norm(h) * w) for the tile from the pieces of h and of the norm weight,
+// with the sum of squares in the order of add_rmsnorm_kernel (thread t adds the squares
+// of h[t + 256 i] in increasing i, then the wavefront butterfly, then the four
+// wavefronts as (w0 + w1) + (w2 + w3)): the row goes through LDS for the strided sums.
+template <int XR>
+__device__ __forceinline__ void norm_x(const uint4 (&h0)[XR], const uint4 (&h1)[XR],
+                                       const uint4 (&wn)[XR], int K, float eps, int tid,
+                                       float* hl, float* red, uint4 (&xs)[XR]) {
+#pragma unroll
+  for (int t = 0; t < XR; ++t) {
+    uint4* dst = reinterpret_cast<uint4*>(hl) + 2 * (tid + kThreads * t);
+    dst[0] = h0[t];
+    dst[1] = h1[t];
+  }
+  lds_barrier();
   float ss = 0.0f;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    float v[kNormVpt / 2];
-#pragma unroll
-    for (int i = 0; i < kNormVpt / 2; ++i)
-      v[i] = __uint_as_float(load_b32_sc1(hr, 4u * (tid + kThreads * (i + half * kNormVpt / 2))));
-#pragma unroll
-    for (int i = 0; i < kNormVpt / 2; ++i) {
-      const int idx = tid + kThreads * (i + half * kNormVpt / 2);
-      if (idx < K) ss = fmaf(v[i], v[i], ss);
-      hl[idx] = v[i];
-    }
+  for (int i = 0; i < kNormVpt; ++i) {
+    const int idx = tid + kThreads * i;
+    if (idx < K) ss = fmaf(hl[idx], hl[idx], ss);
   }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   lds_barrier();
   const float total = (red[0] + red[1]) + (red[2] + red[3]);
   const float inv = 1.0f / sqrtf(total / (float)K + eps);
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(nw, (uint32_t)K * 2u);
 #pragma unroll
   for (int t = 0; t < XR; ++t) {
-    const int i = tid + kThreads * t;  // piece i: values 8i .. 8i+7 (zeros past the row)
-    const uint4 w8 = load_b128(wr, 16u * i);
-    const uint32_t ww[4] = {w8.x, w8.y, w8.z, w8.w};
-    const float4 h0 = reinterpret_cast<const float4*>(hl)[2 * i];
-    const float4 h1 = reinterpret_cast<const float4*>(hl)[2 * i + 1];
-    const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    const uint32_t ww[4] = {wn[t].x, wn[t].y, wn[t].z, wn[t].w};
+    const float hv[8] = {__uint_as_float(h0[t].x), __uint_as_float(h0[t].y),
+                         __uint_as_float(h0[t].z), __uint_as_float(h0[t].w),
+                         __uint_as_float(h1[t].x), __uint_as_float(h1[t].y),
+                         __uint_as_float(h1[t].z), __uint_as_float(h1[t].w)};
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -261,8 +281,12 @@ __device__ __forceinline__ void norm_x(const float* h, const uint16_t* nw, int K
 // One qmv task: one tile of one problem (tiles are numbered across the stage's
 // problems), or for a SiLU*up pair stage one tile of the gate/up pair, whose rows 0-7
 // are gate rows and rows 8-15 the same up rows (wavefronts 0-1 and 2-3).
-template <int NCH, int XR, int XSRC, int EPI>
-__device__ __forceinline__ bool qmv_task(StageRef S, int task, const StepArgs& a, uint4* smem) {
+//
+// The persistent form (kStaged false) issues the weight loads first and then waits for its
+// input stage; a staged launch (kStaged true) has its inputs ready, and issues their loads
+// first so that staging x overlaps the weight stream (loads return in issue order).
+template <int NCH, int XR, int XSRC, int EPI, bool kStaged, typename SRef>
+__device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, uint4* smem) {
   using L = QLds<NCH, XR>;
   constexpr int CP = L::kChunks, SBR = L::kSbr;
   constexpr bool kPair = EPI == kEpiSiluPair;
@@ -289,6 +313,33 @@ __device__ __forceinline__ bool qmv_task(StageRef S, int task, const StepArgs& a
   float* sx = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kSx);
   uint32_t* sbl = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(smem) + L::kSb);
   const uint32_t magic = in_vgpr(kMagic);
+
+  // the activation inputs: x, or the row of h and the norm weight; a residual stage also
+  // reads its rows of h (final once the input stage is done)
+  const bool owner = j == 0 && row < N;
+  constexpr int HX = XSRC == kXNorm ? XR : 1;
+  uint4 xs[XR], h0[HX], h1[HX], wn[HX];
+  float hres = 0.0f;
+  auto load_inputs = [&]() {
+    if constexpr (XSRC == kXNorm)
+      load_h<XR, !kStaged>(S.h, K, tid, h0, h1);
+    else
+      load_x<XR, !kStaged>(S.x, K, tid, xs);
+    if constexpr (EPI == kEpiResidual) {
+      if (owner) hres = kStaged ? S.h[row] : ldf_sc1(S.h + row);
+    }
+  };
+  auto load_norm_weight = [&]() {
+    if constexpr (XSRC == kXNorm) {
+      const __amdgpu_buffer_rsrc_t nr = buffer_rsrc(S.norm_w, (uint32_t)K * 2u);
+#pragma unroll
+      for (int t = 0; t < XR; ++t) wn[t] = load_b128(nr, 16u * (tid + kThreads * t));
+    }
+  };
+  if constexpr (kStaged) {
+    load_inputs();
+    load_norm_weight();
+  }
 
   // the tile's (scale, bias) span (a pair tile: threads 0-127 the 8 gate rows, 128-255
   // the 8 up rows), rounded up to whole dwords (the extra half lies in the same aligned
@@ -317,14 +368,14 @@ __device__ __forceinline__ bool qmv_task(StageRef S, int task, const StepArgs& a
     wv[i] = load_b128(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
   }
 
-  if (S.wait >= 0 && !wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
-
-  uint4 xs[XR];
-  if (XSRC == kXNorm)
-    norm_x<XR>(S.h, S.norm_w, K, S.eps, tid, reinterpret_cast<float*>(smem),
+  if constexpr (!kStaged) {
+    load_norm_weight();
+    if (S.wait >= 0 && !wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
+    load_inputs();
+  }
+  if constexpr (XSRC == kXNorm)
+    norm_x<XR>(h0, h1, wn, K, S.eps, tid, reinterpret_cast<float*>(smem),
                reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + kNormRed), xs);
-  else
-    fetch_x<XR>(S.x, K, tid, xs);
 #pragma unroll
   for (int t = 0; t < XR; ++t) {
     const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
@@ -366,13 +417,12 @@ __device__ __forceinline__ bool qmv_task(StageRef S, int task, const StepArgs& a
   if (sh >= 5) v += __shfl_xor(v, 16);
   if (sh >= 6) v += __shfl_xor(v, 32);
 
-  const bool owner = j == 0 && row < N;
   if (EPI == kEpiBf16) {
     if (owner) store_b16_sc1(buffer_rsrc(S.p[qi].y, (uint32_t)N * 2u), 2u * row, to_bf(v));
   } else if (EPI == kEpiF32) {
     if (owner) static_cast<float*>(S.p[qi].y)[row] = v;
   } else if (EPI == kEpiResidual) {
-    if (owner) stf_sc1(S.h + row, ldf_sc1(S.h + row) + bf(to_bf(v)));
+    if (owner) stf_sc1(S.h + row, hres + bf(to_bf(v)));
   } else {  // SiLU * up: the up rows hand their values to the gate rows
     float* pairx = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kPair);
     if (j == 0 && rl >= 8) pairx[rl - 8] = v;
@@ -416,7 +466,8 @@ __device__ __forceinline__ uint16_t ld16_sc1(const uint16_t* base, uint32_t byte
   return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(base, bytes), off, 0, kSc1);
 }
 
-__device__ __forceinline__ bool attention_task(StageRef S, int task, const StepArgs& a, uint4* smem) {
+template <typename SRef>
+__device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs& a, uint4* smem) {
   AttnLds& L = *reinterpret_cast<AttnLds*>(smem);
   const int splits = S.splits, Hkv = S.Hkv, Hq = S.Hq, G = Hq / Hkv;
   const int s = task % splits, kvh = (task / splits) % Hkv, b = task / (splits * Hkv);
@@ -452,9 +503,10 @@ __device__ __forceinline__ bool attention_task(StageRef S, int task, const StepA
   };
   uint4 k0 = load_b128(krs, chunk_off(first, 0)), k1 = load_b128(krs, chunk_off(first, 1));
   uint4 k2 = load_b128(krs, chunk_off(first, 2)), k3 = load_b128(krs, chunk_off(first, 3));
+  if (!a.staged && !wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
+  // the first chunk's values: in flight while q and the new key are rotated
   uint4 v0 = load_b128(vrs, chunk_off(first, 0)), v1 = load_b128(vrs, chunk_off(first, 1));
   uint4 v2 = load_b128(vrs, chunk_off(first, 2)), v3 = load_b128(vrs, chunk_off(first, 3));
-  if (!wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
 
   // rotated q heads (wavefront per head) and, on wavefront 0, the new key and value
   const float eps = S.eps;
@@ -540,15 +592,19 @@ __device__ __forceinline__ bool attention_task(StageRef S, int task, const StepA
       k2 = load_b128(krs, chunk_off(start + kChunk, 2));
       k3 = load_b128(krs, chunk_off(start + kChunk, 3));
     }
+    // q is re-read from LDS every chunk (an opaque zero offset keeps the compiler from
+    // holding a head's 16 q vectors in registers across the chunk loop)
+    int qoff = 0;
+    asm volatile("" : "+s"(qoff));
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int g = wave + 4 * r;
       if (g < G) {
-        const uint4* qv = reinterpret_cast<const uint4*>(L.qs[g]);
+        const uint4* qv = reinterpret_cast<const uint4*>(L.qs[g]) + qoff;
         float sc = -INFINITY;
         if (lane < count) {
           float d = 0.0f;
-#pragma unroll
+#pragma unroll 2
           for (int jj = 0; jj < 16; ++jj) {
             const uint4 qa = qv[jj], kk = L.kv[lane][jj];
             d = dot2(qa.x, kk.x, d);
@@ -658,13 +714,33 @@ __device__ __forceinline__ bool attention_task(StageRef S, int task, const StepA
 // One qmv instantiation per (x source, epilogue, tile shape) that a program can hold.
 #define IMQ_QMV_CASE(NCH, XR, XSRC, EPI, SHAPE)                   \
   case (XSRC) * 16 + (EPI) * 4 + (SHAPE):                          \
-    good = qmv_task<NCH, XR, XSRC, EPI>(S, task, a, smem);         \
+    good = qmv_task<NCH, XR, XSRC, EPI, false, StageRef>(S, task, a, smem); \
     break;
 #define IMQ_QMV_SHAPES_X2(XSRC, EPI)         \
   IMQ_QMV_CASE(2, 2, XSRC, EPI, kShape22)    \
   IMQ_QMV_CASE(5, 2, XSRC, EPI, kShape52)    \
   IMQ_QMV_CASE(8, 2, XSRC, EPI, kShape82)
 
+__device__ __forceinline__ bool run_task(StageRef S, int task, const StepArgs& a, uint4* smem) {
+  bool good = false;
+  if (S.kind == kKindAttention) {
+    good = attention_task<StageRef>(S, task, a, smem);
+  } else {
+    switch (S.xsrc * 16 + S.epi * 4 + S.shape) {
+      IMQ_QMV_SHAPES_X2(kXVector, kEpiBf16)
+      IMQ_QMV_CASE(5, 5, kXVector, kEpiBf16, kShape55)
+      IMQ_QMV_SHAPES_X2(kXVector, kEpiResidual)
+      IMQ_QMV_CASE(5, 5, kXVector, kEpiResidual, kShape55)
+      IMQ_QMV_SHAPES_X2(kXNorm, kEpiBf16)
+      IMQ_QMV_SHAPES_X2(kXNorm, kEpiSiluPair)
+      IMQ_QMV_SHAPES_X2(kXNorm, kEpiF32)
+      default: break;  // the host plans only the cases above
+    }
+  }
+  return good;
+}
+
+// The persistent form: every stage in one launch.
 __global__ __launch_bounds__(kThreads) void step_kernel(const Stage* __restrict__ stages,
                                                         StepArgs a) {
   extern __shared__ uint4 smem[];
@@ -673,24 +749,25 @@ __global__ __launch_bounds__(kThreads) void step_kernel(const Stage* __restrict_
     while (t >= stages[si].first + stages[si].count) ++si;
     StageRef S = global_stage(stages + si);
     const int task = t - S.first;
-    bool good = false;
-    if (S.kind == kKindAttention) {
-      good = attention_task(S, task, a, smem);
-    } else {
-      switch (S.xsrc * 16 + S.epi * 4 + S.shape) {
-        IMQ_QMV_SHAPES_X2(kXVector, kEpiBf16)
-        IMQ_QMV_CASE(5, 5, kXVector, kEpiBf16, kShape55)
-        IMQ_QMV_SHAPES_X2(kXVector, kEpiResidual)
-        IMQ_QMV_CASE(5, 5, kXVector, kEpiResidual, kShape55)
-        IMQ_QMV_SHAPES_X2(kXNorm, kEpiBf16)
-        IMQ_QMV_SHAPES_X2(kXNorm, kEpiSiluPair)
-        IMQ_QMV_SHAPES_X2(kXNorm, kEpiF32)
-        default: break;  // the host plans only the cases above
-      }
-    }
-    if (!good) return;
+    if (!run_task(S, task, a, smem)) return;
     signal(counter(a, si, task % kSub));
   }
+}
+
+// The staged form: one launch per stage, one task per workgroup, the launches' stream
+// order standing in for the waits.  Each stage gets the kernel of its own task variant, so
+// it carries only that variant's registers.
+// The stage descriptor is a kernel argument here, so its fields arrive with the
+// argument block instead of a second dependent load.
+template <int NCH, int XR, int XSRC, int EPI>
+__global__ __launch_bounds__(kThreads) void qmv_stage_kernel(const Stage S, StepArgs a) {
+  extern __shared__ uint4 smem[];
+  qmv_task<NCH, XR, XSRC, EPI, true, const Stage&>(S, blockIdx.x, a, smem);
+}
+
+__global__ __launch_bounds__(kThreads) void attention_stage_kernel(const Stage S, StepArgs a) {
+  extern __shared__ uint4 smem[];
+  attention_task<const Stage&>(S, blockIdx.x, a, smem);
 }
 
 #undef IMQ_QMV_SHAPES_X2
@@ -748,6 +825,7 @@ int32_t check_qweight(const imq_qweight& q, int64_t N, int64_t K, const char* wh
 
 struct imq_program {
   int device = -1;
+  std::vector<size_t> stage_lds;  // LDS bytes of each stage's staged launch
   std::vector<Stage> stages;
   Stage* d_stages = nullptr;
   uint32_t* d_words = nullptr;  // completion counters, then combine counters, then status
@@ -817,11 +895,17 @@ int32_t add_qmv_stage(imq_program* prog, const std::vector<QProb>& probs, int xs
 int32_t finish_program(imq_program* prog) {
   const int nstages = (int)prog->stages.size();
   if (nstages == 0 || prog->ntasks == 0) return fail(IMQ_EINVAL, "empty program");
-  size_t lds = sizeof(AttnLds);
-  for (const Stage& S : prog->stages)
-    if (S.kind == kKindQmv)
-      lds = std::max(lds, std::max(lds_bytes_for(S.shape), S.xsrc == kXNorm ? kNormBytes : 0));
+  size_t lds = 0;
+  prog->stage_lds.clear();
+  for (const Stage& S : prog->stages) {
+    const size_t b = S.kind == kKindQmv
+                         ? std::max(lds_bytes_for(S.shape), S.xsrc == kXNorm ? kNormBytes : 0)
+                         : sizeof(AttnLds);
+    prog->stage_lds.push_back((b + 15) & ~(size_t)15);
+    lds = std::max(lds, b);
+  }
   prog->lds = (lds + 15) & ~(size_t)15;
+
   // counters: kSub lines per stage; the same sub-counter of consecutive stages are
   // neighbours, and consecutive sub-counters of one stage >= 4 KiB apart
   prog->sub_stride = std::max(nstages, 32);
@@ -1080,10 +1164,63 @@ int32_t imq_program_launch(imq_program* p, void* stream) {
   a.status = p->d_status;
   a.ntasks = p->ntasks;
   a.sub_stride = p->sub_stride;
+  a.staged = 0;
+  a.pad = 0;
   hipLaunchKernelGGL(step_kernel, dim3(p->grid), dim3(kThreads), p->lds, st,
                      static_cast<const Stage*>(p->d_stages), a);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("persistent launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+int32_t imq_program_launch_staged(imq_program* p, void* stream) {
+  if (!p) return fail(IMQ_EINVAL, "null program");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
+    return fail(IMQ_EINVAL, "the program was created on another device");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = p->reset_words;
+  hipLaunchKernelGGL(reset_kernel, dim3((uint32_t)((n + kThreads - 1) / kThreads)), dim3(kThreads),
+                     0, st, p->d_words, n);
+  StepArgs a;
+  a.done = p->d_words;
+  a.status = p->d_status;
+  a.ntasks = p->ntasks;
+  a.sub_stride = p->sub_stride;
+  a.staged = 1;
+  a.pad = 0;
+  for (size_t i = 0; i < p->stages.size(); ++i) {
+    const Stage& S = p->stages[i];
+    const dim3 grid(S.count), block(kThreads);
+    const size_t lds = p->stage_lds[i];
+    if (S.kind == kKindAttention) {
+      hipLaunchKernelGGL(attention_stage_kernel, grid, block, lds, st, S, a);
+      continue;
+    }
+#define IMQ_STAGE_CASE(NCH, XR, XSRC, EPI, SHAPE)                                              \
+  case (XSRC) * 16 + (EPI) * 4 + (SHAPE):                                                   \
+    hipLaunchKernelGGL((qmv_stage_kernel<NCH, XR, XSRC, EPI>), grid, block, lds, st, S, a);   \
+    break;
+#define IMQ_STAGE_SHAPES_X2(XSRC, EPI)      \
+  IMQ_STAGE_CASE(2, 2, XSRC, EPI, kShape22) \
+  IMQ_STAGE_CASE(5, 2, XSRC, EPI, kShape52) \
+  IMQ_STAGE_CASE(8, 2, XSRC, EPI, kShape82)
+    switch (S.xsrc * 16 + S.epi * 4 + S.shape) {
+      IMQ_STAGE_SHAPES_X2(kXVector, kEpiBf16)
+      IMQ_STAGE_CASE(5, 5, kXVector, kEpiBf16, kShape55)
+      IMQ_STAGE_SHAPES_X2(kXVector, kEpiResidual)
+      IMQ_STAGE_CASE(5, 5, kXVector, kEpiResidual, kShape55)
+      IMQ_STAGE_SHAPES_X2(kXNorm, kEpiBf16)
+      IMQ_STAGE_SHAPES_X2(kXNorm, kEpiSiluPair)
+      IMQ_STAGE_SHAPES_X2(kXNorm, kEpiF32)
+      default:
+        return fail(IMQ_EUNSUPPORTED, "stage variant without a kernel");
+    }
+#undef IMQ_STAGE_SHAPES_X2
+#undef IMQ_STAGE_CASE
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("stage launch failed: ") + hipGetErrorString(e));
   return ok();
 }
 

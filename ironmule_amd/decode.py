@@ -179,14 +179,17 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
 
 
 class PersistentDecode:
-    """The batch-1 decode step as a persistent program: `step()` launches the embedding and
-    the program (imq_decode_program_create) and returns state.logits.  Same inputs, same
-    bits as `decode_step`."""
+    """The batch-1 decode step as a program of fused stages (imq_decode_program_create):
+    `step()` launches the embedding and the program and returns state.logits.  With
+    `staged` each stage is its own launch (5 per layer: q/k/v with the RMSNorm, attention
+    with q/k norm + rotary + KV write + the split merge, o with the residual add, gate/up
+    with the RMSNorm and SiLU * up, down with the residual add); otherwise one persistent
+    launch runs them all.  Same inputs, same bits as `decode_step`."""
 
-    def __init__(self, weights: DecoderWeights, state: DecodeState) -> None:
+    def __init__(self, weights: DecoderWeights, state: DecodeState, staged: bool = False) -> None:
         if state.batch != 1:
             raise ValueError("the persistent decode step runs batch 1")
-        self.weights, self.state = weights, state
+        self.weights, self.state, self.staged = weights, state, staged
         self.program = _native.decode_program(
             weights.config, weights.layers, weights.norm, weights.embed, state.k_pool,
             state.v_pool, state.positions, state.slot_ids, state.h, state.logits, state.max_len)
@@ -194,7 +197,7 @@ class PersistentDecode:
     def step(self, stream=None) -> torch.Tensor:
         w, s = self.weights, self.state
         _native.embed(*w.embed, s.tokens, s.h, stream=stream)
-        self.program.launch(stream)
+        self.program.launch(stream, staged=self.staged)
         return s.logits
 
     def failed(self) -> bool:

@@ -68,8 +68,8 @@ def test_qmv_program_chain_matches_per_kernel_calls(env, shapes):
     x0, x1 = _row(torch, shapes["k0"], 1), _row(torch, shapes["k1"], 2)
     prog = n.qmv_program([(wa, x0, ya, False), (wb, ya[0], yb, True), (wc, x1, yc, False),
                           (wd, yc[0], yd, True)])
-    for run in range(2):
-        prog.launch()
+    for run in range(4):
+        prog.launch(staged=run % 2 == 1)
         torch.cuda.synchronize()
         assert not prog.failed()
         for ws, x, ys in ((wa, x0, ya), (wb, ya[0], yb), (wc, x1, yc), (wd, yc[0], yd)):
@@ -99,12 +99,12 @@ def _twin_states(torch, cfg, capacity, seed):
     return a, b
 
 
-def _compare_steps(torch, weights, cfg, capacity, requests, seed):
-    """Runs decode_step on one state and the persistent step on a twin for each request
+def _compare_steps(torch, weights, cfg, capacity, requests, seed, staged=False):
+    """Runs decode_step on one state and the program's step on a twin for each request
     (token, slot, position) in turn; logits, h and every KV pool must agree bit for bit."""
     from ironmule_amd.decode import PersistentDecode, decode_step
     ref, per = _twin_states(torch, cfg, capacity, seed)
-    engine = PersistentDecode(weights, per)
+    engine = PersistentDecode(weights, per, staged=staged)
     for step, (tok, slot, pos) in enumerate(requests):
         ref.set_requests([tok], [slot], [pos])
         per.set_requests([tok], [slot], [pos])
@@ -120,15 +120,16 @@ def _compare_steps(torch, weights, cfg, capacity, requests, seed):
     return engine, per
 
 
-def test_decode_program_matches_decode_step_tiny(env):
+@pytest.mark.parametrize("staged", [False, True])
+def test_decode_program_matches_decode_step_tiny(env, staged):
     torch, n, orc = env
     from ironmule_amd.decode import random_weights
-    announce("persistent decode, tiny decoder")
+    announce("program decode, tiny decoder, staged", staged)
     cfg = _tiny()
     weights = random_weights(cfg, "cuda", seed=5)
     # first token of a slot, a chunk boundary, the last position, then a continuing request
     _compare_steps(torch, weights, cfg, 80, [(5, 1, 0), (17, 0, 63), (300, 2, 64), (511, 2, 79),
-                                             (42, 1, 1)], seed=11)
+                                             (42, 1, 1)], seed=11, staged=staged)
 
 
 def test_decode_program_tiny_against_the_oracle(env):
@@ -160,30 +161,33 @@ def test_decode_program_tiny_against_the_oracle(env):
         tok, pos = int(np.argmax(got[0])), pos + 1
 
 
-def test_decode_program_matches_decode_step_qwen3_4b_shapes(env):
+@pytest.mark.parametrize("staged", [False, True])
+def test_decode_program_matches_decode_step_qwen3_4b_shapes(env, staged):
     """Two Qwen3-4B-shaped layers with the full 151,936-token head and a 512-token
     context, at the first and a later position."""
     torch, n, orc = env
     from ironmule_amd.decode import DecoderConfig, random_weights
-    announce("persistent decode, qwen3-4b shapes, 2 layers")
+    announce("program decode, qwen3-4b shapes, 2 layers, staged", staged)
     cfg = DecoderConfig(layers=2)
     weights = random_weights(cfg, "cuda", seed=9)
     engine, state = _compare_steps(torch, weights, cfg, 520,
-                                   [(11, 0, 512), (151935, 0, 513), (7, 2, 0)], seed=3)
+                                   [(11, 0, 512), (151935, 0, 513), (7, 2, 0)], seed=3,
+                                   staged=staged)
     info = engine.program.info()
     assert info["stages"] == 2 * 5 + 1 and info["workgroups"] >= 256
 
 
-def test_decode_program_replays_in_a_graph(env):
-    """Captured in a HIP graph (embedding, counter reset, persistent kernel) and replayed:
-    every replay gives the eager result's bits, with eager work between replays."""
+@pytest.mark.parametrize("staged", [False, True])
+def test_decode_program_replays_in_a_graph(env, staged):
+    """Captured in a HIP graph (embedding, counter reset, the program's launches) and
+    replayed: every replay gives the eager result's bits, with eager work between."""
     torch, n, orc = env
     from ironmule_amd.decode import PersistentDecode, random_weights
-    announce("persistent decode in a graph")
+    announce("program decode in a graph, staged", staged)
     cfg = _tiny()
     weights = random_weights(cfg, "cuda", seed=12)
     ref, per = _twin_states(torch, cfg, 80, seed=4)
-    engine = PersistentDecode(weights, per)
+    engine = PersistentDecode(weights, per, staged=staged)
     per.set_requests([9], [0], [40])
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
