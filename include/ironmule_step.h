@@ -119,6 +119,44 @@ IMQ_API int32_t imq_program_info(const imq_program* program, int32_t* tasks, int
 
 IMQ_API void imq_program_destroy(imq_program* program);
 
+
+/* ------------------------------------------------------------------ streaming engine
+ *
+ * A chain of one-row 4-bit qmv stages (imq_qmv_stage, as for imq_qmv_program_create)
+ * run by ONE persistent launch that streams the weights of every stage: each wavefront
+ * of the grid takes every V-th tile of the program (V wavefronts) and keeps the next
+ * tile's loads in flight while it computes the current one.
+ *   * With no wait_previous anywhere the stages are independent: their distinct x rows
+ *     (at most 8, 64 KiB staged) are read once per workgroup at the start and the
+ *     wavefronts stream from the first stage to the last with no barrier or wait.
+ *   * With waits, every workgroup enters the stages in order, issuing its weight loads
+ *     for a stage before waiting for that stage's input; the grid is then limited to the
+ *     workgroups the device keeps resident at once, no other kernel may run on the device
+ *     during the launch, and every wait is bounded (imq_stream_status reports a stall).
+ * Each output element is the value imq_qmv computes for the same inputs, bit for bit.
+ * `workgroups` <= 0 picks the resident maximum.  Creation allocates the program's device
+ * tables (hipMalloc); a launch allocates nothing and can be captured in a HIP graph.
+ * Replaces a sequence of qmv launches (ironmule/qmv_k3840.py:299-310, the grouped form
+ * of ironmule/fast.py:186-215, and the chained weights of the reference's bandwidth
+ * measurement, ironmule/hw.py:441-473). */
+typedef struct imq_stream imq_stream; /* opaque */
+
+IMQ_API int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t workgroups,
+                                  imq_stream** out);
+
+/* Enqueues one run on `stream` (for a chained program: a counter reset, then the kernel). */
+IMQ_API int32_t imq_stream_launch(imq_stream* program, void* stream);
+
+/* Waits for the device; *failed = 1 if a run since the last call stopped on a bounded
+ * wait (then clears the flag). */
+IMQ_API int32_t imq_stream_status(imq_stream* program, int32_t* failed);
+
+/* Tiles, stages, workgroups, LDS bytes per workgroup, and 1 if the stages are chained. */
+IMQ_API int32_t imq_stream_info(const imq_stream* program, int32_t* tiles, int32_t* stages,
+                                int32_t* workgroups, int32_t* lds_bytes, int32_t* chained);
+
+IMQ_API void imq_stream_destroy(imq_stream* program);
+
 #ifdef __cplusplus
 }
 #endif

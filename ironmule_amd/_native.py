@@ -123,6 +123,13 @@ _SIGNATURES = {
     "imq_program_info": ([_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32), ctypes.POINTER(_I32),
                           ctypes.POINTER(_I32)], _I32),
     "imq_program_destroy": ([_P], None),
+    # streaming engine (include/ironmule_step.h)
+    "imq_stream_create": ([ctypes.POINTER(QmvStage), _I32, _I32, ctypes.POINTER(_P)], _I32),
+    "imq_stream_launch": ([_P, _P], _I32),
+    "imq_stream_status": ([_P, ctypes.POINTER(_I32)], _I32),
+    "imq_stream_info": ([_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32), ctypes.POINTER(_I32),
+                         ctypes.POINTER(_I32), ctypes.POINTER(_I32)], _I32),
+    "imq_stream_destroy": ([_P], None),
 }
 
 
@@ -485,10 +492,9 @@ def _qweight(w, s, b) -> QWeight:
     return QWeight(w.data_ptr(), s.data_ptr(), b.data_ptr())
 
 
-def qmv_program(stages: list[tuple[list, torch.Tensor, list, bool]]) -> Program:
-    """A chain of one-row qmv stages, each (weights, x, outs, wait_previous): `weights`
-    1-3 (w, scales, biases) triples sharing the bf16 row `x` (K,), `outs` their bf16 (N,)
-    outputs; a stage with wait_previous starts after the previous one has finished."""
+def _qmv_stages(stages: list[tuple[list, torch.Tensor, list, bool]]):
+    """The imq_qmv_stage array of a chain of one-row qmv stages, and the tensors it
+    points at."""
     if not stages:
         raise ValueError("a program needs at least one stage")
     arr = (QmvStage * len(stages))()
@@ -510,9 +516,75 @@ def qmv_program(stages: list[tuple[list, torch.Tensor, list, bool]]) -> Program:
                                          kk, y.data_ptr(), n, n, kk)
             keep += [w, s, b, y]
         keep.append(x)
+    return arr, keep
+
+
+def qmv_program(stages: list[tuple[list, torch.Tensor, list, bool]]) -> Program:
+    """A chain of one-row qmv stages, each (weights, x, outs, wait_previous): `weights`
+    1-3 (w, scales, biases) triples sharing the bf16 row `x` (K,), `outs` their bf16 (N,)
+    outputs; a stage with wait_previous starts after the previous one has finished."""
+    arr, keep = _qmv_stages(stages)
     handle = _P()
     _check(lib().imq_qmv_program_create(arr, len(stages), ctypes.byref(handle)))
     return Program(handle, keep)
+
+
+class StreamProgram:
+    """A chain of one-row qmv stages run by the streaming engine (imq_stream_*): one
+    persistent launch streams every stage's weights.  Holds references to the tensors it
+    points at; `close()` (or garbage collection) frees its device tables."""
+
+    def __init__(self, handle: ctypes.c_void_p, keep: list) -> None:
+        self._handle = handle
+        self._keep = keep
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._handle is None:
+            raise ValueError("the program is closed")
+        return self._handle
+
+    def launch(self, stream=None) -> None:
+        """Enqueue one run on `stream` (capturable in a HIP graph)."""
+        _check(lib().imq_stream_launch(self.handle, _stream(stream)))
+
+    def failed(self) -> bool:
+        """Synchronises the device; True if a run since the last call stopped on a bounded
+        wait (the flag is then cleared)."""
+        flag = _I32(0)
+        _check(lib().imq_stream_status(self.handle, ctypes.byref(flag)))
+        return bool(flag.value)
+
+    def info(self) -> dict:
+        vals = [_I32(0) for _ in range(5)]
+        _check(lib().imq_stream_info(self.handle, *[ctypes.byref(v) for v in vals]))
+        out = dict(zip(("tiles", "stages", "workgroups", "lds_bytes", "chained"),
+                       (v.value for v in vals)))
+        out["chained"] = bool(out["chained"])
+        return out
+
+    def close(self) -> None:
+        if self._handle is not None and _lib is not None:
+            _lib.imq_stream_destroy(self._handle)
+        self._handle = None
+        self._keep = []
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def stream_program(stages: list[tuple[list, torch.Tensor, list, bool]],
+                   workgroups: int = 0) -> StreamProgram:
+    """The chain of `qmv_program` run by the streaming engine: stages without any
+    wait_previous are independent and stream with no synchronisation; with waits, a stage
+    starts after the previous one has finished.  `workgroups` <= 0: the resident maximum."""
+    arr, keep = _qmv_stages(stages)
+    handle = _P()
+    _check(lib().imq_stream_create(arr, len(stages), int(workgroups), ctypes.byref(handle)))
+    return StreamProgram(handle, keep)
 
 
 def decode_program(config, layers: list[dict], final_norm: torch.Tensor, head: tuple,

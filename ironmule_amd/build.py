@@ -12,7 +12,7 @@ import sys
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
-SOURCES = [os.path.join(PKG, "csrc", name) for name in ("runtime.hip", "qmv.hip", "decode.hip", "step.hip")]
+SOURCES = [os.path.join(PKG, "csrc", name) for name in ("runtime.hip", "qmv.hip", "decode.hip", "step.hip", "stream.hip")]
 LIBRARY = os.path.join(PKG, "libironmule_qmv.so")
 ARCH = "gfx950"
 

@@ -128,6 +128,19 @@ __device__ __forceinline__ float chunk_dot(uint4 wv, uint4 x0, uint4 x1, uint4 x
 
 constexpr uint32_t kPastBuffer = 0x80000000u;  // a buffer offset that reads as zero
 
+// Lane shape of the one-row (M = 1) tile, shared by every kernel that computes it so
+// that they all produce the same bits: LPR = 1 << shift lanes share a weight row and
+// lane j takes the 16-byte chunks j, j + LPR, ... of it.  The fewest lanes (16, 32 or
+// 64) that give each lane at most 5 chunks, else at most 8; -1 when even 64 lanes
+// would need more than 8 (K > 16384).
+__host__ __device__ inline int m1_lane_shift(int K) {
+  const int C = K / 32;
+  for (int cap = 5; cap <= 8; cap += 3)
+    for (int sh = 4; sh <= 6; ++sh)
+      if ((C + (1 << sh) - 1) >> sh <= cap) return sh;
+  return -1;
+}
+
 __device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
   const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
   return make_uint4(v.x, v.y, v.z, v.w);

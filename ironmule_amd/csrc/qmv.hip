@@ -1024,11 +1024,10 @@ int choose_batch(const LaunchArgs& a, const int* options, int n_options) {
   return best;
 }
 
-// The one-row kernel's plan: per problem the narrowest row (16, 32 or 64 lanes) whose
-// chunks fit kM1MaxChunks per lane (more rows per tile share one staged x), then the
-// launch's chunk and x-piece bounds.  Returns false when some problem does not qualify
-// (K over 16384, scales/biases not 4-byte aligned, weights of 2 GiB or more).
-constexpr int kM1MaxChunks = 8;
+// The one-row kernel's plan: per problem the lane shape of m1_lane_shift (the narrowest
+// row of 16, 32 or 64 lanes with at most 5 chunks per lane, else 8), then the launch's
+// chunk and x-piece bounds.  Returns false when some problem does not qualify (K over
+// 16384, scales/biases not 4-byte aligned, weights of 2 GiB or more).
 
 struct M1Plan {
   int nch = 0;  // chunks per lane, largest over the problems
@@ -1041,9 +1040,8 @@ bool plan_m1(LaunchArgs& a, M1Plan* plan) {
   for (int i = 0; i < a.count; ++i) {
     Problem& P = a.p[i];
     const int C = P.K / 32;
-    int sh = 4;
-    while (sh <= 6 && (C + (1 << sh) - 1) >> sh > kM1MaxChunks) ++sh;
-    if (sh > 6) return false;
+    const int sh = m1_lane_shift(P.K);
+    if (sh < 0) return false;
     if (!aligned(P.s, 4) || !aligned(P.b, 4)) return false;
     if ((int64_t)P.N * (P.K / 2) >= ((int64_t)1 << 31)) return false;
     P.lpr_shift = sh;

@@ -798,9 +798,8 @@ struct TileShape {
 TileShape tile_shape(int K) {
   TileShape t{-1, 0, 0, -1};
   const int C = K / 32;
-  int sh = 4;
-  while (sh <= 6 && (C + (1 << sh) - 1) >> sh > 8) ++sh;
-  if (sh > 6) return t;
+  const int sh = m1_lane_shift(K);
+  if (sh < 0) return t;
   t.sh = sh;
   t.nch = (C + (1 << sh) - 1) >> sh;
   t.xr = (K / 8 + kThreads - 1) / kThreads;

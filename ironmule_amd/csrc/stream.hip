@@ -1,0 +1,664 @@
+// Streaming engine for chains of one-row (M = 1) 4-bit qmv stages on MI355X (gfx950):
+// one persistent launch streams the weights of every stage of a program.
+// C ABI: include/ironmule_step.h (imq_stream_*).
+//
+// Work.  Every stage is cut into wavefront tiles of 64 / LPR weight rows (LPR lanes per
+// row, the one-row kernel's lane shape, so every output equals imq_qmv's bit for bit).
+// The tiles of all stages form one list in stage order, dealt round-robin to the V
+// wavefronts of the grid: for independent stages wavefront v runs tiles v, v + V, ... of
+// the whole list; for chained stages the same within each stage (counted from the
+// stage's first tile), so that every stage is spread over the whole device.
+//
+// Pipelining.  A wavefront keeps two tiles in registers: while it computes one, the
+// loads of the next are in flight.  Loads are raw buffer loads issued unconditionally
+// (a piece that is not needed reads past its buffer, which returns zero without a memory
+// access), so the number of loads in flight is the same on every path and the waits
+// the compiler places before each tile are exact.
+//
+// Two modes:
+//   * independent stages (no stage reads another's output): every distinct x of the
+//     program is staged in LDS once, at the start, in the pair order of the dot2 chains;
+//     after that a wavefront streams its tiles from the first stage to the last with no
+//     barrier and no wait, the next tile's loads always in flight;
+//   * chained stages (a stage may wait for an earlier one): all wavefronts enter every
+//     stage in order.  Entering a stage, a workgroup signals the previous stage if a later
+//     stage waits for it (each wavefront waits for its own stores, then one atomic add),
+//     issues the loads of its first two tiles of the new stage, waits for the stage's
+//     input (wavefront 0 polls), stages x in LDS (double-buffered by stage parity) and
+//     computes.  The weight loads are issued before the wait, so the weight stream of a
+//     stage overlaps the completion of the one it depends on.
+//
+// Completion counters.  A stage has kSubs counters, each on its own 128-byte line; the
+// workgroups of the grid spread their increments over them (one atomic counter
+// serialises its increments).  A waiter sums the kSubs counters with one load per lane.
+// Activations written and read inside a launch go through sc1 stores and loads, which
+// are coherent across the XCDs' L2 caches; every wait is bounded.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/ironmule_step.h"
+#include "common.h"
+#include "runtime.h"
+
+namespace {
+
+using namespace imq_dev;
+using imq_rt::aligned;
+using imq_rt::current_device;
+using imq_rt::DeviceInfo;
+using imq_rt::fail;
+using imq_rt::ok;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kNch = 5;                // 16-byte chunks per lane: m1_lane_shift gives <= 5 for K <= 10240
+constexpr int kXr = 5;                 // most x pieces of 8 values per thread: K <= 10240
+constexpr int kMaxK = kXr * kThreads * 8;
+constexpr int kSubs = 16;              // completion counters per stage
+constexpr int kLine = 32;              // words per counter line
+constexpr int kMaxPolls = 1 << 22;
+constexpr int kMaxStageProblems = 3;
+constexpr int kMaxSlots = 8;           // distinct x rows of an independent-stage program
+constexpr size_t kSlotLds = 64 * 1024;  // LDS for those rows
+constexpr int kSbWords = 256;           // per wavefront: two packed (scale, bias) words per span dword
+
+// LDS bytes of one staged x row of K values: four planes of C = K/32 uint4 (the pair
+// order of each chunk's four words) followed by the C chunk sums.
+constexpr size_t x_bytes(int K) { return (size_t)(K / 32) * (64 + 4); }
+
+struct SProb {
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  uint16_t* y;
+  int32_t N;
+  int32_t tile_end;  // one past the problem's last tile, counted within the stage
+  int32_t live;      // 1: a later stage of the launch reads y (sc1 stores)
+  int32_t pad;
+};
+
+struct SStage {
+  const uint16_t* x;
+  int32_t K, sh, nch, nprob;
+  int32_t tiles, first;  // the stage's tiles are first .. first + tiles - 1 of the program
+  int32_t wait;          // index of the stage this one waits for, or -1
+  int32_t signal;        // 1: a later stage waits for this one
+  int32_t x_live;        // 1: x is written by an earlier stage of the same launch
+  int32_t xoff;          // byte offset of the stage's staged x in LDS
+  int32_t pad0, pad1;
+  SProb p[kMaxStageProblems];
+};
+
+struct XSlot {
+  const uint16_t* x;
+  int32_t K, off;
+};
+
+struct SArgs {
+  uint32_t* counters;  // kSubs lines per stage
+  uint32_t* status;
+  int32_t nstages, total, waves, sb_off;  // sb_off: LDS byte offset of the scale/bias areas
+  int32_t nslots, pad1[3];
+  XSlot slot[kMaxSlots];
+};
+
+typedef const struct SStage __attribute__((address_space(4)))& StageRef;
+
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<T*>((hi << 32) | lo);
+}
+
+// Stage i's descriptor, seen through the constant address space (nothing writes the table
+// while a launch runs) at a uniform address, so its fields are read with scalar loads
+// that wait on nothing but each other.
+__device__ __forceinline__ StageRef stage_at(const SStage* __restrict__ st, int i) {
+  return *reinterpret_cast<const SStage __attribute__((address_space(4)))*>(
+      reinterpret_cast<uint64_t>(uniform_ptr(st + i)));
+}
+
+__device__ __forceinline__ uint32_t* counter(const SArgs& a, int stage, int sub) {
+  return a.counters + ((size_t)stage * kSubs + sub) * kLine;
+}
+
+// One tile's loads: kNch weight chunks per lane, and the tile's scales and biases as
+// dwords (the span of its rows, which are adjacent in memory, read by consecutive lanes).
+struct Tile {
+  uint4 w[kNch];
+  uint32_t s[2];
+  uint32_t b[2];
+};
+
+// One problem of a stage, resolved once and held in scalar registers while a wavefront
+// works through its tiles: global tiles t0 .. tend-1 of the program.
+struct Site {
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  uint16_t* y;
+  int N, K, sh, nch, xoff, live, t0, tend;
+};
+
+__device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, int pi) {
+  StageRef S = stage_at(st, si);
+  Site c;
+  c.w = S.p[pi].w;
+  c.s = S.p[pi].s;
+  c.b = S.p[pi].b;
+  c.y = S.p[pi].y;
+  c.N = S.p[pi].N;
+  c.live = S.p[pi].live;
+  c.K = S.K;
+  c.sh = S.sh;
+  c.nch = S.nch;
+  c.xoff = S.xoff;
+  c.t0 = S.first + (pi == 0 ? 0 : S.p[pi - 1].tile_end);
+  c.tend = S.first + S.p[pi].tile_end;
+  return c;
+}
+
+// Moves a cursor (stage si, problem pi, resolved site c) forward to the problem holding
+// global tile g, which must lie in stage `last` or before.
+__device__ __forceinline__ void seek(const SStage* __restrict__ st, int& si, int& pi, Site& c, int g) {
+  while (g >= c.tend) {
+    if (pi + 1 < stage_at(st, si).nprob) {
+      ++pi;
+    } else {
+      ++si;
+      pi = 0;
+    }
+    c = site_at(st, si, pi);
+  }
+}
+
+// The scale/bias span of a tile: the halves of rows row0 .. row0 + R - 1 (R = 64 >> sh),
+// R * G of them from half row0 * G on, read as dwords from the dword boundary at or below
+// its start; `mis` is 1 when that start is odd.  At most 5 * 64 + 2 bytes: 81 dwords.
+struct Span {
+  uint32_t a0;
+  int mis, nd;
+};
+
+__device__ __forceinline__ Span span_of(const Site& c, int row0) {
+  const int G = c.K >> 6;
+  const uint32_t h0 = (uint32_t)row0 * (uint32_t)G;
+  const uint32_t h1 = min((uint32_t)(row0 + (64 >> c.sh)), (uint32_t)c.N) * (uint32_t)G;
+  Span sp;
+  sp.a0 = (h0 & ~1u) * 2u;
+  sp.mis = (int)(h0 & 1u);
+  sp.nd = (int)((h1 - (h0 & ~1u) + 1u) >> 1);
+  return sp;
+}
+
+// Issues the loads of global tile g of site c (valid false: every load reads past its
+// buffer, which returns zero without a memory access).
+__device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int lane, Tile& T) {
+  const int C = c.K >> 5, G = c.K >> 6, W = c.K >> 3;
+  const int j = lane & ((1 << c.sh) - 1);
+  const int row0 = (g - c.t0) * (64 >> c.sh);
+  const int row = row0 + (lane >> c.sh);
+  // the scale/bias range rounded up to whole dwords: the extra half lies in the same
+  // aligned dword as the last one, so it is mapped, and it belongs to no row
+  const uint32_t sbb = ((uint32_t)c.N * (uint32_t)G * 2u + 3u) & ~3u;
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(c.w, (uint32_t)c.N * (uint32_t)W * 4u);
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(c.s, sbb);
+  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(c.b, sbb);
+  const bool live = valid && row < c.N;
+  const uint32_t wrow = (uint32_t)row * (uint32_t)W * 4u;
+#pragma unroll
+  for (int i = 0; i < kNch; ++i) {
+    const int kc = j + (i << c.sh);
+    const bool in = live && i < c.nch && kc < C;
+    T.w[i] = load_b128(wr, in ? wrow + 16u * kc : kPastBuffer);
+  }
+  const Span sp = span_of(c, row0);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int d = lane + 64 * q;
+    const uint32_t off = valid && d < sp.nd ? sp.a0 + 4u * d : kPastBuffer;
+    T.s[q] = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
+    T.b[q] = __builtin_amdgcn_raw_buffer_load_b32(br, off, 0, 0);
+  }
+}
+
+// Computes global tile g of site c from its loads, the staged x (LDS at smem + c.xoff)
+// and this wavefront's scale/bias area `sbw` (kSbWords dwords of LDS), and stores the tile's
+// rows as bf16: with sc1 stores when a later stage of the launch reads them.  The chunk
+// order, the dot2 chains and the cross-lane sums are the one-row kernel's.
+__device__ __forceinline__ void compute_site(const Site& c, int g, int lane, const Tile& T,
+                                             const char* smem, uint32_t* sbw, uint32_t magic) {
+  const int C = c.K >> 5, G = c.K >> 6;
+  const int j = lane & ((1 << c.sh) - 1);
+  const int rl = lane >> c.sh;
+  const int row0 = (g - c.t0) * (64 >> c.sh);
+  const int row = row0 + rl;
+  // (scale | bias << 16) per half of the span, in this wavefront's own LDS area
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    *reinterpret_cast<uint2*>(sbw + 2 * (lane + 64 * q)) =
+        make_uint2((T.s[q] & 0xffffu) | (T.b[q] << 16), (T.s[q] >> 16) | (T.b[q] & 0xffff0000u));
+  const int hbase = rl * G + span_of(c, row0).mis;
+  const char* xs = smem + c.xoff;
+  const uint4* xq = reinterpret_cast<const uint4*>(xs);
+  const float* sx = reinterpret_cast<const float*>(xs + (size_t)C * 64);
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNch; ++i) {
+    if (i < c.nch) {
+      const int kc = j + (i << c.sh);
+      const bool valid = kc < C;
+      const int kk = valid ? kc : 0;
+      const uint32_t sb = sbw[hbase + (kk >> 1)];
+      const float sc = __uint_as_float(sb << 16);
+      const float bi = __uint_as_float(sb & 0xffff0000u);
+      const float sxm = sx[kk];
+      const float d = chunk_dot(T.w[i], xq[kk], xq[C + kk], xq[2 * C + kk], xq[3 * C + kk],
+                                -128.0f * sxm, magic);
+      const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
+      acc = valid ? v : acc;
+    }
+  }
+  float v = row16_sum(acc);
+  if (c.sh >= 5) v += __shfl_xor(v, 16);
+  if (c.sh >= 6) v += __shfl_xor(v, 32);
+  if (j == 0 && row < c.N) {
+    if (c.live)
+      store_b16_sc1(buffer_rsrc(c.y, (uint32_t)c.N * 2u), 2u * row, f32_to_bf16_bits(v));
+    else
+      c.y[row] = f32_to_bf16_bits(v);
+  }
+}
+
+// Stages the bf16 row x (K values) in LDS at `dst` in pair order with its chunk sums; the
+// whole workgroup takes part.  `live`: x was written earlier in this launch (sc1 loads).
+__device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, char* dst, int tid) {
+  const int C = K >> 5, W = K >> 3;
+  const __amdgpu_buffer_rsrc_t r = buffer_rsrc(x, (uint32_t)K * 2u);
+  uint4 xs[kXr];
+#pragma unroll
+  for (int t = 0; t < kXr; ++t) {
+    const int i = tid + kThreads * t;
+    const uint32_t off = i < W ? 16u * i : kPastBuffer;
+    xs[t] = live ? load_b128_sc1(r, off) : load_b128(r, off);
+  }
+  uint4* xq = reinterpret_cast<uint4*>(dst);
+  float* sx = reinterpret_cast<float*>(dst + (size_t)C * 64);
+#pragma unroll
+  for (int t = 0; t < kXr; ++t) {
+    const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
+    float part = sum8(xs[t]);
+    part += __shfl_xor(part, 1);
+    part += __shfl_xor(part, 2);
+    if (i < W) {
+      xq[(i & 3) * C + (i >> 2)] = pair_order(xs[t]);
+      if ((i & 3) == 0) sx[i >> 2] = part;
+    }
+  }
+}
+
+// ------------------------------------------------------------ independent stages
+
+// Wavefront v takes tiles v, v + V, v + 2V, ... of the program (V wavefronts), so at any
+// moment the device streams one compact window of the weights.  Its cursors only move
+// forward.  Two tiles are in flight: the loads of tile g + 2V are issued as soon as tile
+// g has been computed.
+__global__ __launch_bounds__(kThreads) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
+  extern __shared__ uint4 smem_raw[];
+  char* smem = reinterpret_cast<char*>(smem_raw);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int v = blockIdx.x * kWaves + wave;
+  const int V = a.waves, total = a.total;
+  uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
+  const uint32_t magic = in_vgpr(kMagic);
+
+  // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp)
+  int ls = 0, lp = 0, cs = 0, cp = 0;
+  Site lc = site_at(st, 0, 0), cc = lc;
+  Tile A, B;
+  auto issue = [&](int g, Tile& T) {
+    if (g < total) seek(st, ls, lp, lc, g);
+    load_site(lc, g, g < total, lane, T);
+  };
+  auto run = [&](int g, Tile& T) {
+    seek(st, cs, cp, cc, g);
+    compute_site(cc, g, lane, T, smem, sbw, magic);
+    issue(g + 2 * V, T);
+  };
+  issue(v, A);
+  issue(v + V, B);
+  for (int k = 0; k < a.nslots; ++k) stage_x(a.slot[k].x, a.slot[k].K, false, smem + a.slot[k].off, tid);
+  lds_barrier();
+
+  for (int g = v; g < total; g += 2 * V) {
+    run(g, A);
+    if (g + V >= total) break;
+    run(g + V, B);
+  }
+}
+
+// ------------------------------------------------------------ chained stages
+
+// Wavefront 0 polls the kSubs counters of `stage` until they add up to `count`; the
+// workgroup then agrees on the outcome (false: timed out, or another workgroup did).
+__device__ bool wait_for(const SArgs& a, int stage, uint32_t count, int* flag) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const uint32_t* c = counter(a, stage, lane < kSubs ? lane : 0);
+    int polls = 0, good = 1;
+    for (;;) {
+      uint32_t n = lane < kSubs ? ld_sc1(c) : 0u;
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) n += __shfl_xor(n, o);
+      n = __shfl(n, 0);
+      if (n >= count) break;
+      if (++polls >= kMaxPolls || ((polls & 63) == 0 && ld_sc1(a.status) != 0)) {
+        good = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) {
+      if (!good) st_sc1(a.status, 1u);
+      *flag = good;
+    }
+  }
+  lds_barrier();
+  return *flag != 0;
+}
+
+// Every workgroup enters every stage in order.  Within a stage the tiles are dealt
+// round-robin: wavefront v runs the stage's tiles v, v + V, ... (counted from the
+// stage's first), so a stage is spread over the whole device.
+__global__ __launch_bounds__(kThreads) void stream_chain_kernel(const SStage* __restrict__ st,
+                                                                SArgs a) {
+  extern __shared__ uint4 smem_raw[];
+  char* smem = reinterpret_cast<char*>(smem_raw);
+  __shared__ int flag;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int v = blockIdx.x * kWaves + wave;
+  const int V = a.waves;
+  uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
+  const uint32_t magic = in_vgpr(kMagic);
+  const uint32_t groups = gridDim.x;
+  Tile A, B;
+
+  for (int s = 0; s < a.nstages; ++s) {
+    StageRef S = stage_at(st, s);
+    if (s > 0 && stage_at(st, s - 1).signal) {  // this workgroup is done with stage s-1
+      wait_vmem();
+      lds_barrier();
+      if (tid == 0)
+        __hip_atomic_fetch_add(counter(a, s - 1, blockIdx.x % kSubs), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const int first = S.first, end = S.first + S.tiles;
+    // this wavefront's first tile of the stage: the smallest g >= first with g - first = v mod V
+    int g = first + v;
+    int lp = 0, cp = 0, ls = s, cs = s;
+    Site lc = site_at(st, s, 0), cc = lc;
+    if (g < end) seek(st, ls, lp, lc, g);
+    load_site(lc, g, g < end, lane, A);
+    if (g + V < end) seek(st, ls, lp, lc, g + V);
+    load_site(lc, g + V, g + V < end, lane, B);
+    if (S.wait >= 0 && !wait_for(a, S.wait, groups, &flag)) return;
+    stage_x(S.x, S.K, S.x_live != 0, smem + S.xoff, tid);
+    lds_barrier();
+    while (g < end) {
+      seek(st, cs, cp, cc, g);
+      compute_site(cc, g, lane, A, smem, sbw, magic);
+      if (g + 2 * V < end) seek(st, ls, lp, lc, g + 2 * V);
+      load_site(lc, g + 2 * V, g + 2 * V < end, lane, A);
+      g += V;
+      if (g >= end) break;
+      seek(st, cs, cp, cc, g);
+      compute_site(cc, g, lane, B, smem, sbw, magic);
+      if (g + 2 * V < end) seek(st, ls, lp, lc, g + 2 * V);
+      load_site(lc, g + 2 * V, g + 2 * V < end, lane, B);
+      g += V;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void clear_kernel(uint32_t* words, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) words[i] = 0u;
+}
+
+}  // namespace
+
+struct imq_stream {
+  int device = -1;
+  bool chained = false;
+  std::vector<SStage> stages;
+  SStage* d_stages = nullptr;
+  uint32_t* d_words = nullptr;  // counters, then the status word
+  int64_t counter_words = 0;
+  SArgs args;
+  int grid = 0;
+  size_t lds = 0;
+};
+
+namespace {
+
+void free_stream(imq_stream* p) {
+  if (!p) return;
+  if (p->d_stages) (void)hipFree(p->d_stages);
+  if (p->d_words) (void)hipFree(p->d_words);
+  delete p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t workgroups,
+                          imq_stream** out) {
+  if (!out) return fail(IMQ_EINVAL, "out must be non-null");
+  *out = nullptr;
+  if (!stages || count < 1) return fail(IMQ_EINVAL, "need at least one stage");
+  int32_t code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
+  imq_stream* p = new imq_stream();
+  (void)hipGetDevice(&p->device);
+  memset(&p->args, 0, sizeof(p->args));
+  int tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    const imq_qmv_stage& st = stages[i];
+    if (st.count < 1 || st.count > kMaxStageProblems) {
+      free_stream(p);
+      return fail(IMQ_EINVAL, "a stage has 1 to 3 problems");
+    }
+    SStage S;
+    memset(&S, 0, sizeof(S));
+    const imq_problem& q0 = st.problems[0];
+    S.x = q0.x;
+    S.K = q0.K;
+    S.nprob = st.count;
+    S.wait = st.wait_previous ? i - 1 : -1;
+    if (S.wait >= 0) p->chained = true;
+    if (i == 0 && st.wait_previous) {
+      free_stream(p);
+      return fail(IMQ_EINVAL, "the first stage has nothing to wait for");
+    }
+    if (q0.K < 64 || q0.K % 64 || q0.K > kMaxK) {
+      free_stream(p);
+      return fail(IMQ_EUNSUPPORTED, "the streaming engine takes K in 64 .. 10240, a multiple of 64");
+    }
+    S.sh = m1_lane_shift(q0.K);
+    S.nch = ((q0.K / 32) + (1 << S.sh) - 1) >> S.sh;
+    const int rows = 64 >> S.sh;
+    int t = 0;
+    for (int k = 0; k < st.count; ++k) {
+      const imq_problem& q = st.problems[k];
+      if (!q.w || !q.scales || !q.biases || !q.x || !q.y || !aligned(q.w, 16) ||
+          !aligned(q.scales, 2) || !aligned(q.biases, 2) || !aligned(q.x, 16) ||
+          !aligned(q.y, 2) || q.N < 1) {
+        free_stream(p);
+        return fail(IMQ_EINVAL, "bad pointer, alignment or shape in a stage");
+      }
+      if (q.x != q0.x || q.K != q0.K) {
+        free_stream(p);
+        return fail(IMQ_EINVAL, "the problems of a stage share one x");
+      }
+      if ((int64_t)q.N * (q.K / 2) >= ((int64_t)1 << 31)) {
+        free_stream(p);
+        return fail(IMQ_EUNSUPPORTED, "weights of 2 GiB or more");
+      }
+      SProb& P = S.p[k];
+      P.w = q.w;
+      P.s = q.scales;
+      P.b = q.biases;
+      P.y = static_cast<uint16_t*>(q.y);
+      P.N = q.N;
+      t += (q.N + rows - 1) / rows;
+      P.tile_end = t;
+    }
+    S.tiles = t;
+    S.first = tiles;
+    tiles += t;
+    p->stages.push_back(S);
+  }
+  for (SStage& S : p->stages)
+    if (S.wait >= 0) p->stages[S.wait].signal = 1;
+  // x rows that overlap an earlier stage's output are read with sc1 loads, and those
+  // outputs are written with sc1 stores
+  for (size_t i = 0; i < p->stages.size(); ++i) {
+    SStage& S = p->stages[i];
+    const uintptr_t x0 = reinterpret_cast<uintptr_t>(S.x), x1 = x0 + (uintptr_t)S.K * 2u;
+    for (size_t e = 0; e < i; ++e)
+      for (int k = 0; k < p->stages[e].nprob; ++k) {
+        SProb& P = p->stages[e].p[k];
+        const uintptr_t y0 = reinterpret_cast<uintptr_t>(P.y), y1 = y0 + (uintptr_t)P.N * 2u;
+        if (x0 < y1 && y0 < x1) {
+          S.x_live = 1;
+          P.live = 1;
+        }
+      }
+  }
+  if (!p->chained) {
+    for (const SStage& S : p->stages)
+      if (S.x_live) {
+        free_stream(p);
+        return fail(IMQ_EINVAL, "a stage reads an output of the program but waits for nothing");
+      }
+    // every distinct x once in LDS
+    int off = 0;
+    for (SStage& S : p->stages) {
+      int k = 0;
+      while (k < p->args.nslots && p->args.slot[k].x != S.x) ++k;
+      if (k == p->args.nslots) {
+        if (k == kMaxSlots || off + x_bytes(S.K) > kSlotLds) {
+          free_stream(p);
+          return fail(IMQ_EUNSUPPORTED, "the distinct x rows of the program exceed 8 or 64 KiB of LDS");
+        }
+        p->args.slot[k] = XSlot{S.x, S.K, off};
+        off += (int)((x_bytes(S.K) + 15) & ~(size_t)15);
+        p->args.nslots = k + 1;
+      } else if (p->args.slot[k].K != S.K) {
+        free_stream(p);
+        return fail(IMQ_EINVAL, "one x used with two different K");
+      }
+      S.xoff = p->args.slot[k].off;
+    }
+    p->args.sb_off = off;
+  } else {
+    for (size_t i = 0; i < p->stages.size(); ++i) p->stages[i].xoff = (int)((i & 1) * x_bytes(kMaxK));
+    p->args.sb_off = (int)(2 * x_bytes(kMaxK));
+  }
+  p->lds = (size_t)p->args.sb_off + (size_t)kWaves * kSbWords * 4;
+  const int nstages = (int)p->stages.size();
+  p->counter_words = p->chained ? (int64_t)nstages * kSubs * kLine : 0;
+  if (hipMalloc(&p->d_words, (size_t)(p->counter_words + 1) * 4) != hipSuccess ||
+      hipMemset(p->d_words, 0, (size_t)(p->counter_words + 1) * 4) != hipSuccess) {
+    free_stream(p);
+    return fail(IMQ_ELAUNCH, "hipMalloc of the stream counters failed");
+  }
+  if (hipMalloc(&p->d_stages, sizeof(SStage) * nstages) != hipSuccess ||
+      hipMemcpy(p->d_stages, p->stages.data(), sizeof(SStage) * nstages, hipMemcpyHostToDevice) !=
+          hipSuccess) {
+    free_stream(p);
+    return fail(IMQ_ELAUNCH, "copying the stage table failed");
+  }
+  const void* fn = p->chained ? reinterpret_cast<const void*>(stream_chain_kernel)
+                              : reinterpret_cast<const void*>(stream_kernel);
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p->lds) != hipSuccess) {
+    free_stream(p);
+    return fail(IMQ_ELAUNCH, "cannot give the streaming kernel its LDS");
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, p->lds) != hipSuccess ||
+      per_cu < 1) {
+    free_stream(p);
+    return fail(IMQ_ELAUNCH, "the streaming kernel does not fit on a CU");
+  }
+  // chained stages need every workgroup resident at once (they wait for each other)
+  const int resident = per_cu * dev->cu_count;
+  int grid = workgroups > 0 ? workgroups : resident;
+  if (p->chained) grid = std::min(grid, resident);
+  grid = std::max(1, std::min(grid, (tiles + kWaves - 1) / kWaves));
+  p->grid = grid;
+  p->args.counters = p->d_words;
+  p->args.status = p->d_words + p->counter_words;
+  p->args.nstages = nstages;
+  p->args.total = tiles;
+  p->args.waves = grid * kWaves;
+  *out = p;
+  return ok();
+}
+
+int32_t imq_stream_launch(imq_stream* p, void* stream) {
+  if (!p) return fail(IMQ_EINVAL, "null program");
+  int dev = -1;
+  (void)hipGetDevice(&dev);
+  if (dev != p->device) return fail(IMQ_EINVAL, "the program belongs to another device");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (p->chained) {
+    const int64_t n = p->counter_words;
+    clear_kernel<<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, s>>>(p->d_words, n);
+    stream_chain_kernel<<<p->grid, kThreads, p->lds, s>>>(p->d_stages, p->args);
+  } else {
+    stream_kernel<<<p->grid, kThreads, p->lds, s>>>(p->d_stages, p->args);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("stream launch: ") + hipGetErrorString(e));
+  return ok();
+}
+
+int32_t imq_stream_status(imq_stream* p, int32_t* failed) {
+  if (!p || !failed) return fail(IMQ_EINVAL, "null argument");
+  uint32_t v = 0;
+  if (hipDeviceSynchronize() != hipSuccess ||
+      hipMemcpy(&v, p->d_words + p->counter_words, 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "reading the stream status failed");
+  *failed = v != 0;
+  if (v && hipMemset(p->d_words + p->counter_words, 0, 4) != hipSuccess)
+    return fail(IMQ_ELAUNCH, "clearing the stream status failed");
+  return ok();
+}
+
+int32_t imq_stream_info(const imq_stream* p, int32_t* tiles, int32_t* stages, int32_t* workgroups,
+                        int32_t* lds_bytes, int32_t* chained) {
+  if (!p) return fail(IMQ_EINVAL, "null program");
+  if (tiles) *tiles = p->args.total;
+  if (stages) *stages = p->args.nstages;
+  if (workgroups) *workgroups = p->grid;
+  if (lds_bytes) *lds_bytes = (int32_t)p->lds;
+  if (chained) *chained = p->chained ? 1 : 0;
+  return ok();
+}
+
+void imq_stream_destroy(imq_stream* p) { free_stream(p); }
+
+}  // extern "C"
