@@ -5,14 +5,18 @@ projections as 4-bit qmv at batch 1 (q 2560->4096, k/v 2560->1024, o 4096->2560,
 gate/up 2560->9728, down 9728->2560), seeded random weights, bf16 activations.
 A step is one pass over one layer's seven projections; consecutive steps rotate over
 36 distinct layer copies (2.05 GB, one Qwen3-4B's worth), so every step streams its
-weights from HBM rather than the 256 MB last-level cache.  Launches are captured in a
-HIP graph (as a decode engine would replay them); inputs are resident in HBM.
+weights from HBM rather than the 256 MB last-level cache.  The streaming engine runs the
+36 layers' projections in one persistent launch (independent stages in decode order),
+captured in a HIP graph; inputs are resident in HBM.
 
 Prints one JSON line.  `value` = algorithmic bytes moved per step (packed weights +
-bf16 scales/biases + x + y) / wall time per step, in GB/s.  `roofline` is the dominant
-kernel (gate/up projection, 2560->9728) timed with HIP events over back-to-back graph
-replays on its own stream.  `cpu_baseline` times the oracle's restatement of the
-reference row kernel on the host cores (rank 0, N=1 only).
+bf16 scales/biases + x + y) / GPU time per step, in GB/s.  `roofline` is the streaming
+kernel (the only kernel of the timed steps): algorithmic bytes per launch over its mean
+launch time from HIP events on its own stream.  The layer breakdown times the same
+layers as per-kernel launches, as one grouped launch per layer, and through the
+streaming engine with decode-order dependencies.  `decode` times the full synthetic
+Qwen3-4B decode step at batch 1 and 32.  `cpu_baseline` times the oracle's restatement of
+the reference row kernel on the host cores (rank 0, N=1 only).
 """
 
 from __future__ import annotations
@@ -94,9 +98,41 @@ LAUNCHES = [("qkv", ["q", "k", "v"], 2560), ("o", ["o"], 4096), ("gate_up", ["ga
             ("down", ["down"], 9728)]
 
 
+def _layer_stages(layers, xs, ys, index, chained=False):
+    """The stages of `layers` in decode order (q/k/v, o, gate/up, down) for the streaming
+    engine.  Independent: every stage reads the fixed x of its K.  Chained: every stage
+    waits for the one before it and reads its output, as a decode step does (o reads q,
+    gate/up read o, down reads gate, the next layer's q/k/v read down)."""
+    stages = []
+    if not chained:
+        for L in layers:
+            for (_, names, k) in LAUNCHES:
+                stages.append(([L[index[nm]] for nm in names], xs[k], [ys[nm] for nm in names],
+                               False))
+        return stages
+    import torch
+    h = xs[2560]
+    for li, L in enumerate(layers):
+        dev = h.device
+        yq = [torch.empty(n, dtype=torch.bfloat16, device=dev) for n in (4096, 1024, 1024)]
+        yo = [torch.empty(2560, dtype=torch.bfloat16, device=dev)]
+        yg = [torch.empty(9728, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+        yd = [torch.empty(2560, dtype=torch.bfloat16, device=dev)]
+        stages += [([L[index["q"]], L[index["k"]], L[index["v"]]], h.reshape(-1), yq, li > 0),
+                   ([L[index["o"]]], yq[0], yo, True),
+                   ([L[index["gate"]], L[index["up"]]], yo[0], yg, True),
+                   ([L[index["down"]]], yg[0], yd, True)]
+        h = yd[0]
+    return stages
+
+
 def bench_layer(torch, native, steps, warmup, device, breakdown=True):
-    """The headline: K steps of one layer's seven projections, rotating 36 layers, as
-    four launches in decode order (q/k/v grouped, o, gate/up grouped, down)."""
+    """The headline: K steps of one layer's seven projections, rotating over 36 distinct
+    layers, streamed by the streaming engine: one launch runs 36 layers' projections as
+    independent stages (as in the reference's bandwidth measurement over chained distinct
+    weights, ironmule/hw.py:441-473).  The breakdown times the same layers as per-kernel
+    launches in decode order, all seven projections in one grouped launch, and the
+    streaming engine with decode-order dependencies."""
     gen = torch.Generator(device=device)
     gen.manual_seed(SEED + 1)
     index = {name: i for i, (name, _, _) in enumerate(LAYER)}
@@ -106,21 +142,15 @@ def bench_layer(torch, native, steps, warmup, device, breakdown=True):
     ys = {name: torch.empty((1, n), dtype=torch.bfloat16, device=device)
           for (name, n, _) in LAYER}
     stream = torch.cuda.Stream(device=device)
+    xrow = {k: v.reshape(-1) for k, v in xs.items()}
+    yrow = {k: v.reshape(-1) for k, v in ys.items()}
 
-    def launch(i, names, k):
-        weights = [layers[i][index[nm]] for nm in names]
-        outs = [ys[nm] for nm in names]
-        return lambda: native.qmv_grouped(weights, [xs[k]] * len(names), outs=outs,
-                                          stream=stream)
-
-    def layer_launches(i):
-        return [launch(i, names, k) for (_, names, k) in LAUNCHES]
-
-    full = GraphRunner(torch, [fn for i in range(LAYERS) for fn in layer_launches(i)], stream)
+    full_prog = native.stream_program(_layer_stages(layers, xrow, yrow, index))
+    full = GraphRunner(torch, [lambda: full_prog.launch(stream)], stream)
     part_n = steps % LAYERS
-    part = (GraphRunner(torch, [fn for i in range(part_n) for fn in layer_launches(i)], stream)
-            if part_n else None)
-    for _ in range(warmup // LAYERS + (1 if warmup % LAYERS else 0)):
+    part_prog = native.stream_program(_layer_stages(layers[:part_n], xrow, yrow, index)) if part_n else None
+    part = GraphRunner(torch, [lambda: part_prog.launch(stream)], stream) if part_n else None
+    for _ in range(max(3, warmup // LAYERS + (1 if warmup % LAYERS else 0))):
         full.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
@@ -138,13 +168,26 @@ def bench_layer(torch, native, steps, warmup, device, breakdown=True):
     wall = time.perf_counter() - t0
     gpu_s = start.elapsed_time(end) / 1e3
     step_bytes = sum(qmv_bytes(n, k, 1) for (_, n, k) in LAYER)
-
+    launches = steps // LAYERS + (1 if part_n else 0)
+    info = full_prog.info()
+    out = {"gpu_s": gpu_s, "wall_s": wall, "step_bytes": step_bytes, "launches": launches,
+           "workgroups": info["workgroups"], "launch_bytes": step_bytes * LAYERS,
+           "avg_launch_s": gpu_s / launches if not part_n else None}
+    if part_n == 0:
+        out["avg_launch_s"] = gpu_s / launches
+    else:  # the full-program launches alone, for the per-launch figure
+        out["avg_launch_s"] = time_graph(torch, full, 10, stream)
     if not breakdown:
-        del layers
+        del full, part, full_prog, part_prog, layers
         torch.cuda.empty_cache()
-        return {"gpu_s": gpu_s, "wall_s": wall, "step_bytes": step_bytes}
+        return out
 
-    # each launch type alone: 36 back-to-back launches over distinct weights
+    # each launch type alone: 36 back-to-back per-kernel launches over distinct weights
+    def launch(i, names, k):
+        weights = [layers[i][index[nm]] for nm in names]
+        outs = [ys[nm] for nm in names]
+        return lambda: native.qmv_grouped(weights, [xs[k]] * len(names), outs=outs, stream=stream)
+
     per_launch = {}
     for (lname, names, k) in LAUNCHES:
         runner = GraphRunner(torch, [launch(i, names, k) for i in range(LAYERS)], stream)
@@ -153,6 +196,12 @@ def bench_layer(torch, native, steps, warmup, device, breakdown=True):
         nbytes = sum(qmv_bytes(n, kk, 1) for (nm, n, kk) in LAYER if nm in names)
         per_launch[lname] = {"us": sec * 1e6, "gbs": nbytes / sec / 1e9, "bytes": nbytes}
         del runner
+    runner = GraphRunner(torch, [fn for i in range(LAYERS)
+                                 for fn in (launch(i, names, k) for (_, names, k) in LAUNCHES)], stream)
+    runner.replay()
+    sec = time_graph(torch, runner, 20, stream) / LAYERS
+    decode_order = {"us": sec * 1e6, "gbs": step_bytes / sec / 1e9}
+    del runner
 
     # all seven projections of a layer in one launch (they are independent here)
     runner = GraphRunner(torch, [
@@ -162,10 +211,19 @@ def bench_layer(torch, native, steps, warmup, device, breakdown=True):
     runner.replay()
     sec = time_graph(torch, runner, 20, stream) / LAYERS
     one_launch = {"us": sec * 1e6, "gbs": step_bytes / sec / 1e9}
-    del runner, layers
+    del runner
+
+    # the streaming engine with decode-order dependencies between the stages
+    chain_prog = native.stream_program(_layer_stages(layers, xrow, yrow, index, chained=True))
+    runner = GraphRunner(torch, [lambda: chain_prog.launch(stream)], stream)
+    runner.replay()
+    sec = time_graph(torch, runner, 10, stream) / LAYERS
+    chained = {"us": sec * 1e6, "gbs": step_bytes / sec / 1e9, "stalled": chain_prog.failed()}
+    del runner, chain_prog, full, part, full_prog, part_prog, layers
     torch.cuda.empty_cache()
-    return {"gpu_s": gpu_s, "wall_s": wall, "step_bytes": step_bytes, "per_launch": per_launch,
-            "one_launch": one_launch}
+    out.update({"per_launch": per_launch, "decode_order": decode_order, "one_launch": one_launch,
+                "chained": chained})
+    return out
 
 
 def bench_config(torch, native, n, k, ms, y_dtype, copies, device, seed, repeats=10):
@@ -200,7 +258,8 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
     """Full synthetic Qwen3-4B decode step (36 layers of 4-bit projections + the 151,936-
     token tied head, GQA attention over a 512-token KV context per request), as one HIP
     graph per batch size; returns tokens/s and the weight + KV bytes per step."""
-    from ironmule_amd.decode import DecodeState, DecoderConfig, decode_step, random_weights
+    from ironmule_amd.decode import (DecodeState, DecoderConfig, PersistentDecode, decode_step,
+                                     random_weights)
 
     cfg = DecoderConfig()
     weights = random_weights(cfg, device, seed=seed)
@@ -215,16 +274,27 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
         state.set_requests(torch.randint(0, cfg.vocab, (b,), generator=gen, device=device).tolist(),
                            list(range(b)), [CONTEXT] * b)
         stream = torch.cuda.Stream(device=device)
-        runner = GraphRunner(torch, [lambda: decode_step(weights, state, stream=stream)], stream)
-        for _ in range(warmup):
-            runner.replay()
-        sec = time_graph(torch, runner, steps, stream)
+        paths = {"per_kernel": (lambda: decode_step(weights, state, stream=stream),
+                                2 + cfg.layers * 9)}
+        if b == 1:
+            staged = PersistentDecode(weights, state, staged=True)
+            paths["staged_program"] = (lambda: staged.step(stream), 2 + cfg.layers * 5)
         kv_bytes = cfg.layers * b * cfg.kv_heads * (CONTEXT + 1) * cfg.head_dim * 2 * 2
+        times = {}
+        for name, (fn, launches) in paths.items():
+            runner = GraphRunner(torch, [fn], stream)
+            for _ in range(warmup):
+                runner.replay()
+            times[name] = (time_graph(torch, runner, steps, stream), launches)
+            del runner
+        best = min(times, key=lambda k: times[k][0])
+        sec, launches = times[best]
         out[str(b)] = {"ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(b / sec, 1),
                        "weight_gbs": round(cfg.weight_bytes() / sec / 1e9, 1),
                        "weight_plus_kv_gbs": round((cfg.weight_bytes() + kv_bytes) / sec / 1e9, 1),
-                       "launches_per_step": 2 + cfg.layers * 9}
-        del runner, state
+                       "path": best, "launches_per_step": launches,
+                       "paths_ms": {k: round(v[0] * 1e3, 4) for k, v in times.items()}}
+        del state
         torch.cuda.empty_cache()
     del weights
     torch.cuda.empty_cache()
@@ -270,10 +340,9 @@ def cpu_baseline(seconds: float = 10.0):
 
 COPY_READ = 1 << 30   # the calibration copy: 2^27 int64 values read ...
 COPY_WRITTEN = 1 << 29  # ... and written back as int32
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmv_layer_m1_hbm_traffic.md")
-# the dominant kernel of the layer step: the gate+up launch, 2 x 9728 rows at 16 rows per
-# workgroup (16 lanes per row, 4 wavefronts)
-DOMINANT = ("qmv_fixed_kernel<1, 4, 5>", 1216)
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "stream_kernel_layer_m1_hbm_traffic.md")
+# the only kernel of the timed layer steps: the streaming engine's independent-stage kernel
+DOMINANT = "stream_kernel"
 
 
 def copy_calibration(torch, device) -> None:
@@ -288,7 +357,7 @@ def copy_calibration(torch, device) -> None:
 
 
 def _short(name: str) -> str:
-    for marker in ("qmv_m1c_kernel", "qmv_m1_kernel", "qmv_rows_kernel", "qmv_mfma_kernel",
+    for marker in ("stream_chain_kernel", "stream_kernel", "qmv_m1c_kernel", "qmv_m1_kernel", "qmv_rows_kernel", "qmv_mfma_kernel",
                    "qmv_mma_kernel", "qmv_reduce_kernel",
                    "dequant_kernel", "embed_kernel", "add_rmsnorm_kernel", "qk_norm_rope_kernel",
                    "attention_partial_kernel", "attention_combine_kernel", "silu_mul_kernel"):
@@ -383,8 +452,8 @@ def profiled_traffic(kernel: str, workgroups: int):
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=360)
-    ap.add_argument("--warmup", type=int, default=36)
+    ap.add_argument("--steps", type=int, default=3600)
+    ap.add_argument("--warmup", type=int, default=3600)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -440,11 +509,13 @@ def main() -> None:
     if args.no_breakdown:
         value = res["step_bytes"] * args.steps / res["gpu_s"] / 1e9
         print(json.dumps({"metric": "layer GB/s (profiling run)", "value": round(value, 2),
-                          "unit": "GB/s", "steps": args.steps}), flush=True)
+                          "unit": "GB/s", "steps": args.steps, "workgroups": res["workgroups"],
+                          "avg_launch_us": round(res["avg_launch_s"] * 1e6, 3)}), flush=True)
         return
     ms_per_step = res["gpu_s"] / args.steps * 1e3
     value = res["step_bytes"] * args.steps / res["gpu_s"] / 1e9
-    gate = res["per_launch"]["gate_up"]
+    launch_us = res["avg_launch_s"] * 1e6
+    achieved = res["launch_bytes"] / res["avg_launch_s"] / 1e9
     line = {
         "metric": "4-bit qmv HBM GB/s (% of peak) + synthetic decode tokens/s at batch 1 and 32",
         "value": round(value, 2),
@@ -461,22 +532,33 @@ def main() -> None:
         "config": {"workload": "qwen3-4b decoder layer, 7 projections as 4-bit qmv, batch 1",
                    "projections": {name: [k, n] for (name, n, k) in LAYER},
                    "group_size": 64, "batch": 1, "rotating_layers": LAYERS,
-                   "launch": "hip graph per 36 layers; per layer 4 launches in decode order: "
-                             "q/k/v grouped, o, gate/up grouped, down"},
+                   "launch": "streaming engine: one persistent launch per 36 layers, each "
+                             "layer's projections as 4 independent stages in decode order "
+                             "(q/k/v, o, gate/up, down), captured in a hip graph"},
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
-        "roofline": {"bound": "hbm", "achieved": round(gate["gbs"], 2), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gate["gbs"] / PEAK_HBM_GBS, 4),
-                     "traffic": profiled_traffic(*DOMINANT),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic(DOMINANT, res["workgroups"]),
                      "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
-                     "kernel": f"{DOMINANT[0]} x {DOMINANT[1]} workgroups: gate+up grouped "
-                               "launch, 2 x (2560->9728), M=1",
-                     "bytes_per_launch": gate["bytes"],
-                     "avg_launch_us": round(gate["us"], 3)},
-        "per_launch": {k: {"us": round(v["us"], 3), "gbs": round(v["gbs"], 1)}
-                       for k, v in res["per_launch"].items()},
-        "layer_one_launch": {"us": round(res["one_launch"]["us"], 3),
-                             "gbs": round(res["one_launch"]["gbs"], 1),
-                             "note": "all 7 independent projections in one grouped launch"},
+                     "kernel": f"{DOMINANT} x {res['workgroups']} workgroups: 36 layers' "
+                               "7 projections (144 stages), M=1",
+                     "bytes_per_launch": res["launch_bytes"],
+                     "avg_launch_us": round(launch_us, 3)},
+        "layer_breakdown": {
+            "per_kernel_launches": {k: {"us": round(v["us"], 3), "gbs": round(v["gbs"], 1)}
+                                    for k, v in res["per_launch"].items()},
+            "per_kernel_decode_order": {"us": round(res["decode_order"]["us"], 3),
+                                        "gbs": round(res["decode_order"]["gbs"], 1),
+                                        "note": "4 per-kernel launches per layer"},
+            "one_grouped_launch": {"us": round(res["one_launch"]["us"], 3),
+                                   "gbs": round(res["one_launch"]["gbs"], 1),
+                                   "note": "all 7 projections of a layer in one launch"},
+            "stream_chained": {"us": round(res["chained"]["us"], 3),
+                               "gbs": round(res["chained"]["gbs"], 1),
+                               "stalled": res["chained"]["stalled"],
+                               "note": "streaming engine, each stage waits for and reads the "
+                                       "previous one's output (decode-order dependencies)"},
+        },
     }
     if not args.no_decode:
         print("[bench] decode step", file=sys.stderr, flush=True)

@@ -141,6 +141,21 @@ __host__ __device__ inline int m1_lane_shift(int K) {
   return -1;
 }
 
+// Decode attention's split of each (request, KV head) pair's keys: whole 64-key chunks per
+// split, as many splits as it takes to give the launch about 4096 workgroups (at most one
+// split per chunk).  Shared by every attention path so that they merge the same partials
+// in the same order.
+__host__ inline void attention_splits(int B, int Hkv, int span, int* splits, int* chunks_per_split) {
+  const int chunks = (span + 63) / 64;
+  const int pairs = B * Hkv;
+  int sp = (4096 + pairs - 1) / pairs;
+  sp = sp < chunks ? sp : chunks;
+  sp = sp > 1 ? sp : 1;
+  const int c = (chunks + sp - 1) / sp;
+  *chunks_per_split = c;
+  *splits = (chunks + c - 1) / c;
+}
+
 __device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
   const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
   return make_uint4(v.x, v.y, v.z, v.w);

@@ -214,30 +214,44 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
   float M[2] = {-INFINITY, -INFINITY}, Ls[2] = {0.0f, 0.0f};
   float a0[2] = {0.0f, 0.0f}, a1[2] = {0.0f, 0.0f};
 
-  auto load = [&](int start, uint4 (&kr)[4], uint4 (&vr)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + kThreads * i;
-      const int row = p >> 4, col = p & 15;
-      const int t = start + row < last ? start + row : last - 1;  // stays in the slot
-      kr[i] = *reinterpret_cast<const uint4*>(k_pool + base + (size_t)t * kD + col * 8);
-      vr[i] = *reinterpret_cast<const uint4*>(v_pool + base + (size_t)t * kD + col * 8);
-    }
+  // The chunk's K and V rows, four 16-byte pieces each per thread, in named registers (an
+  // array filled through a reference would be kept in scratch memory).  Rows past `last`
+  // read row last-1, which stays inside the slot.
+  const uint4* kb = reinterpret_cast<const uint4*>(k_pool + base);
+  const uint4* vb = reinterpret_cast<const uint4*>(v_pool + base);
+  auto piece = [&](int start, int i) {
+    const int p = tid + kThreads * i;
+    const int t = start + (p >> 4) < last ? start + (p >> 4) : last - 1;
+    return (size_t)t * (kD / 8) + (p & 15);
   };
-  uint4 kr[4], vr[4];
-  load(first, kr, vr);
+  uint4 k0 = kb[piece(first, 0)], k1 = kb[piece(first, 1)], k2 = kb[piece(first, 2)],
+        k3 = kb[piece(first, 3)];
+  uint4 v0 = vb[piece(first, 0)], v1 = vb[piece(first, 1)], v2 = vb[piece(first, 2)],
+        v3 = vb[piece(first, 3)];
   for (int start = first; start < last; start += kChunk) {
     const int count = min(kChunk, last - start);
     __syncthreads();  // the previous chunk's readers are done
+    {
+      const uint4 kr[4] = {k0, k1, k2, k3}, vr[4] = {v0, v1, v2, v3};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + kThreads * i;
-      const int row = p >> 4, col = p & 15;
-      L.k[row][col] = kr[i];
-      *reinterpret_cast<uint4*>(&L.v[row][col * 4]) = vr[i];
+      for (int i = 0; i < 4; ++i) {
+        const int p = tid + kThreads * i;
+        const int row = p >> 4, col = p & 15;
+        L.k[row][col] = kr[i];
+        *reinterpret_cast<uint4*>(&L.v[row][col * 4]) = vr[i];
+      }
     }
     __syncthreads();
-    if (start + kChunk < last) load(start + kChunk, kr, vr);  // next chunk in flight
+    if (start + kChunk < last) {  // next chunk in flight
+      k0 = kb[piece(start + kChunk, 0)];
+      k1 = kb[piece(start + kChunk, 1)];
+      k2 = kb[piece(start + kChunk, 2)];
+      k3 = kb[piece(start + kChunk, 3)];
+      v0 = vb[piece(start + kChunk, 0)];
+      v1 = vb[piece(start + kChunk, 1)];
+      v2 = vb[piece(start + kChunk, 2)];
+      v3 = vb[piece(start + kChunk, 3)];
+    }
 
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -353,21 +367,17 @@ int32_t launched(const char* what) {
   return ok();
 }
 
-// Splits per (request, KV head): enough workgroups to cover the chip about twice, each
-// split a whole number of 64-key chunks.
+// Splits per (request, KV head): attention_splits (common.h).
 struct AttnPlan {
   int splits;
   int chunks_per_split;
 };
 
 AttnPlan attention_plan(int32_t B, int32_t Hkv, int32_t span) {
-  const int chunks = (span + kChunk - 1) / kChunk;
-  const int pairs = B * Hkv;
-  int splits = (512 + pairs - 1) / pairs;
-  splits = splits < chunks ? splits : chunks;
-  splits = splits > 1 ? splits : 1;
-  const int cps = (chunks + splits - 1) / splits;
-  return AttnPlan{(chunks + cps - 1) / cps, cps};
+  static_assert(kChunk == 64, "attention_splits counts 64-key chunks");
+  AttnPlan pl;
+  attention_splits(B, Hkv, span, &pl.splits, &pl.chunks_per_split);
+  return pl;
 }
 
 }  // namespace

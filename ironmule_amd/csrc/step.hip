@@ -945,17 +945,11 @@ int32_t finish_program(imq_program* prog) {
   return ok();
 }
 
-// Attention splits: the per-kernel path's plan (decode.hip attention_plan), so both
+// Attention splits: the per-kernel path's plan (attention_splits, common.h), so both
 // paths merge the same partials in the same order.
 void attention_split(int B, int Hkv, int span, int* splits, int* cps) {
-  const int chunks = (span + kChunk - 1) / kChunk;
-  const int pairs = B * Hkv;
-  int sp = (512 + pairs - 1) / pairs;
-  sp = sp < chunks ? sp : chunks;
-  sp = sp > 1 ? sp : 1;
-  const int c = (chunks + sp - 1) / sp;
-  *cps = c;
-  *splits = (chunks + c - 1) / c;
+  static_assert(kChunk == 64, "attention_splits counts 64-key chunks");
+  attention_splits(B, Hkv, span, splits, cps);
 }
 
 }  // namespace
