@@ -122,13 +122,17 @@ IMQ_API int32_t imq_qmv_grouped(const imq_problem* problems, int32_t count, int3
                                 void* stream);
 
 /* Bytes of workspace imq_qmv_grouped_ws can use for these problems at M rows: with it the
- * groups of small-N weights are split over more workgroups (fp32 partials, added in a
- * fixed order by a second launch).  0 when no split helps (M < 3 or enough rows). */
+ * groups of small-N weights are split over more workgroups (fp32 partials, which the
+ * last workgroup of each 128-row tile adds in a fixed order, in the same launch).  0 when
+ * no split helps (M < 3 or enough rows). */
 IMQ_API size_t imq_qmv_grouped_workspace(const imq_problem* problems, int32_t count, int32_t M);
 
-/* imq_qmv_grouped with a caller-provided fp32 workspace of workspace_bytes (16-byte
- * aligned; may be 0 bytes, then no split).  Same results as imq_qmv_grouped up to the
- * fp32 summation order of the splits; calls that share a workspace must not overlap.
+/* imq_qmv_grouped with a caller-provided workspace of workspace_bytes (16-byte aligned;
+ * may be 0 bytes, then no split).  The workspace must be zero-filled before its first
+ * use; every call leaves it ready for the next (its tile counters back at zero), so one
+ * workspace serves any number of calls.  Same results as imq_qmv_grouped up to the fp32
+ * summation order of the splits, and the same bits on every call; calls that share a
+ * workspace must not overlap.
  * Replaces the same reference calls as imq_qmv_grouped, and imq_qmv at M >= 3 (the
  * shared-weight form, ironmule/cuda_native.py:155-168 for M <= 8, up to 32 here). */
 IMQ_API int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, int32_t M,

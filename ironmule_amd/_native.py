@@ -251,19 +251,37 @@ def qmv(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, x: torch.Te
     return out
 
 
+_workspaces: dict = {}
+
+
+def _workspace(nbytes: int, device, stream) -> torch.Tensor:
+    """A zero-filled fp32 workspace of at least nbytes for (device, stream), kept for later
+    calls: the library's split counters must be zero before a workspace's first use and
+    every call leaves them at zero, so one workspace serves every call on that stream
+    (calls on one stream never overlap)."""
+    dev = torch.device(device)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           0 if stream is None else int(stream.cuda_stream))
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        ws = torch.zeros(-(-nbytes // 4), dtype=torch.float32, device=dev)
+        if not torch.cuda.is_current_stream_capturing():
+            torch.cuda.synchronize(dev)  # the fill runs on the current stream
+        _workspaces[key] = ws
+    return ws
+
+
 def _grouped_launch(probs, count: int, m: int, dtype: torch.dtype, device, stream) -> None:
-    """imq_qmv_grouped, through imq_qmv_grouped_ws with a fresh workspace when the library
-    wants one (M >= 3 and small N)."""
+    """imq_qmv_grouped, through imq_qmv_grouped_ws with this stream's workspace when the
+    library wants one (M >= 3 and few rows: the groups are split over more workgroups)."""
     nbytes = int(lib().imq_qmv_grouped_workspace(probs, count, m)) if m >= 3 else 0
     if nbytes == 0:
         _check(lib().imq_qmv_grouped(probs, count, m, GROUP_SIZE, BITS, _DTYPE_CODE[dtype],
                                      _stream(stream)))
         return
-    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=device)
-    if stream is not None:
-        ws.record_stream(stream)  # keep it from reuse until that stream's work is done
+    ws = _workspace(nbytes, device, stream)
     _check(lib().imq_qmv_grouped_ws(probs, count, m, GROUP_SIZE, BITS, _DTYPE_CODE[dtype],
-                                    _ptr(ws), nbytes, _stream(stream)))
+                                    _ptr(ws), ws.numel() * 4, _stream(stream)))
 
 
 def qmv_multi(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,

@@ -14,12 +14,12 @@
 //     s * sum (128+q) x  +  (b - 128 s) * sum x.
 //
 // Kernels sharing that arithmetic:
-//   * qmv_fixed_kernel / qmv_rows_kernel (one or two activation rows): v_dot2_f32_bf16
+//   * qmv_m1_kernel / qmv_m1c_kernel / qmv_rows_kernel (one or two rows): v_dot2_f32_bf16
 //     chains, x staged once per workgroup in LDS already in pair order, each chain
 //     started at -128 * sum(x);
-//   * qmv_mfma_kernel (more rows): v_mfma_f32_16x16x32_bf16 with the activation rows as
-//     the A operand and 16 weight rows as the B operand, one MFMA pair per group of 64,
-//     and a second MFMA pair against a ones operand that yields sum(x) per group.
+//   * qmv_mma_kernel (3 to 32 rows): v_mfma_f32_32x32x16_bf16 with the activation rows
+//     as the A operand and 32 weight rows as the B operand, four MFMAs per group of 64,
+//     and four more against a ones operand that yield sum(x) per group.
 //
 // Layout in HBM is the reference's own (row-major w (N, K/8) uint32, s and b (N, K/64)
 // bf16), so a caller passes its buffers unchanged.  One launch may serve up to
@@ -457,23 +457,7 @@ __global__ __launch_bounds__(kThreads) void qmv_m1c_kernel(M1Args a) {
                    (bx - first) * (kThreads >> sh));
 }
 
-// ------------------------------------------------------- MFMA kernel (more rows)
-//
-// A workgroup owns 16*NT weight rows of one problem; its four wavefronts split the
-// groups of 64 into quarters and add their partial sums through LDS at the end.  In a
-// wavefront, lane (n = lane%16, kg = lane/16) holds, per group g and per 16-row tile,
-// the two words 8g+2kg and 8g+2kg+1 of weight row n (one 8-byte load): as B operands of
-// two v_mfma_f32_16x16x32_bf16 they cover the group's words {0,2,4,6} and {1,3,5,7}.
-// The A operands are the matching x words of activation row m = lane%16 (+16 per
-// m-tile), read from memory with the weights of the same stage (x stays in L2) and put
-// in pair order.
-// D[m][n] lands in lane (n, kg) as rows m = 4*kg + r, r < 4.  Per group:
-//     acc += s * P + (b - 128 s) * P1,
-// where P1 is the same MFMA pair against a ones operand, i.e. sum x over the group.
-//
-// Memory-level parallelism: the weight words of GS groups are loaded at once, and the
-// next GS groups are in flight while these compute.  The scales and biases of the
-// workgroup's rows are staged once in LDS as (s | b << 16) words, [row][group].
+// ------------------------------------------------------- MFMA operand helpers
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   u32x4_t t = {v.x, v.y, v.z, v.w};
@@ -484,215 +468,6 @@ __device__ __forceinline__ bf16x8_t unpack_word(uint32_t u, uint32_t magic) {
   u32x4_t t = {nibble_pair(u, 0, magic), nibble_pair(u, 1, magic), nibble_pair(u, 2, magic),
                nibble_pair(u, 3, magic)};
   return __builtin_bit_cast(bf16x8_t, t);
-}
-
-// One stage: the weight words (per tile) and the x words (per m-tile) of GS groups.
-template <int MT, int NT, int GS>
-struct MfmaStage {
-  uint2 w[GS][NT];
-  uint4 x0[GS][MT];
-  uint4 x1[GS][MT];
-};
-
-// Weight words of groups g .. g+GS-1 as raw buffer loads (one lane offset per tile plus
-// immediate offsets; reads past the matrix return zero, so no group needs a clamp), and
-// the matching x words.  Groups past the wavefront's range are loaded but never used.
-//
-// Every stage is always issued, so the number of loads in flight is the same on every
-// path and the compiler's waits stay exact (a conditional stage would make it wait for
-// everything).  Groups past the range get an offset past the buffer: the hardware
-// returns zero for them without touching memory.
-
-template <int MT, int NT, int GS>
-__device__ __forceinline__ void load_stage(MfmaStage<MT, NT, GS>& st, __amdgpu_buffer_rsrc_t wrsrc,
-                                           const uint32_t (&voff)[NT],
-                                           const uint16_t* const (&xr)[MT], int g, int g1) {
-#pragma unroll
-  for (int i = 0; i < GS; ++i) {
-    const uint32_t goff = g + i < g1 ? 32u * (g + i) : kPastBuffer;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wrsrc, voff[t] + goff, 0, 0);
-      st.w[i][t] = make_uint2(v.x, v.y);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < GS; ++i) {
-    const int gg = g + i < g1 ? g + i : g1 - 1;  // x rows end at K: stay inside them
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const uint4* xv = reinterpret_cast<const uint4*>(xr[mt] + 64 * gg);
-      st.x0[i][mt] = xv[0];
-      st.x1[i][mt] = xv[1];
-    }
-  }
-}
-
-template <int MT, int NT, int GS>
-__device__ __forceinline__ void compute_stage(const MfmaStage<MT, NT, GS>& st, const uint32_t* sb,
-                                              int G, int g, int g1, f32x4_t (&acc)[NT][MT],
-                                              uint32_t magic) {
-  const u32x4_t ones_u = {kOnes, kOnes, kOnes, kOnes};
-  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < GS; ++i) {
-    if (g + i >= g1) break;
-    bf16x8_t a0[MT], a1[MT];
-    f32x4_t sumx[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      a0[mt] = as_bf16x8(pair_order(st.x0[i][mt]));
-      a1[mt] = as_bf16x8(pair_order(st.x1[i][mt]));
-      sumx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mt], ones, zero, 0, 0, 0);
-      sumx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], ones, sumx[mt], 0, 0, 0);
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const bf16x8_t b0 = unpack_word(st.w[i][t].x, magic);
-      const bf16x8_t b1 = unpack_word(st.w[i][t].y, magic);
-      const uint32_t pk = sb[t * 16 * G + g + i];
-      const float sc = bf16_bits_to_f32(pk & 0xffffu);
-      const float bp = fmaf(-128.0f, sc, __uint_as_float(pk & 0xffff0000u));
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        f32x4_t p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mt], b0, zero, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], b1, p, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc[t][mt][r] = fmaf(sc, p[r], fmaf(bp, sumx[mt][r], acc[t][mt][r]));
-      }
-    }
-  }
-}
-
-template <int MT, int NT, int GS>
-__global__ __launch_bounds__(kThreads) void qmv_mfma_kernel(LaunchArgs a) {
-  extern __shared__ uint32_t sb_lds[];  // (s | b << 16) per [row of the workgroup][group]
-  __shared__ f32x4_t red[3][NT][MT][64];
-  const Problem& P = a.p[blockIdx.y];
-  const int K = P.K, N = P.N, M = a.M;
-  if ((int)(blockIdx.x * (16 * NT)) >= N) return;  // past this problem's tiles
-  const int G = K >> 6, W = K >> 3;
-  const int tid = threadIdx.x;
-  // the wave index is uniform across the wavefront: keep it (and the group range and
-  // loop control derived from it) in scalar registers, so branches are scalar
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int n = lane & 15, kg = lane >> 4;
-  const int row0 = blockIdx.x * (16 * NT);
-  const uint32_t magic = in_vgpr(kMagic);
-
-  // Scales and biases of the workgroup's rows (one contiguous span each), loaded first
-  // so they land before the weights: 16-byte loads when aligned and whole, else halves.
-  constexpr int SBV = 4;  // uint4 per thread: spans up to 8192 halves (G <= 8192 / (16 NT))
-  const int span = 16 * NT * G;
-  const uint16_t* s0 = P.s + (size_t)row0 * G;
-  const uint16_t* b0 = P.b + (size_t)row0 * G;
-  const bool vec = ((reinterpret_cast<uintptr_t>(s0) | reinterpret_cast<uintptr_t>(b0)) & 15) == 0 &&
-                   row0 + 16 * NT <= N && span % 8 == 0 && span <= 8 * kThreads * SBV;
-  uint4 sv[SBV], bv[SBV];
-  if (vec) {
-#pragma unroll
-    for (int q = 0; q < SBV; ++q) {
-      const int idx = tid + kThreads * q;
-      if (idx * 8 < span) {
-        sv[q] = reinterpret_cast<const uint4*>(s0)[idx];
-        bv[q] = reinterpret_cast<const uint4*>(b0)[idx];
-      }
-    }
-  }
-
-  // the host guarantees N * K / 2 < 2^31, so byte offsets fit the buffer's 32 bits
-  const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(P.w, (uint32_t)((size_t)N * W * 4));
-  uint32_t voff[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int row = row0 + 16 * t + n;
-    const int r = row < N ? row : N - 1;
-    voff[t] = ((uint32_t)r * (uint32_t)W + 2u * kg) * 4u;
-  }
-  // rows m >= M feed MFMA rows whose results are never stored: read row M-1 for them
-  const uint16_t* xr[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = n + 16 * mt;
-    xr[mt] = x_row(a, P, m < M ? m : M - 1) + 16 * kg;
-  }
-
-  // this wavefront's quarter of the groups, in double-buffered stages of GS groups
-  const int g0 = (G * wave) >> 2, g1 = (G * (wave + 1)) >> 2;
-  MfmaStage<MT, NT, GS> sa, sb2;
-  load_stage<MT, NT, GS>(sa, wrsrc, voff, xr, g0, g1 > g0 ? g1 : g0 + 1);
-
-  if (vec) {
-#pragma unroll
-    for (int q = 0; q < SBV; ++q) {
-      const int idx = tid + kThreads * q;
-      if (idx * 8 < span) {
-        const uint32_t ss[4] = {sv[q].x, sv[q].y, sv[q].z, sv[q].w};
-        const uint32_t bb[4] = {bv[q].x, bv[q].y, bv[q].z, bv[q].w};
-        uint4 lo, hi;  // entries idx*8 .. idx*8+7: (s | b << 16)
-        lo.x = (ss[0] & 0xffffu) | (bb[0] << 16);
-        lo.y = (ss[0] >> 16) | (bb[0] & 0xffff0000u);
-        lo.z = (ss[1] & 0xffffu) | (bb[1] << 16);
-        lo.w = (ss[1] >> 16) | (bb[1] & 0xffff0000u);
-        hi.x = (ss[2] & 0xffffu) | (bb[2] << 16);
-        hi.y = (ss[2] >> 16) | (bb[2] & 0xffff0000u);
-        hi.z = (ss[3] & 0xffffu) | (bb[3] << 16);
-        hi.w = (ss[3] >> 16) | (bb[3] & 0xffff0000u);
-        reinterpret_cast<uint4*>(sb_lds)[2 * idx] = lo;
-        reinterpret_cast<uint4*>(sb_lds)[2 * idx + 1] = hi;
-      }
-    }
-  } else {
-    for (int idx = tid; idx < span; idx += kThreads) {  // tail tile or unaligned scales
-      const int rr = idx / G, g = idx - rr * G;
-      const int row = row0 + rr < N ? row0 + rr : N - 1;
-      sb_lds[idx] = (uint32_t)P.s[(size_t)row * G + g] | ((uint32_t)P.b[(size_t)row * G + g] << 16);
-    }
-  }
-  lds_barrier();
-
-  const uint32_t* sbl = sb_lds + n * G;
-  f32x4_t acc[NT][MT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int g = g0; g < g1; g += 2 * GS) {
-    load_stage<MT, NT, GS>(sb2, wrsrc, voff, xr, g + GS, g1);
-    compute_stage<MT, NT, GS>(sa, sbl, G, g, g1, acc, magic);
-    if (g + GS >= g1) break;
-    load_stage<MT, NT, GS>(sa, wrsrc, voff, xr, g + 2 * GS, g1);
-    compute_stage<MT, NT, GS>(sb2, sbl, G, g + GS, g1, acc, magic);
-  }
-
-  // add the four quarters: waves 1..3 park their sums in LDS, wave 0 adds and stores
-  if (wave > 0) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) red[wave - 1][t][mt][lane] = acc[t][mt];
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int row = row0 + 16 * t + n;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        f32x4_t v = acc[t][mt];
-#pragma unroll
-        for (int q = 0; q < 3; ++q) v += red[q][t][mt][lane];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * mt + 4 * kg + r;
-          if (m < M && row < N) store_y(a, P, m, row, v[r]);
-        }
-      }
-    }
-  }
 }
 
 // ------------------------------------------------ MFMA kernel, 32 x 32 tiles (M >= 3)
@@ -713,17 +488,20 @@ __global__ __launch_bounds__(kThreads) void qmv_mfma_kernel(LaunchArgs a) {
 //
 // A workgroup's four wavefronts split its groups in quarters and add through LDS in a
 // fixed order.  A weight's groups may also be split over SPLITS workgroups (more
-// workgroups when N is small); each split then writes an fp32 partial (M, N) and
-// qmv_reduce_kernel adds the splits in order.  Loads are issued a stage of MS groups
-// ahead, unconditionally (past the range: offsets past the buffer, zero, no traffic).
+// workgroups when N is small): each split writes an fp32 partial of its tile, and the
+// last split of the tile to finish (a counter per tile, in the caller's workspace) adds
+// the partials in split order and writes y, then returns the counter to zero.  One
+// launch, and the same bits whatever order the splits finish in.  Partials and counters
+// go through sc1 accesses (coherent across the XCDs' L2 caches): every thread waits for
+// its partial stores before the workgroup's one atomic add, and the last split reads the
+// partials with sc1 loads, so no cache write-back or invalidate is needed.  Loads are
+// issued a stage of MS groups ahead, unconditionally (past the range: offsets past the
+// buffer, zero, no traffic).
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kMmaStage = 1;
-#ifndef IMQ_MMA
-#define IMQ_MMA 1
-#endif
-constexpr bool kUseMma = IMQ_MMA;
+constexpr int kMaxSplits = 16;  // partials the last split of a tile adds
 
 // One stage: GS groups of NT weight tiles (32 rows each), the matching x pieces and the
 // tiles' scales and biases.
@@ -794,7 +572,9 @@ __device__ __forceinline__ void mma_compute(const MmaStage<NT, GS>& st, int g, i
 template <int NT, bool PARTIAL>
 __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int splits,
                                                            float* __restrict__ partial,
-                                                           int64_t pstride) {
+                                                           int64_t pstride,
+                                                           uint32_t* __restrict__ counters,
+                                                           int tiles_max) {
   __shared__ f32x16_t red[3][NT][64];
   const int pi = blockIdx.y / splits, split = blockIdx.y - pi * splits;
   const Problem& P = a.p[pi];
@@ -842,38 +622,68 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
 #pragma unroll
     for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
   __syncthreads();
-  if (wave != 0) return;
+  if (!PARTIAL) {
+    if (wave != 0) return;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
+    for (int t = 0; t < NT; ++t) {
 #pragma unroll
-    for (int q = 0; q < 3; ++q) acc[t] += red[q][t][lane];
-    const int n = row0 + 32 * t + r;
-    if (n >= N) continue;
+      for (int q = 0; q < 3; ++q) acc[t] += red[q][t][lane];
+      const int n = row0 + 32 * t + r;
+      if (n >= N) continue;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = 8 * (e >> 2) + 4 * h + (e & 3);
-      if (m >= M) continue;
-      if (PARTIAL)
-        partial[pi * pstride + ((int64_t)split * M + m) * N + n] = acc[t][e];
-      else
-        store_y(a, P, m, n, acc[t][e]);
+      for (int e = 0; e < 16; ++e) {
+        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M) store_y(a, P, m, n, acc[t][e]);
+      }
+    }
+    return;
+  }
+  // this split's partial of the tile, then the tile's counter
+  const __amdgpu_buffer_rsrc_t prs =
+      buffer_rsrc(partial + pi * pstride, (uint32_t)((int64_t)splits * M * N * 4));
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) acc[t] += red[q][t][lane];
+      const int n = row0 + 32 * t + r;
+      if (n >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M)
+          store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(acc[t][e]));
+      }
     }
   }
-}
-
-// y[m][n] = sum over the splits (in split order) of the fp32 partials of one problem.
-__global__ __launch_bounds__(kThreads) void qmv_reduce_kernel(LaunchArgs a, int splits,
-                                                              const float* __restrict__ partial,
-                                                              int64_t pstride) {
-  const Problem& P = a.p[blockIdx.y];
-  const int N = P.N, M = a.M;
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= (int64_t)M * N) return;
-  const float* src = partial + pstride * blockIdx.y;
-  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
-  float v = 0.0f;
-  for (int s = 0; s < splits; ++s) v += src[((size_t)s * M + m) * N + n];
-  store_y(a, P, m, n, v);
+  wait_vmem();
+  __shared__ int last;
+  __syncthreads();
+  uint32_t* cnt = counters + (int64_t)pi * tiles_max + blockIdx.x;
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (uint32_t)(splits - 1);
+  __syncthreads();
+  if (!last) return;
+  // the last split: the tile's M x 32 NT outputs, every thread's partials loaded at once
+  // (at most kMaxSplits per output), then added in split order
+  const int cols = 32 * NT;
+  const uint32_t step = (uint32_t)(M * N * 4);
+  for (int i = tid; i < M * cols; i += kThreads) {
+    const int m = i / cols, n = row0 + i % cols;
+    const bool in = n < N;
+    const uint32_t o = (uint32_t)((m * N + n) * 4);
+    float t[kMaxSplits];
+#pragma unroll
+    for (int q = 0; q < kMaxSplits; ++q)
+      t[q] = __uint_as_float(load_b32_sc1(prs, in && q < splits ? o + q * step : kPastBuffer));
+    float v = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kMaxSplits; ++q)
+      if (q < splits) v += t[q];
+    if (in) store_y(a, P, m, n, v);
+  }
+  if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
 }
 
 // ------------------------------------------------------------------ dequantise
@@ -967,8 +777,6 @@ int32_t check_rows(const uint16_t* x, int64_t ldx, const void* y, int64_t ldy, i
 // the launch fits in LDS, the MFMA kernel otherwise.
 constexpr int kValuMaxRows = 2;
 constexpr size_t kValuLdsLimit = 64 * 1024;
-constexpr int kMfmaTiles = 2;  // 16-row tiles per MFMA workgroup
-constexpr size_t kMfmaLdsLimit = 48 * 1024;  // its (scale, bias) table; K up to 24576
 
 // Lanes per weight row for the VALU kernels: the widest of 64/32/16 that still gives
 // each lane at least four 16-byte chunks with at most 10% of the lanes' chunks idle.
@@ -1109,24 +917,23 @@ hipError_t launch_rows(const LaunchArgs& a, int grid_x, size_t lds, hipStream_t 
   return hipGetLastError();
 }
 
-constexpr int kMfmaStage = 4;  // groups of weight and x words loaded at once per wavefront
-
-template <int MT>
-hipError_t launch_mfma(const LaunchArgs& a, int grid_x, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((qmv_mfma_kernel<MT, kMfmaTiles, kMfmaStage>), dim3(grid_x, a.count),
-                     dim3(kThreads), lds, stream, a);
-  return hipGetLastError();
-}
-
 // The 32 x 32 MFMA kernel's plan: tiles of 32 rows and, when a workspace is given,
 // enough splits of the groups that the launch has about two workgroups per CU, each
-// split keeping at least 8 groups (2 per wavefront) and the partials' traffic small next
-// to the weights' (8 * splits * M * N bytes against N * K / 2).
+// split keeping at least 8 groups (2 per wavefront), at most kMaxSplits of them, and the
+// partials' traffic small next to the weights' (8 * splits * M * N bytes against
+// N * K / 2).  Workspace layout: a fixed region of kCounterBytes for the per-tile
+// counters (problem i's tile t at word i * grid_x + t; zero before the first call, and
+// every call leaves them at zero), then each problem's fp32 partials (splits * M * N,
+// pstride floats apart).  The counter region has the same place and size for every
+// launch, so calls of different shapes can share one workspace.
+constexpr size_t kCounterBytes = 64 * 1024;
+
 struct MmaPlan {
   int nt = 1;      // 32-row weight tiles per wavefront
   int grid_x = 0;
   int splits = 1;
   int64_t pstride = 0;  // floats per problem in the workspace
+  size_t bytes = 0;     // workspace the plan uses (0: no split)
 };
 
 #ifndef IMQ_MMA_NT_ROWS
@@ -1147,47 +954,44 @@ MmaPlan plan_mma(const LaunchArgs& a, size_t ws_bytes, int cu_count) {
     kmin = a.p[i].K < kmin ? a.p[i].K : kmin;
     nmax = a.p[i].N > nmax ? a.p[i].N : nmax;
   }
-  if (ws_bytes == 0) return pl;
+  if (ws_bytes <= kCounterBytes || (size_t)a.count * pl.grid_x * 4 > kCounterBytes) return pl;
   int sp = (2 * cu_count + tiles - 1) / tiles;
   sp = sp < gmin / 8 ? sp : gmin / 8;
   sp = sp < kmin / (16 * a.M) ? sp : kmin / (16 * a.M);
-  while (sp > 1 && (size_t)a.count * sp * a.M * nmax * sizeof(float) > ws_bytes) --sp;
-  if (sp > 1) {
+  sp = sp < kMaxSplits ? sp : kMaxSplits;
+  while (sp > 1 && kCounterBytes + (size_t)a.count * sp * a.M * nmax * sizeof(float) > ws_bytes) --sp;
+  if (sp > 1 && (int64_t)sp * a.M * nmax * 4 < ((int64_t)1 << 31)) {
     pl.splits = sp;
     pl.pstride = (int64_t)sp * a.M * nmax;
+    pl.bytes = kCounterBytes + (size_t)a.count * pl.pstride * sizeof(float);
   }
   return pl;
 }
 
 template <int NT>
-void launch_mma_nt(const LaunchArgs& a, const MmaPlan& pl, float* ws, hipStream_t stream) {
-  if (pl.splits == 1)
+void launch_mma_nt(const LaunchArgs& a, const MmaPlan& pl, void* ws, hipStream_t stream) {
+  if (pl.splits == 1) {
     hipLaunchKernelGGL((qmv_mma_kernel<NT, false>), dim3(pl.grid_x, a.count), dim3(kThreads), 0,
-                       stream, a, 1, nullptr, (int64_t)0);
-  else
+                       stream, a, 1, nullptr, (int64_t)0, nullptr, 0);
+  } else {
+    uint32_t* counters = static_cast<uint32_t*>(ws);
+    float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
     hipLaunchKernelGGL((qmv_mma_kernel<NT, true>), dim3(pl.grid_x, a.count * pl.splits),
-                       dim3(kThreads), 0, stream, a, pl.splits, ws, pl.pstride);
+                       dim3(kThreads), 0, stream, a, pl.splits, partial, pl.pstride, counters,
+                       pl.grid_x);
+  }
 }
 
-hipError_t launch_mma(const LaunchArgs& a, const MmaPlan& pl, float* ws, hipStream_t stream) {
+hipError_t launch_mma(const LaunchArgs& a, const MmaPlan& pl, void* ws, hipStream_t stream) {
   if (pl.nt == 2)
     launch_mma_nt<2>(a, pl, ws, stream);
   else
     launch_mma_nt<1>(a, pl, ws, stream);
-  if (pl.splits == 1) return hipGetLastError();
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  int nmax = 0;
-  for (int i = 0; i < a.count; ++i) nmax = a.p[i].N > nmax ? a.p[i].N : nmax;
-  const int64_t elems = (int64_t)a.M * nmax;
-  hipLaunchKernelGGL(qmv_reduce_kernel, dim3((uint32_t)((elems + kThreads - 1) / kThreads), a.count),
-                     dim3(kThreads), 0, stream, a, pl.splits, ws, pl.pstride);
   return hipGetLastError();
 }
 
-// Plans the work of every problem and launches one kernel for all of them (two when the
-// MFMA kernel splits the groups over a workspace).
-int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, float* ws = nullptr,
+// Plans the work of every problem and launches one kernel for all of them.
+int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* ws = nullptr,
                size_t ws_bytes = 0) {
   const int M = a.M;
   hipError_t e;
@@ -1204,27 +1008,12 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, float* 
     } else {
       e = launch_rows<2, 2>(a, grid_x, lds, stream);
     }
-  } else if (kUseMma) {
+  } else {
     for (int i = 0; i < a.count; ++i)
       if ((int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31))
         return fail(IMQ_EUNSUPPORTED, "a weight of 2 GiB or more exceeds the MFMA kernel's offsets");
     const MmaPlan pl = plan_mma(a, ws ? ws_bytes : 0, dev->cu_count);
     e = launch_mma(a, pl, ws, stream);
-  } else {
-    const int rows_per_wg = 16 * kMfmaTiles;
-    int kmax = 0;
-    for (int i = 0; i < a.count; ++i) {
-      const int t = (a.p[i].N + rows_per_wg - 1) / rows_per_wg;
-      grid_x = t > grid_x ? t : grid_x;
-      kmax = a.p[i].K > kmax ? a.p[i].K : kmax;
-    }
-    lds = (size_t)rows_per_wg * (kmax / 64) * 4;  // (s, b) per row and group
-    if (lds > kMfmaLdsLimit) return fail(IMQ_EUNSUPPORTED, "K too large for the MFMA kernel");
-    for (int i = 0; i < a.count; ++i)
-      if ((int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31))
-        return fail(IMQ_EUNSUPPORTED, "a weight of 2 GiB or more exceeds the MFMA kernel's offsets");
-    e = (M <= 16) ? launch_mfma<1>(a, grid_x, lds, stream)
-                  : launch_mfma<2>(a, grid_x, lds, stream);
   }
   if (e != hipSuccess)
     return fail(IMQ_ELAUNCH, std::string("qmv launch failed: ") + hipGetErrorString(e));
@@ -1362,8 +1151,7 @@ size_t imq_qmv_grouped_workspace(const imq_problem* problems, int32_t count, int
   }
   a.count = count;
   a.M = M;
-  const MmaPlan pl = plan_mma(a, (size_t)1 << 40, dev->cu_count);
-  return pl.splits > 1 ? (size_t)count * pl.pstride * sizeof(float) : 0;
+  return plan_mma(a, (size_t)1 << 40, dev->cu_count).bytes;
 }
 
 int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, int32_t M,

@@ -195,3 +195,58 @@ def test_python_errors(native):
         native.qmv(w, s, s, torch.zeros((33, 64), dtype=torch.bfloat16, device="cuda"))
     with pytest.raises(ValueError):
         native.qmv(w, s, s, torch.zeros((1, 64), dtype=torch.float32, device="cuda"))
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 300, 9728), (32, 2560, 4096), (17, 129, 2560)])
+def test_split_groups_repeat_bit_identical(native, oracle, m, n, k):
+    """Few rows, long K: the groups are split over workgroups whose partials the last one of
+    each tile adds in order.  The split is really taken (the library asks for a
+    workspace), five calls in a row give the same bits (the tile counters return to zero
+    after every call) and every call meets the oracle bound."""
+    import ctypes
+    pr = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 60 + m)
+    w, s, b, x = to_device(pr)
+    probs = (native.Problem * 1)()
+    probs[0] = native.Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), k,
+                              0, n, n, k)
+    assert native.lib().imq_qmv_grouped_workspace(probs, 1, m) > 0
+    del ctypes
+    announce("split groups", m, n, k)
+    first = native.qmv(w, s, b, x)
+    _check(oracle, pr, first)
+    for _ in range(4):
+        again = native.qmv(w, s, b, x)
+        assert np.array_equal(bf16_bits(again), bf16_bits(first))
+
+
+def test_split_calls_of_different_shapes_share_a_workspace(native, oracle):
+    """Decode-like alternation of split shapes on one stream (so one cached workspace):
+    q/k/v-like grouped, o-like, gate/up-like grouped and down-like calls at M = 32, three
+    rounds; every output meets the oracle bound and repeats its first round's bits."""
+    shapes = [[(4096, 2560), (1024, 2560), (1024, 2560)], [(2560, 4096)],
+              [(9728, 2560), (9728, 2560)], [(2560, 9728)]]
+    m = 32
+    calls = []
+    for j, group in enumerate(shapes):
+        prs = [oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 80 + 10 * j + i)
+               for i, (n, k) in enumerate(group)]
+        dev = [to_device(p) for p in prs]
+        calls.append((prs, dev))
+    announce("split shapes share a workspace")
+    first = None
+    for rnd in range(3):
+        outs = []
+        for prs, dev in calls:
+            outs.append(native.qmv_grouped([d[:3] for d in dev], [dev[0][3]] * len(dev)))
+        bits = [[bf16_bits(o) for o in group] for group in outs]
+        if first is None:
+            first = bits
+            for (prs, dev), group in zip(calls, outs):
+                for p, d, o in zip(prs, dev, group):
+                    rows = np.arange(0, p.w.shape[0], 7)
+                    pr = oracle.Problem(p.w, p.s, p.b, bf16_bits(dev[0][3]), 0)
+                    _check(oracle, pr, o, rows=rows)
+        else:
+            for a, b in zip(bits, first):
+                for x, y in zip(a, b):
+                    assert np.array_equal(x, y), rnd
