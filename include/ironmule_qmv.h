@@ -149,6 +149,22 @@ IMQ_API int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, i
  *   ironmule/cuda_native.py:265-266      probe reference: dequantise with fp32 scales
  *   ironmule/numeric_plans.py:462-464    the `dequantize` plan's fp32 weights
  */
+/* MoE gather: for each of `pairs` (token, expert) pairs p, the one-row product
+ *   y[p] = x[p / rows_per_x] W[idx[p]]^T
+ * where w, scales and biases hold `experts` stacked weights ((E, N, K/8) words and
+ * (E, N, K/64) bf16) and idx (pairs uint32, device memory) names each pair's expert.
+ * rows_per_x = 1 gives every pair its own activation row (a down projection); a larger
+ * value lets that many consecutive pairs share one row (gate/up: one token's row for all
+ * of its experts).  Each pair's row equals imq_qmv on that expert's weights, bit for bit.
+ * An index outside [0, experts) yields a row of zeros.  N * K / 64 must be even.
+ * Replaces the reference's gather kernel and routing, ironmule/cuda_native.py:130-144
+ * (ironmule_native_gather4) and 182-218 (_gather_qmv, gather_matmul). */
+IMQ_API int32_t imq_gather_qmv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                               int32_t experts, const uint16_t* x, int64_t ldx, int32_t rows_per_x,
+                               const uint32_t* idx, int32_t pairs, void* y, int64_t ldy, int32_t N,
+                               int32_t K, int32_t group_size, int32_t bits, int32_t y_dtype,
+                               void* stream);
+
 IMQ_API int32_t imq_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     void* out, int32_t out_dtype, int32_t N, int32_t K, int32_t group_size,
                     int32_t bits, void* stream);

@@ -104,6 +104,8 @@ _SIGNATURES = {
     "imq_qmv_grouped_ws": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P,
                             ctypes.c_size_t, _P], _I32),
     "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
+    "imq_gather_qmv": ([_P, _P, _P, _I32, _P, _I64, _I32, _P, _I32, _P, _I64, _I32, _I32, _I32,
+                        _I32, _I32, _P], _I32),
     "imq_last_error": ([ctypes.c_char_p, ctypes.c_size_t], _I32),
     # decode-step kernels (include/ironmule_decode.h)
     "imq_embed": ([_P, _P, _P, _P, _P, _I32, _I32, _I32, _P], _I32),
@@ -343,6 +345,40 @@ def qmv_grouped(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
         raise ValueError(f"the qmv kernels take 1 to {MAX_ROWS} rows, got {m}")
     _grouped_launch(probs, count, m, out_dtype, weights[0][0].device, stream)
     return result
+
+
+def gather_qmv(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, x: torch.Tensor,
+               idx: torch.Tensor, rows_per_x: int = 1, out_dtype: torch.dtype = torch.bfloat16,
+               out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """MoE gather (imq_gather_qmv): y[p] = x[p // rows_per_x] @ dequant(w[idx[p]]).T for the
+    P = idx.numel() pairs; w (E, N, K/8) int32, scales/biases (E, N, K/64) bf16, x (R, K)
+    bf16 contiguous rows, idx int32 on the device.  Returns (P, N)."""
+    if w.dim() != 3 or w.dtype != torch.int32:
+        raise ValueError("w must be an (experts, N, K/8) int32 tensor")
+    e, n, k = int(w.shape[0]), int(w.shape[1]), int(w.shape[2]) * 8
+    for name, t in (("scales", scales), ("biases", biases)):
+        if tuple(t.shape) != (e, n, k // GROUP_SIZE) or t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be a bf16 tensor of shape {(e, n, k // GROUP_SIZE)}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if not w.is_contiguous():
+        raise ValueError("w must be contiguous")
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != k or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous bf16 (rows, {k}) tensor")
+    if idx.dtype != torch.int32 or idx.device != w.device:
+        raise ValueError("idx must be an int32 tensor on the weights' device")
+    idx = idx.reshape(-1).contiguous()
+    pairs = int(idx.numel())
+    if pairs < 1 or rows_per_x < 1 or -(-pairs // rows_per_x) > x.shape[0]:
+        raise ValueError("need at least one pair and ceil(pairs / rows_per_x) activation rows")
+    if out is None:
+        out = torch.empty((pairs, n), dtype=out_dtype, device=w.device)
+    elif tuple(out.shape) != (pairs, n) or out.dtype != out_dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous (pairs, N) tensor of the output dtype")
+    _check(lib().imq_gather_qmv(_ptr(w), _ptr(scales), _ptr(biases), e, _ptr(x), k, int(rows_per_x),
+                                _ptr(idx), pairs, _ptr(out), n, n, k, GROUP_SIZE, BITS,
+                                _DTYPE_CODE[out_dtype], _stream(stream)))
+    return out
 
 
 def dequant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,

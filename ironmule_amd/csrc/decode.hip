@@ -170,6 +170,9 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
 // split order and writes the bf16 head.  Both orders are fixed, so results do not depend
 // on scheduling.
 
+constexpr int kMergeBatch = 16;  // splits whose partials a merge loads at once
+constexpr uint32_t kNegZeroPair = 0x80008000u;  // the bf16 pair (-0, -0)
+
 struct AttnLds {
   uint4 k[kChunk][17];        // a key row is 16 uint4; one of padding keeps lanes on
                               // distinct banks when lane t reads row t
@@ -238,7 +241,11 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
         const int p = tid + kThreads * i;
         const int row = p >> 4, col = p & 15;
         L.k[row][col] = kr[i];
-        *reinterpret_cast<uint4*>(&L.v[row][col * 4]) = vr[i];
+        // rows past the chunk's keys hold -0: their weight p is +0, so each adds -0,
+        // which leaves any sum unchanged (the value loop then needs no bound)
+        const uint32_t z = start + row < last ? 0u : kNegZeroPair, keep = start + row < last ? ~0u : 0u;
+        *reinterpret_cast<uint4*>(&L.v[row][col * 4]) =
+            make_uint4((vr[i].x & keep) | z, (vr[i].y & keep) | z, (vr[i].z & keep) | z, (vr[i].w & keep) | z);
       }
     }
     __syncthreads();
@@ -279,7 +286,8 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float c0 = 0.0f, c1 = 0.0f;
-      for (int t = 0; t < count; ++t) {
+#pragma unroll
+      for (int t = 0; t < kChunk; ++t) {  // t >= count: p = +0 times -0
         const float pt = L.p[wave][t];
         const uint32_t vd = L.v[t][lane];
         c0 = fmaf(pt, bf(vd & 0xffffu), c0);
@@ -319,15 +327,34 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(
     return;
   }
   const size_t p0 = ((size_t)b * Hq + h) * splits;
+  // the partials of kMergeBatch splits are loaded together before any is used; the
+  // arithmetic runs in split order
   float M = -INFINITY;
-  for (int s = 0; s < used; ++s) M = fmaxf(M, ml[2 * (p0 + s)]);
+  for (int s0 = 0; s0 < used; s0 += kMergeBatch) {
+    float mv[kMergeBatch];
+#pragma unroll
+    for (int q = 0; q < kMergeBatch; ++q) mv[q] = s0 + q < used ? ml[2 * (p0 + s0 + q)] : -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kMergeBatch; ++q) M = fmaxf(M, mv[q]);
+  }
   float Ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
-  for (int s = 0; s < used; ++s) {
-    const float e = expf(ml[2 * (p0 + s)] - M);
-    Ls = fmaf(ml[2 * (p0 + s) + 1], e, Ls);
-    const float2 pa = reinterpret_cast<const float2*>(part + (p0 + s) * kD)[lane];
-    a0 = fmaf(pa.x, e, a0);
-    a1 = fmaf(pa.y, e, a1);
+  for (int s0 = 0; s0 < used; s0 += kMergeBatch) {
+    float2 mlq[kMergeBatch], pq[kMergeBatch];
+#pragma unroll
+    for (int q = 0; q < kMergeBatch; ++q) {
+      const size_t sq = p0 + (s0 + q < used ? s0 + q : s0);
+      mlq[q] = reinterpret_cast<const float2*>(ml)[sq];
+      pq[q] = reinterpret_cast<const float2*>(part + sq * kD)[lane];
+    }
+#pragma unroll
+    for (int q = 0; q < kMergeBatch; ++q) {
+      if (s0 + q < used) {
+        const float e = expf(mlq[q].x - M);
+        Ls = fmaf(mlq[q].y, e, Ls);
+        a0 = fmaf(pq[q].x, e, a0);
+        a1 = fmaf(pq[q].y, e, a1);
+      }
+    }
   }
   o[2 * lane] = to_bf(a0 / Ls);
   o[2 * lane + 1] = to_bf(a1 / Ls);

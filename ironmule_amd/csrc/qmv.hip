@@ -457,6 +457,49 @@ __global__ __launch_bounds__(kThreads) void qmv_m1c_kernel(M1Args a) {
                    (bx - first) * (kThreads >> sh));
 }
 
+// ---------------------------------------------------- MoE gather (one row per pair)
+//
+// Pair p of a gather call computes y[p] = W[idx[p]] x[p / xs] with the one-row tile above
+// (the same lane shape, chunk order and sums, so each pair's row equals imq_qmv on that
+// expert's weights, bit for bit).  blockIdx.y is the pair and blockIdx.x its tile; the
+// expert index is read once per workgroup from device memory.  An index outside
+// [0, experts) gives a row of zeros.
+
+struct GatherArgs {
+  const uint32_t* w;  // (E, N, K/8)
+  const uint16_t* s;  // (E, N, K/64)
+  const uint16_t* b;
+  const uint16_t* x;  // row p / xs at x + (p / xs) * ldx
+  void* y;            // row p at y + p * ldy elements
+  const uint32_t* idx;
+  int64_t ldx, ldy;
+  int64_t w_stride, sb_stride;  // words / halves per expert
+  int32_t E, N, K, xs, sh, nch, y_f32, pad;
+};
+
+template <int NCH, int XR>
+__global__ __launch_bounds__(kThreads) void qmv_gather_kernel(GatherArgs a) {
+  const int pair = blockIdx.y;
+  const int row0 = blockIdx.x * (kThreads >> a.sh);
+  if (row0 >= a.N) return;
+  const uint32_t ex = __builtin_amdgcn_readfirstlane(a.idx[pair]);
+  void* yp = a.y_f32 ? static_cast<void*>(static_cast<float*>(a.y) + (int64_t)pair * a.ldy)
+                     : static_cast<void*>(static_cast<uint16_t*>(a.y) + (int64_t)pair * a.ldy);
+  if (ex >= (uint32_t)a.E) {
+    const int row = row0 + (int)(threadIdx.x >> a.sh);
+    if ((threadIdx.x & ((1 << a.sh) - 1)) == 0 && row < a.N) {
+      if (a.y_f32)
+        static_cast<float*>(yp)[row] = 0.0f;
+      else
+        static_cast<uint16_t*>(yp)[row] = 0;
+    }
+    return;
+  }
+  m1_tile<NCH, XR>(a.w + (int64_t)ex * a.w_stride, a.s + (int64_t)ex * a.sb_stride,
+                   a.b + (int64_t)ex * a.sb_stride, a.x + (int64_t)(pair / a.xs) * a.ldx, yp,
+                   a.K, a.N, a.sh, a.nch, a.y_f32, row0);
+}
+
 // ------------------------------------------------------- MFMA operand helpers
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
@@ -990,6 +1033,27 @@ hipError_t launch_mma(const LaunchArgs& a, const MmaPlan& pl, void* ws, hipStrea
   return hipGetLastError();
 }
 
+template <int NCH, int XR>
+hipError_t launch_gather_nx(const GatherArgs& a, int P, hipStream_t stream) {
+  const int rows = kThreads >> a.sh;
+  constexpr size_t lds = M1Lds<NCH, XR>::kBytes;
+  hipLaunchKernelGGL((qmv_gather_kernel<NCH, XR>), dim3((a.N + rows - 1) / rows, P), dim3(kThreads),
+                     lds, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const GatherArgs& a, int P, hipStream_t stream) {
+  const int xr = (a.K / 8 + kThreads - 1) / kThreads;
+  if (a.nch <= 2 && xr <= 2) return launch_gather_nx<2, 2>(a, P, stream);
+  if (a.nch <= 5) {
+    if (xr <= 2) return launch_gather_nx<5, 2>(a, P, stream);
+    if (xr <= 5) return launch_gather_nx<5, 5>(a, P, stream);
+  }
+  if (xr <= 2) return launch_gather_nx<8, 2>(a, P, stream);
+  if (xr <= 5) return launch_gather_nx<8, 5>(a, P, stream);
+  return launch_gather_nx<8, 8>(a, P, stream);
+}
+
 // Plans the work of every problem and launches one kernel for all of them.
 int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* ws = nullptr,
                size_t ws_bytes = 0) {
@@ -1165,6 +1229,53 @@ int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, int32_t M
   const DeviceInfo* dev = current_device(&code);
   if (!dev) return code;
   return launch(a, dev, static_cast<hipStream_t>(stream), workspace, workspace_bytes);
+}
+
+int32_t imq_gather_qmv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                       int32_t experts, const uint16_t* x, int64_t ldx, int32_t rows_per_x,
+                       const uint32_t* idx, int32_t pairs, void* y, int64_t ldy, int32_t N,
+                       int32_t K, int32_t group_size, int32_t bits, int32_t y_dtype,
+                       void* stream) {
+  int32_t code = check_format(N, K, group_size, bits);
+  if (code != IMQ_OK) return code;
+  if ((code = check_weights(w, scales, biases)) != IMQ_OK) return code;
+  if ((code = check_dtype(y_dtype)) != IMQ_OK) return code;
+  if (experts < 1) return fail(IMQ_EINVAL, "experts must be >= 1");
+  if (pairs < 1 || pairs > 65535) return fail(IMQ_EINVAL, "pairs must be in 1..65535");
+  if (rows_per_x < 1) return fail(IMQ_EINVAL, "rows_per_x must be >= 1");
+  if (!x || !y || !idx) return fail(IMQ_EINVAL, "x, y and idx must be non-null");
+  if (!aligned(x, 16) || (pairs > rows_per_x && ldx % 8)) return fail(IMQ_EINVAL, "x rows must be 16-byte aligned");
+  if (pairs > rows_per_x && ldx < K) return fail(IMQ_EINVAL, "ldx must be >= K");
+  if (pairs > 1 && ldy < N) return fail(IMQ_EINVAL, "ldy must be >= N");
+  if (!aligned(y, y_dtype == IMQ_F32 ? 4 : 2) || !aligned(idx, 4)) return fail(IMQ_EINVAL, "y or idx is misaligned");
+  const int sh = m1_lane_shift(K);
+  if (sh < 0) return fail(IMQ_EUNSUPPORTED, "K over 16384");
+  if (((int64_t)N * (K / 64)) % 2) return fail(IMQ_EUNSUPPORTED, "N * K / 64 must be even (4-byte aligned expert scales)");
+  if ((int64_t)N * (K / 2) >= ((int64_t)1 << 31)) return fail(IMQ_EUNSUPPORTED, "an expert of 2 GiB or more");
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
+  GatherArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w = w;
+  a.s = scales;
+  a.b = biases;
+  a.x = x;
+  a.y = y;
+  a.idx = idx;
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.w_stride = (int64_t)N * (K / 8);
+  a.sb_stride = (int64_t)N * (K / 64);
+  a.E = experts;
+  a.N = N;
+  a.K = K;
+  a.xs = rows_per_x;
+  a.sh = sh;
+  a.nch = ((K / 32) + (1 << sh) - 1) >> sh;
+  a.y_f32 = y_dtype == IMQ_F32;
+  const hipError_t e = launch_gather(a, pairs, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("gather launch failed: ") + hipGetErrorString(e));
+  return ok();
 }
 
 int32_t imq_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

@@ -447,6 +447,9 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
 // one LDS region.  The last split of a (request, KV head) to finish merges the partials
 // in split order (attention_combine_kernel's arithmetic) into the bf16 output.
 
+constexpr int kMergeBatch = 16;  // splits whose partials a merge loads at once
+constexpr uint32_t kNegZeroPair = 0x80008000u;  // the bf16 pair (-0, -0)
+
 struct AttnLds {
   uint4 kv[kChunk][17];  // K rows (padded), or V as uint32 [64][64]
   float p[4][2][kChunk];
@@ -627,8 +630,11 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
       for (int i = 0; i < 4; ++i) {
         const int p = tid + kThreads * i;
         const int row = p >> 4, col = p & 15;
+        // rows past the chunk's keys hold -0 (weight +0, so they add -0: no change)
+        const uint4 v = select4(start + row == newrow ? ~0u : 0u, vn4[col], vr[i]);
+        const uint32_t z = start + row < last ? 0u : kNegZeroPair, keep = start + row < last ? ~0u : 0u;
         *reinterpret_cast<uint4*>(&vt[row][col * 4]) =
-            select4(start + row == newrow ? ~0u : 0u, vn4[col], vr[i]);
+            make_uint4((v.x & keep) | z, (v.y & keep) | z, (v.z & keep) | z, (v.w & keep) | z);
       }
     }
     __syncthreads();
@@ -643,7 +649,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
       const int g = wave + 4 * r;
       if (g < G) {
         float c0 = 0.0f, c1 = 0.0f;
-        for (int t = 0; t < count; ++t) {
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) {  // t >= count: p = +0 times -0
           const float pt = L.p[wave][r][t];
           const uint32_t vd = vt[t][lane];
           c0 = fmaf(pt, bf(vd & 0xffffu), c0);
@@ -690,17 +697,39 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     if (g < G) {
       const int hh = kvh * G + g;
       const uint32_t p0 = (uint32_t)((b * Hq + hh) * splits);
+      // the partials of kMergeBatch splits are loaded together before any is used; the
+      // arithmetic runs in split order (attention_combine_kernel's)
       float Mx = -INFINITY;
-      for (int s2 = 0; s2 < used; ++s2)
-        Mx = fmaxf(Mx, __uint_as_float(load_b32_sc1(mrs, (p0 + s2) * 8u)));
+      for (int s0 = 0; s0 < used; s0 += kMergeBatch) {
+        float mv[kMergeBatch];
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q)
+          mv[q] = __uint_as_float(load_b32_sc1(mrs, s0 + q < used ? (p0 + s0 + q) * 8u : kPastBuffer));
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q)
+          if (s0 + q < used) Mx = fmaxf(Mx, mv[q]);
+      }
       float Lx = 0.0f, c0 = 0.0f, c1 = 0.0f;
-      for (int s2 = 0; s2 < used; ++s2) {
-        const float e = expf(__uint_as_float(load_b32_sc1(mrs, (p0 + s2) * 8u)) - Mx);
-        Lx = fmaf(__uint_as_float(load_b32_sc1(mrs, (p0 + s2) * 8u + 4u)), e, Lx);
-        const float px = __uint_as_float(load_b32_sc1(prs, ((p0 + s2) * kD + 2 * lane) * 4u));
-        const float py = __uint_as_float(load_b32_sc1(prs, ((p0 + s2) * kD + 2 * lane + 1) * 4u));
-        c0 = fmaf(px, e, c0);
-        c1 = fmaf(py, e, c1);
+      for (int s0 = 0; s0 < used; s0 += kMergeBatch) {
+        float mq[kMergeBatch], lq[kMergeBatch], xq[kMergeBatch], yq[kMergeBatch];
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q) {
+          const bool in = s0 + q < used;
+          const uint32_t po = p0 + s0 + q;
+          mq[q] = __uint_as_float(load_b32_sc1(mrs, in ? po * 8u : kPastBuffer));
+          lq[q] = __uint_as_float(load_b32_sc1(mrs, in ? po * 8u + 4u : kPastBuffer));
+          xq[q] = __uint_as_float(load_b32_sc1(prs, in ? (po * kD + 2 * lane) * 4u : kPastBuffer));
+          yq[q] = __uint_as_float(load_b32_sc1(prs, in ? (po * kD + 2 * lane + 1) * 4u : kPastBuffer));
+        }
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q) {
+          if (s0 + q < used) {
+            const float e = expf(mq[q] - Mx);
+            Lx = fmaf(lq[q], e, Lx);
+            c0 = fmaf(xq[q], e, c0);
+            c1 = fmaf(yq[q], e, c1);
+          }
+        }
       }
       const uint32_t o = (uint32_t)to_bf(c0 / Lx) | ((uint32_t)to_bf(c1 / Lx) << 16);
       store_b32_sc1(buffer_rsrc(out, out_bytes), (uint32_t)((b * Hq + hh) * kD + 2 * lane) * 2u, o);

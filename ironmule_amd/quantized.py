@@ -132,3 +132,50 @@ def library_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biase
         dense = _native.dequant(w, scales, biases, torch.float32)
         y = (rows.to(torch.float32) @ dense.T).to(x.dtype)
     return y.reshape(*lead, int(w.shape[0]))
+
+
+class QuantizedSwitchLinear(torch.nn.Module):
+    """A stack of `experts` 4-bit group-64 affine weights, (E, N, K/8) packed words with
+    (E, N, K/64) bf16 scales and biases (mlx-lm's QuantizedSwitchLinear layout); the call
+    takes activations and each row's expert indices."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 bias: torch.Tensor | None = None, group_size: int = GROUP_SIZE,
+                 bits: int = BITS) -> None:
+        super().__init__()
+        self.register_buffer("weight", weight)
+        self.register_buffer("scales", scales)
+        self.register_buffer("biases", biases)
+        self.register_buffer("bias", bias)
+        self.group_size = int(group_size)
+        self.bits = int(bits)
+
+    @property
+    def num_experts(self) -> int:
+        return int(self.weight.shape[0])
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor, sorted_indices: bool = False) -> torch.Tensor:
+        y = library_gather_matmul(x, self.weight, self.scales, self.biases, indices,
+                                  self.group_size, self.bits)
+        return y + self.bias[indices].unsqueeze(-2) if self.bias is not None else y
+
+
+def library_gather_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                          biases: torch.Tensor, indices: torch.Tensor,
+                          group_size: int = GROUP_SIZE, bits: int = BITS) -> torch.Tensor:
+    """The library gather path: every selected expert dequantised to fp32 and one batched
+    product, (*batch, M, K) x experts -> (*batch, M, N), batch = broadcast(x.shape[:-2],
+    indices.shape)."""
+    if group_size != GROUP_SIZE or bits != BITS:
+        raise ValueError("only 4-bit, group-64 weights are supported")
+    if not x.is_cuda:
+        raise _native.NativeUnavailable("the quantised layers run on the GPU only")
+    batch = torch.broadcast_shapes(x.shape[:-2], indices.shape)
+    xb = x.expand(*batch, *x.shape[-2:]).reshape(-1, x.shape[-2], x.shape[-1])
+    idx = indices.expand(batch).reshape(-1).to(torch.long)
+    dense = _native.dequant(w[idx].reshape(-1, w.shape[-1]).contiguous(),
+                            scales[idx].reshape(-1, scales.shape[-1]).contiguous(),
+                            biases[idx].reshape(-1, biases.shape[-1]).contiguous(), torch.float32)
+    dense = dense.reshape(idx.numel(), int(w.shape[1]), -1)
+    y = torch.bmm(xb.to(torch.float32), dense.transpose(1, 2).contiguous())
+    return y.to(x.dtype).reshape(*batch, x.shape[-2], int(w.shape[1]))

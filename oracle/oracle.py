@@ -182,6 +182,24 @@ def qmv_mlx(w, s, b, x, values_per_thread: int = 8, out_f32: bool = False,
     return y
 
 
+def gather_qmv_f64(w, s, b, x, idx, rows_per_x: int = 1, gs: int = GROUP_SIZE):
+    """The MoE gather (ironmule/cuda_native.py:133-144, 182-196): pair p is the one-row
+    product of expert idx[p] (w (E, N, K/8), s/b (E, N, K/64)) with activation row
+    p // rows_per_x.  Returns the fp64 products (P, N) and their |w*x| sums; an index
+    outside [0, E) gives zeros (this build's rule: the reference leaves it undefined)."""
+    e = w.shape[0]
+    pairs = len(idx)
+    ref = np.zeros((pairs, w.shape[1]), dtype=np.float64)
+    mag = np.zeros((pairs, w.shape[1]), dtype=np.float64)
+    for p in range(pairs):
+        ex = int(idx[p])
+        if not 0 <= ex < e:
+            continue
+        r, m = qmv_f64(w[ex], s[ex], b[ex], x[p // rows_per_x].reshape(1, -1), gs)
+        ref[p], mag[p] = r[0], m[0]
+    return ref, mag
+
+
 def _prep(w, s, b, x):
     w = np.ascontiguousarray(w, dtype=np.uint32)
     s = np.ascontiguousarray(s, dtype=np.uint16)

@@ -262,3 +262,31 @@ def test_synthetic_distribution(oracle):
     assert -0.1001 < b.min() and b.max() < 0.1001
     x = oracle.bf16_to_f32(pr.x)
     assert abs(float(x.mean())) < 0.05 and 0.95 < float(x.std()) < 1.05
+
+
+def test_gather_oracle_is_the_per_pair_product(oracle):
+    """The gather restatement: pair p equals the qmv of expert idx[p] on row p // rows_per_x
+    (the down form rows_per_x = 1 and the gate/up broadcast), and an index outside the
+    stack gives a zero row.  Planted mistake: reading row p instead of p // rows_per_x
+    changes the broadcast result."""
+    rng = np.random.default_rng(5)
+    e, n, k = 5, 12, 128
+    probs = [oracle.synthetic(n, k, 1, seed=oracle.SEED_BASE + 300 + i) for i in range(e)]
+    w = np.stack([p.w for p in probs])
+    s = np.stack([p.s for p in probs])
+    b = np.stack([p.b for p in probs])
+    x = oracle.f32_to_bf16(rng.standard_normal((3, k)).astype(np.float32))
+    idx = np.array([4, 0, 2, 2, 7, 1], dtype=np.int64)
+    for xs in (1, 2):
+        rows = x if xs == 2 else np.concatenate([x, x])
+        ref, mag = oracle.gather_qmv_f64(w, s, b, rows, idx, rows_per_x=xs)
+        for p, ex in enumerate(idx):
+            if ex >= e:
+                assert not ref[p].any() and not mag[p].any()
+                continue
+            want, _ = oracle.qmv_f64(w[ex], s[ex], b[ex], rows[p // xs].reshape(1, -1))
+            assert np.array_equal(ref[p], want[0])
+    # the broadcast reads row p // 2: pairs 0 and 1 share row 0, so a per-pair read differs
+    ref2, _ = oracle.gather_qmv_f64(w, s, b, x, idx[:2], rows_per_x=2)
+    wrong, _ = oracle.qmv_f64(w[idx[1]], s[idx[1]], b[idx[1]], x[1].reshape(1, -1))
+    assert not np.array_equal(ref2[1], wrong[0])
