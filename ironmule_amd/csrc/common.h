@@ -64,13 +64,15 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// Eight natural-order bf16 values (x0..x7 in d.x..d.w) -> the pair order of nibble_pair.
+// Eight natural-order bf16 values (x0..x7 in d.x..d.w) -> the pair order of nibble_pair,
+// one v_perm_b32 per output word (selector bytes 0-3 pick the second operand's bytes,
+// 4-7 the first's).
 __device__ __forceinline__ uint4 pair_order(uint4 d) {
   uint4 p;
-  p.x = (d.x & 0xffffu) | (d.z << 16);      // (x0, x4)
-  p.y = (d.x >> 16) | (d.z & 0xffff0000u);  // (x1, x5)
-  p.z = (d.y & 0xffffu) | (d.w << 16);      // (x2, x6)
-  p.w = (d.y >> 16) | (d.w & 0xffff0000u);  // (x3, x7)
+  p.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);  // (x0, x4)
+  p.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);  // (x1, x5)
+  p.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);  // (x2, x6)
+  p.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);  // (x3, x7)
   return p;
 }
 

@@ -610,6 +610,77 @@ __device__ __forceinline__ void mma_compute(const MmaStage<NT, GS>& st, int g, i
   }
 }
 
+// The end of a workgroup's tile: acc[t] (in the wavefronts with `holder`) covers rows
+// nbase + 32 t + r of y, the workgroup's tile rows [row0, row0 + cols).  Without splits the
+// holders store y.  With splits each split stores its fp32 partial, and the last split of
+// the tile to arrive (the tile's counter in the workspace) adds the partials in split order,
+// writes y and returns the counter to zero.  Every thread waits for its partial stores
+// before the workgroup's one atomic add; partials and counters use sc1 accesses.
+template <int NT, bool PARTIAL, int MAXS = kMaxSplits>
+__device__ __forceinline__ void finish_tiles(const LaunchArgs& a, const Problem& P, int pi,
+                                             int split, int splits, float* partial,
+                                             int64_t pstride, uint32_t* counters, int tiles_max,
+                                             const f32x16_t (&acc)[NT], bool holder, int nbase,
+                                             int row0, int cols, int* last) {
+  const int N = P.N, M = a.M, tid = threadIdx.x, lane = tid & 63;
+  const int r = lane & 31, h = lane >> 5;
+  if (!PARTIAL) {
+    if (!holder) return;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int n = nbase + 32 * t + r;
+      if (n >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M) store_y(a, P, m, n, acc[t][e]);
+      }
+    }
+    return;
+  }
+  const __amdgpu_buffer_rsrc_t prs =
+      buffer_rsrc(partial + pi * pstride, (uint32_t)((int64_t)splits * M * N * 4));
+  if (holder) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int n = nbase + 32 * t + r;
+      if (n >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M)
+          store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(acc[t][e]));
+      }
+    }
+  }
+  wait_vmem();
+  __syncthreads();
+  uint32_t* cnt = counters + (int64_t)pi * tiles_max + blockIdx.x;
+  if (tid == 0)
+    *last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (uint32_t)(splits - 1);
+  __syncthreads();
+  if (!*last) return;
+  // the last split: every thread's partials loaded at once (at most MAXS per output), then
+  // added in split order
+  const uint32_t step = (uint32_t)(M * N * 4);
+  for (int i = tid; i < M * cols; i += kThreads) {
+    const int m = i / cols, n = row0 + i % cols;
+    const bool in = n < N;
+    const uint32_t o = (uint32_t)((m * N + n) * 4);
+    float t[MAXS];
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q)
+      t[q] = __uint_as_float(load_b32_sc1(prs, in && q < splits ? o + q * step : kPastBuffer));
+    float v = 0.0f;
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q)
+      if (q < splits) v += t[q];
+    if (in) store_y(a, P, m, n, v);
+  }
+  if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
+}
+
 // NT weight tiles of 32 rows per wavefront (x, its pair order and the row sums shared by
 // them), four wavefronts splitting the groups of a workgroup's 32 * NT rows.
 template <int NT, bool PARTIAL>
@@ -660,73 +731,206 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
     mma_compute<NT, kMmaStage>(sb, g + kMmaStage, g1, acc, magic);
   }
 
-  // add the four quarters in order: waves 1..3 park theirs, wave 0 adds and stores
+  // add the four quarters in order: waves 1..3 park theirs, wave 0 adds
   if (wave > 0)
 #pragma unroll
     for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
   __syncthreads();
-  if (!PARTIAL) {
-    if (wave != 0) return;
+  if (wave == 0)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-#pragma unroll
-      for (int q = 0; q < 3; ++q) acc[t] += red[q][t][lane];
-      const int n = row0 + 32 * t + r;
-      if (n >= N) continue;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
-        if (m < M) store_y(a, P, m, n, acc[t][e]);
-      }
-    }
-    return;
-  }
-  // this split's partial of the tile, then the tile's counter
-  const __amdgpu_buffer_rsrc_t prs =
-      buffer_rsrc(partial + pi * pstride, (uint32_t)((int64_t)splits * M * N * 4));
-  if (wave == 0) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int q = 0; q < 3; ++q) acc[t] += red[q][t][lane];
-      const int n = row0 + 32 * t + r;
-      if (n >= N) continue;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
-        if (m < M)
-          store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(acc[t][e]));
-      }
-    }
-  }
-  wait_vmem();
   __shared__ int last;
-  __syncthreads();
-  uint32_t* cnt = counters + (int64_t)pi * tiles_max + blockIdx.x;
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           (uint32_t)(splits - 1);
-  __syncthreads();
-  if (!last) return;
-  // the last split: the tile's M x 32 NT outputs, every thread's partials loaded at once
-  // (at most kMaxSplits per output), then added in split order
-  const int cols = 32 * NT;
-  const uint32_t step = (uint32_t)(M * N * 4);
-  for (int i = tid; i < M * cols; i += kThreads) {
-    const int m = i / cols, n = row0 + i % cols;
-    const bool in = n < N;
-    const uint32_t o = (uint32_t)((m * N + n) * 4);
-    float t[kMaxSplits];
+  finish_tiles<NT, PARTIAL>(a, P, pi, split, splits, partial, pstride, counters, tiles_max, acc,
+                            wave == 0, row0, row0, 32 * NT, &last);
+}
+
+// ------------------------------ MFMA kernel, weights and x staged through LDS (M >= 3)
+//
+// The same 32 x 32 MFMA tiles and per-group arithmetic as qmv_mma_kernel, fed from LDS.  A
+// load instruction of qmv_mma_kernel's layout touches 32 rows for 32 bytes each; here
+// every global load reads whole 128-byte lines, and the MFMA layout is read back from LDS.
+//
+// Workgroup: 64 weight rows (two wavefronts along N, one 32-row tile each) times two
+// K-ranges (two wavefronts along K), so the two N-wavefronts of a K-range share its x.  A
+// stage is 4 groups (256 values of k) of both K-ranges:
+//   * weights: 2 x 64 rows x 128 B (one line per row), 144-byte LDS rows;
+//   * x: 2 x 32 rows x 512 B, stored in pair order, 528-byte LDS rows;
+//   * scales and biases: 2 x 64 rows x 8 B each.
+// (The row paddings make the MFMA-layout reads conflict-free.)  A stage's loads are issued
+// into registers before the previous stage is computed and written to LDS after it, one
+// barrier on each side.  Rows m >= M read row M-1 and are never stored; groups past a
+// K-range read zero (buffer offsets past the end).  The bias term is one fp32 MFMA
+// (v_mfma_f32_32x32x2_f32) per pair of groups: A = the two groups' row sums of x, B = the
+// two groups' c = b - 128 s per weight row.  Requires K % 256 == 0 and x rows at
+// x + m * ldx (no row-pointer table).
+namespace staged {
+constexpr int kWN = 2, kWK = 2;                   // wavefronts along N and along K
+constexpr int kRows = 32 * kWN;                   // weight rows per workgroup
+constexpr int kWRow = 144, kXRow = 528;           // LDS row strides (bytes)
+constexpr int kWBytes = kWK * kRows * kWRow;      // weights of a stage
+constexpr int kXBytes = kWK * 32 * kXRow;         // x of a stage
+constexpr int kSBBytes = kWK * kRows * 16;        // scales (8 B) and biases (8 B) per row
+constexpr int kStage = kWBytes + kXBytes + kSBBytes;
+constexpr int kWP = kWK * kRows * 8 / kThreads;   // 16-byte weight pieces per thread
+constexpr int kXP = kWK * 32 * 32 / kThreads;     // 16-byte x pieces per thread
+constexpr int kXPK = kXP / kWK;                   // ... per K-range
+constexpr int kMaxSplitsStaged = 4;
+static_assert(kWK * kRows * 2 == kThreads, "one scale or bias piece per thread");
+static_assert(kStage >= kWN * 64 * 64, "the K-range reduction reuses the stage");
+}  // namespace staged
+
+template <bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, int splits,
+                                                                  float* __restrict__ partial,
+                                                                  int64_t pstride,
+                                                                  uint32_t* __restrict__ counters,
+                                                                  int tiles_max) {
+  using namespace staged;
+  __shared__ __attribute__((aligned(16))) char lds[kStage];
+  __shared__ int last;
+  const int pi = blockIdx.y / splits, split = blockIdx.y - pi * splits;
+  const Problem& P = a.p[pi];
+  const int K = P.K, N = P.N, M = a.M;
+  const int row0 = blockIdx.x * kRows;
+  if (row0 >= N) return;  // past this problem's tiles
+  const int G = K >> 6, W = K >> 3;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wn = wave % kWN, wk = wave / kWN;
+  const int r = lane & 31, h = lane >> 5;
+  const uint32_t magic = in_vgpr(kMagic);
+
+  // the split's groups (whole stages), then the two K-ranges of whole stages
+  const int gs0 = (G * split) / splits / 4 * 4;
+  const int gs1 = split + 1 == splits ? G : (G * (split + 1)) / splits / 4 * 4;
+  const int span = ((gs1 - gs0 + kWK - 1) / kWK + 3) / 4 * 4;
+  const int nst = span / 4;
+  int klo[kWK], khi[kWK];
 #pragma unroll
-    for (int q = 0; q < kMaxSplits; ++q)
-      t[q] = __uint_as_float(load_b32_sc1(prs, in && q < splits ? o + q * step : kPastBuffer));
-    float v = 0.0f;
-#pragma unroll
-    for (int q = 0; q < kMaxSplits; ++q)
-      if (q < splits) v += t[q];
-    if (in) store_y(a, P, m, n, v);
+  for (int k = 0; k < kWK; ++k) {
+    klo[k] = gs0 + k * span;
+    khi[k] = klo[k] + span < gs1 ? klo[k] + span : gs1;
   }
-  if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
+
+  const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(P.w, (uint32_t)N * (uint32_t)W * 4u);
+  const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
+  const __amdgpu_buffer_rsrc_t srsrc = buffer_rsrc(P.s, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc = buffer_rsrc(P.b, sb_bytes);
+  const __amdgpu_buffer_rsrc_t xrsrc =
+      buffer_rsrc(P.x, (uint32_t)((M - 1) * P.ldx * 2 + K * 2));
+
+  // Staging.  x piece i of a thread: K-range i / kXPK, row (tid >> 5) + 8 (i % kXPK), piece
+  // tid & 31 of the row's 512 bytes.  Weight piece i: row slot (tid >> 3) + 32 i (row =
+  // slot % kRows, K-range slot / kRows), piece tid & 7 of the row's 128 bytes.  Scale or
+  // bias piece: threads [0, 128) scales, [128, 256) biases (uniform per wavefront), K-range
+  // and row from tid % 128.
+  const int xp = tid & 31, wp = tid & 7;
+  const uint32_t ldx2 = (uint32_t)P.ldx * 2u;
+  const uint32_t xdst0 = (uint32_t)(kWBytes + (tid >> 5) * kXRow + 16 * xp);
+  const uint32_t wdst0 = (uint32_t)((tid >> 3) * kWRow + 16 * wp);
+  const int sb_is_b = __builtin_amdgcn_readfirstlane(tid / (kWK * kRows));
+  const int sb_rem = tid % (kWK * kRows), sb_k = sb_rem / kRows;
+  const int sb_n = row0 + sb_rem % kRows < N ? row0 + sb_rem % kRows : N - 1;
+  const uint32_t sb_src = (uint32_t)sb_n * (uint32_t)G * 2u;
+  const uint32_t sb_dst = (uint32_t)(kWBytes + kXBytes + sb_rem * 16 + 8 * sb_is_b);
+
+  uint4 wreg[kWP], xreg[kXP];
+  u32x2_t sbreg;
+  auto fetch = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < kXP; ++i) {
+      const int k = i / kXPK, m = (tid >> 5) + 8 * (i % kXPK);
+      const int g = klo[k] + (xp >> 3) + 4 * st;
+      const uint32_t off = (uint32_t)(m < M ? m : M - 1) * ldx2 + 16u * (xp & 7) + 128u * (uint32_t)g;
+      xreg[i] = load_b128(xrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
+    }
+#pragma unroll
+    for (int i = 0; i < kWP; ++i) {
+      const int slot = (tid >> 3) + 32 * i, k = slot / kRows;
+      const int n = row0 + slot % kRows < N ? row0 + slot % kRows : N - 1;
+      const int g = klo[k] + (wp >> 1) + 4 * st;
+      const uint32_t off = (uint32_t)n * (uint32_t)W * 4u + 16u * (wp & 1) + 32u * (uint32_t)g;
+      wreg[i] = load_b128(wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
+    }
+    const int g = klo[sb_k] + 4 * st;
+    const uint32_t off = (sb_src + 2u * (uint32_t)g) | ((uint32_t)(g >= khi[sb_k]) << 31);
+    sbreg = __builtin_bit_cast(u32x2_t,
+                               __builtin_amdgcn_raw_buffer_load_b64(sb_is_b ? brsrc : srsrc, off, 0, 0));
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < kXP; ++i)
+      *reinterpret_cast<uint4*>(lds + xdst0 + (i / kXPK) * 32 * kXRow + 8 * (i % kXPK) * kXRow) =
+          pair_order(xreg[i]);
+#pragma unroll
+    for (int i = 0; i < kWP; ++i) *reinterpret_cast<uint4*>(lds + wdst0 + 32 * i * kWRow) = wreg[i];
+    *reinterpret_cast<u32x2_t*>(lds + sb_dst) = sbreg;
+  };
+
+  f32x16_t acc = {}, accb = {};
+  const u32x4_t ones_u = {kOnes, kOnes, kOnes, kOnes};
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
+  const f32x16_t zero = {};
+  const int wrow = 32 * wn + r;  // this lane's weight row in the workgroup
+  const uint32_t xrd = (uint32_t)(kWBytes + wk * 32 * kXRow + r * kXRow + 64 * h);
+  const uint32_t wrd = (uint32_t)(wk * kRows * kWRow + wrow * kWRow + 16 * h);
+  const uint32_t sbrd = (uint32_t)(kWBytes + kXBytes + (wk * kRows + wrow) * 16);
+
+  fetch(0);
+  for (int st = 0; st < nst; ++st) {
+    __builtin_amdgcn_sched_barrier(0);
+    store();
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(st + 1);  // past the last stage every offset is past its buffer: no traffic
+    __builtin_amdgcn_sched_barrier(0);
+    const u32x2_t s2 = *reinterpret_cast<const u32x2_t*>(lds + sbrd);
+    const u32x2_t b2 = *reinterpret_cast<const u32x2_t*>(lds + sbrd + 8);
+    float spair = 0.0f, cpair = 0.0f;
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      bf16x8_t xa[4];
+      f32x16_t p1 = zero;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        xa[s] = as_bf16x8(*reinterpret_cast<const uint4*>(lds + xrd + gi * 128 + 16 * s));
+        p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, xa[s], p1, 0, 0, 0);  // row sums
+      }
+      const uint4 wv = *reinterpret_cast<const uint4*>(lds + wrd + gi * 32);
+      const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+      f32x16_t pp = zero;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        pp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[s], unpack_word(wd[s], magic), pp, 0, 0, 0);
+      const uint32_t sw = gi < 2 ? s2.x : s2.y, bw = gi < 2 ? b2.x : b2.y;
+      const float sc = __uint_as_float((gi & 1) ? (sw & 0xffff0000u) : (sw << 16));
+      const float bb = __uint_as_float((gi & 1) ? (bw & 0xffff0000u) : (bw << 16));
+      const float cg = fmaf(-128.0f, sc, bb);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = fmaf(sc, pp[e], acc[e]);
+      if (gi & 1)  // lanes h = 0 / 1 carry the pair's first / second group
+        accb = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? p1[0] : spair, h ? cg : cpair, accb, 0, 0, 0);
+      else {
+        spair = p1[0];
+        cpair = cg;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();  // every wavefront is done with this stage
+  }
+  acc += accb;
+
+  // the two K-ranges of each tile add through LDS (K-range 0 holds the sum)
+  f32x16_t* red = reinterpret_cast<f32x16_t*>(lds);
+  if (wk > 0) red[wn * 64 + lane] = acc;
+  __syncthreads();
+  if (wk == 0) acc += red[wn * 64 + lane];
+  f32x16_t tiles[1] = {acc};
+  finish_tiles<1, PARTIAL, kMaxSplitsStaged>(a, P, pi, split, splits, partial, pstride, counters,
+                                             tiles_max, tiles,
+                                             wk == 0, row0 + 32 * wn, row0, kRows, &last);
 }
 
 // ------------------------------------------------------------------ dequantise
@@ -972,7 +1176,8 @@ hipError_t launch_rows(const LaunchArgs& a, int grid_x, size_t lds, hipStream_t 
 constexpr size_t kCounterBytes = 64 * 1024;
 
 struct MmaPlan {
-  int nt = 1;      // 32-row weight tiles per wavefront
+  bool staged = false;  // qmv_mma_staged_kernel (else qmv_mma_kernel)
+  int nt = 1;           // qmv_mma_kernel: 32-row weight tiles per wavefront
   int grid_x = 0;
   int splits = 1;
   int64_t pstride = 0;  // floats per problem in the workspace
@@ -983,8 +1188,46 @@ struct MmaPlan {
 #define IMQ_MMA_NT_ROWS 8192
 #endif
 
+// The staged kernel's plan, when it applies: every K a multiple of 256, x rows strided (no
+// pointer table) with every row offset inside a 2 GiB buffer, and either at least half a
+// workgroup per CU without splitting (64-row tiles), or K >= 8192 with a workspace, split
+// into at most 4 ranges of whole stages toward 0.6 workgroups per CU.  (Measured on MI355X
+// at M = 4..32: these are the launches where it beats qmv_mma_kernel.)
+bool plan_staged(const LaunchArgs& a, size_t ws_bytes, int cu_count, MmaPlan* pl) {
+  if (a.table) return false;
+  int tiles = 0, gmin = 1 << 30, nmax = 0, grid_x = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const Problem& P = a.p[i];
+    if (P.K % 256 != 0) return false;
+    if ((int64_t)(a.M - 1) * P.ldx * 2 + (int64_t)P.K * 2 >= ((int64_t)1 << 31)) return false;
+    const int t = (P.N + staged::kRows - 1) / staged::kRows;
+    tiles += t;
+    grid_x = t > grid_x ? t : grid_x;
+    gmin = P.K / 64 < gmin ? P.K / 64 : gmin;
+    nmax = P.N > nmax ? P.N : nmax;
+  }
+  if ((size_t)a.count * grid_x * 4 > kCounterBytes) return false;
+  int sp = 1;
+  if (2 * tiles < cu_count) {
+    if (gmin < 128 || ws_bytes <= kCounterBytes) return false;
+    sp = (6 * cu_count + 10 * tiles - 1) / (10 * tiles);
+    sp = sp < staged::kMaxSplitsStaged ? sp : staged::kMaxSplitsStaged;
+    while (sp > 1 && kCounterBytes + (size_t)a.count * sp * a.M * nmax * sizeof(float) > ws_bytes) --sp;
+    if (sp < 2 || (int64_t)sp * a.M * nmax * 4 >= ((int64_t)1 << 31)) return false;
+  }
+  pl->staged = true;
+  pl->grid_x = grid_x;
+  pl->splits = sp;
+  if (sp > 1) {
+    pl->pstride = (int64_t)sp * a.M * nmax;
+    pl->bytes = kCounterBytes + (size_t)a.count * pl->pstride * sizeof(float);
+  }
+  return true;
+}
+
 MmaPlan plan_mma(const LaunchArgs& a, size_t ws_bytes, int cu_count) {
   MmaPlan pl;
+  if (plan_staged(a, ws_bytes, cu_count, &pl)) return pl;
   int ntotal = 0;
   for (int i = 0; i < a.count; ++i) ntotal += a.p[i].N;
   pl.nt = ntotal >= IMQ_MMA_NT_ROWS ? 2 : 1;  // wide launches share x over two tiles
@@ -1026,6 +1269,19 @@ void launch_mma_nt(const LaunchArgs& a, const MmaPlan& pl, void* ws, hipStream_t
 }
 
 hipError_t launch_mma(const LaunchArgs& a, const MmaPlan& pl, void* ws, hipStream_t stream) {
+  if (pl.staged) {
+    if (pl.splits == 1) {
+      hipLaunchKernelGGL((qmv_mma_staged_kernel<false>), dim3(pl.grid_x, a.count), dim3(kThreads),
+                         0, stream, a, 1, nullptr, (int64_t)0, nullptr, 0);
+    } else {
+      uint32_t* counters = static_cast<uint32_t*>(ws);
+      float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+      hipLaunchKernelGGL((qmv_mma_staged_kernel<true>), dim3(pl.grid_x, a.count * pl.splits),
+                         dim3(kThreads), 0, stream, a, pl.splits, partial, pl.pstride, counters,
+                         pl.grid_x);
+    }
+    return hipGetLastError();
+  }
   if (pl.nt == 2)
     launch_mma_nt<2>(a, pl, ws, stream);
   else
