@@ -358,8 +358,8 @@ def copy_calibration(torch, device) -> None:
 
 def _short(name: str) -> str:
     for marker in ("stream_chain_kernel", "stream_kernel", "qmv_stage_kernel", "attention_stage_kernel",
-                   "step_kernel", "reset_kernel", "qmv_gather_kernel", "qmv_m1c_kernel", "qmv_m1_kernel", "qmv_rows_kernel", "qmv_mfma_kernel",
-                   "qmv_mma_kernel", "qmv_reduce_kernel",
+                   "step_kernel", "reset_kernel", "qmv_gather_kernel", "qmv_m1c_kernel", "qmv_m1_kernel", "qmv_rows_kernel",
+                   "qmv_mma_staged_kernel", "qmv_mma_kernel",
                    "dequant_kernel", "embed_kernel", "add_rmsnorm_kernel", "qk_norm_rope_kernel",
                    "attention_partial_kernel", "attention_combine_kernel", "silu_mul_kernel"):
         if marker in name:

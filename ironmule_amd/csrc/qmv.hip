@@ -776,7 +776,7 @@ constexpr int kStage = kWBytes + kXBytes + kSBBytes;
 constexpr int kWP = kWK * kRows * 8 / kThreads;   // 16-byte weight pieces per thread
 constexpr int kXP = kWK * 32 * 32 / kThreads;     // 16-byte x pieces per thread
 constexpr int kXPK = kXP / kWK;                   // ... per K-range
-constexpr int kMaxSplitsStaged = 4;
+constexpr int kMaxSplitsStaged = 8;
 static_assert(kWK * kRows * 2 == kThreads, "one scale or bias piece per thread");
 static_assert(kStage >= kWN * 64 * 64, "the K-range reduction reuses the stage");
 }  // namespace staged
@@ -1189,10 +1189,11 @@ struct MmaPlan {
 #endif
 
 // The staged kernel's plan, when it applies: every K a multiple of 256, x rows strided (no
-// pointer table) with every row offset inside a 2 GiB buffer, and either at least half a
-// workgroup per CU without splitting (64-row tiles), or K >= 8192 with a workspace, split
-// into at most 4 ranges of whole stages toward 0.6 workgroups per CU.  (Measured on MI355X
-// at M = 4..32: these are the launches where it beats qmv_mma_kernel.)
+// pointer table) with every row offset inside a 2 GiB buffer, and either at least 0.3
+// workgroups per CU without splitting (64-row tiles), or K >= 4096 with a workspace, the
+// groups split toward about one workgroup per CU (at most kMaxSplitsStaged ways, at least
+// 16 groups per split).  (Measured on MI355X at M = 4..32, Qwen3-4B projections and the
+// K = 3840 shape: these are the launches where it beats qmv_mma_kernel.)
 bool plan_staged(const LaunchArgs& a, size_t ws_bytes, int cu_count, MmaPlan* pl) {
   if (a.table) return false;
   int tiles = 0, gmin = 1 << 30, nmax = 0, grid_x = 0;
@@ -1208,10 +1209,11 @@ bool plan_staged(const LaunchArgs& a, size_t ws_bytes, int cu_count, MmaPlan* pl
   }
   if ((size_t)a.count * grid_x * 4 > kCounterBytes) return false;
   int sp = 1;
-  if (2 * tiles < cu_count) {
-    if (gmin < 128 || ws_bytes <= kCounterBytes) return false;
-    sp = (6 * cu_count + 10 * tiles - 1) / (10 * tiles);
+  if (10 * tiles < 3 * cu_count) {
+    if (gmin < 64 || ws_bytes <= kCounterBytes) return false;
+    sp = (15 * cu_count + 16 * tiles - 1) / (16 * tiles);
     sp = sp < staged::kMaxSplitsStaged ? sp : staged::kMaxSplitsStaged;
+    sp = sp < gmin / 16 ? sp : gmin / 16;
     while (sp > 1 && kCounterBytes + (size_t)a.count * sp * a.M * nmax * sizeof(float) > ws_bytes) --sp;
     if (sp < 2 || (int64_t)sp * a.M * nmax * 4 >= ((int64_t)1 << 31)) return false;
   }

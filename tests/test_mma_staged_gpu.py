@@ -1,7 +1,7 @@
 """GPU parity of the staged MFMA kernel (qmv_mma_staged_kernel, M >= 3), through the C ABI.
 
 The launch plan takes it when every K is a multiple of 256, x rows are strided (no row
-pointer table) and either the launch has at least 128 tiles of 64 weight rows, or K >= 8192
+pointer table) and either the launch has at least 77 tiles of 64 weight rows, or K >= 4096
 and a split workspace is given.  The shapes below are chosen to meet those conditions (or,
 for the fallback case, to miss exactly one).  Bars are the oracle's (oracle.check_bf16 /
 check_f32): bf16 outputs within 1 bf16 ulp of the exactly computed product plus the fp32
@@ -53,7 +53,7 @@ def test_staged_wide_launch_matches_oracle(native, oracle, m):
 
 @pytest.mark.parametrize("m,n", [(4, 200), (32, 129)])
 def test_staged_split_repeats_bit_identical(native, oracle, m, n):
-    """Few rows and K = 8192: the groups are split four ways (the library asks for a
+    """Few rows and K = 8192: the groups are split eight ways (the library asks for a
     workspace), the last split of each tile adds the partials in order; five calls give
     the same bits and meet the oracle."""
     k = 8192
