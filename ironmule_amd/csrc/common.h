@@ -144,13 +144,16 @@ __host__ __device__ inline int m1_lane_shift(int K) {
 }
 
 // Decode attention's split of each (request, KV head) pair's keys: whole 64-key chunks per
-// split, as many splits as it takes to give the launch about 4096 workgroups (at most one
-// split per chunk).  Shared by every attention path so that they merge the same partials
-// in the same order.
+// split, as many splits as it takes to give the launch about IMQ_ATTN_WORKGROUPS
+// workgroups (at most one split per chunk).  Shared by every attention path so that they
+// merge the same partials in the same order.
+#ifndef IMQ_ATTN_WORKGROUPS
+#define IMQ_ATTN_WORKGROUPS 4096
+#endif
 __host__ inline void attention_splits(int B, int Hkv, int span, int* splits, int* chunks_per_split) {
   const int chunks = (span + 63) / 64;
   const int pairs = B * Hkv;
-  int sp = (4096 + pairs - 1) / pairs;
+  int sp = (IMQ_ATTN_WORKGROUPS + pairs - 1) / pairs;
   sp = sp < chunks ? sp : chunks;
   sp = sp > 1 ? sp : 1;
   const int c = (chunks + sp - 1) / sp;

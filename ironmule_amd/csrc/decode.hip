@@ -161,10 +161,10 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
 // attention_partial_kernel: workgroup (split s, KV head, request b) walks its share of
 // the request's keys in 64-key chunks (the next chunk's loads in flight while one
 // computes) and serves the G query heads that read that KV head (one wavefront per head,
-// G <= 8).  Per chunk, lane t scores key t (64 bf16 dot2 against the head's q), the chunk
-// max and sum come from butterflies, lane i accumulates dimensions 2i, 2i+1 of p . V, and
-// the chunk is merged into the running (max, sum, acc) of the split.  The split's partial
-// goes to the workspace.
+// G <= 8, their q staged in LDS once).  Per chunk, lane t scores key t (64 bf16 dot2
+// against the head's q), the chunk max and sum come from butterflies, lane i accumulates
+// dimensions 2i, 2i+1 of p . V, and the chunk is merged into the running (max, sum, acc)
+// of the split.  The split's partial goes to the workspace.
 //
 // attention_combine_kernel: one wavefront per (request, query head) merges the splits in
 // split order and writes the bf16 head.  Both orders are fixed, so results do not depend
@@ -178,6 +178,7 @@ struct AttnLds {
                               // distinct banks when lane t reads row t
   uint32_t v[kChunk][kD / 2];  // lane i reads dword i of a row: conflict-free
   float p[4][kChunk];
+  uint4 q[8][kD / 8];         // the workgroup's query heads (read as broadcasts)
 };
 
 struct AttnGeometry {
@@ -231,6 +232,10 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
         k3 = kb[piece(first, 3)];
   uint4 v0 = vb[piece(first, 0)], v1 = vb[piece(first, 1)], v2 = vb[piece(first, 2)],
         v3 = vb[piece(first, 3)];
+  // the G query heads of this KV head, once (the loop's first barrier publishes them)
+  if (tid < G * (kD / 8))
+    L.q[tid / (kD / 8)][tid % (kD / 8)] =
+        reinterpret_cast<const uint4*>(q + ((size_t)b * Hq + kvh * G) * kD)[tid];
   for (int start = first; start < last; start += kChunk) {
     const int count = min(kChunk, last - start);
     __syncthreads();  // the previous chunk's readers are done
@@ -264,13 +269,12 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
     for (int r = 0; r < 2; ++r) {
       const int g = wave + 4 * r;
       if (g >= G) break;
-      const uint4* qv = reinterpret_cast<const uint4*>(q + ((size_t)b * Hq + kvh * G + g) * kD);
       float sc = -INFINITY;
       if (lane < count) {
         float d = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const uint4 a = qv[j], kk = L.k[lane][j];
+          const uint4 a = L.q[g][j], kk = L.k[lane][j];
           d = dot2(a.x, kk.x, d);
           d = dot2(a.y, kk.y, d);
           d = dot2(a.z, kk.z, d);
