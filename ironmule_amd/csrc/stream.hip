@@ -138,22 +138,25 @@ struct Tile {
   uint32_t b[2];
 };
 
-// One problem of a stage, resolved once and held in scalar registers while a wavefront
-// works through its tiles: global tiles t0 .. tend-1 of the program.
+// One problem of a stage (global tiles t0 .. tend-1 of the program), resolved once while
+// a wavefront works through its tiles, with what every tile needs: the buffer descriptors
+// and row stride (scalar), and per lane its chunk column j, its row in the tile rl, the
+// byte offsets those give and how many of its kNch chunk slots hold chunks of the row.
 struct Site {
-  const uint32_t* w;
-  const uint16_t* s;
-  const uint16_t* b;
+  __amdgpu_buffer_rsrc_t wr, sr, br, yr;
   uint16_t* y;
   int N, K, sh, nch, xoff, live, t0, tend;
+  int rows;        // rows per tile: 64 >> sh
+  uint32_t w4;     // bytes per weight row (K / 2)
+  // per lane
+  uint32_t wlane;  // rl * w4 + 16 j
+  int rlG;         // rl * G: the lane's row's first scale/bias half within the tile
+  int rl, j, nvalid;
 };
 
 __device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, int pi) {
   StageRef S = stage_at(st, si);
   Site c;
-  c.w = S.p[pi].w;
-  c.s = S.p[pi].s;
-  c.b = S.p[pi].b;
   c.y = S.p[pi].y;
   c.N = S.p[pi].N;
   c.live = S.p[pi].live;
@@ -163,6 +166,24 @@ __device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, i
   c.xoff = S.xoff;
   c.t0 = S.first + (pi == 0 ? 0 : S.p[pi - 1].tile_end);
   c.tend = S.first + S.p[pi].tile_end;
+  const int G = c.K >> 6, C = c.K >> 5;
+  c.w4 = (uint32_t)c.K >> 1;
+  // the scale/bias range rounded up to whole dwords: the extra half lies in the same
+  // aligned dword as the last one, so it is mapped, and it belongs to no row
+  const uint32_t sbb = ((uint32_t)c.N * (uint32_t)G * 2u + 3u) & ~3u;
+  c.wr = buffer_rsrc(S.p[pi].w, (uint32_t)c.N * c.w4);
+  c.sr = buffer_rsrc(S.p[pi].s, sbb);
+  c.br = buffer_rsrc(S.p[pi].b, sbb);
+  c.yr = buffer_rsrc(c.y, (uint32_t)c.N * 2u);
+  c.rows = 64 >> c.sh;
+  const int lane = threadIdx.x & 63;
+  c.j = lane & ((1 << c.sh) - 1);
+  c.rl = lane >> c.sh;
+  c.wlane = (uint32_t)c.rl * c.w4 + 16u * (uint32_t)c.j;
+  c.rlG = c.rl * G;
+  // chunks j, j + 2^sh, ... below C, at most nch of them
+  const int nv = (C - c.j + (1 << c.sh) - 1) >> c.sh;
+  c.nvalid = nv < c.nch ? nv : c.nch;
   return c;
 }
 
@@ -202,31 +223,22 @@ __device__ __forceinline__ Span span_of(const Site& c, int row0) {
 // Issues the loads of global tile g of site c (valid false: every load reads past its
 // buffer, which returns zero without a memory access).
 __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int lane, Tile& T) {
-  const int C = c.K >> 5, G = c.K >> 6, W = c.K >> 3;
-  const int j = lane & ((1 << c.sh) - 1);
-  const int row0 = (g - c.t0) * (64 >> c.sh);
-  const int row = row0 + (lane >> c.sh);
-  // the scale/bias range rounded up to whole dwords: the extra half lies in the same
-  // aligned dword as the last one, so it is mapped, and it belongs to no row
-  const uint32_t sbb = ((uint32_t)c.N * (uint32_t)G * 2u + 3u) & ~3u;
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(c.w, (uint32_t)c.N * (uint32_t)W * 4u);
-  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(c.s, sbb);
-  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(c.b, sbb);
-  const bool live = valid && row < c.N;
-  const uint32_t wrow = (uint32_t)row * (uint32_t)W * 4u;
+  const int row0 = (g - c.t0) * c.rows;
+  const bool live = valid && row0 + c.rl < c.N;
+  const uint32_t wbase = (uint32_t)row0 * c.w4 + c.wlane;
+  const uint32_t cstep = 16u << c.sh;  // bytes between a lane's chunks
 #pragma unroll
   for (int i = 0; i < kNch; ++i) {
-    const int kc = j + (i << c.sh);
-    const bool in = live && i < c.nch && kc < C;
-    T.w[i] = load_b128(wr, in ? wrow + 16u * kc : kPastBuffer);
+    const bool in = live && i < c.nvalid;
+    T.w[i] = load_b128(c.wr, in ? wbase + cstep * i : kPastBuffer);
   }
   const Span sp = span_of(c, row0);
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int d = lane + 64 * q;
     const uint32_t off = valid && d < sp.nd ? sp.a0 + 4u * d : kPastBuffer;
-    T.s[q] = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
-    T.b[q] = __builtin_amdgcn_raw_buffer_load_b32(br, off, 0, 0);
+    T.s[q] = __builtin_amdgcn_raw_buffer_load_b32(c.sr, off, 0, 0);
+    T.b[q] = __builtin_amdgcn_raw_buffer_load_b32(c.br, off, 0, 0);
   }
 }
 
@@ -236,43 +248,41 @@ __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int 
 // order, the dot2 chains and the cross-lane sums are the one-row kernel's.
 __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, const Tile& T,
                                              const char* smem, uint32_t* sbw, uint32_t magic) {
-  const int C = c.K >> 5, G = c.K >> 6;
-  const int j = lane & ((1 << c.sh) - 1);
-  const int rl = lane >> c.sh;
-  const int row0 = (g - c.t0) * (64 >> c.sh);
-  const int row = row0 + rl;
+  const int C = c.K >> 5;
+  const int row0 = (g - c.t0) * c.rows;
+  const int row = row0 + c.rl;
   // (scale | bias << 16) per half of the span, in this wavefront's own LDS area
 #pragma unroll
   for (int q = 0; q < 2; ++q)
     *reinterpret_cast<uint2*>(sbw + 2 * (lane + 64 * q)) =
         make_uint2((T.s[q] & 0xffffu) | (T.b[q] << 16), (T.s[q] >> 16) | (T.b[q] & 0xffff0000u));
-  const int hbase = rl * G + span_of(c, row0).mis;
+  const int hbase = c.rlG + span_of(c, row0).mis;
   const char* xs = smem + c.xoff;
   const uint4* xq = reinterpret_cast<const uint4*>(xs);
   const float* sx = reinterpret_cast<const float*>(xs + (size_t)C * 64);
+  // Every chunk slot is computed (no branch, so the LDS reads of all chunks can be issued
+  // early); a slot past the lane's chunks is discarded by the select, as its zero weights
+  // would not be (they stand for q = 0, not for nothing).
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < kNch; ++i) {
-    if (i < c.nch) {
-      const int kc = j + (i << c.sh);
-      const bool valid = kc < C;
-      const int kk = valid ? kc : 0;
-      const uint32_t sb = sbw[hbase + (kk >> 1)];
-      const float sc = __uint_as_float(sb << 16);
-      const float bi = __uint_as_float(sb & 0xffff0000u);
-      const float sxm = sx[kk];
-      const float d = chunk_dot(T.w[i], xq[kk], xq[C + kk], xq[2 * C + kk], xq[3 * C + kk],
-                                -128.0f * sxm, magic);
-      const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
-      acc = valid ? v : acc;
-    }
+    const bool valid = i < c.nvalid;
+    const int kk = valid ? c.j + (i << c.sh) : 0;
+    const uint32_t sb = sbw[hbase + (kk >> 1)];
+    const float sc = __uint_as_float(sb << 16);
+    const float bi = __uint_as_float(sb & 0xffff0000u);
+    const float sxm = sx[kk];
+    const float d = chunk_dot(T.w[i], xq[kk], xq[C + kk], xq[2 * C + kk], xq[3 * C + kk],
+                              -128.0f * sxm, magic);
+    const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
+    acc = valid ? v : acc;
   }
   float v = row16_sum(acc);
   if (c.sh >= 5) v += __shfl_xor(v, 16);
   if (c.sh >= 6) v += __shfl_xor(v, 32);
-  if (j == 0 && row < c.N) {
+  if (c.j == 0 && row < c.N) {
     if (c.live)
-      store_b16_sc1(buffer_rsrc(c.y, (uint32_t)c.N * 2u), 2u * row, f32_to_bf16_bits(v));
+      store_b16_sc1(c.yr, 2u * row, f32_to_bf16_bits(v));
     else
       c.y[row] = f32_to_bf16_bits(v);
   }
