@@ -331,8 +331,34 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(
     return;
   }
   const size_t p0 = ((size_t)b * Hq + h) * splits;
-  // the partials of kMergeBatch splits are loaded together before any is used; the
-  // arithmetic runs in split order
+  // the partials of kMergeBatch splits are loaded together before any is used (all of them
+  // in one round when they fit); the arithmetic runs in split order
+  if (used <= kMergeBatch) {
+    float2 mlq[kMergeBatch], pq[kMergeBatch];
+#pragma unroll
+    for (int q = 0; q < kMergeBatch; ++q) {
+      const size_t sq = p0 + (q < used ? q : 0);
+      mlq[q] = reinterpret_cast<const float2*>(ml)[sq];
+      pq[q] = reinterpret_cast<const float2*>(part + sq * kD)[lane];
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kMergeBatch; ++q)
+      if (q < used) M = fmaxf(M, mlq[q].x);
+    float Ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kMergeBatch; ++q) {
+      if (q < used) {
+        const float e = expf(mlq[q].x - M);
+        Ls = fmaf(mlq[q].y, e, Ls);
+        a0 = fmaf(pq[q].x, e, a0);
+        a1 = fmaf(pq[q].y, e, a1);
+      }
+    }
+    o[2 * lane] = to_bf(a0 / Ls);
+    o[2 * lane + 1] = to_bf(a1 / Ls);
+    return;
+  }
   float M = -INFINITY;
   for (int s0 = 0; s0 < used; s0 += kMergeBatch) {
     float mv[kMergeBatch];

@@ -511,40 +511,51 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   uint4 v0 = load_b128(vrs, chunk_off(first, 0)), v1 = load_b128(vrs, chunk_off(first, 1));
   uint4 v2 = load_b128(vrs, chunk_off(first, 2)), v3 = load_b128(vrs, chunk_off(first, 3));
 
-  // rotated q heads (wavefront per head) and, on wavefront 0, the new key and value
+  // Rotated q heads (wavefront per head) and, on wavefront 0, the new key and value.  Every
+  // element load is issued first, so their round trips overlap each other and the chunk's.
   const float eps = S.eps;
-  auto rotate = [&](const uint16_t* src, uint32_t bytes, uint32_t off, const uint16_t* nw,
-                    uint16_t* dst) {
-    float x0 = bf(ld16_sc1(src, bytes, off + 2u * lane));
-    float x1 = bf(ld16_sc1(src, bytes, off + 2u * (lane + 64)));
+  const uint32_t qbytes = (uint32_t)(b + 1) * Hq * kD * 2u;
+  const uint32_t kvbytes = (uint32_t)(b + 1) * Hkv * kD * 2u;
+  const uint32_t kvoff = (uint32_t)((b * Hkv + kvh) * kD) * 2u;
+  uint32_t qx[2][2], kx[2] = {0u, 0u}, vx[2] = {0u, 0u};
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int g = wave + 4 * r;
+    const uint32_t off = (uint32_t)((b * Hq + kvh * G + (g < G ? g : 0)) * kD) * 2u;
+    qx[r][0] = g < G ? ld16_sc1(S.q, qbytes, off + 2u * lane) : 0u;
+    qx[r][1] = g < G ? ld16_sc1(S.q, qbytes, off + 2u * (lane + 64)) : 0u;
+  }
+  if (wave == 0) {
+    kx[0] = ld16_sc1(S.k, kvbytes, kvoff + 2u * lane);
+    kx[1] = ld16_sc1(S.k, kvbytes, kvoff + 2u * (lane + 64));
+    vx[0] = ld16_sc1(S.v, kvbytes, kvoff + 2u * lane);
+    vx[1] = ld16_sc1(S.v, kvbytes, kvoff + 2u * (lane + 64));
+  }
+  const float inv_freq = exp2f(-(float)lane * (S.log2_theta / 64.0f));
+  float sn, cs;
+  sincosf((float)pos * inv_freq, &sn, &cs);
+  auto rotate = [&](uint32_t h0, uint32_t h1, const uint16_t* nw, uint16_t* dst) {
+    float x0 = bf(h0), x1 = bf(h1);
     const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
     const float inv = 1.0f / sqrtf(ss / (float)kD + eps);
     x0 = bf(to_bf(x0 * inv * bf(nw[lane])));
     x1 = bf(to_bf(x1 * inv * bf(nw[lane + 64])));
-    const float inv_freq = exp2f(-(float)lane * (S.log2_theta / 64.0f));
-    float sn, cs;
-    sincosf((float)pos * inv_freq, &sn, &cs);
     const float r0 = x0 * cs - x1 * sn;
     const float r1 = x0 * sn + x1 * cs;
     dst[lane] = to_bf(r0);
     dst[lane + 64] = to_bf(r1);
   };
-  const uint32_t qbytes = (uint32_t)(b + 1) * Hq * kD * 2u;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int g = wave + 4 * r;
-    if (g < G)
-      rotate(S.q, qbytes, (uint32_t)((b * Hq + kvh * G + g) * kD) * 2u, S.q_norm,
-             reinterpret_cast<uint16_t*>(L.qs[g]));
+    if (g < G) rotate(qx[r][0], qx[r][1], S.q_norm, reinterpret_cast<uint16_t*>(L.qs[g]));
   }
   if (wave == 0) {
-    const uint32_t kvbytes = (uint32_t)(b + 1) * Hkv * kD * 2u;
-    const uint32_t off = (uint32_t)((b * Hkv + kvh) * kD) * 2u;
     uint16_t* kn = reinterpret_cast<uint16_t*>(L.knew);
     uint16_t* vn = reinterpret_cast<uint16_t*>(L.vnew);
-    rotate(S.k, kvbytes, off, S.k_norm, kn);
-    vn[lane] = ld16_sc1(S.v, kvbytes, off + 2u * lane);
-    vn[lane + 64] = ld16_sc1(S.v, kvbytes, off + 2u * (lane + 64));
+    rotate(kx[0], kx[1], S.k_norm, kn);
+    vn[lane] = (uint16_t)vx[0];
+    vn[lane + 64] = (uint16_t)vx[1];
     if (s == writer) {  // this step's key and value into the pools (read by later launches)
       uint16_t* kd = S.k_pool + base + (size_t)pos * kD;
       uint16_t* vd = S.v_pool + base + (size_t)pos * kD;
@@ -697,8 +708,38 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     if (g < G) {
       const int hh = kvh * G + g;
       const uint32_t p0 = (uint32_t)((b * Hq + hh) * splits);
-      // the partials of kMergeBatch splits are loaded together before any is used; the
-      // arithmetic runs in split order (attention_combine_kernel's)
+      // the partials of kMergeBatch splits are loaded together before any is used (all of
+      // them in one round when they fit); the arithmetic runs in split order
+      // (attention_combine_kernel's)
+      if (used <= kMergeBatch) {
+        float mq[kMergeBatch], lq[kMergeBatch], xq[kMergeBatch], yq[kMergeBatch];
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q) {
+          const bool in = q < used;
+          const uint32_t po = p0 + q;
+          mq[q] = __uint_as_float(load_b32_sc1(mrs, in ? po * 8u : kPastBuffer));
+          lq[q] = __uint_as_float(load_b32_sc1(mrs, in ? po * 8u + 4u : kPastBuffer));
+          xq[q] = __uint_as_float(load_b32_sc1(prs, in ? (po * kD + 2 * lane) * 4u : kPastBuffer));
+          yq[q] = __uint_as_float(load_b32_sc1(prs, in ? (po * kD + 2 * lane + 1) * 4u : kPastBuffer));
+        }
+        float Mx = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q)
+          if (q < used) Mx = fmaxf(Mx, mq[q]);
+        float Lx = 0.0f, c0 = 0.0f, c1 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q) {
+          if (q < used) {
+            const float e = expf(mq[q] - Mx);
+            Lx = fmaf(lq[q], e, Lx);
+            c0 = fmaf(xq[q], e, c0);
+            c1 = fmaf(yq[q], e, c1);
+          }
+        }
+        const uint32_t o = (uint32_t)to_bf(c0 / Lx) | ((uint32_t)to_bf(c1 / Lx) << 16);
+        store_b32_sc1(buffer_rsrc(out, out_bytes), (uint32_t)((b * Hq + hh) * kD + 2 * lane) * 2u, o);
+        continue;
+      }
       float Mx = -INFINITY;
       for (int s0 = 0; s0 < used; s0 += kMergeBatch) {
         float mv[kMergeBatch];
