@@ -618,7 +618,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
         float sc = -INFINITY;
         if (lane < count) {
           float d = 0.0f;
-#pragma unroll 2
+#pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
             const uint4 qa = qv[jj], kk = L.kv[lane][jj];
             d = dot2(qa.x, kk.x, d);

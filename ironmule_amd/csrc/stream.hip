@@ -130,12 +130,12 @@ __device__ __forceinline__ uint32_t* counter(const SArgs& a, int stage, int sub)
   return a.counters + ((size_t)stage * kSubs + sub) * kLine;
 }
 
-// One tile's loads: kNch weight chunks per lane, and the tile's scales and biases as
-// dwords (the span of its rows, which are adjacent in memory, read by consecutive lanes).
+// One tile's loads: kNch weight chunks per lane, and the tile's scales and biases (the
+// span of its rows, adjacent in memory: at most 81 dwords, read 16 bytes per lane by the
+// first 21 lanes).
 struct Tile {
   uint4 w[kNch];
-  uint32_t s[2];
-  uint32_t b[2];
+  uint4 s, b;
 };
 
 // One problem of a stage (global tiles t0 .. tend-1 of the program), resolved once while
@@ -233,13 +233,9 @@ __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int 
     T.w[i] = load_b128(c.wr, in ? wbase + cstep * i : kPastBuffer);
   }
   const Span sp = span_of(c, row0);
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int d = lane + 64 * q;
-    const uint32_t off = valid && d < sp.nd ? sp.a0 + 4u * d : kPastBuffer;
-    T.s[q] = __builtin_amdgcn_raw_buffer_load_b32(c.sr, off, 0, 0);
-    T.b[q] = __builtin_amdgcn_raw_buffer_load_b32(c.br, off, 0, 0);
-  }
+  const uint32_t off = valid && 4 * lane < sp.nd ? sp.a0 + 16u * lane : kPastBuffer;
+  T.s = load_b128(c.sr, off);
+  T.b = load_b128(c.br, off);
 }
 
 // Computes global tile g of site c from its loads, the staged x (LDS at smem + c.xoff)
@@ -251,11 +247,15 @@ __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, con
   const int C = c.K >> 5;
   const int row0 = (g - c.t0) * c.rows;
   const int row = row0 + c.rl;
-  // (scale | bias << 16) per half of the span, in this wavefront's own LDS area
-#pragma unroll
-  for (int q = 0; q < 2; ++q)
-    *reinterpret_cast<uint2*>(sbw + 2 * (lane + 64 * q)) =
-        make_uint2((T.s[q] & 0xffffu) | (T.b[q] << 16), (T.s[q] >> 16) | (T.b[q] & 0xffff0000u));
+  // (scale | bias << 16) per half of the span, in this wavefront's own LDS area (lanes
+  // past the first 32 hold nothing of the span)
+  if (lane < kSbWords / 8) {
+    uint4* d = reinterpret_cast<uint4*>(sbw + 8 * lane);
+    d[0] = make_uint4((T.s.x & 0xffffu) | (T.b.x << 16), (T.s.x >> 16) | (T.b.x & 0xffff0000u),
+                      (T.s.y & 0xffffu) | (T.b.y << 16), (T.s.y >> 16) | (T.b.y & 0xffff0000u));
+    d[1] = make_uint4((T.s.z & 0xffffu) | (T.b.z << 16), (T.s.z >> 16) | (T.b.z & 0xffff0000u),
+                      (T.s.w & 0xffffu) | (T.b.w << 16), (T.s.w >> 16) | (T.b.w & 0xffff0000u));
+  }
   const int hbase = c.rlG + span_of(c, row0).mis;
   const char* xs = smem + c.xoff;
   const uint4* xq = reinterpret_cast<const uint4*>(xs);
