@@ -122,9 +122,9 @@ IMQ_API int32_t imq_qmv_grouped(const imq_problem* problems, int32_t count, int3
                                 void* stream);
 
 /* Bytes of workspace imq_qmv_grouped_ws can use for these problems at M rows: with it the
- * groups of small-N weights are split over more workgroups (fp32 partials, which the
- * last workgroup of each 128-row tile adds in a fixed order, in the same launch).  0 when
- * no split helps (M < 3 or enough rows). */
+ * groups of weights with few rows (for a given K) are split over more workgroups (fp32
+ * partials, which the last workgroup of each tile adds in a fixed order, in the same
+ * launch).  0 when no split helps (M < 3 or enough rows). */
 IMQ_API size_t imq_qmv_grouped_workspace(const imq_problem* problems, int32_t count, int32_t M);
 
 /* imq_qmv_grouped with a caller-provided workspace of workspace_bytes (16-byte aligned;
