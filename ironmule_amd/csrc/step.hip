@@ -1033,7 +1033,7 @@ int32_t imq_qmv_program_create(const imq_qmv_stage* stages, int32_t count, imq_p
   int32_t code;
   if (!current_device(&code)) return code;
   imq_program* prog = new imq_program();
-  hipGetDevice(&prog->device);
+  (void)hipGetDevice(&prog->device);
   for (int i = 0; i < count; ++i) {
     const imq_qmv_stage& st = stages[i];
     if (st.count < 1 || st.count > kMaxStageProblems) {
@@ -1115,7 +1115,7 @@ int32_t imq_decode_program_create(const imq_step_desc* d, imq_program** out) {
     return fail(IMQ_EUNSUPPORTED, "a KV pool of 2 GiB or more exceeds the attention's offsets");
 
   imq_program* prog = new imq_program();
-  hipGetDevice(&prog->device);
+  (void)hipGetDevice(&prog->device);
   const int span = std::min(d->max_len, d->capacity);
   int splits, cps;
   attention_split(B, Hkv, span, &splits, &cps);

@@ -68,9 +68,12 @@ constexpr int kMaxSlots = 8;           // distinct x rows of an independent-stag
 constexpr size_t kSlotLds = 64 * 1024;  // LDS for those rows
 constexpr int kSbWords = 256;           // per wavefront: two packed (scale, bias) words per span dword
 
-// LDS bytes of one staged x row of K values: four planes of C = K/32 uint4 (the pair
-// order of each chunk's four words) followed by the C chunk sums.
-constexpr size_t x_bytes(int K) { return (size_t)(K / 32) * (64 + 4); }
+// LDS bytes of one staged x row of K values: C = K/32 chunks of 80 bytes each, the
+// chunk's four words in pair order (64 bytes), its sum (4 bytes) and 12 bytes of padding.
+// A lane reads all five pieces of its chunk from one address (immediate offsets), and the
+// 20-dword chunk stride puts the lanes of a quarter-wave on distinct banks.
+constexpr int kXChunk = 80;
+constexpr size_t x_bytes(int K) { return (size_t)(K / 32) * kXChunk; }
 
 struct SProb {
   const uint32_t* w;
@@ -244,7 +247,6 @@ __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int 
 // order, the dot2 chains and the cross-lane sums are the one-row kernel's.
 __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, const Tile& T,
                                              const char* smem, uint32_t* sbw, uint32_t magic) {
-  const int C = c.K >> 5;
   const int row0 = (g - c.t0) * c.rows;
   const int row = row0 + c.rl;
   // (scale | bias << 16) per half of the span, in this wavefront's own LDS area (lanes
@@ -256,26 +258,27 @@ __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, con
     d[1] = make_uint4((T.s.z & 0xffffu) | (T.b.z << 16), (T.s.z >> 16) | (T.b.z & 0xffff0000u),
                       (T.s.w & 0xffffu) | (T.b.w << 16), (T.s.w >> 16) | (T.b.w & 0xffff0000u));
   }
-  const int hbase = c.rlG + span_of(c, row0).mis;
-  const char* xs = smem + c.xoff;
-  const uint4* xq = reinterpret_cast<const uint4*>(xs);
-  const float* sx = reinterpret_cast<const float*>(xs + (size_t)C * 64);
+  // this lane's chunk j: its (scale, bias) dword and its staged x; chunk i of the lane is
+  // 2^sh chunks further on (the LPR-step of the chunk index, LPR/2 dwords of the area)
+  const uint32_t* sbl = sbw + c.rlG + span_of(c, row0).mis + (c.j >> 1);
+  const char* xl = smem + c.xoff + kXChunk * c.j;
+  const int sstep = 1 << (c.sh - 1), xstep = kXChunk << c.sh;
   // Every chunk slot is computed (no branch, so the LDS reads of all chunks can be issued
-  // early); a slot past the lane's chunks is discarded by the select, as its zero weights
-  // would not be (they stand for q = 0, not for nothing).
+  // early); a slot past the lane's chunks rereads the lane's first chunk and is discarded
+  // by the select, as its zero weights would not be (they stand for q = 0, not for
+  // nothing).
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < kNch; ++i) {
-    const bool valid = i < c.nvalid;
-    const int kk = valid ? c.j + (i << c.sh) : 0;
-    const uint32_t sb = sbw[hbase + (kk >> 1)];
+    const int ii = i < c.nvalid ? i : 0;
+    const uint32_t sb = sbl[sstep * ii];
     const float sc = __uint_as_float(sb << 16);
     const float bi = __uint_as_float(sb & 0xffff0000u);
-    const float sxm = sx[kk];
-    const float d = chunk_dot(T.w[i], xq[kk], xq[C + kk], xq[2 * C + kk], xq[3 * C + kk],
-                              -128.0f * sxm, magic);
+    const uint4* xc = reinterpret_cast<const uint4*>(xl + xstep * ii);
+    const float sxm = reinterpret_cast<const float*>(xc + 4)[0];
+    const float d = chunk_dot(T.w[i], xc[0], xc[1], xc[2], xc[3], -128.0f * sxm, magic);
     const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
-    acc = valid ? v : acc;
+    acc = i < c.nvalid ? v : acc;
   }
   float v = row16_sum(acc);
   if (c.sh >= 5) v += __shfl_xor(v, 16);
@@ -291,7 +294,7 @@ __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, con
 // Stages the bf16 row x (K values) in LDS at `dst` in pair order with its chunk sums; the
 // whole workgroup takes part.  `live`: x was written earlier in this launch (sc1 loads).
 __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, char* dst, int tid) {
-  const int C = K >> 5, W = K >> 3;
+  const int W = K >> 3;
   const __amdgpu_buffer_rsrc_t r = buffer_rsrc(x, (uint32_t)K * 2u);
   uint4 xs[kXr];
 #pragma unroll
@@ -300,8 +303,6 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
     const uint32_t off = i < W ? 16u * i : kPastBuffer;
     xs[t] = live ? load_b128_sc1(r, off) : load_b128(r, off);
   }
-  uint4* xq = reinterpret_cast<uint4*>(dst);
-  float* sx = reinterpret_cast<float*>(dst + (size_t)C * 64);
 #pragma unroll
   for (int t = 0; t < kXr; ++t) {
     const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
@@ -309,8 +310,9 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
     part += __shfl_xor(part, 1);
     part += __shfl_xor(part, 2);
     if (i < W) {
-      xq[(i & 3) * C + (i >> 2)] = pair_order(xs[t]);
-      if ((i & 3) == 0) sx[i >> 2] = part;
+      char* chunk = dst + (size_t)kXChunk * (i >> 2);
+      reinterpret_cast<uint4*>(chunk)[i & 3] = pair_order(xs[t]);
+      if ((i & 3) == 0) reinterpret_cast<float*>(chunk + 64)[0] = part;
     }
   }
 }
@@ -584,8 +586,12 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
     }
     p->args.sb_off = off;
   } else {
-    for (size_t i = 0; i < p->stages.size(); ++i) p->stages[i].xoff = (int)((i & 1) * x_bytes(kMaxK));
-    p->args.sb_off = (int)(2 * x_bytes(kMaxK));
+    // two x buffers (stages alternate), each sized for the program's largest K
+    int kmax = 0;
+    for (const SStage& S : p->stages) kmax = std::max(kmax, (int)S.K);
+    const int xb = (int)((x_bytes(kmax) + 15) & ~(size_t)15);
+    for (size_t i = 0; i < p->stages.size(); ++i) p->stages[i].xoff = (int)(i & 1) * xb;
+    p->args.sb_off = 2 * xb;
   }
   p->lds = (size_t)p->args.sb_off + (size_t)kWaves * kSbWords * 4;
   const int nstages = (int)p->stages.size();
