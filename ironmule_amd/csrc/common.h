@@ -166,6 +166,15 @@ __device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t rsrc, uint32_t
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Loads of data read once per launch (streamed weights), with the nt (non-temporal)
+// cache-policy bit: the lines are not kept for reuse, which measured 2-3% faster on the
+// weight stream than the default policy.
+constexpr int kNt = 2;  // cache-policy operand of the raw buffer intrinsics: nt
+__device__ __forceinline__ uint4 load_b128_nt(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, kNt);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // ------------------------------------------------------------------ wavefront sums
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -335,7 +335,7 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int kc = j + (i << sh);
-    wv[i] = load_b128(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
+    wv[i] = load_b128_nt(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
   }
 
   // staging, unconditionally (pieces past x and past the span are zeros)
@@ -565,7 +565,7 @@ __device__ __forceinline__ void mma_load(MmaStage<NT, GS>& st, __amdgpu_buffer_r
     const bool in = g + i < g1;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      st.w[i][t] = load_b128(wrsrc, in ? woff[t] + 32u * (g + i) : kPastBuffer);
+      st.w[i][t] = load_b128_nt(wrsrc, in ? woff[t] + 32u * (g + i) : kPastBuffer);
       st.s[i][t] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, in ? sboff[t] + 2u * (g + i) : kPastBuffer, 0, 0);
       st.b[i][t] = __builtin_amdgcn_raw_buffer_load_b16(brsrc, in ? sboff[t] + 2u * (g + i) : kPastBuffer, 0, 0);
     }
@@ -852,7 +852,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
       const int n = row0 + slot % kRows < N ? row0 + slot % kRows : N - 1;
       const int g = klo[k] + (wp >> 1) + 4 * st;
       const uint32_t off = (uint32_t)n * (uint32_t)W * 4u + 16u * (wp & 1) + 32u * (uint32_t)g;
-      wreg[i] = load_b128(wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
+      wreg[i] = load_b128_nt(wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
     }
     const int g = klo[sb_k] + 4 * st;
     const uint32_t off = (sb_src + 2u * (uint32_t)g) | ((uint32_t)(g >= khi[sb_k]) << 31);

@@ -365,7 +365,7 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int kc = j + (i << sh);
-    wv[i] = load_b128(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
+    wv[i] = load_b128_nt(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
   }
 
   if constexpr (!kStaged) {

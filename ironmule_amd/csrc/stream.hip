@@ -67,6 +67,7 @@ constexpr int kMaxStageProblems = 3;
 constexpr int kMaxSlots = 8;           // distinct x rows of an independent-stage program
 constexpr size_t kSlotLds = 64 * 1024;  // LDS for those rows
 constexpr int kSbWords = 256;           // per wavefront: two packed (scale, bias) words per span dword
+constexpr int kDepth = 2;                // tiles in flight per wavefront (independent stages)
 
 // LDS bytes of one staged x row of K values: C = K/32 chunks of 80 bytes each, the
 // chunk's four words in pair order (64 bytes), its sum (4 bytes) and 12 bytes of padding.
@@ -233,7 +234,7 @@ __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int 
 #pragma unroll
   for (int i = 0; i < kNch; ++i) {
     const bool in = live && i < c.nvalid;
-    T.w[i] = load_b128(c.wr, in ? wbase + cstep * i : kPastBuffer);
+    T.w[i] = load_b128_nt(c.wr, in ? wbase + cstep * i : kPastBuffer);
   }
   const Span sp = span_of(c, row0);
   const uint32_t off = valid && 4 * lane < sp.nd ? sp.a0 + 16u * lane : kPastBuffer;
@@ -243,10 +244,12 @@ __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int 
 
 // Computes global tile g of site c from its loads, the staged x (LDS at smem + c.xoff)
 // and this wavefront's scale/bias area `sbw` (kSbWords dwords of LDS), and stores the tile's
-// rows as bf16: with sc1 stores when a later stage of the launch reads them.  The chunk
-// order, the dot2 chains and the cross-lane sums are the one-row kernel's.
+// rows as bf16 unless `keep` is false: with sc1 stores when a later stage of the launch
+// reads them.  The chunk order, the dot2 chains and the cross-lane sums are the one-row
+// kernel's.
 __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, const Tile& T,
-                                             const char* smem, uint32_t* sbw, uint32_t magic) {
+                                             const char* smem, uint32_t* sbw, uint32_t magic,
+                                             bool keep = true) {
   const int row0 = (g - c.t0) * c.rows;
   const int row = row0 + c.rl;
   // (scale | bias << 16) per half of the span, in this wavefront's own LDS area (lanes
@@ -283,7 +286,7 @@ __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, con
   float v = row16_sum(acc);
   if (c.sh >= 5) v += __shfl_xor(v, 16);
   if (c.sh >= 6) v += __shfl_xor(v, 32);
-  if (c.j == 0 && row < c.N) {
+  if (keep && c.j == 0 && row < c.N) {
     if (c.live)
       store_b16_sc1(c.yr, 2u * row, f32_to_bf16_bits(v));
     else
@@ -321,8 +324,8 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
 
 // Wavefront v takes tiles v, v + V, v + 2V, ... of the program (V wavefronts), so at any
 // moment the device streams one compact window of the weights.  Its cursors only move
-// forward.  Two tiles are in flight: the loads of tile g + 2V are issued as soon as tile
-// g has been computed.
+// forward.  kDepth tiles are in flight: the loads of tile g + kDepth V are issued as soon
+// as tile g has been computed.
 __global__ __launch_bounds__(kThreads) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
   extern __shared__ uint4 smem_raw[];
   char* smem = reinterpret_cast<char*>(smem_raw);
@@ -336,25 +339,30 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const SStage* __restri
   // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp)
   int ls = 0, lp = 0, cs = 0, cp = 0;
   Site lc = site_at(st, 0, 0), cc = lc;
-  Tile A, B;
-  auto issue = [&](int g, Tile& T) {
+  Tile T[kDepth];
+  auto issue = [&](int g, Tile& t) {
     if (g < total) seek(st, ls, lp, lc, g);
-    load_site(lc, g, g < total, lane, T);
+    load_site(lc, g, g < total, lane, t);
   };
-  auto run = [&](int g, Tile& T) {
-    seek(st, cs, cp, cc, g);
-    compute_site(cc, g, lane, T, smem, sbw, magic);
-    issue(g + 2 * V, T);
-  };
-  issue(v, A);
-  issue(v + V, B);
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) issue(v + d * V, T[d]);
   for (int k = 0; k < a.nslots; ++k) stage_x(a.slot[k].x, a.slot[k].K, false, smem + a.slot[k].off, tid);
   lds_barrier();
 
-  for (int g = v; g < total; g += 2 * V) {
-    run(g, A);
-    if (g + V >= total) break;
-    run(g + V, B);
+  // Every pass runs all kDepth tiles with no exit in between, so that every path into the
+  // loop head has issued the tiles' loads in the same order and each tile's compute waits
+  // only for its own loads.  A tile past the end (the last pass) was loaded as zeros; it
+  // is computed at tile g's site and not stored.
+  for (int g = v; g < total; g += kDepth * V) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      const int gd = g + d * V;
+      const bool in = gd < total;
+      const int gc = in ? gd : g;
+      seek(st, cs, cp, cc, gc);
+      compute_site(cc, gc, lane, T[d], smem, sbw, magic, in);
+      issue(gd + kDepth * V, T[d]);
+    }
   }
 }
 
