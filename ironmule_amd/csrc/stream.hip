@@ -70,7 +70,8 @@ constexpr int kSbWords = 256;           // per wavefront: two packed (scale, bia
 constexpr int kDepth = 2;                // tiles in flight per wavefront (independent stages)
 
 // LDS bytes of one staged x row of K values: C = K/32 chunks of 80 bytes each, the
-// chunk's four words in pair order (64 bytes), its sum (4 bytes) and 12 bytes of padding.
+// chunk's four words in pair order (64 bytes), its sum and -128 times its sum (8 bytes)
+// and 8 bytes of padding.
 // A lane reads all five pieces of its chunk from one address (immediate offsets), and the
 // 20-dword chunk stride puts the lanes of a quarter-wave on distinct banks.
 constexpr int kXChunk = 80;
@@ -144,8 +145,9 @@ struct Tile {
 
 // One problem of a stage (global tiles t0 .. tend-1 of the program), resolved once while
 // a wavefront works through its tiles, with what every tile needs: the buffer descriptors
-// and row stride (scalar), and per lane its chunk column j, its row in the tile rl, the
-// byte offsets those give and how many of its kNch chunk slots hold chunks of the row.
+// and row stride (scalar), and per lane its chunk column j, its row in the tile rl, how
+// many of its kNch chunk slots hold chunks of the row, and for each slot the offsets
+// that slot reads: in the tile's weights, in the staged x and in the scale/bias area.
 struct Site {
   __amdgpu_buffer_rsrc_t wr, sr, br, yr;
   uint16_t* y;
@@ -153,8 +155,9 @@ struct Site {
   int rows;        // rows per tile: 64 >> sh
   uint32_t w4;     // bytes per weight row (K / 2)
   // per lane
-  uint32_t wlane;  // rl * w4 + 16 j
-  int rlG;         // rl * G: the lane's row's first scale/bias half within the tile
+  uint32_t woff[kNch];  // weight byte offset from the tile's first row; kPastBuffer past the lane's chunks
+  uint32_t xo[kNch];    // LDS byte offset of the slot's staged x chunk
+  uint32_t so[kNch];    // (scale, bias) word of the slot in the area, before the span's misalignment
   int rl, j, nvalid;
 };
 
@@ -183,11 +186,20 @@ __device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, i
   const int lane = threadIdx.x & 63;
   c.j = lane & ((1 << c.sh) - 1);
   c.rl = lane >> c.sh;
-  c.wlane = (uint32_t)c.rl * c.w4 + 16u * (uint32_t)c.j;
-  c.rlG = c.rl * G;
   // chunks j, j + 2^sh, ... below C, at most nch of them
   const int nv = (C - c.j + (1 << c.sh) - 1) >> c.sh;
   c.nvalid = nv < c.nch ? nv : c.nch;
+  // chunk slot i is chunk j + i 2^sh of the row; a slot past the lane's chunks reads no
+  // weights and rereads the lane's first chunk of x and its scale/bias word
+  const uint32_t wlane = (uint32_t)c.rl * c.w4 + 16u * (uint32_t)c.j;
+#pragma unroll
+  for (int i = 0; i < kNch; ++i) {
+    const bool in = i < c.nvalid;
+    const int ii = in ? i : 0;
+    c.woff[i] = in ? wlane + ((16u << c.sh) * (uint32_t)i) : kPastBuffer;
+    c.xo[i] = (uint32_t)c.xoff + (uint32_t)kXChunk * (uint32_t)(c.j + (ii << c.sh));
+    c.so[i] = (uint32_t)(c.rl * G + (c.j >> 1) + (ii << (c.sh - 1)));
+  }
   return c;
 }
 
@@ -225,28 +237,35 @@ __device__ __forceinline__ Span span_of(const Site& c, int row0) {
 }
 
 // Issues the loads of global tile g of site c (valid false: every load reads past its
-// buffer, which returns zero without a memory access).
+// buffer, which returns zero without a memory access).  The tile's first row offset is
+// added with saturation, so that a slot past the lane's chunks (kPastBuffer) stays past
+// the buffer on every row.
 __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int lane, Tile& T) {
   const int row0 = (g - c.t0) * c.rows;
-  const bool live = valid && row0 + c.rl < c.N;
-  const uint32_t wbase = (uint32_t)row0 * c.w4 + c.wlane;
-  const uint32_t cstep = 16u << c.sh;  // bytes between a lane's chunks
+  const uint32_t base = valid && row0 + c.rl < c.N ? (uint32_t)row0 * c.w4 : kPastBuffer;
 #pragma unroll
-  for (int i = 0; i < kNch; ++i) {
-    const bool in = live && i < c.nvalid;
-    T.w[i] = load_b128_nt(c.wr, in ? wbase + cstep * i : kPastBuffer);
-  }
+  for (int i = 0; i < kNch; ++i) T.w[i] = load_b128_nt(c.wr, __builtin_elementwise_add_sat(base, c.woff[i]));
   const Span sp = span_of(c, row0);
   const uint32_t off = valid && 4 * lane < sp.nd ? sp.a0 + 16u * lane : kPastBuffer;
   T.s = load_b128(c.sr, off);
   T.b = load_b128(c.br, off);
 }
 
-// Computes global tile g of site c from its loads, the staged x (LDS at smem + c.xoff)
-// and this wavefront's scale/bias area `sbw` (kSbWords dwords of LDS), and stores the tile's
-// rows as bf16 unless `keep` is false: with sc1 stores when a later stage of the launch
-// reads them.  The chunk order, the dot2 chains and the cross-lane sums are the one-row
-// kernel's.
+// Adds lane 15 of the previous row of 16 lanes (CTRL row_bcast:15) or lane 31 (row_bcast:31)
+// to the rows of ROWS; the other rows are left as they are.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float add_bcast(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                   CTRL, ROWS, 0xF, false));
+}
+
+// Computes global tile g of site c from its loads, the staged x (LDS at smem) and this
+// wavefront's scale/bias area `sbw` (kSbWords dwords of LDS), and stores the tile's rows
+// as bf16 unless `keep` is false: with sc1 stores when a later stage of the launch reads
+// them.  The chunk order and the dot2 chains are the one-row kernel's; its cross-lane sums
+// (row of 16, then lanes 16 and 32 apart) are formed here by row broadcasts, the same
+// additions with their operands swapped, so the row sums have the same bits and end in
+// the row's last lane.
 __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, const Tile& T,
                                              const char* smem, uint32_t* sbw, uint32_t magic,
                                              bool keep = true) {
@@ -261,32 +280,26 @@ __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, con
     d[1] = make_uint4((T.s.z & 0xffffu) | (T.b.z << 16), (T.s.z >> 16) | (T.b.z & 0xffff0000u),
                       (T.s.w & 0xffffu) | (T.b.w << 16), (T.s.w >> 16) | (T.b.w & 0xffff0000u));
   }
-  // this lane's chunk j: its (scale, bias) dword and its staged x; chunk i of the lane is
-  // 2^sh chunks further on (the LPR-step of the chunk index, LPR/2 dwords of the area)
-  const uint32_t* sbl = sbw + c.rlG + span_of(c, row0).mis + (c.j >> 1);
-  const char* xl = smem + c.xoff + kXChunk * c.j;
-  const int sstep = 1 << (c.sh - 1), xstep = kXChunk << c.sh;
+  const uint32_t* sbm = sbw + span_of(c, row0).mis;
   // Every chunk slot is computed (no branch, so the LDS reads of all chunks can be issued
-  // early); a slot past the lane's chunks rereads the lane's first chunk and is discarded
-  // by the select, as its zero weights would not be (they stand for q = 0, not for
-  // nothing).
+  // early); a slot past the lane's chunks is discarded by the select, as its zero weights
+  // would not be (they stand for q = 0, not for nothing).
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < kNch; ++i) {
-    const int ii = i < c.nvalid ? i : 0;
-    const uint32_t sb = sbl[sstep * ii];
+    const uint32_t sb = sbm[c.so[i]];
     const float sc = __uint_as_float(sb << 16);
     const float bi = __uint_as_float(sb & 0xffff0000u);
-    const uint4* xc = reinterpret_cast<const uint4*>(xl + xstep * ii);
-    const float sxm = reinterpret_cast<const float*>(xc + 4)[0];
-    const float d = chunk_dot(T.w[i], xc[0], xc[1], xc[2], xc[3], -128.0f * sxm, magic);
-    const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
+    const uint4* xc = reinterpret_cast<const uint4*>(smem + c.xo[i]);
+    const float2 sum = reinterpret_cast<const float2*>(xc + 4)[0];  // (chunk sum, -128 sum)
+    const float d = chunk_dot(T.w[i], xc[0], xc[1], xc[2], xc[3], sum.y, magic);
+    const float v = fmaf(sc, d, fmaf(bi, sum.x, acc));
     acc = i < c.nvalid ? v : acc;
   }
   float v = row16_sum(acc);
-  if (c.sh >= 5) v += __shfl_xor(v, 16);
-  if (c.sh >= 6) v += __shfl_xor(v, 32);
-  if (keep && c.j == 0 && row < c.N) {
+  if (c.sh >= 5) v = add_bcast<0x142, 0xA>(v);  // rows 1 and 3 add rows 0 and 2
+  if (c.sh >= 6) v = add_bcast<0x143, 0xC>(v);  // rows 2 and 3 add lane 31 (rows 0 + 1)
+  if (keep && c.j == (1 << c.sh) - 1 && row < c.N) {
     if (c.live)
       store_b16_sc1(c.yr, 2u * row, f32_to_bf16_bits(v));
     else
@@ -315,17 +328,21 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
     if (i < W) {
       char* chunk = dst + (size_t)kXChunk * (i >> 2);
       reinterpret_cast<uint4*>(chunk)[i & 3] = pair_order(xs[t]);
-      if ((i & 3) == 0) reinterpret_cast<float*>(chunk + 64)[0] = part;
+      if ((i & 3) == 0) reinterpret_cast<float2*>(chunk + 64)[0] = make_float2(part, -128.0f * part);
     }
   }
 }
 
 // ------------------------------------------------------------ independent stages
 
-// Wavefront v takes tiles v, v + V, v + 2V, ... of the program (V wavefronts), so at any
-// moment the device streams one compact window of the weights.  Its cursors only move
-// forward.  kDepth tiles are in flight: the loads of tile g + kDepth V are issued as soon
-// as tile g has been computed.
+// Wavefront v takes runs of kRun consecutive tiles: run v, v + V, v + 2V, ... of the
+// program (V wavefronts), so at any moment the device streams one compact window of the
+// weights, and a wavefront resolves a problem's descriptors once per run rather than once
+// per tile.  Its cursors only move forward.  kDepth tiles are in flight: the loads of a
+// wavefront's tile k + kDepth are issued as soon as its tile k has been computed.
+constexpr int kRun = 4;
+static_assert(kRun % kDepth == 0, "runs hold whole passes");
+
 __global__ __launch_bounds__(kThreads) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
   extern __shared__ uint4 smem_raw[];
   char* smem = reinterpret_cast<char*>(smem_raw);
@@ -335,6 +352,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const SStage* __restri
   const int V = a.waves, total = a.total;
   uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
   const uint32_t magic = in_vgpr(kMagic);
+  // this wavefront's k-th tile (increasing in k)
+  auto tile_of = [&](int k) {
+    return (int)((((unsigned)k / kRun) * (unsigned)V + (unsigned)v) * kRun + (unsigned)k % kRun);
+  };
 
   // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp)
   int ls = 0, lp = 0, cs = 0, cp = 0;
@@ -345,23 +366,24 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const SStage* __restri
     load_site(lc, g, g < total, lane, t);
   };
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d) issue(v + d * V, T[d]);
+  for (int d = 0; d < kDepth; ++d) issue(tile_of(d), T[d]);
   for (int k = 0; k < a.nslots; ++k) stage_x(a.slot[k].x, a.slot[k].K, false, smem + a.slot[k].off, tid);
   lds_barrier();
 
   // Every pass runs all kDepth tiles with no exit in between, so that every path into the
   // loop head has issued the tiles' loads in the same order and each tile's compute waits
   // only for its own loads.  A tile past the end (the last pass) was loaded as zeros; it
-  // is computed at tile g's site and not stored.
-  for (int g = v; g < total; g += kDepth * V) {
+  // is computed at the pass's first tile's site and not stored.
+  for (int k = 0; tile_of(k) < total; k += kDepth) {
+    const int g0 = tile_of(k);
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
-      const int gd = g + d * V;
+      const int gd = tile_of(k + d);
       const bool in = gd < total;
-      const int gc = in ? gd : g;
+      const int gc = in ? gd : g0;
       seek(st, cs, cp, cc, gc);
       compute_site(cc, gc, lane, T[d], smem, sbw, magic, in);
-      issue(gd + kDepth * V, T[d]);
+      issue(tile_of(k + d + kDepth), T[d]);
     }
   }
 }
