@@ -66,7 +66,8 @@ constexpr int kMaxPolls = 1 << 22;
 constexpr int kMaxStageProblems = 3;
 constexpr int kMaxSlots = 8;           // distinct x rows of an independent-stage program
 constexpr size_t kSlotLds = 64 * 1024;  // LDS for those rows
-constexpr int kSbWords = 256;           // per wavefront: two packed (scale, bias) words per span dword
+constexpr int kSbWords = 256;           // per wavefront: the span's scale halves, then at kBiasArea its bias halves
+constexpr int kBiasArea = 512;          // byte offset of the bias halves in the area
 constexpr int kDepth = 2;                // tiles in flight per wavefront (independent stages)
 
 // LDS bytes of one staged x row of K values: C = K/32 chunks of 80 bytes each, the
@@ -157,8 +158,9 @@ struct Site {
   // per lane
   uint32_t woff[kNch];  // weight byte offset from the tile's first row; kPastBuffer past the lane's chunks
   uint32_t xo[kNch];    // LDS byte offset of the slot's staged x chunk
-  uint32_t so[kNch];    // (scale, bias) word of the slot in the area, before the span's misalignment
+  uint32_t so[kNch];    // byte offset of the slot's scale half in the area, before the span's misalignment
   int rl, j, nvalid;
+  int cls;  // 0: every lane has kNch chunks, 1: every lane has kNch - 1, 2: lanes differ
 };
 
 __device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, int pi) {
@@ -189,6 +191,9 @@ __device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, i
   // chunks j, j + 2^sh, ... below C, at most nch of them
   const int nv = (C - c.j + (1 << c.sh) - 1) >> c.sh;
   c.nvalid = nv < c.nch ? nv : c.nch;
+  // lane j = 0 has the most chunks, lane j = 2^sh - 1 the fewest
+  const int nv_hi = min((C + (1 << c.sh) - 1) >> c.sh, c.nch), nv_lo = min(C >> c.sh, c.nch);
+  c.cls = nv_lo != nv_hi ? 2 : nv_hi == kNch ? 0 : nv_hi == kNch - 1 ? 1 : 2;
   // chunk slot i is chunk j + i 2^sh of the row; a slot past the lane's chunks reads no
   // weights and rereads the lane's first chunk of x and its scale/bias word
   const uint32_t wlane = (uint32_t)c.rl * c.w4 + 16u * (uint32_t)c.j;
@@ -198,7 +203,7 @@ __device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, i
     const int ii = in ? i : 0;
     c.woff[i] = in ? wlane + ((16u << c.sh) * (uint32_t)i) : kPastBuffer;
     c.xo[i] = (uint32_t)c.xoff + (uint32_t)kXChunk * (uint32_t)(c.j + (ii << c.sh));
-    c.so[i] = (uint32_t)(c.rl * G + (c.j >> 1) + (ii << (c.sh - 1)));
+    c.so[i] = 2u * (uint32_t)(c.rl * G + (c.j >> 1) + (ii << (c.sh - 1)));
   }
   return c;
 }
@@ -242,13 +247,14 @@ __device__ __forceinline__ Span span_of(const Site& c, int row0) {
 // the buffer on every row.
 __device__ __forceinline__ void load_site(const Site& c, int g, bool valid, int lane, Tile& T) {
   const int row0 = (g - c.t0) * c.rows;
-  const uint32_t base = valid && row0 + c.rl < c.N ? (uint32_t)row0 * c.w4 : kPastBuffer;
-#pragma unroll
-  for (int i = 0; i < kNch; ++i) T.w[i] = load_b128_nt(c.wr, __builtin_elementwise_add_sat(base, c.woff[i]));
+  // scales and biases first: the tile's compute needs them before its first chunk
   const Span sp = span_of(c, row0);
   const uint32_t off = valid && 4 * lane < sp.nd ? sp.a0 + 16u * lane : kPastBuffer;
   T.s = load_b128(c.sr, off);
   T.b = load_b128(c.br, off);
+  const uint32_t base = valid && row0 + c.rl < c.N ? (uint32_t)row0 * c.w4 : kPastBuffer;
+#pragma unroll
+  for (int i = 0; i < kNch; ++i) T.w[i] = load_b128_nt(c.wr, __builtin_elementwise_add_sat(base, c.woff[i]));
 }
 
 // Adds lane 15 of the previous row of 16 lanes (CTRL row_bcast:15) or lane 31 (row_bcast:31)
@@ -257,6 +263,28 @@ template <int CTRL, int ROWS>
 __device__ __forceinline__ float add_bcast(float v) {
   return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
                                                                    CTRL, ROWS, 0xF, false));
+}
+
+// The sum over a lane's first NS chunk slots of one tile: scale * (chunk dot) + bias *
+// (chunk sum), accumulated slot by slot; with SEL a slot past the lane's chunks is
+// discarded by a select (its zero weights stand for q = 0, not for nothing).  No branch,
+// so the LDS reads of all slots can be issued early.
+template <int NS, bool SEL>
+__device__ __forceinline__ float lane_sum(const Site& c, const Tile& T, const char* smem,
+                                          const char* sbm, uint32_t magic) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const char* sb = sbm + c.so[i];
+    const float sc = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(sb) << 16);
+    const float bi = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(sb + kBiasArea) << 16);
+    const uint4* xc = reinterpret_cast<const uint4*>(smem + c.xo[i]);
+    const float2 sum = reinterpret_cast<const float2*>(xc + 4)[0];  // (chunk sum, -128 sum)
+    const float d = chunk_dot(T.w[i], xc[0], xc[1], xc[2], xc[3], sum.y, magic);
+    const float v = fmaf(sc, d, fmaf(bi, sum.x, acc));
+    acc = !SEL || i < c.nvalid ? v : acc;
+  }
+  return acc;
 }
 
 // Computes global tile g of site c from its loads, the staged x (LDS at smem) and this
@@ -271,31 +299,16 @@ __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, con
                                              bool keep = true) {
   const int row0 = (g - c.t0) * c.rows;
   const int row = row0 + c.rl;
-  // (scale | bias << 16) per half of the span, in this wavefront's own LDS area (lanes
+  // the span's scale and bias halves as loaded, in this wavefront's own LDS area (lanes
   // past the first 32 hold nothing of the span)
-  if (lane < kSbWords / 8) {
-    uint4* d = reinterpret_cast<uint4*>(sbw + 8 * lane);
-    d[0] = make_uint4((T.s.x & 0xffffu) | (T.b.x << 16), (T.s.x >> 16) | (T.b.x & 0xffff0000u),
-                      (T.s.y & 0xffffu) | (T.b.y << 16), (T.s.y >> 16) | (T.b.y & 0xffff0000u));
-    d[1] = make_uint4((T.s.z & 0xffffu) | (T.b.z << 16), (T.s.z >> 16) | (T.b.z & 0xffff0000u),
-                      (T.s.w & 0xffffu) | (T.b.w << 16), (T.s.w >> 16) | (T.b.w & 0xffff0000u));
+  if (lane < 32) {
+    reinterpret_cast<uint4*>(sbw)[lane] = T.s;
+    reinterpret_cast<uint4*>(reinterpret_cast<char*>(sbw) + kBiasArea)[lane] = T.b;
   }
-  const uint32_t* sbm = sbw + span_of(c, row0).mis;
-  // Every chunk slot is computed (no branch, so the LDS reads of all chunks can be issued
-  // early); a slot past the lane's chunks is discarded by the select, as its zero weights
-  // would not be (they stand for q = 0, not for nothing).
-  float acc = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kNch; ++i) {
-    const uint32_t sb = sbm[c.so[i]];
-    const float sc = __uint_as_float(sb << 16);
-    const float bi = __uint_as_float(sb & 0xffff0000u);
-    const uint4* xc = reinterpret_cast<const uint4*>(smem + c.xo[i]);
-    const float2 sum = reinterpret_cast<const float2*>(xc + 4)[0];  // (chunk sum, -128 sum)
-    const float d = chunk_dot(T.w[i], xc[0], xc[1], xc[2], xc[3], sum.y, magic);
-    const float v = fmaf(sc, d, fmaf(bi, sum.x, acc));
-    acc = i < c.nvalid ? v : acc;
-  }
+  const char* sbm = reinterpret_cast<const char*>(sbw) + 2 * span_of(c, row0).mis;
+  const float acc = c.cls == 0   ? lane_sum<kNch, false>(c, T, smem, sbm, magic)
+                    : c.cls == 1 ? lane_sum<kNch - 1, false>(c, T, smem, sbm, magic)
+                                 : lane_sum<kNch, true>(c, T, smem, sbm, magic);
   float v = row16_sum(acc);
   if (c.sh >= 5) v = add_bcast<0x142, 0xA>(v);  // rows 1 and 3 add rows 0 and 2
   if (c.sh >= 6) v = add_bcast<0x143, 0xC>(v);  // rows 2 and 3 add lane 31 (rows 0 + 1)
@@ -343,7 +356,7 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
 constexpr int kRun = 4;
 static_assert(kRun % kDepth == 0, "runs hold whole passes");
 
-__global__ __launch_bounds__(kThreads) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
   extern __shared__ uint4 smem_raw[];
   char* smem = reinterpret_cast<char*>(smem_raw);
   const int tid = threadIdx.x, lane = tid & 63;
