@@ -109,6 +109,7 @@ struct XSlot {
 struct SArgs {
   uint32_t* counters;  // kSubs lines per stage
   uint32_t* status;
+  const int32_t* run_site;  // independent stages: (stage << 2) | problem of each run's first tile
   int32_t nstages, total, waves, sb_off;  // sb_off: LDS byte offset of the scale/bias areas
   int32_t nslots, pad1[3];
   XSlot slot[kMaxSlots];
@@ -208,18 +209,27 @@ __device__ __forceinline__ Site site_at(const SStage* __restrict__ st, int si, i
   return c;
 }
 
-// Moves a cursor (stage si, problem pi, resolved site c) forward to the problem holding
-// global tile g, which must lie in stage `last` or before.
-__device__ __forceinline__ void seek(const SStage* __restrict__ st, int& si, int& pi, Site& c, int g) {
-  while (g >= c.tend) {
-    if (pi + 1 < stage_at(st, si).nprob) {
+// Moves (stage si, problem pi) forward to the problem holding global tile g, reading only
+// the problems' tile ranges on the way.
+__device__ __forceinline__ void advance(const SStage* __restrict__ st, int& si, int& pi, int g) {
+  for (;;) {
+    StageRef S = stage_at(st, si);
+    if (g < S.first + S.p[pi].tile_end) return;
+    if (pi + 1 < S.nprob) {
       ++pi;
     } else {
       ++si;
       pi = 0;
     }
-    c = site_at(st, si, pi);
   }
+}
+
+// Moves a cursor (stage si, problem pi, resolved site c) forward to the problem holding
+// global tile g; the site is resolved once, at the end.
+__device__ __forceinline__ void seek(const SStage* __restrict__ st, int& si, int& pi, Site& c, int g) {
+  if (g < c.tend) return;
+  advance(st, si, pi, g);
+  c = site_at(st, si, pi);
 }
 
 // The scale/bias span of a tile: the halves of rows row0 .. row0 + R - 1 (R = 64 >> sh),
@@ -370,12 +380,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     return (int)((((unsigned)k / kRun) * (unsigned)V + (unsigned)v) * kRun + (unsigned)k % kRun);
   };
 
-  // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp)
+  // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp); a cursor that
+  // leaves its problem starts from the problem of its run's first tile (a table lookup)
+  // rather than walking through the problems in between
   int ls = 0, lp = 0, cs = 0, cp = 0;
   Site lc = site_at(st, 0, 0), cc = lc;
+  const int32_t __attribute__((address_space(4)))* runs =
+      reinterpret_cast<const int32_t __attribute__((address_space(4)))*>(
+          reinterpret_cast<uint64_t>(uniform_ptr(a.run_site)));
+  auto move = [&](int& si, int& pi, Site& c, int g) {
+    if (g < c.tend) return;
+    const int e = runs[g / kRun];
+    si = e >> 2;
+    pi = e & 3;
+    advance(st, si, pi, g);
+    c = site_at(st, si, pi);
+  };
   Tile T[kDepth];
   auto issue = [&](int g, Tile& t) {
-    if (g < total) seek(st, ls, lp, lc, g);
+    if (g < total) move(ls, lp, lc, g);
     load_site(lc, g, g < total, lane, t);
   };
 #pragma unroll
@@ -394,7 +417,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
       const int gd = tile_of(k + d);
       const bool in = gd < total;
       const int gc = in ? gd : g0;
-      seek(st, cs, cp, cc, gc);
+      move(cs, cp, cc, gc);
       compute_site(cc, gc, lane, T[d], smem, sbw, magic, in);
       issue(tile_of(k + d + kDepth), T[d]);
     }
@@ -498,6 +521,7 @@ struct imq_stream {
   std::vector<SStage> stages;
   SStage* d_stages = nullptr;
   uint32_t* d_words = nullptr;  // counters, then the status word
+  int32_t* d_runs = nullptr;    // independent stages: the problem of each run's first tile
   int64_t counter_words = 0;
   SArgs args;
   int grid = 0;
@@ -509,6 +533,7 @@ namespace {
 void free_stream(imq_stream* p) {
   if (!p) return;
   if (p->d_stages) (void)hipFree(p->d_stages);
+  if (p->d_runs) (void)hipFree(p->d_runs);
   if (p->d_words) (void)hipFree(p->d_words);
   delete p;
 }
@@ -649,6 +674,31 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
           hipSuccess) {
     free_stream(p);
     return fail(IMQ_ELAUNCH, "copying the stage table failed");
+  }
+  if (!p->chained) {
+    // the problem of the first tile of every run of kRun tiles
+    const int nruns = (tiles + kRun - 1) / kRun;
+    std::vector<int32_t> runs((size_t)nruns);
+    int si = 0, pi = 0;
+    for (int r = 0; r < nruns; ++r) {
+      const int g = r * kRun;
+      while (g >= p->stages[si].first + p->stages[si].p[pi].tile_end) {
+        if (pi + 1 < p->stages[si].nprob) {
+          ++pi;
+        } else {
+          ++si;
+          pi = 0;
+        }
+      }
+      runs[(size_t)r] = (si << 2) | pi;
+    }
+    if (hipMalloc(&p->d_runs, sizeof(int32_t) * (size_t)nruns) != hipSuccess ||
+        hipMemcpy(p->d_runs, runs.data(), sizeof(int32_t) * (size_t)nruns, hipMemcpyHostToDevice) !=
+            hipSuccess) {
+      free_stream(p);
+      return fail(IMQ_ELAUNCH, "copying the run table failed");
+    }
+    p->args.run_site = p->d_runs;
   }
   const void* fn = p->chained ? reinterpret_cast<const void*>(stream_chain_kernel)
                               : reinterpret_cast<const void*>(stream_kernel);
