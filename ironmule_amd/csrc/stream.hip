@@ -111,7 +111,7 @@ struct SArgs {
   uint32_t* status;
   const int32_t* run_site;  // independent stages: (stage << 2) | problem of each run's first tile
   int32_t nstages, total, waves, sb_off;  // sb_off: LDS byte offset of the scale/bias areas
-  int32_t nslots, pad1[3];
+  int32_t nslots, run, pad1[2];            // run: tiles per run (independent stages)
   XSlot slot[kMaxSlots];
 };
 
@@ -358,13 +358,13 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
 
 // ------------------------------------------------------------ independent stages
 
-// Wavefront v takes runs of kRun consecutive tiles: run v, v + V, v + 2V, ... of the
-// program (V wavefronts), so at any moment the device streams one compact window of the
-// weights, and a wavefront resolves a problem's descriptors once per run rather than once
-// per tile.  Its cursors only move forward.  kDepth tiles are in flight: the loads of a
+// Wavefront v takes runs of R consecutive tiles: run v, v + V, v + 2V, ... of the program
+// (V wavefronts), so at any moment the device streams one compact window of the weights,
+// and a wavefront resolves a problem's descriptors once per run rather than once per
+// tile.  R (16 or a little more) is chosen so that the runs split the program evenly over
+// the wavefronts.  Its cursors only move forward.  kDepth tiles are in flight: the loads of a
 // wavefront's tile k + kDepth are issued as soon as its tile k has been computed.
-constexpr int kRun = 4;
-static_assert(kRun % kDepth == 0, "runs hold whole passes");
+constexpr int kRunTarget = 16;
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
   extern __shared__ uint4 smem_raw[];
@@ -372,12 +372,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int v = blockIdx.x * kWaves + wave;
-  const int V = a.waves, total = a.total;
+  const int V = a.waves, total = a.total, R = a.run;
   uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
   const uint32_t magic = in_vgpr(kMagic);
-  // this wavefront's k-th tile (increasing in k)
-  auto tile_of = [&](int k) {
-    return (int)((((unsigned)k / kRun) * (unsigned)V + (unsigned)v) * kRun + (unsigned)k % kRun);
+  // a position in this wavefront's sequence of tiles: run r (global), tile t of the run
+  struct Pos {
+    int r, t;
+  };
+  auto tile = [&](const Pos& p) { return p.r * R + p.t; };
+  auto step = [&](Pos& p) {
+    if (++p.t == R) {
+      p.t = 0;
+      p.r += V;
+    }
   };
 
   // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp); a cursor that
@@ -388,21 +395,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   const int32_t __attribute__((address_space(4)))* runs =
       reinterpret_cast<const int32_t __attribute__((address_space(4)))*>(
           reinterpret_cast<uint64_t>(uniform_ptr(a.run_site)));
-  auto move = [&](int& si, int& pi, Site& c, int g) {
+  auto move = [&](int& si, int& pi, Site& c, int g, int r) {
     if (g < c.tend) return;
-    const int e = runs[g / kRun];
+    const int e = runs[r];
     si = e >> 2;
     pi = e & 3;
     advance(st, si, pi, g);
     c = site_at(st, si, pi);
   };
   Tile T[kDepth];
-  auto issue = [&](int g, Tile& t) {
-    if (g < total) move(ls, lp, lc, g);
+  Pos lpos{v, 0}, cpos{v, 0};
+  auto issue = [&](Tile& t) {
+    const int g = tile(lpos);
+    if (g < total) move(ls, lp, lc, g, lpos.r);
     load_site(lc, g, g < total, lane, t);
+    step(lpos);
   };
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d) issue(tile_of(d), T[d]);
+  for (int d = 0; d < kDepth; ++d) issue(T[d]);
   for (int k = 0; k < a.nslots; ++k) stage_x(a.slot[k].x, a.slot[k].K, false, smem + a.slot[k].off, tid);
   lds_barrier();
 
@@ -410,16 +420,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   // loop head has issued the tiles' loads in the same order and each tile's compute waits
   // only for its own loads.  A tile past the end (the last pass) was loaded as zeros; it
   // is computed at the pass's first tile's site and not stored.
-  for (int k = 0; tile_of(k) < total; k += kDepth) {
-    const int g0 = tile_of(k);
+  for (;;) {
+    const Pos p0 = cpos;
+    const int g0 = tile(p0);
+    if (g0 >= total) break;
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
-      const int gd = tile_of(k + d);
+      const int gd = tile(cpos);
       const bool in = gd < total;
-      const int gc = in ? gd : g0;
-      move(cs, cp, cc, gc);
-      compute_site(cc, gc, lane, T[d], smem, sbw, magic, in);
-      issue(tile_of(k + d + kDepth), T[d]);
+      move(cs, cp, cc, in ? gd : g0, in ? cpos.r : p0.r);
+      compute_site(cc, in ? gd : g0, lane, T[d], smem, sbw, magic, in);
+      step(cpos);
+      issue(T[d]);
     }
   }
 }
@@ -675,31 +687,6 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
     free_stream(p);
     return fail(IMQ_ELAUNCH, "copying the stage table failed");
   }
-  if (!p->chained) {
-    // the problem of the first tile of every run of kRun tiles
-    const int nruns = (tiles + kRun - 1) / kRun;
-    std::vector<int32_t> runs((size_t)nruns);
-    int si = 0, pi = 0;
-    for (int r = 0; r < nruns; ++r) {
-      const int g = r * kRun;
-      while (g >= p->stages[si].first + p->stages[si].p[pi].tile_end) {
-        if (pi + 1 < p->stages[si].nprob) {
-          ++pi;
-        } else {
-          ++si;
-          pi = 0;
-        }
-      }
-      runs[(size_t)r] = (si << 2) | pi;
-    }
-    if (hipMalloc(&p->d_runs, sizeof(int32_t) * (size_t)nruns) != hipSuccess ||
-        hipMemcpy(p->d_runs, runs.data(), sizeof(int32_t) * (size_t)nruns, hipMemcpyHostToDevice) !=
-            hipSuccess) {
-      free_stream(p);
-      return fail(IMQ_ELAUNCH, "copying the run table failed");
-    }
-    p->args.run_site = p->d_runs;
-  }
   const void* fn = p->chained ? reinterpret_cast<const void*>(stream_chain_kernel)
                               : reinterpret_cast<const void*>(stream_kernel);
   if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p->lds) != hipSuccess) {
@@ -723,6 +710,37 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
   p->args.nstages = nstages;
   p->args.total = tiles;
   p->args.waves = grid * kWaves;
+  if (!p->chained) {
+    // runs of kRunTarget tiles or a little more, in whole rounds of one run per wavefront
+    // (the last round short by less than one tile per run), and the problem of the first
+    // tile of every run
+    const int V = grid * kWaves;
+    const int rounds = std::max(1, tiles / (V * kRunTarget));
+    const int R = (tiles + V * rounds - 1) / (V * rounds);
+    p->args.run = R;
+    const int nruns = (tiles + R - 1) / R;
+    std::vector<int32_t> runs((size_t)nruns);
+    int si = 0, pi = 0;
+    for (int r = 0; r < nruns; ++r) {
+      const int g = r * R;
+      while (g >= p->stages[si].first + p->stages[si].p[pi].tile_end) {
+        if (pi + 1 < p->stages[si].nprob) {
+          ++pi;
+        } else {
+          ++si;
+          pi = 0;
+        }
+      }
+      runs[(size_t)r] = (si << 2) | pi;
+    }
+    if (hipMalloc(&p->d_runs, sizeof(int32_t) * (size_t)nruns) != hipSuccess ||
+        hipMemcpy(p->d_runs, runs.data(), sizeof(int32_t) * (size_t)nruns, hipMemcpyHostToDevice) !=
+            hipSuccess) {
+      free_stream(p);
+      return fail(IMQ_ELAUNCH, "copying the run table failed");
+    }
+    p->args.run_site = p->d_runs;
+  }
   *out = p;
   return ok();
 }
