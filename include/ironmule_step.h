@@ -123,13 +123,15 @@ IMQ_API void imq_program_destroy(imq_program* program);
 /* ------------------------------------------------------------------ streaming engine
  *
  * A chain of one-row 4-bit qmv stages (imq_qmv_stage, as for imq_qmv_program_create)
- * run by ONE persistent launch that streams the weights of every stage: each wavefront
- * of the grid takes every V-th tile of the program (V wavefronts) and keeps the next
- * tile's loads in flight while it computes the current one.
+ * run by ONE persistent launch that streams the weights of every stage; each wavefront
+ * keeps its next tile's loads in flight while it computes the current one.
  *   * With no wait_previous anywhere the stages are independent: their distinct x rows
  *     (at most 8, 64 KiB staged) are read once per workgroup at the start and the
- *     wavefronts stream from the first stage to the last with no barrier or wait.
- *   * With waits, every workgroup enters the stages in order, issuing its weight loads
+ *     wavefronts stream from the first stage to the last with no barrier or wait, each
+ *     taking every V-th run of consecutive tiles (V wavefronts; 16 or more tiles per run
+ *     when the program has at least 16 tiles per wavefront).
+ *   * With waits, each wavefront takes every V-th tile of a stage.
+ *     Every workgroup enters the stages in order, issuing its weight loads
  *     for a stage before waiting for that stage's input; the grid is then limited to the
  *     workgroups the device keeps resident at once, no other kernel may run on the device
  *     during the launch, and every wait is bounded (imq_stream_status reports a stall).
