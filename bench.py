@@ -35,6 +35,7 @@ PEAK_HBM_GBS = 8000.0
 LAYER = [("q", 4096, 2560), ("k", 1024, 2560), ("v", 1024, 2560), ("o", 2560, 4096),
          ("gate", 9728, 2560), ("up", 9728, 2560), ("down", 2560, 9728)]
 LAYERS = 36
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 SEED = 20261201
 
 
@@ -244,6 +245,9 @@ def bench_config(torch, native, n, k, ms, y_dtype, copies, device, seed, repeats
         sec = time_graph(torch, runner, repeats, stream) / copies
         out[str(m)] = {"us": sec * 1e6, "gbs": qmv_bytes(n, k, m, ybytes) / sec / 1e9,
                        "weight_gbs": weight_bytes(n, k) / sec / 1e9}
+        if m >= 3:  # the MFMA path: algorithmic 2 M N K flops against the dense bf16 peak
+            tflops = 2.0 * m * n * k / sec / 1e12
+            out[str(m)].update({"tflops": tflops, "mfma_frac": tflops / MFMA_BF16_PEAK_TFLOPS})
         del runner
     del ws
     torch.cuda.empty_cache()
