@@ -123,7 +123,9 @@ __device__ __forceinline__ void load_batch(Batch<B>& t, const uint32_t* wrow, co
   for (int q = 0; q < B; ++q) {
     const int kc = j + ((batch * B + q) << sh);
     const int kk = kc < C ? kc : 0;
-    t.w[q] = *reinterpret_cast<const uint4*>(wrow + kk * 4);
+    // streamed once: the non-temporal cache policy
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + kk * 4));
+    t.w[q] = make_uint4(v.x, v.y, v.z, v.w);
     t.s[q] = srow[kk >> 1];
     t.b[q] = brow[kk >> 1];
   }
