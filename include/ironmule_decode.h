@@ -84,6 +84,26 @@ IMQ_API int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool,
                                      int32_t max_len, float scale, float* workspace,
                                      void* stream);
 
+/* The attention of one decode step fused into one launch, as the decode programs run it:
+ * per-head RMSNorm (q_norm, k_norm, eps) and rotary embedding (theta, at positions[b])
+ * of q (B, Hq, 128) and k (B, Hkv, 128); this step's k and v written into the pools at
+ * row positions[b] of slot slots[b]; then out[b][h] = softmax(q . K / sqrt(128)) V over
+ * rows 0 .. positions[b] of the slot (clamped to max_len and capacity), split over 64-key
+ * chunks with the split plan of imq_attention_decode and merged in split order by the
+ * last split of each (request, KV head).  The same bits as imq_qk_norm_rope followed by
+ * imq_attention_decode with lengths = positions + 1.  `workspace`: at least
+ * imq_attention_workspace(B, Hq, max_len) bytes; `counters`: B * Hkv uint32, zero before
+ * the first call and left at zero by every call (one set per stream).  Replaces the
+ * q_norm, k_norm, rope, KV write and attention steps of the decode composition
+ * (ironmule/dense_cpu.py:201-220). */
+IMQ_API int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    const uint16_t* q_norm, const uint16_t* k_norm,
+                                    const int32_t* positions, const int32_t* slots,
+                                    uint16_t* k_pool, uint16_t* v_pool, uint16_t* out, int32_t B,
+                                    int32_t Hq, int32_t Hkv, int32_t capacity, int32_t num_slots,
+                                    int32_t max_len, float theta, float eps, float* workspace,
+                                    uint32_t* counters, void* stream);
+
 /* out = bf16(silu(gate) * up), silu(g) = g / (1 + exp(-g)), n elements.
  * Replaces swiglu(gate, up) (ironmule/dense_plan.py:374-375; nn.silu in dense_cpu.py:216). */
 IMQ_API int32_t imq_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,

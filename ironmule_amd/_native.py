@@ -115,6 +115,8 @@ _SIGNATURES = {
     "imq_attention_workspace": ([_I32, _I32, _I32], ctypes.c_size_t),
     "imq_attention_decode": ([_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                               ctypes.c_float, _P, _P], _I32),
+    "imq_attention_fused": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                             _I32, _I32, ctypes.c_float, ctypes.c_float, _P, _P, _P], _I32),
     "imq_silu_mul": ([_P, _P, _P, _I64, _P], _I32),
     # persistent programs (include/ironmule_step.h)
     "imq_decode_program_create": ([ctypes.POINTER(StepDesc), ctypes.POINTER(_P)], _I32),
@@ -460,6 +462,38 @@ def qk_norm_rope(q, k, v, q_norm, k_norm, positions, slots, q_out, k_pool, v_poo
 def attention_workspace(b: int, hq: int, max_len: int) -> int:
     """fp32 elements of workspace imq_attention_decode needs."""
     return int(lib().imq_attention_workspace(b, hq, max_len)) // 4
+
+
+def attention_fused(q, k, v, q_norm, k_norm, positions, slots, k_pool, v_pool, out,
+                    max_len: int, theta: float, eps: float, workspace: torch.Tensor,
+                    counters: torch.Tensor, stream=None) -> torch.Tensor:
+    """One launch: q/k RMSNorm + rotary, this step's k and v into the pools at `positions`,
+    and out (B, Hq, 128) bf16 = grouped-query attention over rows 0 .. positions[b] of each
+    request's slot; the same bits as qk_norm_rope followed by attention_decode.  `counters`
+    is (B * kv_heads,) int32, zero before the first call and left at zero."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_norm", q_norm), ("k_norm", k_norm),
+                    ("k_pool", k_pool), ("v_pool", v_pool), ("out", out)):
+        _require(t, torch.bfloat16, name)
+    _require(positions, torch.int32, "positions")
+    _require(slots, torch.int32, "slots")
+    _require(workspace, torch.float32, "workspace")
+    _require(counters, torch.int32, "counters")
+    num_slots, hkv, capacity, d = k_pool.shape
+    b = int(positions.numel())
+    hq = q.numel() // (b * d)
+    if (d != 128 or v_pool.shape != k_pool.shape or k.numel() != b * hkv * d
+            or v.numel() != b * hkv * d or out.numel() != q.numel() or slots.numel() != b):
+        raise ValueError("inconsistent q/k/v/pool/out shapes (head dim 128)")
+    if workspace.numel() < attention_workspace(b, hq, max_len):
+        raise ValueError("workspace too small")
+    if counters.numel() < b * hkv:
+        raise ValueError("counters too small")
+    _check(lib().imq_attention_fused(_ptr(q), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm),
+                                     _ptr(positions), _ptr(slots), _ptr(k_pool), _ptr(v_pool),
+                                     _ptr(out), b, hq, hkv, capacity, num_slots, int(max_len),
+                                     float(theta), float(eps), _ptr(workspace), _ptr(counters),
+                                     _stream(stream)))
+    return out
 
 
 def attention_decode(q, k_pool, v_pool, lengths, slots, out, max_len: int, scale: float,

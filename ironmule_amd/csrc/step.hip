@@ -36,6 +36,7 @@
 #include <string>
 #include <vector>
 
+#include "../../include/ironmule_decode.h"
 #include "../../include/ironmule_step.h"
 #include "common.h"
 #include "runtime.h"
@@ -702,6 +703,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
                                     __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(used - 1);
   __syncthreads();
   if (!L.last) return true;
+  // every split has arrived: the counter is ready for the next launch
+  if (tid == 0) st_sc1(S.combine + b * Hkv + kvh, 0u);
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int g = wave + 4 * r;
@@ -1025,6 +1028,66 @@ void attention_split(int B, int Hkv, int span, int* splits, int* cps) {
 }  // namespace
 
 extern "C" {
+
+int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            const uint16_t* q_norm, const uint16_t* k_norm,
+                            const int32_t* positions, const int32_t* slots, uint16_t* k_pool,
+                            uint16_t* v_pool, uint16_t* out, int32_t B, int32_t Hq, int32_t Hkv,
+                            int32_t capacity, int32_t num_slots, int32_t max_len, float theta,
+                            float eps, float* workspace, uint32_t* counters, void* stream) {
+  if (!q || !k || !v || !q_norm || !k_norm || !positions || !slots || !k_pool || !v_pool || !out ||
+      !workspace || !counters)
+    return fail(IMQ_EINVAL, "null pointer");
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || Hq / Hkv > 8)
+    return fail(IMQ_EINVAL, "bad head counts (Hq a multiple of Hkv, at most 8 query heads per KV head)");
+  if (capacity < 1 || num_slots < 1 || max_len < 1 || !(theta > 0.0f) || !(eps >= 0.0f))
+    return fail(IMQ_EINVAL, "bad capacity, slot count, max_len, theta or eps");
+  if ((int64_t)num_slots * Hkv * capacity * kD * 2 >= ((int64_t)1 << 31))
+    return fail(IMQ_EUNSUPPORTED, "a KV pool of 2 GiB or more exceeds the attention's offsets");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  const int span = std::min(max_len, capacity);
+  int splits, cps;
+  attention_split(B, Hkv, span, &splits, &cps);
+  Stage A;
+  memset(&A, 0, sizeof(A));
+  A.kind = kKindAttention;
+  A.wait = -1;
+  A.count = B * Hkv * splits;
+  A.eps = eps;
+  A.log2_theta = log2f(theta);
+  A.scale = 1.0f / sqrtf((float)kD);
+  A.q = q;
+  A.k = k;
+  A.v = v;
+  A.q_norm = q_norm;
+  A.k_norm = k_norm;
+  A.k_pool = k_pool;
+  A.v_pool = v_pool;
+  A.attn_out = out;
+  A.positions = positions;
+  A.slots = slots;
+  A.part = workspace;
+  A.ml = workspace + (size_t)B * Hq * splits * kD;
+  A.combine = counters;
+  A.Hq = Hq;
+  A.Hkv = Hkv;
+  A.capacity = capacity;
+  A.num_slots = num_slots;
+  A.max_len = span;
+  A.splits = splits;
+  A.cps = cps;
+  StepArgs a;
+  memset(&a, 0, sizeof(a));
+  a.ntasks = A.count;
+  a.staged = 1;
+  const size_t lds = (sizeof(AttnLds) + 15) & ~(size_t)15;
+  hipLaunchKernelGGL(attention_stage_kernel, dim3(A.count), dim3(kThreads), lds,
+                     static_cast<hipStream_t>(stream), A, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused attention launch: ") + hipGetErrorString(e));
+  return ok();
+}
 
 int32_t imq_qmv_program_create(const imq_qmv_stage* stages, int32_t count, imq_program** out) {
   if (!out) return fail(IMQ_EINVAL, "out must be non-null");

@@ -135,6 +135,7 @@ class DecodeState:
         self.logits = torch.empty((batch, c.vocab), dtype=torch.float32, device=device)
         self.workspace = torch.empty(_native.attention_workspace(batch, c.heads, self.max_len),
                                      dtype=torch.float32, device=device)
+        self.attn_counters = torch.zeros(batch * c.kv_heads, dtype=torch.int32, device=device)
         self.tokens = torch.zeros(batch, dtype=torch.int32, device=device)
         self.slot_ids = torch.arange(batch, dtype=torch.int32, device=device) % slots
         self.positions = torch.zeros(batch, dtype=torch.int32, device=device)
@@ -157,16 +158,21 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
     c, s = weights.config, state
     n = _native
     n.embed(*weights.embed, s.tokens, s.h, stream=stream)
-    scale = c.head_dim ** -0.5
     delta = None
     for i, layer in enumerate(weights.layers):
         n.add_rmsnorm(s.h, layer["input_norm"], s.x, c.eps, delta=delta, stream=stream)
         n.qmv_grouped([layer["q"], layer["k"], layer["v"]], [s.x, s.x, s.x],
                       outs=[s.q, s.k, s.v], stream=stream)
-        n.qk_norm_rope(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions, s.slot_ids,
-                       s.q_rot, s.k_pool[i], s.v_pool[i], c.theta, c.eps, stream=stream)
-        n.attention_decode(s.q_rot, s.k_pool[i], s.v_pool[i], s.lengths, s.slot_ids, s.attn,
-                           s.max_len, scale, s.workspace, stream=stream)
+        if s.batch == 1:  # one launch (the decode programs' attention stage, same bits)
+            n.attention_fused(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
+                              s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len, c.theta,
+                              c.eps, s.workspace, s.attn_counters, stream=stream)
+        else:  # three launches: measured faster than the fused form at batch 32
+            n.qk_norm_rope(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
+                           s.slot_ids, s.q_rot, s.k_pool[i], s.v_pool[i], c.theta, c.eps,
+                           stream=stream)
+            n.attention_decode(s.q_rot, s.k_pool[i], s.v_pool[i], s.lengths, s.slot_ids, s.attn,
+                               s.max_len, c.head_dim ** -0.5, s.workspace, stream=stream)
         n.qmv(*layer["o"], s.attn, out=s.delta, stream=stream)
         n.add_rmsnorm(s.h, layer["post_norm"], s.x, c.eps, delta=s.delta, stream=stream)
         n.qmv_grouped([layer["gate"], layer["up"]], [s.x, s.x], outs=[s.gate, s.up], stream=stream)
