@@ -279,19 +279,24 @@ __global__ __launch_bounds__(kThreads) void qmv_rows_kernel(LaunchArgs a) {
 // LDS layout of the one-row kernel, sized by its template so that every staging write
 // is unconditional (pieces past the data are written as zeros): x in pair order as four
 // planes of XR * 64 chunks, their chunk sums, and 2 * SBR * 256 (scale, bias) dwords.
-template <int NCH, int XR>
+template <int NCH, int XR, int MR = 1>
 struct M1Lds {
   static constexpr int kChunks = XR * 64;                        // per plane, >= K / 32
   static constexpr int kSbr = (64 * NCH + kThreads - 1) / kThreads;  // dwords per thread
-  static constexpr size_t kBytes = (size_t)kChunks * (64 + 4) + (size_t)kSbr * kThreads * 8;
+  static constexpr size_t kBytes =
+      (size_t)MR * kChunks * (64 + 4) + (size_t)kSbr * kThreads * 8;
 };
 
 // One tile of the one-row kernel, its problem's arguments already in scalar registers.
-template <int NCH, int XR>
+// With MR = 2 the tile serves two activation rows (xp, xp1 -> yp, yp1) from one read of
+// the weights; each row's chunk order and sums are those of MR = 1, so each output row
+// is the one-row result, bit for bit.
+template <int NCH, int XR, int MR = 1>
 __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, const uint16_t* bp,
                                         const uint16_t* xp, void* yp, int K, int N, int sh,
-                                        int nch, int yf32, int row0) {
-  using L = M1Lds<NCH, XR>;
+                                        int nch, int yf32, int row0,
+                                        const uint16_t* xp1 = nullptr, void* yp1 = nullptr) {
+  using L = M1Lds<NCH, XR, MR>;
   constexpr int CP = L::kChunks, SBR = L::kSbr;
   extern __shared__ uint4 smem[];
   const int C = K >> 5, G = K >> 6, W = K >> 3;
@@ -299,18 +304,22 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
   const int j = tid & ((1 << sh) - 1);
   const int rl = tid >> sh;  // the lane's row within the tile
   const int row = row0 + rl;
-  uint4* xq = smem;                                     // [4][CP]
-  float* sx = reinterpret_cast<float*>(smem + 4 * CP);  // [CP]
-  uint32_t* sbl = reinterpret_cast<uint32_t*>(sx + CP); // [rows][G], padded
+  uint4* xq = smem;                                          // [MR][4][CP]
+  float* sx = reinterpret_cast<float*>(smem + MR * 4 * CP);  // [MR][CP]
+  uint32_t* sbl = reinterpret_cast<uint32_t*>(sx + MR * CP);  // [rows][G], padded
   const uint32_t magic = in_vgpr(kMagic);
 
-  // x: XR pieces of 8 values per thread
-  const __amdgpu_buffer_rsrc_t xrsrc = buffer_rsrc(xp, (uint32_t)K * 2u);
-  uint4 xs[XR];
+  // x: XR pieces of 8 values per thread and row
+  const uint16_t* xps[2] = {xp, xp1};
+  uint4 xs[MR][XR];
 #pragma unroll
-  for (int t = 0; t < XR; ++t) {
-    const int i = tid + kThreads * t;
-    xs[t] = load_b128(xrsrc, i < W ? 16u * i : kPastBuffer);
+  for (int m = 0; m < MR; ++m) {
+    const __amdgpu_buffer_rsrc_t xrsrc = buffer_rsrc(xps[m], (uint32_t)K * 2u);
+#pragma unroll
+    for (int t = 0; t < XR; ++t) {
+      const int i = tid + kThreads * t;
+      xs[m][t] = load_b128(xrsrc, i < W ? 16u * i : kPastBuffer);
+    }
   }
   // the tile's scales and biases: rows * G halves from row0 * G on, as dwords (rows is
   // even, so the span starts 4-byte aligned); rows past N read as zero.  The range is
@@ -342,13 +351,16 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
 
   // staging, unconditionally (pieces past x and past the span are zeros)
 #pragma unroll
-  for (int t = 0; t < XR; ++t) {
-    const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
-    xq[(i & 3) * CP + (i >> 2)] = pair_order(xs[t]);
-    float part = sum8(xs[t]);
-    part += __shfl_xor(part, 1);
-    part += __shfl_xor(part, 2);
-    if ((i & 3) == 0) sx[i >> 2] = part;
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int t = 0; t < XR; ++t) {
+      const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
+      xq[(m * 4 + (i & 3)) * CP + (i >> 2)] = pair_order(xs[m][t]);
+      float part = sum8(xs[m][t]);
+      part += __shfl_xor(part, 1);
+      part += __shfl_xor(part, 2);
+      if ((i & 3) == 0) sx[m * CP + (i >> 2)] = part;
+    }
   }
 #pragma unroll
   for (int q = 0; q < SBR; ++q) {
@@ -358,7 +370,9 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
   }
   lds_barrier();
 
-  float acc = 0.0f;
+  float acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
   const uint32_t* sbr = sbl + rl * G;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
@@ -369,22 +383,44 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
       const uint32_t sb = sbr[kk >> 1];
       const float sc = __uint_as_float(sb << 16);
       const float bi = __uint_as_float(sb & 0xffff0000u);
-      const float sxm = sx[kk];
-      const float d = chunk_dot(wv[i], xq[kk], xq[CP + kk], xq[2 * CP + kk], xq[3 * CP + kk],
-                                -128.0f * sxm, magic);
-      const float v = fmaf(sc, d, fmaf(bi, sxm, acc));
-      acc = valid ? v : acc;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const uint4* xm = xq + m * 4 * CP;
+        const float sxm = sx[m * CP + kk];
+        const float d = chunk_dot(wv[i], xm[kk], xm[CP + kk], xm[2 * CP + kk], xm[3 * CP + kk],
+                                  -128.0f * sxm, magic);
+        const float v = fmaf(sc, d, fmaf(bi, sxm, acc[m]));
+        acc[m] = valid ? v : acc[m];
+      }
     }
   }
-  float v = row16_sum(acc);
-  if (sh >= 5) v += __shfl_xor(v, 16);
-  if (sh >= 6) v += __shfl_xor(v, 32);
-  if (j == 0 && row < N) {
-    if (yf32)
-      static_cast<float*>(yp)[row] = v;
-    else
-      static_cast<uint16_t*>(yp)[row] = f32_to_bf16_bits(v);
+  void* yps[2] = {yp, yp1};
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float v = row16_sum(acc[m]);
+    if (sh >= 5) v += __shfl_xor(v, 16);
+    if (sh >= 6) v += __shfl_xor(v, 32);
+    if (j == 0 && row < N) {
+      if (yf32)
+        static_cast<float*>(yps[m])[row] = v;
+      else
+        static_cast<uint16_t*>(yps[m])[row] = f32_to_bf16_bits(v);
+    }
   }
+}
+
+// Two activation rows: blockIdx.y is the problem, blockIdx.x its tile.
+template <int NCH, int XR>
+__global__ __launch_bounds__(kThreads) void qmv_m2_kernel(LaunchArgs a) {
+  const Problem& P = a.p[blockIdx.y];
+  const int K = P.K, N = P.N, sh = P.lpr_shift, nch = P.nch, yf32 = a.y_f32;
+  const int row0 = blockIdx.x * (kThreads >> sh);
+  if (row0 >= N) return;  // past this problem's tiles
+  const size_t ybytes = yf32 ? 4 : 2;
+  void* y0 = a.table ? a.yt[0] : P.y;
+  void* y1 = a.table ? a.yt[1] : static_cast<char*>(P.y) + (size_t)P.ldy * ybytes;
+  m1_tile<NCH, XR, 2>(P.w, P.s, P.b, x_row(a, P, 0), y0, K, N, sh, nch, yf32, row0,
+                      x_row(a, P, 1), y1);
 }
 
 // Any number of problems: blockIdx.y is the problem, blockIdx.x its tile.
@@ -1159,6 +1195,26 @@ hipError_t launch_m1_for(const LaunchArgs& a, const M1Plan& pl, hipStream_t stre
   return launch_m1<8, 8>(a, pl, stream);
 }
 
+template <int NCH, int XR>
+hipError_t launch_m2(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream) {
+  constexpr size_t lds = M1Lds<NCH, XR, 2>::kBytes;
+  hipLaunchKernelGGL((qmv_m2_kernel<NCH, XR>), dim3(pl.grid_x, a.count), dim3(kThreads), lds,
+                     stream, a);
+  return hipGetLastError();
+}
+
+// Two rows through the one-row tile: the instantiations whose LDS stays under 64 KiB
+// (x pieces per thread <= 5, K <= 10240); false for the other plans.
+bool launch_m2_for(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream, hipError_t* e) {
+  if (pl.nch <= 2 && pl.xr <= 2) *e = launch_m2<2, 2>(a, pl, stream);
+  else if (pl.nch <= 5 && pl.xr <= 2) *e = launch_m2<5, 2>(a, pl, stream);
+  else if (pl.nch <= 5 && pl.xr <= 5) *e = launch_m2<5, 5>(a, pl, stream);
+  else if (pl.xr <= 2) *e = launch_m2<8, 2>(a, pl, stream);
+  else if (pl.xr <= 5) *e = launch_m2<8, 5>(a, pl, stream);
+  else return false;
+  return true;
+}
+
 template <int M, int B>
 hipError_t launch_rows(const LaunchArgs& a, int grid_x, size_t lds, hipStream_t stream) {
   hipLaunchKernelGGL((qmv_rows_kernel<M, B>), dim3(grid_x, a.count), dim3(kThreads), lds, stream,
@@ -1324,6 +1380,8 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* w
   size_t lds = 0;
   if (M == 1 && plan_m1(a, &m1)) {
     e = launch_m1_for(a, m1, stream);
+  } else if (M == 2 && plan_m1(a, &m1) && launch_m2_for(a, m1, stream, &e)) {
+    // launched
   } else if (M <= kValuMaxRows && (lds = plan_rows(a, &grid_x)) > 0) {
     if (M == 1) {
       static const int opts[] = {4, 5};
