@@ -287,15 +287,21 @@ struct M1Lds {
       (size_t)MR * kChunks * (64 + 4) + (size_t)kSbr * kThreads * 8;
 };
 
+// Activation rows 1 .. MR-1 of a few-row tile (row 0 comes in xp / yp).
+struct MoreRows {
+  const uint16_t* x[3];
+  void* y[3];
+};
+
 // One tile of the one-row kernel, its problem's arguments already in scalar registers.
-// With MR = 2 the tile serves two activation rows (xp, xp1 -> yp, yp1) from one read of
-// the weights; each row's chunk order and sums are those of MR = 1, so each output row
-// is the one-row result, bit for bit.
+// With MR > 1 the tile serves MR activation rows (xp, more.x -> yp, more.y) from one read
+// of the weights; each row's chunk order and sums are those of MR = 1, so each output
+// row is the one-row result, bit for bit.
 template <int NCH, int XR, int MR = 1>
 __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, const uint16_t* bp,
                                         const uint16_t* xp, void* yp, int K, int N, int sh,
-                                        int nch, int yf32, int row0,
-                                        const uint16_t* xp1 = nullptr, void* yp1 = nullptr) {
+                                        int nch, int yf32, int row0, const MoreRows& more = {}) {
+  static_assert(MR >= 1 && MR <= 4, "one to four activation rows");
   using L = M1Lds<NCH, XR, MR>;
   constexpr int CP = L::kChunks, SBR = L::kSbr;
   extern __shared__ uint4 smem[];
@@ -310,7 +316,7 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
   const uint32_t magic = in_vgpr(kMagic);
 
   // x: XR pieces of 8 values per thread and row
-  const uint16_t* xps[2] = {xp, xp1};
+  const uint16_t* xps[4] = {xp, more.x[0], more.x[1], more.x[2]};
   uint4 xs[MR][XR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
@@ -394,7 +400,7 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
       }
     }
   }
-  void* yps[2] = {yp, yp1};
+  void* yps[4] = {yp, more.y[0], more.y[1], more.y[2]};
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     float v = row16_sum(acc[m]);
@@ -409,18 +415,22 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
   }
 }
 
-// Two activation rows: blockIdx.y is the problem, blockIdx.x its tile.
-template <int NCH, int XR>
-__global__ __launch_bounds__(kThreads) void qmv_m2_kernel(LaunchArgs a) {
+// MR = 2..4 activation rows: blockIdx.y is the problem, blockIdx.x its tile.
+template <int NCH, int XR, int MR>
+__global__ __launch_bounds__(kThreads) void qmv_mr_kernel(LaunchArgs a) {
   const Problem& P = a.p[blockIdx.y];
   const int K = P.K, N = P.N, sh = P.lpr_shift, nch = P.nch, yf32 = a.y_f32;
   const int row0 = blockIdx.x * (kThreads >> sh);
   if (row0 >= N) return;  // past this problem's tiles
   const size_t ybytes = yf32 ? 4 : 2;
-  void* y0 = a.table ? a.yt[0] : P.y;
-  void* y1 = a.table ? a.yt[1] : static_cast<char*>(P.y) + (size_t)P.ldy * ybytes;
-  m1_tile<NCH, XR, 2>(P.w, P.s, P.b, x_row(a, P, 0), y0, K, N, sh, nch, yf32, row0,
-                      x_row(a, P, 1), y1);
+  MoreRows more = {};
+#pragma unroll
+  for (int m = 1; m < MR; ++m) {
+    more.x[m - 1] = x_row(a, P, m);
+    more.y[m - 1] = a.table ? a.yt[m] : static_cast<char*>(P.y) + (size_t)m * P.ldy * ybytes;
+  }
+  m1_tile<NCH, XR, MR>(P.w, P.s, P.b, x_row(a, P, 0), a.table ? a.yt[0] : P.y, K, N, sh, nch,
+                       yf32, row0, more);
 }
 
 // Any number of problems: blockIdx.y is the problem, blockIdx.x its tile.
@@ -1195,22 +1205,25 @@ hipError_t launch_m1_for(const LaunchArgs& a, const M1Plan& pl, hipStream_t stre
   return launch_m1<8, 8>(a, pl, stream);
 }
 
-template <int NCH, int XR>
-hipError_t launch_m2(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream) {
-  constexpr size_t lds = M1Lds<NCH, XR, 2>::kBytes;
-  hipLaunchKernelGGL((qmv_m2_kernel<NCH, XR>), dim3(pl.grid_x, a.count), dim3(kThreads), lds,
+template <int NCH, int XR, int MR>
+hipError_t launch_mr(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream) {
+  constexpr size_t lds = M1Lds<NCH, XR, MR>::kBytes;
+  static_assert(lds <= 64 * 1024, "the few-row tile stays within 64 KiB of LDS");
+  hipLaunchKernelGGL((qmv_mr_kernel<NCH, XR, MR>), dim3(pl.grid_x, a.count), dim3(kThreads), lds,
                      stream, a);
   return hipGetLastError();
 }
 
-// Two rows through the one-row tile: the instantiations whose LDS stays under 64 KiB
-// (x pieces per thread <= 5, K <= 10240); false for the other plans.
-bool launch_m2_for(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream, hipError_t* e) {
-  if (pl.nch <= 2 && pl.xr <= 2) *e = launch_m2<2, 2>(a, pl, stream);
-  else if (pl.nch <= 5 && pl.xr <= 2) *e = launch_m2<5, 2>(a, pl, stream);
-  else if (pl.nch <= 5 && pl.xr <= 5) *e = launch_m2<5, 5>(a, pl, stream);
-  else if (pl.xr <= 2) *e = launch_m2<8, 2>(a, pl, stream);
-  else if (pl.xr <= 5) *e = launch_m2<8, 5>(a, pl, stream);
+// Two to four rows through the one-row tile: two rows with x pieces per thread <= 5 (K <=
+// 10240), three or four with <= 2 (K <= 4096); false for the other plans.
+template <int MR>
+bool launch_mr_for(const LaunchArgs& a, const M1Plan& pl, hipStream_t stream, hipError_t* e) {
+  if (pl.nch <= 2 && pl.xr <= 2) *e = launch_mr<2, 2, MR>(a, pl, stream);
+  else if (pl.nch <= 5 && pl.xr <= 2) *e = launch_mr<5, 2, MR>(a, pl, stream);
+  else if (pl.xr <= 2) *e = launch_mr<8, 2, MR>(a, pl, stream);
+  else if (MR > 2) return false;
+  else if (pl.nch <= 5 && pl.xr <= 5) *e = launch_mr<5, 5, 2>(a, pl, stream);
+  else if (pl.xr <= 5) *e = launch_mr<8, 5, 2>(a, pl, stream);
   else return false;
   return true;
 }
@@ -1380,7 +1393,11 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* w
   size_t lds = 0;
   if (M == 1 && plan_m1(a, &m1)) {
     e = launch_m1_for(a, m1, stream);
-  } else if (M == 2 && plan_m1(a, &m1) && launch_m2_for(a, m1, stream, &e)) {
+  } else if (M == 2 && plan_m1(a, &m1) && launch_mr_for<2>(a, m1, stream, &e)) {
+    // launched
+  } else if (M == 3 && plan_m1(a, &m1) && launch_mr_for<3>(a, m1, stream, &e)) {
+    // launched
+  } else if (M == 4 && plan_m1(a, &m1) && launch_mr_for<4>(a, m1, stream, &e)) {
     // launched
   } else if (M <= kValuMaxRows && (lds = plan_rows(a, &grid_x)) > 0) {
     if (M == 1) {
