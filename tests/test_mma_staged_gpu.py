@@ -43,7 +43,8 @@ def _rows(n, step):
 
 @pytest.mark.parametrize("m", [3, 5, 16, 32])
 def test_staged_wide_launch_matches_oracle(native, oracle, m):
-    """8200 rows = 129 tiles of 64 (the last one ragged), K = 512 (two stages)."""
+    """8200 rows = 129 tiles of 64 (the last one ragged), K = 512 (two stages).  M = 3 at
+    this K takes the few-row VALU tile instead; the oracle bar is the same."""
     pr = oracle.synthetic(8200, 512, m, seed=oracle.SEED_BASE + 500 + m)
     w, s, b, x = to_device(pr)
     announce("staged wide", m)
