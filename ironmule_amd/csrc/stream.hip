@@ -4,16 +4,21 @@
 //
 // Work.  Every stage is cut into wavefront tiles of 64 / LPR weight rows (LPR lanes per
 // row, the one-row kernel's lane shape, so every output equals imq_qmv's bit for bit).
-// The tiles of all stages form one list in stage order, dealt round-robin to the V
-// wavefronts of the grid: for independent stages wavefront v runs tiles v, v + V, ... of
-// the whole list; for chained stages the same within each stage (counted from the
-// stage's first tile), so that every stage is spread over the whole device.
+// The tiles of all stages form one list in stage order.  For independent stages the
+// list is cut into runs of R consecutive tiles (16 or a little more, sized on the host
+// so that the runs split the list into whole rounds) and wavefront v of the V in the
+// grid runs runs v, v + V, ...: the device streams one compact window of the weights, and
+// a wavefront resolves a problem's descriptors once per run, jumping to a run's problem
+// through a per-program run table.  For chained stages wavefront v runs tiles v, v + V,
+// ... of each stage (counted from the stage's first tile), so that every stage is spread
+// over the whole device.
 //
 // Pipelining.  A wavefront keeps two tiles in registers: while it computes one, the
 // loads of the next are in flight.  Loads are raw buffer loads issued unconditionally
 // (a piece that is not needed reads past its buffer, which returns zero without a memory
-// access), so the number of loads in flight is the same on every path and the waits
-// the compiler places before each tile are exact.
+// access), and a pass over the two tiles has no exit in between, so the number of loads
+// in flight is the same on every path and the waits the compiler places before each tile
+// are exact.  Weights are read with the non-temporal cache policy.
 //
 // Two modes:
 //   * independent stages (no stage reads another's output): every distinct x of the
