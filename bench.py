@@ -82,16 +82,37 @@ class GraphRunner:
 
 
 def time_graph(torch, runner, repeats, stream):
-    """Seconds per replay: events on the graph's own stream around `repeats` replays."""
+    """Seconds per replay: events on the graph's own stream around `repeats` replays,
+    queued behind one untimed replay so the GPU never waits on the host inside them."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    runner.replay()
     start.record(stream)
     for _ in range(repeats):
         runner.replay()
     end.record(stream)
     end.synchronize()
     return start.elapsed_time(end) / 1e3 / repeats
+
+
+def warm_up(torch, runner, stream, min_seconds=0.2, max_seconds=3.0, tol=0.01, batch=4):
+    """Replays `runner` until at least `min_seconds` have passed and two successive timed
+    batches of `batch` replays agree within `tol`: the GPU's clocks ramp over tens of
+    milliseconds, so a fixed count of short replays would time the ramp (the reference's
+    GEMV probe also warms up before it takes the median of repeats, ironmule/hw.py:421-438).
+    Returns what was done, for the result line."""
+    t0 = time.perf_counter()
+    prev, replays = None, 0
+    while True:
+        sec = time_graph(torch, runner, batch, stream)
+        replays += batch
+        elapsed = time.perf_counter() - t0
+        settled = prev is not None and abs(sec - prev) <= tol * prev
+        if (elapsed >= min_seconds and settled) or elapsed >= max_seconds:
+            return {"replays": replays, "seconds": round(elapsed, 3), "settled": settled,
+                    "last_replay_us": round(sec * 1e6, 3)}
+        prev = sec
 
 
 # The layer in decode order: launches that read the same activation share one launch.
@@ -151,12 +172,20 @@ def bench_layer(torch, native, steps, warmup, device, breakdown=True):
     part_n = steps % LAYERS
     part_prog = native.stream_program(_layer_stages(layers[:part_n], xrow, yrow, index)) if part_n else None
     part = GraphRunner(torch, [lambda: part_prog.launch(stream)], stream) if part_n else None
-    for _ in range(max(3, warmup // LAYERS + (1 if warmup % LAYERS else 0))):
+    # at least `warmup` layers, and in any case until the launch time has settled
+    for _ in range(warmup // LAYERS + (1 if warmup % LAYERS else 0)):
         full.replay()
+    warm = warm_up(torch, full, stream)
+    if part is not None:
+        part.replay()  # the first replay of a freshly captured graph is not timed
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    # One untimed launch ahead of the start event keeps the GPU busy while the host queues
+    # the event and the timed launches behind it, so the timed region holds GPU work only
+    # (not the host's graph-submission latency, which is tens of microseconds).
+    full.replay()
     t0 = time.perf_counter()
     start.record(stream)
     for _ in range(steps // LAYERS):
@@ -173,7 +202,7 @@ def bench_layer(torch, native, steps, warmup, device, breakdown=True):
     info = full_prog.info()
     out = {"gpu_s": gpu_s, "wall_s": wall, "step_bytes": step_bytes, "launches": launches,
            "workgroups": info["workgroups"], "launch_bytes": step_bytes * LAYERS,
-           "avg_launch_s": gpu_s / launches if not part_n else None}
+           "avg_launch_s": gpu_s / launches if not part_n else None, "warm_up": warm}
     if part_n == 0:
         out["avg_launch_s"] = gpu_s / launches
     else:  # the full-program launches alone, for the per-launch figure
@@ -241,7 +270,7 @@ def bench_config(torch, native, n, k, ms, y_dtype, copies, device, seed, repeats
         runner = GraphRunner(torch, [
             (lambda w=w, s=s, b=b: native.qmv(w, s, b, x, out=y, stream=stream))
             for (w, s, b) in ws], stream)
-        runner.replay()
+        warm_up(torch, runner, stream, min_seconds=0.05, batch=2)
         sec = time_graph(torch, runner, repeats, stream) / copies
         out[str(m)] = {"us": sec * 1e6, "gbs": qmv_bytes(n, k, m, ybytes) / sec / 1e9,
                        "weight_gbs": weight_bytes(n, k) / sec / 1e9}
@@ -289,6 +318,7 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
             runner = GraphRunner(torch, [fn], stream)
             for _ in range(warmup):
                 runner.replay()
+            warm_up(torch, runner, stream, min_seconds=0.1)
             times[name] = (time_graph(torch, runner, steps, stream), launches)
             del runner
         best = min(times, key=lambda k: times[k][0])
@@ -539,7 +569,8 @@ def main() -> None:
                    "group_size": 64, "batch": 1, "rotating_layers": LAYERS,
                    "launch": "streaming engine: one persistent launch per 36 layers, each "
                              "layer's projections as 4 independent stages in decode order "
-                             "(q/k/v, o, gate/up, down), captured in a hip graph"},
+                             "(q/k/v, o, gate/up, down), captured in a hip graph",
+                   "warm_up": res["warm_up"]},
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),

@@ -258,19 +258,31 @@ def qmv(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, x: torch.Te
 _workspaces: dict = {}
 
 
+def _workspace_key(device, stream) -> tuple[int, int]:
+    """(device index, stream handle) of a launch; stream None is the current stream of
+    that device, resolved here so that launches under different current streams never
+    share a workspace."""
+    dev = torch.device(device)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    if stream is None:
+        stream = torch.cuda.current_stream(index)
+    return index, int(stream.cuda_stream)
+
+
 def _workspace(nbytes: int, device, stream) -> torch.Tensor:
     """A zero-filled fp32 workspace of at least nbytes for (device, stream), kept for later
     calls: the library's split counters must be zero before a workspace's first use and
     every call leaves them at zero, so one workspace serves every call on that stream
-    (calls on one stream never overlap)."""
-    dev = torch.device(device)
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
-           0 if stream is None else int(stream.cuda_stream))
+    (calls on one stream never overlap).  It is allocated and filled on that stream, so
+    the fill is ordered before the launch that uses it; a replaced smaller workspace is
+    released only after the work already queued on the stream."""
+    index, handle = _workspace_key(device, stream)
+    key = (index, handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
-        ws = torch.zeros(-(-nbytes // 4), dtype=torch.float32, device=dev)
-        if not torch.cuda.is_current_stream_capturing():
-            torch.cuda.synchronize(dev)  # the fill runs on the current stream
+        s = stream if stream is not None else torch.cuda.current_stream(index)
+        with torch.cuda.stream(s):
+            ws = torch.zeros(-(-nbytes // 4), dtype=torch.float32, device=torch.device("cuda", index))
         _workspaces[key] = ws
     return ws
 

@@ -121,3 +121,20 @@ def test_ctypes_structures_match_the_header():
         assert got[name] == ctypes.sizeof(cls), name
         for f, _ in cls._fields_:
             assert got[f"{name}.{f}"] == getattr(cls, f).offset, (name, f)
+
+
+def test_workspace_keys_follow_the_current_stream(monkeypatch):
+    """A launch with stream=None keys its split workspace by the stream that is current
+    at the call, so calls under different current streams never share split counters."""
+    from types import SimpleNamespace
+
+    current = {"s": SimpleNamespace(cuda_stream=0x1000)}
+    monkeypatch.setattr(_native.torch.cuda, "current_stream", lambda *a, **k: current["s"])
+    monkeypatch.setattr(_native.torch.cuda, "current_device", lambda: 0)
+    first = _native._workspace_key("cuda:0", None)
+    current["s"] = SimpleNamespace(cuda_stream=0x2000)
+    second = _native._workspace_key("cuda:0", None)
+    assert first != second
+    explicit = _native._workspace_key("cuda:0", SimpleNamespace(cuda_stream=0x2000))
+    assert explicit == second
+    assert _native._workspace_key("cuda:1", None)[0] == 1
