@@ -139,6 +139,27 @@ IMQ_API int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, i
                                    int32_t group_size, int32_t bits, int32_t y_dtype,
                                    float* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the library's static split scratch (one per device, held until the process
+ * ends), the largest split workspace imq_qmv_grouped_noalloc serves. */
+#define IMQ_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/*
+ * imq_qmv_grouped_ws without a caller workspace and without any allocation: the split
+ * partials and counters live in the library's own static device scratch (a per-device
+ * array of IMQ_NOALLOC_SCRATCH_BYTES), so the call performs no hipMalloc, hipFree or other
+ * allocation and can be made where allocating is not allowed.  Same plan, hence the same
+ * bits, as imq_qmv_grouped_ws given imq_qmv_grouped_workspace bytes.  A call whose split
+ * workspace would exceed the scratch returns IMQ_EUNSUPPORTED.  When the call splits, a
+ * small fill kernel clears the scratch's counters first (two launches on `stream`).
+ * Every call on one device shares that device's scratch: calls that overlap on a device
+ * (different streams, or threads) race and must be serialised by the caller.
+ * No counterpart in the reference: this entry point is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ */
+IMQ_API int32_t imq_qmv_grouped_noalloc(const imq_problem* problems, int32_t count, int32_t M,
+                                        int32_t group_size, int32_t bits, int32_t y_dtype,
+                                        void* stream);
+
 /*
  * out[n][k] = scales[n][k/64] * q[n][k] + biases[n][k/64] as fp32 (bit-exact:
  * scale*q is exact in fp32, so only the add rounds), or that fp32 value rounded

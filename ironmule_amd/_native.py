@@ -103,6 +103,8 @@ _SIGNATURES = {
     "imq_qmv_grouped_workspace": ([ctypes.POINTER(Problem), _I32, _I32], ctypes.c_size_t),
     "imq_qmv_grouped_ws": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P,
                             ctypes.c_size_t, _P], _I32),
+    "imq_qmv_grouped_noalloc": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P],
+                                _I32),
     "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_gather_qmv": ([_P, _P, _P, _I32, _P, _I64, _I32, _P, _I32, _P, _I64, _I32, _I32, _I32,
                         _I32, _I32, _P], _I32),

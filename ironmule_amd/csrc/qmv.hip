@@ -1027,6 +1027,51 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t* __res
   }
 }
 
+// Zeroes `words` 32-bit words (the split counters before a call that uses the library's
+// static scratch; a kernel rather than a memset so the call stays capturable in a graph).
+__global__ __launch_bounds__(kThreads) void clear_words_kernel(uint32_t* __restrict__ p, int words) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < words) p[i] = 0u;
+}
+
+}  // namespace
+
+// ------------------------------------------------------ static split scratch
+//
+// The split workspace of imq_qmv_grouped_noalloc: device memory of the library itself, one
+// copy per device (each holds it until the process ends), so that entry point calls no
+// allocator.  Host code never passes `scratch` itself to a kernel (on the host the name is
+// a stand-in, not a device address): the per-device address comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+static __device__ __align__(256) char scratch[IMQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[imq_rt::kMaxDevices];
+
+// The current device's address of `scratch` (looked up once per device, with that device
+// current), or nullptr with *code set.
+void* scratch_address(int32_t* code) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= imq_rt::kMaxDevices) {
+    *code = imq_rt::fail(IMQ_EUNAVAILABLE, "no HIP device is available");
+    return nullptr;
+  }
+  ScratchSlot& s = g_scratch[dev];
+  std::call_once(s.once, [&s] { s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch)); });
+  if (s.err != hipSuccess || s.ptr == nullptr) {
+    *code = imq_rt::fail(IMQ_ELAUNCH, std::string("hipGetSymbolAddress(scratch) failed: ") +
+                                          hipGetErrorString(s.err));
+    return nullptr;
+  }
+  return s.ptr;
+}
+
 // ================================================================== host side
 
 using imq_rt::aligned;
@@ -1564,6 +1609,36 @@ int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, int32_t M
   const DeviceInfo* dev = current_device(&code);
   if (!dev) return code;
   return launch(a, dev, static_cast<hipStream_t>(stream), workspace, workspace_bytes);
+}
+
+int32_t imq_qmv_grouped_noalloc(const imq_problem* problems, int32_t count, int32_t M,
+                                int32_t group_size, int32_t bits, int32_t y_dtype, void* stream) {
+  LaunchArgs a;
+  int32_t code = build_grouped(a, problems, count, M, group_size, bits, y_dtype);
+  if (code != IMQ_OK) return code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
+  // the plan imq_qmv_grouped_ws makes with a workspace of imq_qmv_grouped_workspace bytes,
+  // so both entry points split the same way and give the same bits
+  const size_t need = M >= 3 ? plan_mma(a, (size_t)1 << 40, dev->cu_count).bytes : 0;
+  if (need > IMQ_NOALLOC_SCRATCH_BYTES)
+    return fail(IMQ_EUNSUPPORTED,
+                "this call's split workspace (" + std::to_string(need) +
+                    " bytes) exceeds the library's static scratch of " +
+                    std::to_string((size_t)IMQ_NOALLOC_SCRATCH_BYTES) +
+                    " bytes; use imq_qmv_grouped_ws with a caller workspace");
+  if (need == 0) return launch(a, dev, static_cast<hipStream_t>(stream));
+  void* ws = scratch_address(&code);
+  if (!ws) return code;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // the counters must start at zero; the split kernels leave them at zero, but a kernel
+  // fill before every call keeps that true whatever ran on the device before
+  constexpr int words = (int)(kCounterBytes / 4);
+  hipLaunchKernelGGL(clear_words_kernel, dim3(words / kThreads), dim3(kThreads), 0, st,
+                     static_cast<uint32_t*>(ws), words);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("scratch clear failed: ") + hipGetErrorString(e));
+  return launch(a, dev, st, ws, need);
 }
 
 int32_t imq_gather_qmv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
