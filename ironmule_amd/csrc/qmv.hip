@@ -981,6 +981,360 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
                                              wk == 0, row0 + 32 * wn, row0, kRows, &last);
 }
 
+// ------------------------------ MFMA kernel with the activations held in registers (M >= 3)
+//
+// The x-stationary kernel, for launches with many 32-row weight tiles per CU (the LM head).
+// A workgroup owns a set of tiles of one weight, every r-th one.  Each of its wavefronts
+// owns a slice of K (at most GW groups) and loads that slice of every activation row into
+// registers once, already in the A-operand layout of v_mfma_f32_16x16x32_bf16: lane
+// (i = lane % 16, kb = lane / 16) of m-block mb holds x[16 mb + i][64 g + 16 kb ..+16] in
+// pair order, k-step j using the 8 values of word 2 kb + j of the group.  Tile after tile
+// only weights stream: lane (j = lane % 16, kb) reads the 8 bytes of row 16 nb + j at words
+// 2kb, 2kb+1 of each group (16 rows x 32 bytes per load instruction), so the activations
+// are read from L2 once per workgroup rather than once per tile.  MB = 1 m-block serves
+// M <= 16 with 16 wavefronts of at most 4 groups, MB = 2 serves M <= 32 with 8 wavefronts of
+// at most 8 groups (the register file holds the x slices of all of them).
+//
+// Nibbles become bf16 in the form 1 + q/16 (q in mantissa bits 3..6 of bf16 1.0, exact),
+// so with v = 1 + q/16 the group's contribution is
+//     sum (s q + b) x  =  16 s * sum v x  +  (b - 16 s) * sum x,
+// the first term from two bf16 MFMAs per (m-block, n-block) and one fp32 multiply-add
+// per output, the second from one v_mfma_f32_16x16x4_f32 per block of four groups (A =
+// the rows' sums of x over the four groups, B = b - 16 s per weight row).  Against the
+// 128 + q form the offset term is 8x smaller next to the signal, and so is the fp32
+// rounding it brings.
+//
+// Per tile every wavefront parks its partial in LDS and the workgroup adds them in
+// wavefront order (the same bits on every run).  Each tile's scales and biases are staged
+// in LDS by the whole workgroup (8-byte pieces).  The next tile's weights are loaded group
+// by group right after the current tile's group is multiplied (into the registers just
+// freed), its scales and biases at the start of the tile; every load is unconditional (past
+// the weight or the range: an offset past the buffer, zero, no traffic), so the number of
+// loads between any load and its use is the same on every path and every wait is exact;
+// MB = 1 keeps two tiles of weights in flight (two register sets, the tile loop unrolled by
+// two), MB = 2 one.  Groups past a wavefront's share contribute nothing (x, its sums and the
+// scales read as zero).  Requires K % 256 == 0 and K <= 4096.
+namespace xs {
+constexpr int kRows = 32;                 // weight rows per tile (two 16-row n-blocks)
+constexpr uint32_t kOne = 0x3f803f80u;    // bf16 pair (1.0, 1.0)
+constexpr uint32_t kQMask = 0x00780078u;  // mantissa bits 3..6 of each half
+template <int MB>
+struct Shape {
+  static constexpr int kWaves = MB == 1 ? 16 : 8;   // wavefronts per workgroup
+  static constexpr int kAcc = 8 * MB;               // accumulator floats per lane
+  static constexpr int kRange = 64;                 // most groups per K-range
+  static constexpr int kDepth = MB == 1 ? 2 : 1;    // tiles of weights in flight
+};
+template <int MB>
+constexpr size_t red_bytes() {
+  return (size_t)Shape<MB>::kWaves * 64 * (Shape<MB>::kAcc + 1) * sizeof(float);
+}
+}  // namespace xs
+
+struct XsProblem {
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  const uint16_t* x;  // row m at x + m * ldx
+  void* y;            // row m at y + m * ldy elements
+  int64_t ldx;
+  int64_t ldy;
+  int32_t N;
+  int32_t K;
+  int32_t wgs;        // workgroups
+  int32_t wg0;        // this problem's first workgroup
+  int32_t tiles;      // 32-row tiles
+  int32_t pad;
+};
+
+struct XsArgs {
+  XsProblem p[kMaxProblems];
+  int32_t count;
+  int32_t M;
+  int32_t y_f32;
+  int32_t scs;        // LDS row stride of the staged scales/biases (odd, >= every Gs)
+};
+
+// Word u's nibble pair (p, p + 4) as the bf16 pair (1 + q_p/16, 1 + q_{p+4}/16).
+// `one` must be in_vgpr(xs::kOne).
+template <int P>
+__device__ __forceinline__ uint32_t nib16(uint32_t u, uint32_t one) {
+  const uint32_t t = P == 0 ? (u << 3) : (u >> (4 * P - 3));
+  return (t & xs::kQMask) | one;
+}
+
+__device__ __forceinline__ bf16x8_t unpack16(uint32_t u, uint32_t one) {
+  u32x4_t t = {nib16<0>(u, one), nib16<1>(u, one), nib16<2>(u, one), nib16<3>(u, one)};
+  return __builtin_bit_cast(bf16x8_t, t);
+}
+
+// Stores issued from inline assembly, so the compiler's wait-count model does not see
+// them.  Inside a loop that keeps loads in flight from one iteration to the next, a store
+// the compiler knows of sits between those loads and their uses and makes it wait for every
+// older load; hidden stores only make each of its waits count more operations than it
+// assumed, so every wait is at least as strict as it computed (loads complete in issue
+// order).  Everything that must see a hidden store waits for it with wait_vmem().
+__device__ __forceinline__ u32x4_t rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t u = reinterpret_cast<uint64_t>(base);
+  u32x4_t w;
+  w.x = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  w.y = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32)) & 0xffffu;  // stride 0
+  w.z = __builtin_amdgcn_readfirstlane(bytes);
+  w.w = 0x00020000u;
+  return w;
+}
+__device__ __forceinline__ void hidden_store_b16(u32x4_t rs, uint32_t off, uint32_t v) {
+  asm volatile("buffer_store_short %0, %1, %2, 0 offen" ::"v"(v), "v"(off), "s"(rs) : "memory");
+}
+__device__ __forceinline__ void hidden_store_b32(u32x4_t rs, uint32_t off, uint32_t v) {
+  asm volatile("buffer_store_dword %0, %1, %2, 0 offen" ::"v"(v), "v"(off), "s"(rs) : "memory");
+}
+
+template <int MB, int GW, int D, bool Y32>
+__global__ __launch_bounds__(64 * xs::Shape<MB>::kWaves) void qmv_xs_kernel(XsArgs a) {
+  using namespace xs;
+  constexpr int NW = Shape<MB>::kWaves, NT = 64 * NW, RS = Shape<MB>::kAcc + 1;
+  constexpr int NBLK = (GW + 3) / 4;  // blocks of four groups (bias MFMAs)
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  float* red = reinterpret_cast<float*>(lds);  // [NW][64][RS] parked partials
+  const int scs = a.scs;
+  // [32][scs] 16 * scale, then [32][scs] bias, then spare slots for idle threads
+  float* s16l = red + NW * 64 * RS;
+  float* bl = s16l + kRows * scs;
+
+  // this workgroup's problem, K-range and tiles
+  const int bid = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProblems; ++i)
+    if (i < a.count && bid >= a.p[i].wg0) pi = i;
+  const XsProblem& P = a.p[pi];
+  const int c = bid - P.wg0;
+  const int T = P.tiles, C = P.wgs;
+  if (c >= T) return;
+  const int ntiles = (T - c + C - 1) / C;
+  const int N = P.N, K = P.K, M = a.M;
+  const int G = K >> 6, W = K >> 3;
+  const int gs0 = 0, Gs = G;  // the whole K is this workgroup's range
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int j16 = lane & 15, kb = lane >> 4;
+  const int wl0 = (Gs * wave) / NW;              // first group of this wavefront (in the range)
+  const int gc = (Gs * (wave + 1)) / NW - wl0;   // its groups (<= GW)
+  const int wg0 = gs0 + wl0;
+  const uint32_t one = in_vgpr(kOne);
+
+  const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(P.w, (uint32_t)N * (uint32_t)W * 4u);
+  const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
+  const __amdgpu_buffer_rsrc_t srsrc = buffer_rsrc(P.s, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc = buffer_rsrc(P.b, sb_bytes);
+  const __amdgpu_buffer_rsrc_t xrsrc = buffer_rsrc(P.x, (uint32_t)((M - 1) * P.ldx * 2 + K * 2));
+  const int ysz = Y32 ? 4 : 2;
+  const u32x4_t yrs = rsrc_words(P.y, (uint32_t)(((int64_t)(M - 1) * P.ldy + N) * ysz));
+
+  // Scale and bias pieces of a tile: piece q < 8 Gs of each is the quad of row q / (Gs/4)
+  // at groups gs0 + 4 (q % (Gs/4)) .. +3 (8 bytes); thread tid takes piece tid of the
+  // scales and of the biases.  Rows past N lie past the buffer and read zero; threads
+  // without a piece load nothing and park their (zero) values in a spare LDS slot.
+  // (An offset with bit 31 set lies past every buffer here: the load reads zero and moves
+  // nothing, the store is dropped.  Adding a row offset to it cannot carry out of bit 31
+  // because every buffer is below 2 GiB.)
+  uint32_t sbrel, sbdst;
+  {
+    const int quarter = Gs >> 2;
+    const int row = tid / quarter, pr = tid - row * quarter;
+    const bool in = tid < 8 * Gs;
+    sbrel = (uint32_t)(row * G + gs0 + 4 * pr) * 2u | ((uint32_t)!in << 31);
+    sbdst = in ? (uint32_t)(row * scs + 4 * pr) : (uint32_t)(2 * kRows * scs);
+  }
+  u32x2_t sv[D], bv[D];
+  auto load_sb = [&](int d, int row0, bool valid) {
+    const uint32_t off = sbrel + ((uint32_t)row0 * (uint32_t)G * 2u | ((uint32_t)!valid << 31));
+    sv[d] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(srsrc, off, 0, 0));
+    bv[d] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(brsrc, off, 0, 0));
+  };
+  auto store_sb = [&](int d) {
+    float* ds = s16l + sbdst;
+    float* db = bl + sbdst;
+    ds[0] = 16.0f * bf16_bits_to_f32(sv[d].x & 0xffffu);
+    ds[1] = 16.0f * bf16_bits_to_f32(sv[d].x >> 16);
+    ds[2] = 16.0f * bf16_bits_to_f32(sv[d].y & 0xffffu);
+    ds[3] = 16.0f * bf16_bits_to_f32(sv[d].y >> 16);
+    db[0] = bf16_bits_to_f32(bv[d].x & 0xffffu);
+    db[1] = bf16_bits_to_f32(bv[d].x >> 16);
+    db[2] = bf16_bits_to_f32(bv[d].y & 0xffffu);
+    db[3] = bf16_bits_to_f32(bv[d].y >> 16);
+  };
+
+  // Weight loads: lane (j16, kb) reads, for n-block nb, row row0 + 16 nb + j16 (rows past N
+  // read zero) at words 2 kb, 2 kb + 1 of each of its groups.
+  // D register sets: tile i of this workgroup's list lives in set i % D, and its loads are
+  // issued while tile i - D is computed (the first D tiles' at the start).
+  u32x2_t wv[D][GW][2];
+  const uint32_t wlane = (uint32_t)j16 * (uint32_t)W * 4u + 32u * (uint32_t)wg0 + 8u * kb;
+  auto load_w = [&](int d, int g, int row0, bool valid) {
+    const uint32_t dead = (uint32_t)!(valid && g < gc) << 31;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const uint32_t off = (wlane + (uint32_t)(row0 + 16 * nb) * (uint32_t)W * 4u + 32u * g) | dead;
+      wv[d][g][nb] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wrsrc, off, 0, 0));
+    }
+  };
+
+  // The first D tiles' scale/bias and weight loads, in the order the loop issues them (so
+  // that every path into the loop has the same loads in flight in the same order), then
+  // x of this wavefront's groups into registers and the groups' row sums.
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load_sb(d, (c + d * C) * kRows, d < ntiles);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      load_w(d, g, (c + d * C) * kRows, d < ntiles);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  bf16x8_t xa[MB][GW][2];
+  float sxa[MB][NBLK];
+  {
+    uint4 xv[MB][GW][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = 16 * mb + j16;
+      const uint32_t xl = (uint32_t)m * (uint32_t)P.ldx * 2u + (uint32_t)(64 * wg0 + 16 * kb) * 2u;
+#pragma unroll
+      for (int g = 0; g < GW; ++g)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          xv[mb][g][p] = load_b128(xrsrc, (xl + 128u * g + 16u * p) | ((uint32_t)!(m < M && g < gc) << 31));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t ones = in_vgpr(kOnes);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b) sxa[mb][b] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        float part = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint4 v = xv[mb][g][p];
+          part = dot2(v.x, ones, part);
+          part = dot2(v.y, ones, part);
+          part = dot2(v.z, ones, part);
+          part = dot2(v.w, ones, part);
+          xa[mb][g][p] = as_bf16x8(pair_order(v));
+        }
+        part += __shfl_xor(part, 16);
+        part += __shfl_xor(part, 32);  // the row's sum over the group, in every kb lane
+        if (kb == (g & 3)) sxa[mb][g >> 2] = part;
+      }
+      __builtin_amdgcn_sched_barrier(0);  // group by group: the raw x dies as it is converted
+    }
+  }
+
+  const f32x4_t zero = {};
+  for (int it = 0; it < ntiles; it += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+    // tile it + d of the list (past the list's end when ntiles is not a multiple of D:
+    // its loads read zero and its stores are dropped)
+    const int ti = it + d;
+    const bool live = ti < ntiles;
+    const int row0 = (c + ti * C) * kRows;
+    const int nrow0 = (c + (ti + D) * C) * kRows;
+    const bool has_next = ti + D < ntiles;
+    __builtin_amdgcn_sched_barrier(0);
+    store_sb(d);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    load_sb(d, nrow0, has_next);
+    f32x4_t acc[MB][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb][0] = acc[mb][1] = zero;
+    float cbv[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      // (LDS reads past a wavefront's groups stay inside the staged area; their values are
+      // replaced by zero)
+      float s16v[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int base = (16 * nb + j16) * scs + wl0;
+        s16v[nb] = s16l[base + g];
+        if ((g & 3) == 0) cbv[nb] = bl[base + g + kb] - s16l[base + g + kb];
+      }
+      f32x4_t pp[MB][2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const bf16x8_t w0 = unpack16(wv[d][g][nb].x, one), w1 = unpack16(wv[d][g][nb].y, one);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          pp[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mb][g][0], w0, zero, 0, 0, 0);
+          pp[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mb][g][1], w1, pp[mb][nb], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one n-block's unpacked weights at a time
+      }
+      load_w(d, g, nrow0, has_next);  // tile ti + D's group g, into the registers just freed
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const float s16 = g < gc ? s16v[nb] : 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[mb][nb][e] = fmaf(s16, pp[mb][nb][e], acc[mb][nb][e]);
+      }
+      if ((g & 3) == 3 || g == GW - 1) {  // the block of four groups g & ~3 ..: lane kb its group
+        const int gg = (g & ~3) + kb;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const float cb = gg < gc && gg <= g ? cbv[nb] : 0.0f;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(sxa[mb][g >> 2], cb, acc[mb][nb], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one group at a time: bounds the live registers
+    }
+    // park this wavefront's partial; the workgroup adds them in order
+    {
+      float* dst = red + (wave * 64 + lane) * RS;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[(mb * 2 + nb) * 4 + e] = acc[mb][nb][e];
+    }
+    lds_barrier();
+    // element e of the tile: row n = e % 32 of the tile, activation row m = e / 32; its
+    // holder lane is 16 (m % 16 / 4) + n % 16, register (m / 16, n / 16, m % 4)
+    constexpr int kPer = (kRows * 16 * MB + NT - 1) / NT;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int e0 = tid + NT * q;
+      const bool ein = e0 < kRows * 16 * MB;
+      const int e = ein ? e0 : 0;
+      const int m = e >> 5, n = e & 31;
+      const int hl = 16 * ((m & 15) >> 2) + (n & 15);
+      const int reg = ((m >> 4) * 2 + (n >> 4)) * 4 + (m & 3);
+      const float* src = red + hl * RS + reg;
+      float sum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sum += src[w * 64 * RS];
+      const uint32_t dead = (uint32_t)!(live && ein && m < M && row0 + n < N) << 31;
+      if (Y32)
+        hidden_store_b32(yrs, (uint32_t)((m * P.ldy + row0 + n) * 4) | dead, __float_as_uint(sum));
+      else
+        hidden_store_b16(yrs, (uint32_t)((m * P.ldy + row0 + n) * 2) | dead, f32_to_bf16_bits(sum));
+    }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ dequantise
 //
 // One thread per packed word: eight outputs.  fp32 output is fl32(s*q + b), which is
@@ -1407,6 +1761,120 @@ hipError_t launch_mma(const LaunchArgs& a, const MmaPlan& pl, void* ws, hipStrea
   return hipGetLastError();
 }
 
+// The x-stationary kernel's plan: per problem 32-row tiles and the whole K in one range
+// (at most Shape<MB>::kRange groups: K <= 4096), MB = 1 m-block for M <= 16, else 2.  Each
+// workgroup takes every r-th tile of its problem, r = ceil(tiles / CUs), so that its x is
+// loaded once for r tiles.  The kernel carries a fixed cost per workgroup (x into
+// registers) and per tile (the cross-wavefront reduction and the staged scales) that only
+// many tiles per workgroup amortise: measured on MI355X it beats the staged MFMA kernel on
+// the LM head (151936 x 2560: 72 against 84-95 us at M = 32) and loses on launches of 1-3
+// tiles per CU (C3 15360 x 3840, the decoder layer's projections), so it takes launches with
+// at least kXsMinTilesPerCu tiles per CU.  Not applicable: K % 256 != 0, K > 4096, or a
+// pointer table.
+#ifndef IMQ_XS_MIN_TILES_PER_CU
+#define IMQ_XS_MIN_TILES_PER_CU 8
+#endif
+
+struct XsPlan {
+  int mb = 1;           // m-blocks of 16 activation rows
+  int gw = 0;           // groups per wavefront of the instantiation
+  int grid = 0;
+  size_t lds = 0;
+};
+
+bool plan_xs(const LaunchArgs& a, int cu_count, XsArgs* xa, XsPlan* pl) {
+  if (a.count > kMaxProblems || a.table) return false;
+  const int mb = a.M <= 16 ? 1 : 2;
+  const int waves = mb == 1 ? xs::Shape<1>::kWaves : xs::Shape<2>::kWaves;
+  int ttot = 0, gmax = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const Problem& P = a.p[i];
+    if (P.K % 256 != 0 || P.K / 64 > xs::Shape<1>::kRange) return false;
+    if ((int64_t)(a.M - 1) * P.ldx * 2 + (int64_t)P.K * 2 >= ((int64_t)1 << 31)) return false;
+    if (((int64_t)(a.M - 1) * P.ldy + P.N) * 4 >= ((int64_t)1 << 31)) return false;
+    ttot += (P.N + xs::kRows - 1) / xs::kRows;
+    gmax = P.K / 64 > gmax ? P.K / 64 : gmax;
+  }
+  if (ttot < IMQ_XS_MIN_TILES_PER_CU * cu_count) return false;
+  const int per_wave = (gmax + waves - 1) / waves;
+  if (per_wave > (mb == 1 ? 4 : 8)) return false;
+  pl->mb = mb;
+  pl->gw = per_wave <= 2 ? 2 : per_wave == 7 ? 8 : per_wave;
+  const int r = (ttot + cu_count - 1) / cu_count;
+  memset(xa, 0, sizeof(*xa));
+  int wg = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const Problem& P = a.p[i];
+    XsProblem& X = xa->p[i];
+    X.w = P.w;
+    X.s = P.s;
+    X.b = P.b;
+    X.x = P.x;
+    X.y = P.y;
+    X.ldx = P.ldx;
+    X.ldy = P.ldy;
+    X.N = P.N;
+    X.K = P.K;
+    X.tiles = (P.N + xs::kRows - 1) / xs::kRows;
+    X.wgs = (X.tiles + r - 1) / r;
+    X.wg0 = wg;
+    wg += X.wgs;
+  }
+  xa->count = a.count;
+  xa->M = a.M;
+  xa->y_f32 = a.y_f32;
+  xa->scs = gmax | 1;
+  pl->grid = wg;
+  // the parked partials, then the staged scales and biases and the spare slots (bl's
+  // spare at 2 * 32 * scs from bl: 3 * 32 * scs + 4 floats from the start of the staging)
+  pl->lds = (mb == 1 ? xs::red_bytes<1>() : xs::red_bytes<2>()) +
+            ((size_t)3 * xs::kRows * xa->scs + 4) * sizeof(float);
+  return true;
+}
+
+template <int MB, int GW, bool Y32>
+hipError_t launch_xs_one(const XsArgs& x, const XsPlan& pl, hipStream_t stream) {
+  auto kern = qmv_xs_kernel<MB, GW, xs::Shape<MB>::kDepth, Y32>;
+  hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(64 * xs::Shape<MB>::kWaves), pl.lds, stream, x);
+  return hipGetLastError();
+}
+
+template <int MB, int GW>
+hipError_t launch_xs_gw(const XsArgs& x, const XsPlan& pl, hipStream_t stream) {
+  return x.y_f32 ? launch_xs_one<MB, GW, true>(x, pl, stream) : launch_xs_one<MB, GW, false>(x, pl, stream);
+}
+
+hipError_t launch_xs(const XsArgs& x, const XsPlan& pl, hipStream_t stream) {
+  if (pl.mb == 1) {
+    switch (pl.gw) {
+      case 2: return launch_xs_gw<1, 2>(x, pl, stream);
+      case 3: return launch_xs_gw<1, 3>(x, pl, stream);
+      default: return launch_xs_gw<1, 4>(x, pl, stream);
+    }
+  }
+  switch (pl.gw) {
+    case 2: return launch_xs_gw<2, 2>(x, pl, stream);
+    case 3: return launch_xs_gw<2, 3>(x, pl, stream);
+    case 4: return launch_xs_gw<2, 4>(x, pl, stream);
+    case 5: return launch_xs_gw<2, 5>(x, pl, stream);
+    case 6: return launch_xs_gw<2, 6>(x, pl, stream);
+    default: return launch_xs_gw<2, 8>(x, pl, stream);
+  }
+}
+
+#ifndef IMQ_XS_MIN_ROWS
+#define IMQ_XS_MIN_ROWS 3
+#endif
+
+// Workspace bytes the launch would use given as much as it wants (0: no split).
+size_t wanted_workspace(const LaunchArgs& a, int cu_count) {
+  if (a.M < 3) return 0;
+  XsArgs x;
+  XsPlan xp;
+  if (a.M >= IMQ_XS_MIN_ROWS && plan_xs(a, cu_count, &x, &xp)) return 0;
+  return plan_mma(a, (size_t)1 << 40, cu_count).bytes;
+}
+
 template <int NCH, int XR>
 hipError_t launch_gather_nx(const GatherArgs& a, int P, hipStream_t stream) {
   const int rows = kThreads >> a.sh;
@@ -1436,7 +1904,14 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* w
   M1Plan m1;
   int grid_x = 0;
   size_t lds = 0;
-  if (M == 1 && plan_m1(a, &m1)) {
+  XsArgs xa;
+  XsPlan xp;
+  bool big = false;
+  for (int i = 0; i < a.count; ++i)
+    big = big || (int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31);
+  if (M >= IMQ_XS_MIN_ROWS && !big && plan_xs(a, dev->cu_count, &xa, &xp)) {
+    e = launch_xs(xa, xp, stream);
+  } else if (M == 1 && plan_m1(a, &m1)) {
     e = launch_m1_for(a, m1, stream);
   } else if (M == 2 && plan_m1(a, &m1) && launch_mr_for<2>(a, m1, stream, &e)) {
     // launched
@@ -1592,10 +2067,11 @@ size_t imq_qmv_grouped_workspace(const imq_problem* problems, int32_t count, int
     if (problems[i].N < 1 || problems[i].K < 64 || problems[i].K % 64) return 0;
     a.p[i].N = problems[i].N;
     a.p[i].K = problems[i].K;
+    a.p[i].ldx = problems[i].ldx > problems[i].K ? problems[i].ldx : problems[i].K;
   }
   a.count = count;
   a.M = M;
-  return plan_mma(a, (size_t)1 << 40, dev->cu_count).bytes;
+  return wanted_workspace(a, dev->cu_count);
 }
 
 int32_t imq_qmv_grouped_ws(const imq_problem* problems, int32_t count, int32_t M,
@@ -1620,7 +2096,7 @@ int32_t imq_qmv_grouped_noalloc(const imq_problem* problems, int32_t count, int3
   if (!dev) return code;
   // the plan imq_qmv_grouped_ws makes with a workspace of imq_qmv_grouped_workspace bytes,
   // so both entry points split the same way and give the same bits
-  const size_t need = M >= 3 ? plan_mma(a, (size_t)1 << 40, dev->cu_count).bytes : 0;
+  const size_t need = wanted_workspace(a, dev->cu_count);
   if (need > IMQ_NOALLOC_SCRATCH_BYTES)
     return fail(IMQ_EUNSUPPORTED,
                 "this call's split workspace (" + std::to_string(need) +
