@@ -200,6 +200,19 @@ def gather_qmv_f64(w, s, b, x, idx, rows_per_x: int = 1, gs: int = GROUP_SIZE):
     return ref, mag
 
 
+def gather_qmv_dequant_f32(w, s, b, x, idx, rows_per_x: int = 1, gs: int = GROUP_SIZE):
+    """The gather's fp32 dequantise-then-matmul reference (P, N): pair p is
+    qmv_dequant_f32 of expert idx[p] on row p // rows_per_x; zeros for an index outside
+    [0, E) (as gather_qmv_f64)."""
+    e = w.shape[0]
+    out = np.zeros((len(idx), w.shape[1]), dtype=np.float32)
+    for p in range(len(idx)):
+        ex = int(idx[p])
+        if 0 <= ex < e:
+            out[p] = qmv_dequant_f32(w[ex], s[ex], b[ex], x[p // rows_per_x].reshape(1, -1), gs)[0]
+    return out
+
+
 def _prep(w, s, b, x):
     w = np.ascontiguousarray(w, dtype=np.uint32)
     s = np.ascontiguousarray(s, dtype=np.uint16)
@@ -278,6 +291,61 @@ def check_bf16(y_bits: np.ndarray, ref64: np.ndarray, abssum: np.ndarray) -> Ver
     ok = not bad.any()
     detail = "" if ok else f"{int(bad.sum())} outputs outside 1 ulp+allowance; max_rel={max_rel:.3g}"
     return Verdict(ok, max_rel, worst, int(bad.sum()), detail)
+
+
+#: Where the literal bf16 bar may be missed: outputs whose exact value is below this
+#: fraction of sum_k |w_k x_k|.  There the fp32 summation noise of any order (the
+#: reference's own included) exceeds a bf16 ulp of the result, so bf16(fp32 reference)
+#: is not determined to one ulp: the exactly rounded product itself misses the literal bar
+#: there (17 of 491,520 outputs at K = 3840, N = 15360, M = 32, all below 2^-17.5).
+LITERAL_CANCELLATION = 2.0 ** -16
+
+
+@dataclass
+class LiteralVerdict:
+    ok: bool
+    violations: int        # outputs with |y - bf16(ref32)| > 1 bf16 ulp
+    exact_violations: int  # the same count for bf16(fl32(exact product)): the floor
+    outside: int           # violations at outputs that are not deep cancellations
+    outputs: int
+    detail: str
+
+
+def check_bf16_literal(y_bits: np.ndarray, ref32: np.ndarray, ref64: np.ndarray,
+                       abssum: np.ndarray) -> LiteralVerdict:
+    """The north star's literal bar for bf16 outputs: |y - bf16(ref32)| <= 1 bf16 ulp per
+    output, ref32 being the reference's fp32 dequantise-then-matmul (qmv_dequant_f32,
+    ironmule/cuda_native.py:265-268).  Counts the violations, and the violations of the
+    exactly rounded product bf16(fl32(ref64)) against the same ref32 (what no fp32
+    implementation can get under).  Passes when every violation lies at a deep
+    cancellation, |ref64| < LITERAL_CANCELLATION * sum|w x|."""
+    r = f32_to_bf16(ref32)
+    rf = bf16_to_f32(r).astype(np.float64)
+    ulp = bf16_ulp(rf)
+    y = bf16_to_f32(y_bits).astype(np.float64)
+    bad = np.abs(y - rf) > ulp
+    e32 = bf16_to_f32(f32_to_bf16(np.asarray(ref64, dtype=np.float64).astype(np.float32)))
+    exact_bad = np.abs(e32.astype(np.float64) - rf) > ulp
+    deep = np.abs(ref64) < LITERAL_CANCELLATION * abssum
+    outside = int((bad & ~deep).sum())
+    ok = outside == 0
+    detail = (f"literal bar: {int(bad.sum())} of {bad.size} outputs beyond 1 ulp of "
+              f"bf16(fp32 reference) (exact product: {int(exact_bad.sum())}); "
+              f"{outside} outside deep cancellation")
+    return LiteralVerdict(ok, int(bad.sum()), int(exact_bad.sum()), outside, int(bad.size), detail)
+
+
+def check_bf16_both(y_bits, w, s, b, x, gs: int = GROUP_SIZE):
+    """check_bf16 (against the exact product) and check_bf16_literal (against the fp32
+    reference) on the same inputs; returns (Verdict, LiteralVerdict) and prints the
+    literal counts."""
+    ref64, mag = qmv_f64(w, s, b, x, gs)
+    ref32 = qmv_dequant_f32(w, s, b, x, gs)
+    y_bits = np.asarray(y_bits).reshape(ref64.shape)
+    v = check_bf16(y_bits, ref64, mag)
+    lit = check_bf16_literal(y_bits, ref32, ref64, mag)
+    print(lit.detail, flush=True)
+    return v, lit
 
 
 def check_f32(y: np.ndarray, ref64: np.ndarray, abssum: np.ndarray) -> Verdict:

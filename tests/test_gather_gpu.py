@@ -65,6 +65,10 @@ def test_gather_matches_per_expert_calls_and_the_oracle(env, e, n, k, pairs, xs)
     ref, mag = orc.gather_qmv_f64(host[0], host[1], host[2], bf16_bits(x), idx.cpu().numpy(), xs)
     verdict = orc.check_bf16(bf16_bits(y), ref, mag)
     assert verdict.ok, verdict.detail
+    ref32 = orc.gather_qmv_dequant_f32(host[0], host[1], host[2], bf16_bits(x), idx.cpu().numpy(), xs)
+    lit = orc.check_bf16_literal(bf16_bits(y), ref32, ref, mag)
+    print(lit.detail)
+    assert lit.ok, lit.detail
 
 
 def test_gather_fp32_output_and_invalid_experts(env):

@@ -29,11 +29,12 @@ def native():
 
 
 def _check(oracle, pr, y, rows, out_f32=False):
-    ref, mag = oracle.qmv_f64(pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
     if out_f32:
+        ref, mag = oracle.qmv_f64(pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
         v = oracle.check_f32(y.float().cpu().numpy()[:, rows], ref, mag)
     else:
-        v = oracle.check_bf16(bf16_bits(y)[:, rows], ref, mag)
+        v, lit = oracle.check_bf16_both(bf16_bits(y)[:, rows], pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
+        assert lit.ok, lit.detail
     assert v.ok, v.detail
 
 

@@ -251,6 +251,50 @@ def test_check_bf16_rejects_a_two_ulp_error(oracle):
     assert not oracle.check_bf16(bad, ref, mag).ok
 
 
+def test_check_f32_rejects_a_planted_error(oracle):
+    """check_f32 passes the fp32 dequantise-then-matmul reference and rejects it with one
+    output moved by 1e-4 of max|ref| (far inside the 1e-3 max-relative bound, so the
+    per-output summation allowance is what catches it) and with one output scaled by 1.01."""
+    pr = oracle.synthetic(64, 2560, 2, seed=oracle.SEED_BASE + 42)
+    ref, mag = oracle.qmv_f64(pr.w, pr.s, pr.b, pr.x)
+    y = oracle.qmv_dequant_f32(pr.w, pr.s, pr.b, pr.x)
+    assert oracle.check_f32(y, ref, mag).ok
+    i = int(np.argmax(np.abs(ref[0])))
+    nudged = y.copy()
+    nudged[0, i] += np.float32(1e-4 * np.max(np.abs(ref)))
+    v = oracle.check_f32(nudged, ref, mag)
+    assert not v.ok and v.violations == 1, v.detail
+    scaled = y.copy()
+    scaled[1, 7] *= np.float32(1.01)
+    assert not oracle.check_f32(scaled, ref, mag).ok
+
+
+def test_literal_bar_counts_and_the_cancellation_exemption(oracle):
+    """check_bf16_literal: the fp32 reference rounded to bf16 has no violations; the exactly
+    rounded product misses the literal bar only at deep cancellations (the floor reported
+    beside every GPU count); a planted two-ulp error at an ordinary output fails; the same
+    error at an output below the cancellation threshold is counted but exempt."""
+    pr = oracle.synthetic(3072, 3840, 4, seed=oracle.SEED_BASE + 43)
+    ref, mag = oracle.qmv_f64(pr.w, pr.s, pr.b, pr.x)
+    ref32 = oracle.qmv_dequant_f32(pr.w, pr.s, pr.b, pr.x)
+    own = oracle.check_bf16_literal(oracle.f32_to_bf16(ref32), ref32, ref, mag)
+    assert own.ok and own.violations == 0
+    exact = oracle.f32_to_bf16(ref.astype(np.float32))
+    v = oracle.check_bf16_literal(exact, ref32, ref, mag)
+    assert v.ok and v.violations == v.exact_violations, v.detail
+    big = np.unravel_index(int(np.argmax(np.abs(ref))), ref.shape)
+    bad = oracle.f32_to_bf16(ref32).copy()
+    bad[big] += 2
+    v = oracle.check_bf16_literal(bad, ref32, ref, mag)
+    assert not v.ok and v.outside == 1, v.detail
+    tiny = np.unravel_index(int(np.argmin(np.abs(ref) / mag)), ref.shape)
+    assert abs(ref[tiny]) < oracle.LITERAL_CANCELLATION * mag[tiny]
+    bad = oracle.f32_to_bf16(ref32).copy()
+    bad[tiny] += 2
+    v = oracle.check_bf16_literal(bad, ref32, ref, mag)
+    assert v.ok and v.violations == 1, v.detail
+
+
 def test_synthetic_distribution(oracle):
     pr = oracle.synthetic(256, 2560, 2, seed=oracle.SEED_BASE + 1)
     q = oracle.unpack(pr.w)

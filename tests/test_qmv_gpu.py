@@ -46,7 +46,8 @@ def _check(oracle, pr, y, out_f32=False, rows=None):
         got = bf16_bits(y)
         if rows is not None:
             got = got[:, rows]
-        v = oracle.check_bf16(got, ref, mag)
+        v, lit = oracle.check_bf16_both(got, w, s, b, x)
+        assert lit.ok, lit.detail
     assert v.ok, v.detail
     return v
 
@@ -153,6 +154,10 @@ def test_golden_fixtures(native, oracle):
         _, mag = oracle.qmv_f64(pr.w, pr.s, pr.b, pr.x)
         v = oracle.check_bf16(bf16_bits(y), exact, mag)
         assert v.ok, (p["name"], v.detail)
+        lit = oracle.check_bf16_literal(bf16_bits(y), oracle.qmv_dequant_f32(pr.w, pr.s, pr.b, pr.x),
+                                        exact, mag)
+        print(p["name"], lit.detail)
+        assert lit.ok, (p["name"], lit.detail)
 
 
 def test_shared_weight_config_full_size(native, oracle):

@@ -100,9 +100,9 @@ def test_independent_ragged_shapes_and_the_oracle(env):
         _check_stages(torch, n, stages, run)
     pr = orc.synthetic(130, 192, 1, seed=310)
     x = bf16_bits(xs[192]).reshape(1, -1)
-    ref, mag = orc.qmv_f64(pr.w, pr.s, pr.b, x)
-    verdict = orc.check_bf16(bf16_bits(stages[1][2][0]).reshape(1, -1), ref, mag)
+    verdict, lit = orc.check_bf16_both(bf16_bits(stages[1][2][0]), pr.w, pr.s, pr.b, x)
     assert verdict.ok, verdict.detail
+    assert lit.ok, lit.detail
     prog.close()
 
 

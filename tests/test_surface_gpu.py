@@ -28,9 +28,9 @@ def _module(oracle, n, k, seed):
 
 def _bound(oracle, pr, y, x_bits=None):
     x = pr.x if x_bits is None else x_bits
-    ref, mag = oracle.qmv_f64(pr.w, pr.s, pr.b, x)
-    v = oracle.check_bf16(bf16_bits(y).reshape(ref.shape), ref, mag)
+    v, lit = oracle.check_bf16_both(bf16_bits(y), pr.w, pr.s, pr.b, x)
     assert v.ok, v.detail
+    assert lit.ok, lit.detail
 
 
 def test_k3840_run_and_module(oracle):

@@ -41,11 +41,12 @@ def test_lm_head_shape_matches_oracle(native, oracle, m, out_f32):
     y = native.qmv(w, s, b, x, out_dtype=torch.float32 if out_f32 else torch.bfloat16)
     torch.cuda.synchronize()
     rows = _rows(n, 997)
-    ref, mag = oracle.qmv_f64(pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
     if out_f32:
+        ref, mag = oracle.qmv_f64(pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
         v = oracle.check_f32(y.cpu().numpy()[:, rows], ref, mag)
     else:
-        v = oracle.check_bf16(bf16_bits(y)[:, rows], ref, mag)
+        v, lit = oracle.check_bf16_both(bf16_bits(y)[:, rows], pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
+        assert lit.ok, lit.detail
     assert v.ok, v.detail
 
 
@@ -63,7 +64,7 @@ def test_grouped_many_tiles_repeat_bits(native, oracle):
     torch.cuda.synchronize()
     for pr, y, y2 in zip(prs, outs, again):
         rows = _rows(pr.n, 331)
-        ref, mag = oracle.qmv_f64(pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
-        v = oracle.check_bf16(bf16_bits(y)[:, rows], ref, mag)
+        v, lit = oracle.check_bf16_both(bf16_bits(y)[:, rows], pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
         assert v.ok, v.detail
+        assert lit.ok, lit.detail
         assert np.array_equal(bf16_bits(y), bf16_bits(y2))

@@ -63,9 +63,9 @@ def _case(native, oracle, shapes, m, seed):
     for i, (pr, a, b) in enumerate(zip(prs, y_ref, y_new)):
         assert np.array_equal(bf16_bits(a), bf16_bits(b)), f"problem {i} differs"
         rows = np.unique(np.concatenate([np.arange(0, pr.n, 7), np.arange(max(0, pr.n - 40), pr.n)]))
-        ref, mag = oracle.qmv_f64(pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
-        v = oracle.check_bf16(bf16_bits(b)[:, rows], ref, mag)
+        v, lit = oracle.check_bf16_both(bf16_bits(b)[:, rows], pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
         assert v.ok, v.detail
+        assert lit.ok, lit.detail
     return nbytes
 
 
