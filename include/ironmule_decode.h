@@ -91,7 +91,11 @@ IMQ_API int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool,
  * rows 0 .. positions[b] of the slot (clamped to max_len and capacity), split over 64-key
  * chunks with the split plan of imq_attention_decode and merged in split order by the
  * last split of each (request, KV head).  The same bits as imq_qk_norm_rope followed by
- * imq_attention_decode with lengths = positions + 1.  `workspace`: at least
+ * imq_attention_decode with lengths = positions + 1 for every valid request; a request with
+ * its slot outside [0, num_slots) or its position outside [0, capacity) is invalid: its
+ * output is zeros and it writes nothing (as imq_attention_decode with length 0; given the
+ * length positions + 1 past the capacity that entry would attend over the stored rows of a
+ * valid slot).  `workspace`: at least
  * imq_attention_workspace(B, Hq, max_len) bytes; `counters`: B * Hkv uint32, zero before
  * the first call and left at zero by every call (one set per stream).  Replaces the
  * q_norm, k_norm, rope, KV write and attention steps of the decode composition

@@ -1042,6 +1042,12 @@ int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t
     return fail(IMQ_EINVAL, "bad head counts (Hq a multiple of Hkv, at most 8 query heads per KV head)");
   if (capacity < 1 || num_slots < 1 || max_len < 1 || !(theta > 0.0f) || !(eps >= 0.0f))
     return fail(IMQ_EINVAL, "bad capacity, slot count, max_len, theta or eps");
+  // the same layout requirements as imq_attention_decode, whose attention this computes
+  if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(workspace, 16))
+    return fail(IMQ_EINVAL, "q, pools and workspace must be 16-byte aligned");
+  if (!aligned(counters, 4)) return fail(IMQ_EINVAL, "counters must be 4-byte aligned");
+  if (B > 65535 || Hkv > 65535 || Hq > 65535)
+    return fail(IMQ_EINVAL, "B and the head counts must be <= 65535");
   if ((int64_t)num_slots * Hkv * capacity * kD * 2 >= ((int64_t)1 << 31))
     return fail(IMQ_EUNSUPPORTED, "a KV pool of 2 GiB or more exceeds the attention's offsets");
   int32_t code;

@@ -142,6 +142,76 @@ def test_qk_norm_rope_refuses_out_of_range_requests(env):
     assert not kp.any() and not vp.any() and not q_out.any()
 
 
+def _fused_pair(torch, n, B, positions, slots, slots_n, hq=32, hkv=8, cap=700, max_len=700,
+                seed=0):
+    """The same inputs through imq_attention_fused and through imq_qk_norm_rope followed
+    by imq_attention_decode (lengths positions + 1, or 0 for an invalid request, the fused
+    entry's contract); returns both (out, k_pool, v_pool), the fused call's arguments and
+    its split counters."""
+    g = np.random.default_rng(seed)
+    q, _ = _bf16(torch, g.standard_normal((B, hq * 128)))
+    k, _ = _bf16(torch, g.standard_normal((B, hkv * 128)))
+    v, _ = _bf16(torch, g.standard_normal((B, hkv * 128)))
+    qn, _ = _bf16(torch, g.uniform(0.8, 1.2, 128))
+    kn, _ = _bf16(torch, g.uniform(0.8, 1.2, 128))
+    kp, _ = _bf16(torch, g.standard_normal((slots_n, hkv, cap, 128)))
+    vp, _ = _bf16(torch, g.standard_normal((slots_n, hkv, cap, 128)))
+    pos = torch.tensor(positions, dtype=torch.int32, device="cuda")
+    sl = torch.tensor(slots, dtype=torch.int32, device="cuda")
+    theta, eps = 1e6, 1e-6
+    kp_a, vp_a = kp.clone(), vp.clone()
+    q_rot = torch.empty_like(q)
+    out_a = torch.full((B, hq, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(n.attention_workspace(B, hq, max_len), dtype=torch.float32, device="cuda")
+    n.qk_norm_rope(q, k, v, qn, kn, pos, sl, q_rot, kp_a, vp_a, theta, eps)
+    valid = (pos >= 0) & (pos < cap) & (sl >= 0) & (sl < slots_n)
+    lengths = torch.where(valid, pos + 1, torch.zeros_like(pos))  # the fused entry's contract
+    n.attention_decode(q_rot, kp_a, vp_a, lengths, sl, out_a, max_len, 128 ** -0.5, ws)
+    kp_b, vp_b = kp.clone(), vp.clone()
+    out_b = torch.full((B, hq, 128), -7.0, dtype=torch.bfloat16, device="cuda")
+    ws_b = torch.empty_like(ws)
+    counters = torch.zeros(B * hkv, dtype=torch.int32, device="cuda")
+    fused = (q, k, v, qn, kn, pos, sl, kp_b, vp_b, out_b, max_len, theta, eps, ws_b, counters)
+    n.attention_fused(*fused)
+    torch.cuda.synchronize()
+    return (out_a, kp_a, vp_a), (out_b, kp_b, vp_b), fused, counters
+
+
+@pytest.mark.parametrize("B,positions", [(1, [63]), (1, [64]), (1, [511]), (1, [699]),
+                                         (3, [0, 127, 128]), (3, [64, 650, 5])])
+def test_attention_fused_equals_the_three_launch_form(env, B, positions):
+    """imq_attention_fused gives the bits of imq_qk_norm_rope + imq_attention_decode: the
+    attention output and both KV pools, with positions on both sides of the 64-key chunk
+    (split) boundaries, at the last row of the pools, and for three requests; a second call
+    (its split counters back at zero) repeats them."""
+    torch, n, do, orc = env
+    announce("attention fused vs three launches", B, positions)
+    slots = list(RNG.permutation(B + 2)[:B].astype(int))
+    a, b, fused, counters = _fused_pair(torch, n, B, positions, slots, B + 2, seed=B * 1000 + positions[0])
+    for x, y in zip(a, b):
+        assert np.array_equal(bf16_bits(x), bf16_bits(y))
+    assert not counters.any()
+    first = bf16_bits(b[0]).copy()
+    n.attention_fused(*fused)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(b[0]), first)
+
+
+def test_attention_fused_bad_requests(env):
+    """A request with a slot outside the pools or a position at the capacity gets a zero
+    output and writes nothing, in both forms, and the valid request beside them keeps the
+    three-launch form's bits."""
+    torch, n, do, orc = env
+    announce("attention fused bad requests")
+    cap = 96
+    a, b, _, _ = _fused_pair(torch, n, 3, [40, 10, cap], [1, 7, 0], 3, cap=cap, max_len=cap, seed=5)
+    for x, y in zip(a, b):
+        assert np.array_equal(bf16_bits(x), bf16_bits(y))
+    out = _vals(b[0])
+    assert np.isfinite(out[0]).all() and out[0].any()
+    assert not out[1].any() and not out[2].any()
+
+
 def _attention_case(torch, n, do, B, hq, hkv, lengths, cap=600, slots_n=None, max_len=None):
     slots_n = slots_n or B + 1
     kp, kpv = _bf16(torch, RNG.standard_normal((slots_n, hkv, cap, 128)))
@@ -256,14 +326,16 @@ def test_decode_step_matches_oracle(env):
         positions = [p + 1 if p + 1 < 80 else p for p in positions]
 
 
-def test_decode_step_at_qwen3_4b_shapes_is_deterministic(env):
-    """Real Qwen3-4B layer shapes (2 of the 36 layers, full vocabulary head), B = 32 and
-    B = 1: the step runs, its logits are finite, and a replay gives the same bits."""
+@pytest.mark.parametrize("layers,batches", [(2, (32, 1)), (36, (32,))])
+def test_decode_step_at_qwen3_4b_shapes_is_deterministic(env, layers, batches):
+    """Real Qwen3-4B shapes (2 layers, and the full 36), full vocabulary head, a 512-token
+    context, B = 32 (and 1): the step runs, its logits are finite, and a second call on
+    the same state gives the same bits."""
     torch, n, do, orc = env
     from ironmule_amd.decode import DecodeState, DecoderConfig, decode_step, random_weights
-    cfg = DecoderConfig(layers=2)
+    cfg = DecoderConfig(layers=layers)
     weights = random_weights(cfg, "cuda", seed=9)
-    for batch in (32, 1):
+    for batch in batches:
         announce("decode step qwen3-4b shapes", batch)
         state = DecodeState(cfg, batch=batch, slots=batch, capacity=520, max_len=520, device="cuda")
         for kp in state.k_pool + state.v_pool:

@@ -122,6 +122,33 @@ def test_grouped_equals_separate_calls(native, oracle, m):
         _check(oracle, pr, single)
 
 
+@pytest.mark.parametrize("m", [3, 4])
+def test_few_row_tile_rows_equal_one_row_calls(native, oracle, m):
+    """Three and four rows with every K <= 4096 take the few-row tile (the one-row tile
+    serving several activation rows from one weight read), in a grouped launch and with
+    the pointer table of qmv_multi: each output row equals the one-row call on that row,
+    bit for bit, and the oracle."""
+    shapes = [(512, 2560), (128, 2560), (320, 4096), (33, 192)]
+    probs = [oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 60 + i)
+             for i, (n, k) in enumerate(shapes)]
+    dev = [to_device(p) for p in probs]
+    xs = [dev[0][3], dev[0][3], dev[2][3], dev[3][3]]
+    announce("few-row grouped", m)
+    outs = native.qmv_grouped([d[:3] for d in dev], xs)
+    for i, (p, d) in enumerate(zip(probs, dev)):
+        for r in range(m):
+            one = native.qmv(d[0], d[1], d[2], xs[i][r:r + 1].contiguous())
+            assert np.array_equal(bf16_bits(outs[i])[r], bf16_bits(one)[0]), (i, r)
+        _check(oracle, oracle.Problem(p.w, p.s, p.b, bf16_bits(xs[i]), 0), outs[i])
+    announce("few-row qmv_multi", m)
+    w, s, b, x = dev[2]
+    rows = [x[r].clone() for r in range(m)]  # separate allocations: the pointer table
+    multi = native.qmv_multi(w, s, b, rows)
+    stacked = native.qmv(w, s, b, x)
+    for r in range(m):
+        assert np.array_equal(bf16_bits(multi[r])[0], bf16_bits(stacked)[r]), r
+
+
 @pytest.mark.parametrize("n,k", [(256, 2560), (64, 15360), (33, 192)])
 def test_dequant_is_bit_exact(native, oracle, n, k):
     import torch
@@ -160,14 +187,16 @@ def test_golden_fixtures(native, oracle):
         assert lit.ok, (p["name"], lit.detail)
 
 
-def test_shared_weight_config_full_size(native, oracle):
-    """K=3840, N=15360 at M = 32 (the weight read once for 32 requests); rows sampled
-    for the oracle, all rows checked for agreement between M and single-row calls."""
-    pr = oracle.synthetic(15360, 3840, 32, seed=oracle.SEED_BASE + 2)
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32])
+def test_shared_weight_config_full_size(native, oracle, m):
+    """The shared-weight configuration at its own shape, K=3840, N=15360, over its M sweep
+    (the weight read once for all M requests; each M takes its own launch plan); rows
+    sampled for the oracle, including the last ones."""
+    pr = oracle.synthetic(15360, 3840, m, seed=oracle.SEED_BASE + 2)
     w, s, b, x = to_device(pr)
-    announce("shared K3840 N15360 M32")
+    announce("shared K3840 N15360", m)
     y = native.qmv(w, s, b, x)
-    rows = np.arange(0, 15360, 37)
+    rows = np.unique(np.concatenate([np.arange(0, 15360, 37), np.arange(15300, 15360)]))
     _check(oracle, pr, y, rows=rows)
 
 

@@ -177,6 +177,23 @@ def test_decode_program_matches_decode_step_qwen3_4b_shapes(env, staged):
     assert info["stages"] == 2 * 5 + 1 and info["workgroups"] >= 256
 
 
+def test_decode_program_matches_decode_step_full_36_layers(env):
+    """The full synthetic Qwen3-4B step (36 layers, the 151,936-token head, a 512-token
+    context): the staged batch-1 program behind the bench's batch-1 figure gives the
+    per-kernel step's bits over two consecutive steps."""
+    torch, n, orc = env
+    from ironmule_amd.decode import DecoderConfig, random_weights
+    announce("program decode, qwen3-4b, 36 layers, staged")
+    cfg = DecoderConfig()
+    assert cfg.layers == 36
+    weights = random_weights(cfg, "cuda", seed=21)
+    engine, state = _compare_steps(torch, weights, cfg, 520, [(11, 0, 512), (4097, 0, 513)],
+                                   seed=5, staged=True)
+    assert engine.program.info()["stages"] == 36 * 5 + 1
+    del engine, state, weights
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("staged", [False, True])
 def test_decode_program_replays_in_a_graph(env, staged):
     """Captured in a HIP graph (embedding, counter reset, the program's launches) and
