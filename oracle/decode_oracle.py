@@ -24,7 +24,10 @@ them, giving the all-fp32 composition of the CPU plan.  Each helper names the re
 lines it restates; tests/test_decode_oracle.py pins every helper against an independent
 implementation (torch's rms_norm / scaled_dot_product_attention / silu on the CPU) or a
 closed form (rotations compose and preserve length, position 0 is the identity, one key
-returns its value).
+returns its value), and tests/test_decode_oracle_hf.py pins the composition itself: with
+round_bf16=False, step-by-step decoding matches transformers' Qwen3ForCausalLM (same
+weights, one causal forward) at the fp32 rounding level, while compositions with the rotary
+or the q/k-norm skipped, or the MLP fed from the residual stream, do not.
 """
 
 from __future__ import annotations
