@@ -33,16 +33,7 @@ def _kernel(k: int, width: int):
 
 
 KERNELS = {(k, width): _kernel(k, width) for k in SUPPORTED_K for width in (1, 2)}
-_SHAPES: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def shape_array(in_features: int, out_features: int) -> torch.Tensor:
-    key = (in_features, out_features)
-    cached = _SHAPES.get(key)
-    if cached is None:
-        cached = torch.tensor([in_features, out_features], dtype=torch.int32)
-        _SHAPES[key] = cached
-    return cached
+shape_array = kernel_registry.shape_tensor
 
 
 def run_fast(w, scales, biases, vectors, out_features: int, in_features: int):

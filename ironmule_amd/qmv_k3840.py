@@ -1,26 +1,28 @@
-"""The fixed-K (3840) decode qmv behind an admission gate, on the gfx950 kernels.
+"""The K=3840 decode qmv as a drop-in for a model's projections, on the gfx950 kernels.
 
-Mirrors ironmule/qmv_k3840.py.  The reference ships MLX 0.32.0's `qmv_impl` transcribed
-to Metal at K=3840 (`K3840`) and at runtime K (`PORT`), dispatched as MLX does, and swaps
-admitted projections for `K3840QuantizedLinear` after a narrow, fail-closed admission.
-Here the kernels are the gfx950 library's (libironmule_qmv.so, `imq_qmv`); the Python
-surface, the admission rules, the module swap and its restore are the reference's:
+Mirrors the call surface of ironmule/qmv_k3840.py: the kernels `K3840` (fixed K) and
+`PORT` (runtime K), `run`, `shape_array`, `K3840QuantizedLinear`, `enable`/`disable`, the
+admission helpers `_admit_environment`/`_admit_projection` and `K3840Unsupported`.  The
+reference runs a Metal transcription of MLX's qmv; here both kernels are the library's
+`imq_qmv` (libironmule_qmv.so), reached through `kernel_registry.HipKernel`.
 
-* `run(kernel, w, scales, biases, x, out_features, in_features)` dispatches with the
-  reference's geometry arguments (grid (32, 2*ceil(N/8), 1), threadgroup (32, 2, 1)),
-  which are validated and recorded; the library picks the HIP launch;
-* `K3840QuantizedLinear` runs the kernel for single-token decode (x of shape (1, 1, K))
-  and calls the original module for everything else;
-* `enable` admits or raises `K3840Unsupported` before mutating anything; `disable`
-  restores the original module objects.
+How a model is changed:
 
-Admission differs in what it pins.  The reference pins one Apple machine fingerprint,
-MLX/mlx_lm versions and one model revision digest, because its kernel was qualified as
-byte-identical to MLX on that stack.  These kernels are qualified by the parity tests
-against the oracle over any weights of the admitted format, so admission pins the
-device architecture (gfx950), requires a model identity (architecture and a sha256
-digest, as the reference's identity object carries) and checks every projection's
-format exactly as the reference does.
+* `enable(model, identity)` first checks the caller and the machine (a model identity
+  with an architecture this path is qualified for and a sha256 digest; a gfx950 device
+  with the library loaded), then lists every `QuantizedLinear` whose reduction length is
+  3840, sorts them into admitted and declined by their format, and only then swaps the
+  admitted ones.  Any refusal raises `K3840Unsupported` with the model unchanged.
+* A swapped projection is a `K3840QuantizedLinear`: a (1, 1, 3840) activation runs the
+  kernel, anything else (prefill, batches) runs the original module on the same tensors.
+* `disable(model)` puts the original module objects back.
+
+What admission pins differs from the reference.  The reference qualified its kernel as
+byte-identical to MLX on one Apple machine, one MLX/mlx_lm version pair and one model
+revision, and pins those.  These kernels are qualified by parity tests against the oracle
+over any weights of the admitted format, so admission pins the device architecture and
+the format (4-bit, group 64, bf16 scales and biases, contiguous, N a multiple of 8) and
+asks for a model identity in the same shape as the reference's.
 """
 
 from __future__ import annotations
@@ -31,11 +33,13 @@ from typing import Any
 import torch
 
 from . import _native, kernel_registry
+from .module_swap import DecodeOverride, find_sites, in_features, replace, restore
 from .quantized import QuantizedLinear
 
 
 class K3840Unsupported(RuntimeError):
-    """The candidate is not admitted here. The library path stays in charge."""
+    """Raised by `enable` when this machine, this model or none of its projections
+    qualifies; the model is left as it was."""
 
 
 VERIFIED_DEVICE_ARCH = "gfx950"
@@ -55,6 +59,8 @@ RESULTS_PER_SIMDGROUP = 4
 BYTES_PER_PACK = 4
 PACK_FACTOR = 8
 GROUP_SIZE = 64
+
+ROWS_PER_THREADGROUP = NUM_SIMDGROUPS * RESULTS_PER_SIMDGROUP  # 8
 
 SOURCE = ("imq_qmv (libironmule_qmv.so): y = x @ dequantize(w, scales, biases).T, 4-bit "
           "affine, group 64, bf16 activations, fp32 accumulation, bf16 output")
@@ -76,157 +82,160 @@ def _kernel(name: str, fixed_k: int | None):
 PORT = _kernel("qmv_port", None)
 K3840 = _kernel("qmv_k3840", TARGET_K)
 
-_SHAPES: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def shape_array(in_features: int, out_features: int) -> torch.Tensor:
-    """One shared constant per geometry (K, N); building it per call would be measured work."""
-    key = (in_features, out_features)
-    cached = _SHAPES.get(key)
-    if cached is None:
-        cached = torch.tensor([in_features, out_features], dtype=torch.int32)
-        _SHAPES[key] = cached
-    return cached
+shape_array = kernel_registry.shape_tensor
 
 
 def run(kernel, w, scales, biases, x, out_features: int, in_features: int):
-    """Dispatch with the reference's arguments: (32, 2, 1) threads, ceil(N/8) groups in y."""
-    groups = (out_features + 7) // 8
-    return kernel(
-        inputs=[w, scales, biases, x, shape_array(in_features, out_features)],
-        output_shapes=[(1, out_features)],
-        output_dtypes=[x.dtype],
-        grid=(SIMD_SIZE, NUM_SIMDGROUPS * groups, 1),
-        threadgroup=(SIMD_SIZE, NUM_SIMDGROUPS, 1),
-    )[0]
+    """`x @ dequantize(w).T` for one (1, K) row through `kernel`, with the dispatch a Metal
+    caller passes: threadgroups of two 32-lane simdgroups, each simdgroup owning four
+    output rows, enough threadgroups to cover N."""
+    threadgroups = -(-out_features // ROWS_PER_THREADGROUP)
+    (y,) = kernel(inputs=[w, scales, biases, x, shape_array(in_features, out_features)],
+                  output_shapes=[(1, out_features)], output_dtypes=[x.dtype],
+                  grid=(SIMD_SIZE, NUM_SIMDGROUPS * threadgroups, 1),
+                  threadgroup=(SIMD_SIZE, NUM_SIMDGROUPS, 1))
+    return y
 
 
-class K3840QuantizedLinear(torch.nn.Module):
-    """The admitted projection with its matmul replaced. Same buffers, same bytes.
-
-    Decode reaches the kernel; anything else calls the original module on the very same
-    buffers, so a shape this module was not admitted for costs one comparison.
-    """
+class K3840QuantizedLinear(DecodeOverride):
+    """An admitted projection: (1, 1, 3840) activations run `K3840`; every other input
+    runs the original module, whose tensors this one shares."""
 
     def __init__(self, source: QuantizedLinear) -> None:
-        super().__init__()
-        # Kept outside the module tree, so a walk never mistakes it for a live projection.
-        object.__setattr__(self, "_source", source)
-        self.weight = source.weight
-        self.scales = source.scales
-        self.biases = source.biases
-        self.group_size = source.group_size
-        self.bits = source.bits
-        self.out_features = int(source.weight.shape[0])
+        super().__init__(source)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        shape = x.shape
-        # Single-token decode only. Prefill and every wider input keep the library path.
-        if len(shape) != 3 or shape[0] != 1 or shape[1] != 1:
-            return self._source(x)
-        out = run(K3840, self.weight, self.scales, self.biases, x[0], self.out_features,
-                  TARGET_K)
-        return out[None]
+    def decode(self, row: torch.Tensor) -> torch.Tensor:
+        return run(K3840, self.weight, self.scales, self.biases, row, self.out_features,
+                   TARGET_K)
 
 
-_SHA256 = re.compile(r"^[0-9a-f]{64}$")
+# ------------------------------------------------------------------ admission
+
+_HEX_DIGEST = re.compile(r"[0-9a-f]{64}")
+
+
+def _identity_problem(identity: Any) -> str | None:
+    if identity is None:
+        return "enable() needs the model's identity (architecture, sha256 digest); got None"
+    digest = getattr(identity, "identity_sha256", None)
+    if not isinstance(digest, str) or not _HEX_DIGEST.fullmatch(digest):
+        return f"identity_sha256 is not 64 lowercase hex digits: {str(digest)[:16]!r}"
+    architecture = getattr(identity, "architecture", None)
+    if architecture not in VERIFIED_ARCHITECTURES:
+        return f"architecture {architecture!r} is not one of {VERIFIED_ARCHITECTURES}"
+    return None
+
+
+def _device_problem() -> str | None:
+    try:
+        code, arch, _ = _native.device_check()
+    except Exception as exc:  # the library or the HIP runtime is missing
+        return f"libironmule_qmv.so cannot run here: {exc}"
+    if code != 0 or not arch.startswith(VERIFIED_DEVICE_ARCH):
+        return f"the device is {arch or 'absent'}; these kernels are qualified on {VERIFIED_DEVICE_ARCH}"
+    return None
 
 
 def _admit_environment(identity: Any) -> None:
-    """Everything expensive happens here, once, and never per token."""
-    if identity is None:
-        raise K3840Unsupported("no model identity available; the candidate fails closed")
-    digest = getattr(identity, "identity_sha256", None)
-    if not isinstance(digest, str) or not _SHA256.match(digest):
-        raise K3840Unsupported(f"model identity digest missing or malformed: {str(digest)[:16]}")
-    architecture = getattr(identity, "architecture", None)
-    if architecture not in VERIFIED_ARCHITECTURES:
-        raise K3840Unsupported(
-            f"admitted architectures are {VERIFIED_ARCHITECTURES}, found {architecture}")
-    try:
-        code, arch, _ = _native.device_check()
-    except Exception as exc:  # no library, no HIP runtime
-        raise K3840Unsupported(f"the gfx950 library is unavailable: {exc}") from exc
-    if code != 0 or not arch.startswith(VERIFIED_DEVICE_ARCH):
-        raise K3840Unsupported(f"qualified on {VERIFIED_DEVICE_ARCH}, found {arch or 'no device'}")
+    """Raise K3840Unsupported unless the identity qualifies and the device is gfx950.
+    Called once per `enable`, never per token."""
+    problem = _identity_problem(identity) or _device_problem()
+    if problem is not None:
+        raise K3840Unsupported(problem)
+
+
+def _format_problems(module: QuantizedLinear) -> list[str]:
+    """Every way this projection differs from the admitted format (empty: admitted).
+
+    The format: 4-bit codes in groups of 64 over K=3840, N a multiple of the eight rows a
+    Metal threadgroup writes, packed int32 (or uint32) words of shape (N, 480) and bf16
+    scales and biases of shape (N, 60), all contiguous
+    (the conditions of ironmule/qmv_k3840.py:379-408)."""
+    problems = []
+    if int(module.bits) != VERIFIED_BITS:
+        problems.append(f"bits={module.bits}")
+    if int(module.group_size) != VERIFIED_GROUP_SIZE:
+        problems.append(f"group_size={module.group_size}")
+    if in_features(module) != TARGET_K:
+        problems.append(f"K={in_features(module)}")
+    n = int(module.weight.shape[0])
+    if n % ROWS_PER_THREADGROUP:
+        problems.append(f"N={n} is not a multiple of {ROWS_PER_THREADGROUP}")
+    groups = TARGET_K // VERIFIED_GROUP_SIZE
+    expected = {
+        "weight": ((n, TARGET_K * VERIFIED_BITS // 32), (torch.int32, torch.uint32)),
+        "scales": ((n, groups), (VERIFIED_DTYPE,)),
+        "biases": ((n, groups), (VERIFIED_DTYPE,)),
+    }
+    for name, (shape, dtypes) in expected.items():
+        tensor = getattr(module, name, None)
+        if tensor is None:
+            problems.append(f"no {name}")
+        elif tuple(tensor.shape) != shape or tensor.dtype not in dtypes:
+            problems.append(f"{name} {tuple(tensor.shape)} {tensor.dtype}")
+        elif not tensor.is_contiguous():
+            problems.append(f"{name} not contiguous")
+    return problems
 
 
 def _admit_projection(module: QuantizedLinear) -> bool:
-    """K alone is not enough: bits, group size, dtype, width and layout all decide
-    (the reference's checks, ironmule/qmv_k3840.py:379-408)."""
-    if int(module.bits) != VERIFIED_BITS or int(module.group_size) != VERIFIED_GROUP_SIZE:
-        return False
-    columns = int(module.weight.shape[1]) * 32 // int(module.bits)
-    if columns != TARGET_K:
-        return False
-    out_features = int(module.weight.shape[0])
-    if out_features % (NUM_SIMDGROUPS * RESULTS_PER_SIMDGROUP):
-        return False  # the reference's kernel writes eight rows per threadgroup
-    for array in (module.scales, module.biases):
-        if array.dtype != VERIFIED_DTYPE:
-            return False
-    if module.weight.dtype not in (torch.int32, torch.uint32):
-        return False
-    if int(module.scales.shape[1]) != TARGET_K // VERIFIED_GROUP_SIZE:
-        return False
-    if module.scales.shape != module.biases.shape:
-        return False
-    expected = (
-        (module.weight, out_features * (TARGET_K * VERIFIED_BITS // 32) * 4),
-        (module.scales, out_features * (TARGET_K // VERIFIED_GROUP_SIZE) * 2),
-        (module.biases, out_features * (TARGET_K // VERIFIED_GROUP_SIZE) * 2),
-    )
-    return all(array.is_contiguous() and array.numel() * array.element_size() == size
-               for array, size in expected)
+    """True when the projection is exactly in the admitted format."""
+    return not _format_problems(module)
+
+
+def _candidates(model: torch.nn.Module):
+    """The sites of every QuantizedLinear with K=3840, admitted or not; installed
+    replacements are not looked into."""
+    return find_sites(model, lambda m: isinstance(m, QuantizedLinear)
+                      and in_features(m) == TARGET_K, opaque=(DecodeOverride,))
 
 
 def _replace(module: torch.nn.Module, admitted: list[str], skipped: list[str],
              prefix: str = "") -> None:
-    for name, child in list(module.named_children()):
-        path = f"{prefix}.{name}" if prefix else name
-        if isinstance(child, QuantizedLinear):
-            columns = int(child.weight.shape[1]) * 32 // int(child.bits)
-            if columns != TARGET_K:
-                continue
-            if _admit_projection(child):
-                setattr(module, name, K3840QuantizedLinear(child))
-                admitted.append(path)
-            else:
-                skipped.append(path)
-        elif not isinstance(child, K3840QuantizedLinear):
-            _replace(child, admitted, skipped, path)
+    """Swap every admitted K=3840 projection under `module` for a K3840QuantizedLinear;
+    append the dotted paths (under `prefix`) of the swapped ones to `admitted` and of the
+    refused ones to `skipped`."""
+    take, leave = [], []
+    for site in _candidates(module):
+        (take if _admit_projection(site.module) else leave).append(site)
+    replace(take, K3840QuantizedLinear)
+    head = f"{prefix}." if prefix else ""
+    admitted.extend(head + site.path for site in take)
+    skipped.extend(head + site.path for site in leave)
 
 
 def _restore(module: torch.nn.Module, restored: list[str], prefix: str = "") -> None:
-    for name, child in list(module.named_children()):
-        path = f"{prefix}.{name}" if prefix else name
-        if isinstance(child, K3840QuantizedLinear):
-            setattr(module, name, child._source)
-            restored.append(path)
-        else:
-            _restore(child, restored, path)
-
-
-def disable(model: torch.nn.Module) -> int:
-    """Put every admitted projection back on the library path. Returns how many."""
-    restored: list[str] = []
-    _restore(model, restored)
-    return len(restored)
+    """Put back the original of every K3840QuantizedLinear under `module`; append their
+    dotted paths to `restored`."""
+    head = f"{prefix}." if prefix else ""
+    restored.extend(head + path for path in restore(module, K3840QuantizedLinear))
 
 
 def enable(model: torch.nn.Module, identity: Any) -> dict[str, Any]:
-    """Admit the candidate on this model, or raise and leave it untouched."""
+    """Swap the model's admitted K=3840 projections, or raise K3840Unsupported and change
+    nothing.  Returns what was done: counts and dotted paths of the admitted and declined
+    projections, the device architecture and the identity digest."""
     _admit_environment(identity)
+    candidates = _candidates(model)
+    if not any(_admit_projection(site.module) for site in candidates):
+        raise K3840Unsupported(
+            f"none of the model's {len(candidates)} K={TARGET_K} projections is in the "
+            "admitted format")
     admitted: list[str] = []
-    skipped: list[str] = []
-    _replace(model, admitted, skipped)
-    if not admitted:
-        raise K3840Unsupported("no projection met the admission conditions")
+    declined: list[str] = []
+    _replace(model, admitted, declined)
     return {
         "admitted": len(admitted),
-        "declined": len(skipped),
+        "declined": len(declined),
         "admitted_paths": admitted,
-        "declined_paths": skipped,
+        "declined_paths": declined,
         "device_arch": VERIFIED_DEVICE_ARCH,
-        "identity_sha256": getattr(identity, "identity_sha256", None),
+        "identity_sha256": identity.identity_sha256,
     }
+
+
+def disable(model: torch.nn.Module) -> int:
+    """Undo `enable`: the original modules go back in place. Returns how many."""
+    restored: list[str] = []
+    _restore(model, restored)
+    return len(restored)

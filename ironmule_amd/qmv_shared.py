@@ -32,16 +32,7 @@ def _kernel(width: int):
 
 
 SHARED = {width: _kernel(width) for width in (1, 2)}
-_SHAPES: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def shape_array(in_features: int, out_features: int) -> torch.Tensor:
-    key = (in_features, out_features)
-    cached = _SHAPES.get(key)
-    if cached is None:
-        cached = torch.tensor([in_features, out_features], dtype=torch.int32)
-        _SHAPES[key] = cached
-    return cached
+shape_array = kernel_registry.shape_tensor
 
 
 def run_shared(w, scales, biases, vectors, out_features: int):

@@ -1,18 +1,20 @@
-"""A second dispatch geometry of the K=3840 qmv, installable and gated at run time.
+"""A second dispatch geometry of the K=3840 qmv, installed per model and switched at run time.
 
-Mirrors ironmule/qmv_variant.py: `QUALIFIED_GEOMETRY`, `VariantGate` (one mutable bool
-plus a permanent kill), `kernel_for(geometry)`, `GatedVariantLinear` (one boolean and one
-shape check, then the kernel or the *original module*), `_identical` (the contract: an
-admitted projection's output is byte-identical to the library path on its own weights
-and a probe), `install` (all-or-nothing) and `uninstall`.
+Mirrors the call surface of ironmule/qmv_variant.py: `QUALIFIED_GEOMETRY`,
+`QUALIFIED_ACTION_ID`, `CORRECTNESS_CONTRACT`, `VariantUnsupported`, `VariantGate`,
+`kernel_for`, `GatedVariantLinear`, `_identical`, `install` and `uninstall`.
 
-On gfx950 the geometry is the reference's Metal dispatch description: it is validated
-(N must be a multiple of simdgroups x rows) and recorded in the kernel's specification,
-so each geometry registers its own identifier, while the HIP launch inside the library
-is chosen by the library.  The library path the contract compares against is the
-original module's own call, which for a single decode row runs the same qmv kernel, so
-an admitted projection is byte-identical by construction and the check still guards
-against anything else (a different build, a different device) changing that.
+A geometry is (simdgroups per threadgroup, output rows per simdgroup), the dispatch a
+Metal caller describes.  On gfx950 it does not choose the HIP launch (the library does);
+it is part of the kernel's specification, so each geometry is registered under its own
+name, and every call is checked to cover all N rows with it.
+
+`install` works in three passes over the model and changes it only in the last: it checks
+the environment as `qmv_k3840.enable` does; it qualifies every K=3840 projection (format,
+N a multiple of the geometry's rows per threadgroup, then `_identical` on the projection's
+own weights); and only if no projection failed `_identical` does it swap the qualified
+ones for `GatedVariantLinear`s that share one `VariantGate`.  The gate starts shut: while
+it is shut, or for any input but a single decode row, the original module runs.
 """
 
 from __future__ import annotations
@@ -22,45 +24,58 @@ from typing import Any
 
 import torch
 
-from . import kernel_registry
+from . import _native, kernel_registry
 from . import qmv_k3840 as qmv
+from .module_swap import DecodeOverride, replace, restore
 from .quantized import QuantizedLinear
 
 #: The geometry the reference qualified, and the identifier its evidence names it by.
 QUALIFIED_GEOMETRY = (4, 8)
 QUALIFIED_ACTION_ID = "k3840_geometry_sg4_r8"
+
+#: `_identical`'s bound: the bf16 rounding of the output (2^-8 of |ref|) plus an
+#: allowance for fp32 summation order of 2^-14 of sum(|w|*|x|) over the row.
+ROUNDING = 2.0 ** -8
+SUMMATION = 2.0 ** -14
+#: Rows of the float64 reference computed at a time (at K=3840: 126 MB per chunk).
+REFERENCE_CHUNK = 4096
+
 CORRECTNESS_CONTRACT = (
-    "every admitted projection is byte-identical to the library path on its own buffers "
-    "before it is installed, and a projection that differs is left on the library path")
+    "before it is installed, every admitted projection's decode output on its own weights "
+    "and a seeded probe row is within 2^-8 |ref| + 2^-14 sum|w*x| of ref, a float64 product "
+    "of the weight dequantised by imq_dequant; if any projection misses that bound nothing "
+    "is installed")
 
 
 class VariantUnsupported(RuntimeError):
-    """The variant is not admitted here. The library path stays in charge."""
+    """Raised by `install` when the variant cannot be installed on this model; the model
+    is left as it was."""
 
 
 @dataclass
 class VariantGate:
-    """One mutable boolean the installed projections read, and the reason it is shut."""
+    """The switch every projection of one `install` consults on each call.
+
+    `open` and `close` flip it with a reason the caller can log; `kill` shuts it for the
+    rest of the process, after which `open` is ignored."""
 
     active: bool = False
     killed: bool = False
     reason: str = "not activated"
 
     def open(self, reason: str) -> None:
-        if self.killed:
-            return
-        self.active, self.reason = True, reason
+        if not self.killed:
+            self.active, self.reason = True, reason
 
     def close(self, reason: str) -> None:
         self.active, self.reason = False, reason
 
     def kill(self, reason: str) -> None:
-        """Permanent for the life of this process. There is no second experimental path."""
         self.active, self.killed, self.reason = False, True, reason
 
 
 def kernel_for(geometry: tuple[int, int], fixed_k: int = qmv.TARGET_K):
-    """The kernel at this geometry, named by the registry from its whole specification."""
+    """The registered kernel for this geometry at K=`fixed_k`."""
     simdgroups, results = geometry
     if simdgroups < 1 or results < 1:
         raise ValueError(f"geometry {geometry} must be positive")
@@ -72,92 +87,94 @@ def kernel_for(geometry: tuple[int, int], fixed_k: int = qmv.TARGET_K):
                   "results_per_simdgroup": results})
 
 
-class GatedVariantLinear(torch.nn.Module):
-    """An admitted projection that uses the variant only while its gate is open."""
+class GatedVariantLinear(DecodeOverride):
+    """A qualified projection that runs the variant for a single decode row while `gate`
+    is open, and the original module otherwise."""
 
     def __init__(self, source: QuantizedLinear, kernel, geometry: tuple[int, int],
                  gate: VariantGate) -> None:
-        super().__init__()
-        object.__setattr__(self, "_source", source)
+        super().__init__(source)
         self._kernel = kernel
         self._gate = gate
-        self.weight, self.scales, self.biases = source.weight, source.scales, source.biases
-        self.group_size, self.bits = source.group_size, source.bits
-        self.out_features = int(source.weight.shape[0])
-        self._simdgroups = geometry[0]
-        self._groups = self.out_features // (geometry[0] * geometry[1])
+        simdgroups, results = geometry
+        threadgroups = self.out_features // (simdgroups * results)
+        self._grid = (qmv.SIMD_SIZE, simdgroups * threadgroups, 1)
+        self._threadgroup = (qmv.SIMD_SIZE, simdgroups, 1)
         self._shape = qmv.shape_array(qmv.TARGET_K, self.out_features)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        shape = x.shape
-        # One boolean and one shape check, then the original module for everything else.
-        if not self._gate.active or len(shape) != 3 or shape[0] != 1 or shape[1] != 1:
-            return self._source(x)
-        out = self._kernel(
-            inputs=[self.weight, self.scales, self.biases, x[0], self._shape],
-            output_shapes=[(1, self.out_features)], output_dtypes=[x.dtype],
-            grid=(qmv.SIMD_SIZE, self._simdgroups * self._groups, 1),
-            threadgroup=(qmv.SIMD_SIZE, self._simdgroups, 1))[0]
-        return out[None]
+    def serves(self, x: torch.Tensor) -> bool:
+        return self._gate.active and super().serves(x)
+
+    def decode(self, row: torch.Tensor) -> torch.Tensor:
+        (y,) = self._kernel(inputs=[self.weight, self.scales, self.biases, row, self._shape],
+                            output_shapes=[(1, self.out_features)], output_dtypes=[row.dtype],
+                            grid=self._grid, threadgroup=self._threadgroup)
+        return y
+
+
+def _reference(module: QuantizedLinear, probe: torch.Tensor):
+    """(ref, sum|w*x|) per output row in float64, from imq_dequant's fp32 weight."""
+    x = probe.reshape(-1).to(torch.float64)
+    ref, mag = [], []
+    for start in range(0, module.out_features, REFERENCE_CHUNK):
+        rows = slice(start, start + REFERENCE_CHUNK)
+        dense = _native.dequant(module.weight[rows].contiguous(), module.scales[rows].contiguous(),
+                                module.biases[rows].contiguous(), torch.float32).to(torch.float64)
+        ref.append(dense @ x)
+        mag.append(dense.abs() @ x.abs())
+    ref, mag = torch.cat(ref), torch.cat(mag)
+    bias = getattr(module, "bias", None)
+    if bias is not None:
+        ref = ref + bias.to(torch.float64).reshape(-1)
+        mag = mag + bias.to(torch.float64).abs().reshape(-1)
+    return ref, mag
 
 
 def _identical(module: QuantizedLinear, kernel, geometry: tuple[int, int],
                probe_seed: int = 0) -> bool:
-    """The contract, run on this projection's own weights before it is installed."""
-    gate = VariantGate(active=True)
+    """Whether the variant meets the correctness contract on this projection: one seeded
+    bf16 probe row through the variant, against an independent float64 reference."""
     gen = torch.Generator(device=module.weight.device)
     gen.manual_seed(probe_seed)
     probe = torch.randn((1, 1, qmv.TARGET_K), generator=gen,
-                        device=module.weight.device).to(module.scales.dtype)
-    want = module(probe)
-    got = GatedVariantLinear(module, kernel, geometry, gate)(probe)
-    return torch.equal(want.view(torch.int16), got.view(torch.int16))
+                        device=module.weight.device).to(torch.bfloat16)
+    variant = GatedVariantLinear(module, kernel, geometry, VariantGate(active=True))
+    got = variant(probe).reshape(-1).to(torch.float64)
+    ref, mag = _reference(module, probe)
+    return bool(torch.all((got - ref).abs() <= ROUNDING * ref.abs() + SUMMATION * mag))
 
 
 def install(model: torch.nn.Module, identity: Any,
             geometry: tuple[int, int] = QUALIFIED_GEOMETRY) -> tuple[VariantGate, dict[str, Any]]:
-    """Admit the variant on this model, or raise and leave it untouched.
-
-    The gate comes back shut. Opening it is the caller's decision and nothing here makes it.
-    """
+    """Qualify the variant on every K=3840 projection of `model` and install it on those
+    that qualify, or raise (K3840Unsupported for the environment, VariantUnsupported
+    otherwise) with the model unchanged.  Returns the shut gate and a record."""
     qmv._admit_environment(identity)
-    simdgroups, results = geometry
-    rows_per_group = simdgroups * results
     kernel = kernel_for(geometry)
-    gate = VariantGate()
-    admitted: list[str] = []
-    declined: list[str] = []
-    mismatched: list[str] = []
-
-    def walk(parent: torch.nn.Module, prefix: str = "") -> None:
-        for name, child in list(parent.named_children()):
-            path = f"{prefix}.{name}" if prefix else name
-            if isinstance(child, QuantizedLinear):
-                columns = int(child.weight.shape[1]) * 32 // int(child.bits)
-                if columns != qmv.TARGET_K:
-                    continue
-                if not qmv._admit_projection(child) or int(child.weight.shape[0]) % rows_per_group:
-                    declined.append(path)
-                    continue
-                if not _identical(child, kernel, geometry):
-                    mismatched.append(path)
-                    continue
-                setattr(parent, name, GatedVariantLinear(child, kernel, geometry, gate))
-                admitted.append(path)
-            elif not isinstance(child, GatedVariantLinear):
-                walk(child, path)
-
-    walk(model)
+    simdgroups, results = geometry
+    qualified, declined, mismatched = [], [], []
+    for site in qmv._candidates(model):
+        fits = qmv._admit_projection(site.module) and \
+            site.module.out_features % (simdgroups * results) == 0
+        if not fits:
+            declined.append(site.path)
+        elif _identical(site.module, kernel, geometry):
+            qualified.append(site)
+        else:
+            mismatched.append(site.path)
     if mismatched:
-        # A single byte difference anywhere means this build is not the qualified one.
-        uninstall(model)
         raise VariantUnsupported(
-            f"{len(mismatched)} projections were not byte-identical to the library; "
-            f"nothing is installed")
-    if not admitted:
-        raise VariantUnsupported("no projection met the admission conditions")
-    return gate, {"admitted": len(admitted), "declined": len(declined),
-                  "mismatched": len(mismatched), "admitted_paths": admitted,
+            f"the variant missed its bound on {len(mismatched)} projection(s), first "
+            f"{mismatched[0]}; the model is unchanged")
+    if not qualified:
+        raise VariantUnsupported(
+            f"no K={qmv.TARGET_K} projection has the admitted format with N a multiple of "
+            f"{simdgroups * results}")
+    gate = VariantGate()
+    replace(qualified, lambda module: GatedVariantLinear(module, kernel, geometry, gate))
+    return gate, {"admitted": len(qualified), "declined": len(declined),
+                  "mismatched": len(mismatched),
+                  "admitted_paths": [site.path for site in qualified],
                   "declined_paths": declined,
                   "geometry": {"num_simdgroups": simdgroups, "results_per_simdgroup": results},
                   "action_id": QUALIFIED_ACTION_ID,
@@ -165,17 +182,5 @@ def install(model: torch.nn.Module, identity: Any,
 
 
 def uninstall(model: torch.nn.Module) -> int:
-    """Put every installed projection back. Returns how many were restored."""
-    restored = 0
-
-    def walk(parent: torch.nn.Module) -> None:
-        nonlocal restored
-        for name, child in list(parent.named_children()):
-            if isinstance(child, GatedVariantLinear):
-                setattr(parent, name, child._source)
-                restored += 1
-            else:
-                walk(child)
-
-    walk(model)
-    return restored
+    """Undo `install`: the original modules go back in place. Returns how many."""
+    return len(restore(model, GatedVariantLinear))
