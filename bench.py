@@ -286,8 +286,35 @@ def bench_config(torch, native, n, k, ms, y_dtype, copies, device, seed, repeats
 CONTEXT = 512  # tokens already in every request's KV slot
 
 
+def bench_prefill(torch, weights, device, gen, count: int = CONTEXT, repeats: int = 3):
+    """Wall time of `decode.prefill` over a `count`-token prompt (one request), median of
+    `repeats` runs after one untimed run; the host-side prompt upload is included, as in
+    a serving engine's time to first token."""
+    from ironmule_amd.decode import DecodeState, prefill
+
+    cfg = weights.config
+    state = DecodeState(cfg, batch=1, slots=1, capacity=count + 8, max_len=count + 8,
+                        device=device)
+    tokens = torch.randint(0, cfg.vocab, (count,), generator=gen, device=device).tolist()
+    times = []
+    for trial in range(repeats + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        prefill(weights, state, tokens, 0)
+        torch.cuda.synchronize()
+        if trial:
+            times.append(time.perf_counter() - t0)
+    del state
+    torch.cuda.empty_cache()
+    sec = sorted(times)[len(times) // 2]
+    return {"tokens": count, "ms": round(sec * 1e3, 3), "ns": int(sec * 1e9),
+            "tokens_per_s": round(count / sec, 1),
+            "path": "imq_dequant to fp16 + GEMM per projection, fp32 causal attention, "
+                    "head at the last position only"}
+
+
 def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, device="cuda:0",
-                 seed: int = SEED + 4):
+                 seed: int = SEED + 4, prefill_tokens: bool = True):
     """Full synthetic Qwen3-4B decode step (36 layers of 4-bit projections + the 151,936-
     token tied head, GQA attention over a 512-token KV context per request), as one HIP
     graph per batch size; returns tokens/s and the weight + KV bytes per step."""
@@ -298,7 +325,7 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
     weights = random_weights(cfg, device, seed=seed)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed + 1)
-    out = {}
+    out = {"prefill": bench_prefill(torch, weights, device, gen)} if prefill_tokens else {}
     for b in batches:
         state = DecodeState(cfg, batch=b, slots=b, capacity=CONTEXT + 8, max_len=CONTEXT + 8,
                             device=device)
@@ -324,6 +351,7 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
         best = min(times, key=lambda k: times[k][0])
         sec, launches = times[best]
         out[str(b)] = {"ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(b / sec, 1),
+                       "timed_steps": steps, "seconds_per_step": sec,
                        "weight_gbs": round(cfg.weight_bytes() / sec / 1e9, 1),
                        "weight_plus_kv_gbs": round((cfg.weight_bytes() + kv_bytes) / sec / 1e9, 1),
                        "path": best, "launches_per_step": launches,
@@ -333,6 +361,104 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
     del weights
     torch.cuda.empty_cache()
     return out
+
+
+def decode_traffic(cfg, batch: int) -> dict:
+    """Bytes per generated token of the synthetic decode step at `batch` requests: the
+    weights (shared by the batch), each request's K and V rows over CONTEXT + 1 positions,
+    its new K and V rows, and its fp32 logits plus embedding row."""
+    row = cfg.layers * cfg.kv_heads * cfg.head_dim * 2 * 2  # K and V, bf16, every layer
+    return {"active_weight_bytes_per_token": cfg.weight_bytes() / batch,
+            "kv_read_bytes_per_token": row * (CONTEXT + 1),
+            "kv_write_bytes_per_token": row,
+            "extra_bytes_per_token": cfg.vocab * 4 + cfg.hidden // 2 + cfg.hidden // 64 * 4}
+
+
+def phase_rooflines(dec: dict, probe: dict) -> dict:
+    """The reference's phase roofline diagnostic for each decode batch, fed with the
+    measured prefill and decode times and the GEMV probe's large-matrix bandwidth."""
+    from ironmule_amd.decode import DecoderConfig
+    from ironmule_amd.measure import phase_roofline_diagnostic
+
+    cfg = DecoderConfig()
+    prefill_ns = dec.get("prefill", {}).get("ns")
+    out = {}
+    for key, entry in dec.items():
+        if key == "prefill":
+            continue
+        b = int(key)
+        out[f"batch_{b}"] = phase_roofline_diagnostic(
+            prefill_ns=prefill_ns,
+            decode_ns=entry["seconds_per_step"] * entry["timed_steps"] * 1e9,
+            decode_steps=entry["timed_steps"] * b,
+            effective_bandwidth_gbps=probe.get("gemv_gbps_large"),
+            bandwidth_source="measure.gemv_gbps(262144, 1 GiB): streaming engine, "
+                             f"{probe.get('gemv_chain', {}).get('large')} distinct K=2560 "
+                             "weights per launch, cache flushed",
+            bandwidth_source_kind="measured_effective", **decode_traffic(cfg, b))
+    return out
+
+
+def host_cpu() -> dict:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo) and counts."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((line.split(":", 1)[1].strip() for line in f
+                          if line.lower().startswith("model name")), None)
+    except OSError:
+        pass
+    if model is None:
+        import subprocess
+        try:
+            text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+            model = next((line.split(":", 1)[1].strip() for line in text.splitlines()
+                          if line.lower().startswith("model name")), None)
+        except (OSError, subprocess.SubprocessError):
+            pass
+    return {"model": model, "logical_cpus": os.cpu_count(),
+            "usable_cpus": len(os.sched_getaffinity(0))}
+
+
+def cpu_dequantized_gemv(seconds: float):
+    """The reference's `dequantize` plan on the host (ironmule/numeric_plans.py:449-497):
+    every weight expanded once to dense fp32 (untimed, as at model load), then each
+    decode projection is an fp32 GEMV (numpy over OpenBLAS).  Rate in the metric's unit:
+    the same 4-bit bytes per layer as the qmv rows, over the time the fp32 GEMVs take."""
+    import numpy as np
+    import threadpoolctl
+
+    from oracle import oracle as orc
+
+    copies = []
+    for c in range(4):
+        layer = []
+        for i, (_, n, k) in enumerate(LAYER):
+            pr = orc.synthetic(n, k, 1, seed=SEED + 7 + c * 10 + i)
+            layer.append((orc.dequant_f32(pr.w, pr.s, pr.b),
+                          orc.bf16_to_f32(pr.x).reshape(-1).astype(np.float32)))
+        copies.append(layer)
+    step_bytes = sum(qmv_bytes(n, k, 1) for (_, n, k) in LAYER)
+    dense_bytes = sum(n * k * 4 for (_, n, k) in LAYER)
+    info = threadpoolctl.threadpool_info()
+    threads = max((p.get("num_threads", 1) for p in info if p.get("user_api") == "blas"),
+                  default=1)
+    for w, x in copies[0]:
+        w @ x
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for w, x in copies[done % 4]:
+            w @ x
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done * step_bytes / el / 1e9, 3), "unit": "GB/s",
+            "fp32_weight_gbs": round(done * dense_bytes / el / 1e9, 3), "cores": threads,
+            "sample": (f"{done} passes over one layer's 7 projections at batch 1, weights "
+                       f"pre-expanded to fp32 ({dense_bytes / 1e6:.0f} MB per layer, 4 "
+                       f"rotating copies), {el:.1f} s, numpy fp32 GEMV on OpenBLAS "
+                       f"({threads} threads); value counts the 4-bit bytes of the same work")}
 
 
 def cpu_baseline(seconds: float = 10.0):
@@ -369,6 +495,8 @@ def cpu_baseline(seconds: float = 10.0):
                    f"oracle restatement of the reference row kernel, {threads} OpenMP threads"),
         "single_thread_gbs": round(gbs1, 3),
         "single_thread_sample": f"{layers1} passes, {el1:.1f} s, 1 thread",
+        "host_cpu": host_cpu(),
+        "dequantize_fp32_gemv": cpu_dequantized_gemv(seconds / 2),
     }
 
 
@@ -493,6 +621,8 @@ def main() -> None:
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the full decode step")
+    ap.add_argument("--no-probe", action="store_true",
+                    help="skip the GEMV bandwidth probe (and with it the phase roofline)")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the full decode step and exit (a short program for profilers)")
     ap.add_argument("--no-breakdown", action="store_true",
@@ -605,6 +735,18 @@ def main() -> None:
                                       "151936-token head, 4-bit group-64 weights, GQA 32/8 "
                                       f"heads, {CONTEXT}-token KV context per request, one "
                                       "hip graph per step", **dec}
+    if not args.no_probe:
+        from ironmule_amd import measure
+        print("[bench] gemv bandwidth probe", file=sys.stderr, flush=True)
+        probe = measure.measure(repeats=5)
+        line["hardware"] = {k: probe[k] for k in (
+            "device_name", "peak_bandwidth_gbps", "dispatch_us", "gemv_gbps_small",
+            "gemv_gbps_large", "gemv_size_sensitivity", "gemv_frac_of_peak", "gemv_chain",
+            "cache_flushed", "repeats")}
+        line["hardware"]["gemv_gbps_small_warm"] = measure.gemv_gbps(
+            *measure.GEMV_SMALL, 5, flush=False)
+        if "decode" in line:
+            line["decode"]["phase_roofline"] = phase_rooflines(dec, probe)
     if not args.no_extra:
         print("[bench] secondary configs", file=sys.stderr, flush=True)
         line["configs"] = {

@@ -23,10 +23,17 @@ through the C ABI; there is no host fallback.
 `PersistentDecode` runs the same step at batch 1 as one persistent-kernel program
 (include/ironmule_step.h): the embedding launch, then one launch for all layers and the
 head, with bit-identical results.
+
+`prefill` runs a whole prompt through the same model at once, the library path a prompt
+takes (ironmule/cuda_native.py:171-179): every projection of more than 32 rows is
+imq_dequant to fp16 and one GEMM, attention is causal over the prompt in fp32, the KV
+pools of the request's slot are written for positions 0..T-1, and the head is computed
+for the last position only (ironmule/cuda_native.py:271-303, `head_skip_prefill`).
 """
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass, field
 
 import torch
@@ -208,3 +215,79 @@ class PersistentDecode:
 
     def failed(self) -> bool:
         return self.program.failed()
+
+
+# ------------------------------------------------------------------ prefill
+
+def _rms_norm(h: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """fp32 rows scaled to unit root-mean-square, times a bf16 weight, rounded to bf16."""
+    inv = torch.rsqrt(h.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (h * inv * weight.float()).to(torch.bfloat16)
+
+
+def _rotary(x: torch.Tensor, positions: torch.Tensor, theta: float) -> torch.Tensor:
+    """Non-interleaved rotary embedding of (T, H, D) fp32 rows: the pair (i, i + D/2) turns
+    by position * theta^(-2i/D), as the decode kernels apply it."""
+    half = x.shape[-1] // 2
+    freq = theta ** (-torch.arange(half, dtype=torch.float64, device=x.device) * 2.0 / x.shape[-1])
+    angle = positions.to(torch.float64)[:, None] * freq[None, :]
+    cos, sin = angle.cos().float()[:, None, :], angle.sin().float()[:, None, :]
+    lo, hi = x[..., :half], x[..., half:]
+    return torch.cat([lo * cos - hi * sin, lo * sin + hi * cos], dim=-1)
+
+
+def _project(x: torch.Tensor, quant: Quant, stream=None) -> torch.Tensor:
+    """bf16 rows times a 4-bit weight: the qmv kernel up to 32 rows, else imq_dequant to
+    fp16 and one GEMM (fp16 products, fp32 accumulation), rounded to bf16."""
+    w, s, b = quant
+    if x.shape[0] <= _native.MAX_ROWS:
+        return _native.qmv(w, s, b, x, stream=stream)
+    dense = _native.dequant(w, s, b, torch.float16, stream=stream)
+    return torch.matmul(x.to(torch.float16), dense.T).to(torch.bfloat16)
+
+
+def prefill(weights: DecoderWeights, state: DecodeState, tokens, slot: int,
+            stream=None) -> torch.Tensor:
+    """Runs the prompt `tokens` (positions 0..T-1) of one request through the model,
+    writes its keys and values into KV slot `slot` of `state`'s pools, and returns the
+    fp32 logits (vocab,) of the last position.  A decode step for this request then
+    continues at position T."""
+    c = weights.config
+    count = len(tokens)
+    if not 1 <= count <= state.max_len:
+        raise ValueError(f"a prompt holds 1 to {state.max_len} tokens, got {count}")
+    if not 0 <= slot < state.slots:
+        raise ValueError(f"slot must lie in [0, {state.slots})")
+    device = state.h.device
+    with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+        ids = torch.as_tensor(list(tokens), dtype=torch.int32).to(device)
+        h = torch.empty((count, c.hidden), dtype=torch.float32, device=device)
+        _native.embed(*weights.embed, ids, h, stream=stream)
+        positions = torch.arange(count, device=device)
+        causal = torch.ones((count, count), dtype=torch.bool, device=device).tril()
+        group = c.heads // c.kv_heads
+        for i, layer in enumerate(weights.layers):
+            x = _rms_norm(h, layer["input_norm"], c.eps)
+            q = _project(x, layer["q"], stream).float().view(count, c.heads, c.head_dim)
+            k = _project(x, layer["k"], stream).float().view(count, c.kv_heads, c.head_dim)
+            v = _project(x, layer["v"], stream).view(count, c.kv_heads, c.head_dim)
+            q = _rotary(_rms_norm(q, layer["q_norm"], c.eps).float(), positions, c.theta)
+            k = _rotary(_rms_norm(k, layer["k_norm"], c.eps).float(), positions, c.theta)
+            state.k_pool[i][slot, :, :count] = k.to(torch.bfloat16).transpose(0, 1)
+            state.v_pool[i][slot, :, :count] = v.transpose(0, 1)
+            # causal attention in fp32 over the bf16 q, keys and values
+            qh = q.to(torch.bfloat16).float().transpose(0, 1).contiguous()       # (H, T, D)
+            kh = state.k_pool[i][slot, :, :count].float().repeat_interleave(group, dim=0)
+            vh = state.v_pool[i][slot, :, :count].float().repeat_interleave(group, dim=0)
+            scores = torch.matmul(qh, kh.transpose(1, 2).contiguous()) * c.head_dim ** -0.5
+            scores = scores.masked_fill(~causal, float("-inf"))
+            attn = torch.matmul(torch.softmax(scores, dim=-1), vh)                 # (H, T, D)
+            attn = attn.transpose(0, 1).reshape(count, c.heads * c.head_dim).to(torch.bfloat16)
+            h = h + _project(attn, layer["o"], stream).float()
+            x = _rms_norm(h, layer["post_norm"], c.eps)
+            gate = _project(x, layer["gate"], stream).float()
+            up = _project(x, layer["up"], stream).float()
+            act = (torch.nn.functional.silu(gate) * up).to(torch.bfloat16)
+            h = h + _project(act, layer["down"], stream).float()
+        last = _rms_norm(h[-1:], weights.norm, c.eps)
+        return _native.qmv(*weights.embed, last, out_dtype=torch.float32, stream=stream)[0]
