@@ -1335,6 +1335,236 @@ __global__ __launch_bounds__(64 * xs::Shape<MB>::kWaves) void qmv_xs_kernel(XsAr
   }
 }
 
+// ------------------------------ MFMA kernel fed by direct-to-LDS weight loads (M >= 3)
+//
+// For launches with about one 64-row weight tile per CU (K = 3840 x 15360, the decoder
+// layer's gate/up): every workgroup owns 64 weight rows (two 32 x 32 MFMA tiles) over the
+// whole K, and each of its W wavefronts owns GMAX consecutive groups of them, so each
+// weight byte and each activation byte reaches a workgroup once.
+//   * Activations come prepared by xprep_kernel (once per distinct x of the launch): for
+//     each group g and k-step t the 64 lanes' 16-byte A operands of
+//     v_mfma_f32_32x32x16_bf16 are one contiguous KiB (lane (m, kb) holds x[m][64 g +
+//     8 (4 kb + t) ..+8] in pair order, rows m >= M zero), followed by every group's 32
+//     row sums in fp32.  A wavefront loads them straight into registers with whole-line
+//     loads, two groups ahead of its use.
+//   * Weights go from memory to LDS by the buffer loads' LDS path (16 bytes a lane): an
+//     instruction moves 8 rows x 128 bytes (four groups of a row: whole lines), lane l to
+//     LDS byte 16 l, piece c of row r stored at slot c ^ ((r >> 1) & 7) so that the reads
+//     in MFMA-operand order are free of bank conflicts.  Each wavefront issues every weight
+//     load of its groups at the start, one LDS array per four groups, so that the compiler's
+//     wait for a group's weights counts only the loads before them.
+//   * The workgroup's scales and biases (64 rows x K/64 groups, one contiguous block of
+//     each array) go to LDS the same way, 4 bytes a lane, first of all; one barrier
+//     publishes them.
+// Per group: P = sum_k v x from four bf16 MFMAs (v = 1 + q/16, exact), acc += 16 s * P; per
+// pair of groups one v_mfma_f32_32x32x2_f32 adds (b - 16 s) * sum x.  Groups past a
+// wavefront's range are not computed (their loads read valid bytes or zeros).  At the end
+// the wavefronts' accumulators are added in wavefront order (K order) through LDS and the
+// workgroup writes its 64 rows of y.  Requires K % 256 == 0, K <= 4096 and x rows 16-byte
+// aligned.
+#ifndef IMQ_DMA_XDEPTH
+#define IMQ_DMA_XDEPTH 8
+#endif
+namespace dm {
+constexpr int kRows = 64;                  // weight rows per workgroup
+constexpr int kChunkBytes = kRows * 128;   // a wavefront's four groups of the 64 rows
+constexpr int kXrGroup = 4096;             // prepared x per group
+constexpr int kXsGroup = 32 * 4;           // row sums per group
+constexpr int kMaxGroups = 64;             // K <= 4096
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+// s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9 encoding)
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+}  // namespace dm
+
+struct XprepArgs {
+  const uint16_t* x[kMaxProblems];
+  int64_t ldx[kMaxProblems];
+  char* dst[kMaxProblems];
+  int32_t K[kMaxProblems];
+  int32_t count;
+  int32_t M;
+};
+
+// One workgroup per (group, distinct x): thread (m, c) moves the 16 bytes x[m][64 g + 8 c ..]
+// to their A-operand slot in pair order, and the eight threads of a row add its sum.
+__global__ __launch_bounds__(256) void xprep_kernel(XprepArgs a) {
+  const int xi = blockIdx.y, g = blockIdx.x;
+  const int K = a.K[xi];
+  if (g >= K / 64) return;
+  const int tid = threadIdx.x, m = tid >> 3, c = tid & 7;
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (m < a.M) v = *reinterpret_cast<const uint4*>(a.x[xi] + m * a.ldx[xi] + 64 * g + 8 * c);
+  float sum = sum8(v);
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  char* d = a.dst[xi];
+  *reinterpret_cast<uint4*>(d + (size_t)(g * 4 + (c & 3)) * 1024 + (m + 32 * (c >> 2)) * 16) =
+      pair_order(v);
+  if (c == 0) reinterpret_cast<float*>(d + (size_t)(K / 64) * dm::kXrGroup)[g * 32 + m] = sum;
+}
+
+struct DmaArgs {
+  const char* xr[kMaxProblems];  // problem i's prepared x
+};
+
+template <int W, int GMAX>
+__global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d) {
+  constexpr int NC = GMAX / 4;  // LDS arrays of four groups per wavefront
+  static_assert(NC == 1 || NC == 2, "GMAX is 4 or 8");
+  constexpr int XD = IMQ_DMA_XDEPTH < GMAX ? IMQ_DMA_XDEPTH : GMAX;  // x groups in flight
+  __shared__ __attribute__((aligned(16))) char wb0[W * dm::kChunkBytes];
+  __shared__ __attribute__((aligned(16))) char wb1[NC > 1 ? W * dm::kChunkBytes : 16];
+  __shared__ __attribute__((aligned(16))) uint32_t sbl[dm::kRows * W * GMAX];
+  const int pi = blockIdx.y;
+  const Problem& P = a.p[pi];
+  const int N = P.N, K = P.K, M = a.M, G = K >> 6;
+  const int row0 = blockIdx.x * dm::kRows;
+  if (row0 >= N) return;  // past this problem's tiles
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, kb = lane >> 5;
+
+  // this wavefront's groups [g0, g0 + nw) of [gs0, gs1) = [0, G)
+  const int gs0 = 0, gs1 = G, Gs = G;
+  const int g0 = wave * GMAX;
+  const int nw = __builtin_amdgcn_readfirstlane(min(GMAX, max(0, gs1 - g0)));
+
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(P.w, (uint32_t)N * (uint32_t)(K >> 1));
+  const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.s, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(P.b, sb_bytes);
+  const uint32_t xs_base = (uint32_t)G * dm::kXrGroup;
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(d.xr[pi], xs_base + (uint32_t)G * dm::kXsGroup);
+
+  // 1. scales, then biases, of rows [row0, row0 + 64): Gs instructions of 64 dwords, dword
+  //    dd of an array at LDS dword array * 32 Gs + dd
+  {
+    const int hp = Gs >> 1;  // dwords per row and array
+    for (int i = wave; i < Gs; i += W) {
+      const int arr = i >= hp ? 1 : 0;
+      const int dd = (i - arr * hp) * 64 + lane;
+      const int r = dd / hp, pr = dd - r * hp;
+      const int row = row0 + r < N ? row0 + r : N - 1;
+      const uint32_t off = (uint32_t)row * (uint32_t)G * 2u + 2u * (uint32_t)gs0 + 4u * (uint32_t)pr;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          arr ? brs : srs, (__attribute__((address_space(3))) void*)(sbl + arr * 32 * Gs + (i - arr * hp) * 64),
+          4, off, 0, 0, 0);
+    }
+  }
+  // 2. weights: per four groups, 8 instructions of 8 rows x 128 bytes
+  auto load_w = [&](char* buf, int q) {
+#pragma unroll
+    for (int i8 = 0; i8 < 8; ++i8) {
+      const int r = 8 * i8 + (lane >> 3);
+      const int c = (lane & 7) ^ dm::swz(r);
+      int gg = g0 + 4 * q + (c >> 1);
+      gg = gg < gs1 ? gg : gs1 - 1;
+      const int row = row0 + r < N ? row0 + r : N - 1;
+      const uint32_t off = (uint32_t)row * (uint32_t)(K >> 1) + 32u * (uint32_t)gg + 16u * (uint32_t)(c & 1);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wrs, (__attribute__((address_space(3))) void*)(buf + wave * dm::kChunkBytes + i8 * 1024), 16, off,
+          0, 0, kNt);
+    }
+  };
+  // 3. prepared x of group gi (4 operands) and, for an even gi, the pair's row sums
+  struct XG {
+    uint4 v[4];
+    float sum;
+  };
+  auto load_x = [&](XG& xg, int gi) {
+    const int g = g0 + gi;
+    const uint32_t dead = g < gs1 ? 0u : kPastBuffer;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      xg.v[t] = load_b128(xrs, ((uint32_t)(g * 4 + t) * 1024u + 16u * (uint32_t)lane) | dead);
+    if ((gi & 1) == 0) {
+      const uint32_t dsum = g + kb < gs1 ? 0u : kPastBuffer;
+      xg.sum = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          xrs, (xs_base + 4u * (uint32_t)((g + kb) * 32 + j)) | dsum, 0, 0));
+    }
+  };
+
+  XG xq[GMAX];
+  __builtin_amdgcn_sched_barrier(0);  // the wait below counts the loads issued after these
+  load_w(wb0, 0);
+#pragma unroll
+  for (int gi = 0; gi < XD; ++gi) load_x(xq[gi], gi);
+  if (NC > 1) load_w(wb1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  // this wavefront's scales and biases have landed (the weight and x loads issued after
+  // them may not have); past the barrier every wavefront's have
+  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(8 * NC + 4 * XD + (XD + 1) / 2));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  const uint32_t one = in_vgpr(xs::kOne);
+  const f32x16_t zero = {};
+  f32x16_t acc[2] = {zero, zero}, accb[2] = {zero, zero};
+  uint32_t sp[2] = {0u, 0u}, bp[2] = {0u, 0u};
+  const int gl0 = g0 - gs0;  // this wavefront's first group within the split
+#pragma unroll
+  for (int gi = 0; gi < GMAX; ++gi) {
+    if (gi + XD < GMAX) load_x(xq[gi + XD], gi + XD);
+    if (gi < nw) {
+      const char* wb = (gi >> 2) ? wb1 : wb0;
+      const XG& xg = xq[gi];
+      bf16x8_t xa[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xa[t] = __builtin_bit_cast(bf16x8_t, xg.v[t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int r = 32 * t + j;
+        if ((gi & 1) == 0) {
+          const int gl = gl0 + gi;
+          sp[t] = sbl[r * (Gs >> 1) + (gl >> 1)];
+          bp[t] = sbl[32 * Gs + r * (Gs >> 1) + (gl >> 1)];
+        }
+        const int c = 2 * (gi & 3) + kb;
+        const uint4 wv = *reinterpret_cast<const uint4*>(
+            wb + wave * dm::kChunkBytes + (r >> 3) * 1024 + 16 * (8 * (r & 7) + (c ^ dm::swz(r))));
+        f32x16_t p = zero;
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[0], unpack16(wv.x, one), p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[1], unpack16(wv.y, one), p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[2], unpack16(wv.z, one), p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[3], unpack16(wv.w, one), p, 0, 0, 0);
+        const float s16 = 16.0f * __uint_as_float((gi & 1) ? (sp[t] & 0xffff0000u) : (sp[t] << 16));
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(s16, p[e], acc[t][e]);
+        // the pair's offset term once its second group is done (or at an unpaired last one)
+        if ((gi & 1) || gi + 1 == nw) {
+          const uint32_t sw = kb ? (sp[t] & 0xffff0000u) : (sp[t] << 16);
+          const uint32_t bw = kb ? (bp[t] & 0xffff0000u) : (bp[t] << 16);
+          float cg = fmaf(-16.0f, __uint_as_float(sw), __uint_as_float(bw));
+          cg = (kb && !(gi & 1)) ? 0.0f : cg;
+          accb[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xq[gi & ~1].sum, cg, accb[t], 0, 0, 0);
+        }
+      }
+    }
+  }
+  acc[0] += accb[0];
+  acc[1] += accb[1];
+
+  // the wavefronts' accumulators, added in wavefront order: wave w's slice of wb0 holds
+  // [tile][e][lane] floats (a wavefront without groups never waited for its weight loads
+  // into that slice: wait for them first)
+  wait_vmem();
+  float* red = reinterpret_cast<float*>(wb0);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[((wave * 2 + t) * 16 + e) * 64 + lane] = acc[t][e];
+  __syncthreads();
+  const int nl = tid & 63, t = nl >> 5, jn = nl & 31, n = row0 + nl;
+  for (int m = wave; m < M; m += W) {
+    const int h = (m >> 2) & 1, e = 4 * (m >> 3) + (m & 3);
+    float v = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < W; ++w2) v += red[((w2 * 2 + t) * 16 + e) * 64 + jn + 32 * h];
+    if (n < N) store_y(a, P, m, n, v);
+  }
+}
+
 // ------------------------------------------------------------------ dequantise
 //
 // One thread per packed word: eight outputs.  fp32 output is fl32(s*q + b), which is
@@ -1862,6 +2092,114 @@ hipError_t launch_xs(const XsArgs& x, const XsPlan& pl, hipStream_t stream) {
   }
 }
 
+// The direct-to-LDS kernel's plan: 64-row tiles over the whole K (K <= 4096), GMAX = 4
+// groups per wavefront for K <= 2048 (W = 2..8 wavefronts), else 8.  Each distinct x of the
+// launch is prepared once (xprep_kernel) into the workspace after the counter region.
+// Taken when the launch has IMQ_DMA_MIN_TILES to one tile per CU and M >= IMQ_DMA_MIN_ROWS:
+// measured on MI355X it is then ahead of the staged kernel (K = 3840 x 15360 at M = 32:
+// 17.8 against 19.4 us a call, the prepare kernel included; one 9728 x 2560 weight: 15.4
+// against about 17), while launches of fewer tiles (the q/k/v, o and down projections, which
+// the staged kernel splits over the K groups), of more tiles than CUs (a workgroup's LDS
+// holds one per CU, so the surplus runs as a second round: the 2 x 9728 x 2560 gate/up launch
+// of the batch-32 decode step lost 6 us) and M <= 4 (the few-row VALU tiles) are faster
+// elsewhere.  Not applicable: a pointer table, M > 32, K % 256 != 0, K > 4096, x rows not
+// 16-byte aligned, or offsets past 2 GiB.
+#ifndef IMQ_DMA_MIN_ROWS
+#define IMQ_DMA_MIN_ROWS 5
+#endif
+#ifndef IMQ_DMA_MIN_TILES
+#define IMQ_DMA_MIN_TILES 128
+#endif
+
+struct DmaPlan {
+  int waves = 0;
+  int gmax = 0;
+  int grid_x = 0;
+  int nx = 0;
+  int groups_max = 0;      // largest K / 64 of the launch
+  size_t x_stride = 0;     // workspace bytes per prepared x
+  size_t bytes = 0;        // workspace the plan uses
+  int xi[kMaxProblems];    // problem -> its prepared x
+  const uint16_t* x[kMaxProblems];
+  int64_t ldx[kMaxProblems];
+  int32_t kx[kMaxProblems];
+};
+
+bool plan_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
+  if (a.table || a.M < 3 || a.M > 32 || a.count < 1 || a.count > kMaxProblems) return false;
+  int tiles = 0, grid_x = 0, gmax = 0;
+  pl->nx = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const Problem& P = a.p[i];
+    if (P.K % 256 != 0 || P.K / 64 > dm::kMaxGroups || P.N < 1) return false;
+    if ((int64_t)P.N * (P.K / 2) >= ((int64_t)1 << 31)) return false;
+    if (P.ldx % 8 != 0 || !imq_rt::aligned(P.x, 16)) return false;
+    if (((int64_t)(a.M - 1) * P.ldy + P.N) * 4 >= ((int64_t)1 << 31)) return false;
+    int k = 0;
+    while (k < pl->nx && !(pl->x[k] == P.x && pl->ldx[k] == P.ldx && pl->kx[k] == P.K)) ++k;
+    if (k == pl->nx) {
+      pl->x[k] = P.x;
+      pl->ldx[k] = P.ldx;
+      pl->kx[k] = P.K;
+      ++pl->nx;
+    }
+    pl->xi[i] = k;
+    const int t = (P.N + dm::kRows - 1) / dm::kRows;
+    tiles += t;
+    grid_x = t > grid_x ? t : grid_x;
+    gmax = P.K / 64 > gmax ? P.K / 64 : gmax;
+  }
+  if (tiles < IMQ_DMA_MIN_TILES || tiles > cu_count) return false;
+  pl->gmax = gmax <= 32 ? 4 : 8;
+  int w = (gmax + pl->gmax - 1) / pl->gmax;
+  pl->waves = w <= 2 ? 2 : (w + 1) / 2 * 2;  // instantiated: 2, 4, 6, 8
+  pl->grid_x = grid_x;
+  pl->groups_max = gmax;
+  pl->x_stride = ((size_t)gmax * (dm::kXrGroup + dm::kXsGroup) + 255) / 256 * 256;
+  pl->bytes = kCounterBytes + (size_t)pl->nx * pl->x_stride;
+  return true;
+}
+
+template <int W, int GMAX>
+hipError_t launch_dma_w(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl, hipStream_t stream) {
+  hipLaunchKernelGGL((qmv_dma_kernel<W, GMAX>), dim3(pl.grid_x, a.count), dim3(64 * W), 0, stream, a, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_dma(const LaunchArgs& a, const DmaPlan& pl, void* ws, hipStream_t stream) {
+  char* base = static_cast<char*>(ws);
+  XprepArgs xp;
+  memset(&xp, 0, sizeof(xp));
+  for (int k = 0; k < pl.nx; ++k) {
+    xp.x[k] = pl.x[k];
+    xp.ldx[k] = pl.ldx[k];
+    xp.K[k] = pl.kx[k];
+    xp.dst[k] = base + kCounterBytes + (size_t)k * pl.x_stride;
+  }
+  xp.count = pl.nx;
+  xp.M = a.M;
+  hipLaunchKernelGGL(xprep_kernel, dim3(pl.groups_max, pl.nx), dim3(256), 0, stream, xp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  DmaArgs d;
+  memset(&d, 0, sizeof(d));
+  for (int i = 0; i < a.count; ++i) d.xr[i] = xp.dst[pl.xi[i]];
+  if (pl.gmax == 4) {
+    switch (pl.waves) {
+      case 2: return launch_dma_w<2, 4>(a, d, pl, stream);
+      case 4: return launch_dma_w<4, 4>(a, d, pl, stream);
+      case 6: return launch_dma_w<6, 4>(a, d, pl, stream);
+      default: return launch_dma_w<8, 4>(a, d, pl, stream);
+    }
+  }
+  switch (pl.waves) {
+    case 2: return launch_dma_w<2, 8>(a, d, pl, stream);
+    case 4: return launch_dma_w<4, 8>(a, d, pl, stream);
+    case 6: return launch_dma_w<6, 8>(a, d, pl, stream);
+    default: return launch_dma_w<8, 8>(a, d, pl, stream);
+  }
+}
+
 #ifndef IMQ_XS_MIN_ROWS
 #define IMQ_XS_MIN_ROWS 3
 #endif
@@ -1872,6 +2210,8 @@ size_t wanted_workspace(const LaunchArgs& a, int cu_count) {
   XsArgs x;
   XsPlan xp;
   if (a.M >= IMQ_XS_MIN_ROWS && plan_xs(a, cu_count, &x, &xp)) return 0;
+  DmaPlan dp;
+  if (a.M >= IMQ_DMA_MIN_ROWS && plan_dma(a, cu_count, &dp)) return dp.bytes;
   return plan_mma(a, (size_t)1 << 40, cu_count).bytes;
 }
 
@@ -1909,8 +2249,11 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* w
   bool big = false;
   for (int i = 0; i < a.count; ++i)
     big = big || (int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31);
+  DmaPlan dp;
   if (M >= IMQ_XS_MIN_ROWS && !big && plan_xs(a, dev->cu_count, &xa, &xp)) {
     e = launch_xs(xa, xp, stream);
+  } else if (M >= IMQ_DMA_MIN_ROWS && ws && plan_dma(a, dev->cu_count, &dp) && dp.bytes <= ws_bytes) {
+    e = launch_dma(a, dp, ws, stream);
   } else if (M == 1 && plan_m1(a, &m1)) {
     e = launch_m1_for(a, m1, stream);
   } else if (M == 2 && plan_m1(a, &m1) && launch_mr_for<2>(a, m1, stream, &e)) {

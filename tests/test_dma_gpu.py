@@ -1,0 +1,97 @@
+"""GPU parity of the direct-to-LDS MFMA kernel (qmv_dma_kernel, with its activation
+preparation xprep_kernel), through the C ABI.
+
+The launch plan takes it for M >= 5 when the launch has from 128 tiles of 64 weight rows
+(8192 rows over all its weights) to one tile per CU (256 on MI355X) and every K is a multiple
+of 256 up to 4096.  The shapes below cover its
+variants: K = 3840 x 15360 (8 groups per wavefront, eight wavefronts, the last one with four
+groups), K = 512 with a ragged last tile (four groups per wavefront, two wavefronts), K = 256
+(the second wavefront has no groups), K = 4096 (eight full wavefronts), K = 2304 (a part-full
+and an idle wavefront), two weights sharing one x and two weights with their own x.  Bars are
+the oracle's (check_bf16 and the literal bar / check_f32) on sampled rows, which include the
+ragged last tile; repeated calls give the same bits.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests.conftest import gpu_available
+from tests.gpu_util import announce, bf16_bits, to_device
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+
+
+@pytest.fixture(scope="module")
+def native():
+    from ironmule_amd import _native
+    code, arch, _ = _native.device_check()
+    assert code == 0, f"device {arch} is not supported"
+    return _native
+
+
+def _rows(n, step):
+    return np.unique(np.concatenate([np.arange(0, n, step), np.arange(max(0, n - 70), n)]))
+
+
+def _check(oracle, pr, y, rows, out_f32=False):
+    if out_f32:
+        ref, mag = oracle.qmv_f64(pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
+        v = oracle.check_f32(y.float().cpu().numpy()[:, rows], ref, mag)
+    else:
+        v, lit = oracle.check_bf16_both(bf16_bits(y)[:, rows], pr.w[rows], pr.s[rows], pr.b[rows], pr.x)
+        assert lit.ok, lit.detail
+    assert v.ok, v.detail
+
+
+@pytest.mark.parametrize("n,k,m,out_f32", [
+    (15360, 3840, 5, False), (15360, 3840, 8, False), (15360, 3840, 31, False),
+    (15360, 3840, 32, False), (15360, 3840, 32, True),
+    (8200, 512, 5, False), (8200, 512, 32, True),
+    (8192, 256, 16, False),
+    (8192, 4096, 32, True),
+    (8256, 2304, 7, False),
+])
+def test_single_weight_matches_oracle(native, oracle, n, k, m, out_f32):
+    pr = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 800 + m + k // 64)
+    w, s, b, x = to_device(pr)
+    announce("dma single", n, k, m, out_f32)
+    dtype = torch.float32 if out_f32 else torch.bfloat16
+    y = native.qmv(w, s, b, x, out_dtype=dtype)
+    y2 = native.qmv(w, s, b, x, out_dtype=dtype)
+    torch.cuda.synchronize()
+    _check(oracle, pr, y, _rows(n, 97), out_f32)
+    assert torch.equal(y, y2)
+
+
+def test_two_weights_share_one_x(native, oracle):
+    """Two 6144 x 2560 weights (96 tiles each), one x of 32 rows (prepared once), one
+    launch."""
+    m, n, k = 32, 6144, 2560
+    pg = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 850)
+    pu = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 851)
+    pu = oracle.Problem(pu.w, pu.s, pu.b, pg.x, 0)
+    wg, sg, bg, x = to_device(pg)
+    wu, su, bu, _ = to_device(pu)
+    announce("dma gate/up", m)
+    g, u = native.qmv_grouped([(wg, sg, bg), (wu, su, bu)], [x, x])
+    torch.cuda.synchronize()
+    rows = _rows(n, 89)
+    _check(oracle, pg, g, rows)
+    _check(oracle, pu, u, rows)
+
+
+def test_two_weights_with_their_own_x(native, oracle):
+    """Two 4096 x 1024 weights (64 tiles each), each with its own 9 activation rows: two
+    prepared x in the workspace."""
+    m = 9
+    prs = [oracle.synthetic(4096, 1024, m, seed=oracle.SEED_BASE + 860 + i) for i in range(2)]
+    dev = [to_device(pr) for pr in prs]
+    announce("dma two x", m)
+    outs = native.qmv_grouped([(w, s, b) for (w, s, b, _) in dev], [x for (*_, x) in dev])
+    torch.cuda.synchronize()
+    for pr, y in zip(prs, outs):
+        _check(oracle, pr, y, _rows(4096, 37))

@@ -1,5 +1,6 @@
 """GPU parity of imq_qmv_grouped_noalloc, the entry point that allocates nothing: its split
-partials and counters live in the library's static per-device scratch.  Through the C ABI,
+partials and counters, and the activations the direct-to-LDS kernel prepares, live in the
+library's static per-device scratch.  Through the C ABI,
 two calls in a row (the second smaller) must give the same bits as imq_qmv_grouped_ws with
 a caller workspace of imq_qmv_grouped_workspace bytes (the same plan), and meet the oracle's
 bar on sampled rows.  Outputs are bf16, so the bar against the other entry point is
@@ -78,8 +79,17 @@ def test_noalloc_matches_workspace_entry_twice(native, oracle):
     assert second < first
 
 
+def test_noalloc_prepared_x_twice(native, oracle):
+    """Launches of the direct-to-LDS kernel, whose prepared activations go to the scratch:
+    K = 3840 x 15360 at 8 rows, then a smaller call (8192 x 1024, 16 rows), both
+    bit-identical to imq_qmv_grouped_ws."""
+    first = _case(native, oracle, [(15360, 3840)], 8, oracle.SEED_BASE + 940)
+    second = _case(native, oracle, [(8192, 1024)], 16, oracle.SEED_BASE + 950)
+    assert first > second > 0
+
+
 def test_noalloc_without_split(native, oracle):
-    """Calls that need no workspace (one row; a wide launch) go through the same kernels
-    as the other entry points and never touch the scratch."""
+    """Calls that need no workspace (one row; a staged launch of 94 tiles) go through the
+    same kernels as the other entry points and never touch the scratch."""
     assert _case(native, oracle, [(2560, 2560)], 1, oracle.SEED_BASE + 920) == 0
-    assert _case(native, oracle, [(8192, 1024)], 16, oracle.SEED_BASE + 930) == 0
+    assert _case(native, oracle, [(6000, 512)], 16, oracle.SEED_BASE + 930) == 0
