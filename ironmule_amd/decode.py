@@ -291,3 +291,96 @@ def prefill(weights: DecoderWeights, state: DecodeState, tokens, slot: int,
             h = h + _project(act, layer["down"], stream).float()
         last = _rms_norm(h[-1:], weights.norm, c.eps)
         return _native.qmv(*weights.embed, last, out_dtype=torch.float32, stream=stream)[0]
+
+
+# ------------------------------------------------------------------ module form
+
+class KVCache:
+    """One request's keys and values for one layer: (kv_heads, capacity, head_dim) bf16, the
+    first `offset` positions filled."""
+
+    def __init__(self, kv_heads: int, capacity: int, head_dim: int, device) -> None:
+        self.keys = torch.zeros((kv_heads, capacity, head_dim), dtype=torch.bfloat16, device=device)
+        self.values = torch.zeros_like(self.keys)
+        self.offset = 0
+
+    @property
+    def capacity(self) -> int:
+        return int(self.keys.shape[1])
+
+    def update_and_fetch(self, k: torch.Tensor, v: torch.Tensor):
+        """Appends one position's (kv_heads, head_dim) key and value; returns the filled
+        keys and values (kv_heads, offset, head_dim)."""
+        if self.offset >= self.capacity:
+            raise ValueError(f"the cache holds {self.capacity} positions")
+        self.keys[:, self.offset] = k
+        self.values[:, self.offset] = v
+        self.offset += 1
+        return self.keys[:, :self.offset], self.values[:, :self.offset]
+
+
+class DecoderLayer(torch.nn.Module):
+    """One layer's 4-bit projections (QuantizedLinear over the layer's tensors) and norms."""
+
+    def __init__(self, layer: dict) -> None:
+        super().__init__()
+        from .quantized import QuantizedLinear
+        for name in ("q", "k", "v", "o", "gate", "up", "down"):
+            setattr(self, f"{name}_proj", QuantizedLinear(*layer[name]))
+        for name in ("input_norm", "post_norm", "q_norm", "k_norm"):
+            self.register_buffer(name, layer[name])
+
+
+class Decoder(torch.nn.Module):
+    """The decoder of `DecoderWeights` as modules: each projection a QuantizedLinear (its
+    forward is the library path: imq_qmv for a decode row), the tied 4-bit embedding and
+    head.  `step` decodes one token of one request over that request's KVCaches; the
+    composition is `ironmule_amd.paired.paired_forward`'s, which steps several requests."""
+
+    def __init__(self, weights: DecoderWeights) -> None:
+        super().__init__()
+        from .quantized import QuantizedEmbedding
+        self.config = weights.config
+        self.layers = torch.nn.ModuleList([DecoderLayer(layer) for layer in weights.layers])
+        self.embed_tokens = QuantizedEmbedding(*weights.embed)
+        self.register_buffer("norm", weights.norm)
+
+    def make_caches(self, capacity: int) -> list[KVCache]:
+        c = self.config
+        device = self.norm.device
+        return [KVCache(c.kv_heads, capacity, c.head_dim, device) for _ in range(c.layers)]
+
+    def embed(self, token: int) -> torch.Tensor:
+        """The token's embedding row, fp32 (1, hidden)."""
+        ids = torch.tensor([int(token)], dtype=torch.int32, device=self.norm.device)
+        h = torch.empty((1, self.config.hidden), dtype=torch.float32, device=self.norm.device)
+        e = self.embed_tokens
+        return _native.embed(e.weight, e.scales, e.biases, ids, h)
+
+    def attend(self, layer: DecoderLayer, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+               cache: KVCache) -> torch.Tensor:
+        """q/k norm, rotary at the cache's next position, the KV append and attention over
+        the cache, for one request's (1, ...) bf16 q, k, v; returns bf16 (1, heads * head_dim)."""
+        c = self.config
+        pos = torch.tensor([cache.offset], device=q.device)
+        qh = _rotary(_rms_norm(q.float().view(1, c.heads, c.head_dim), layer.q_norm, c.eps).float(),
+                     pos, c.theta).to(torch.bfloat16)
+        kh = _rotary(_rms_norm(k.float().view(1, c.kv_heads, c.head_dim), layer.k_norm, c.eps).float(),
+                     pos, c.theta).to(torch.bfloat16)
+        keys, values = cache.update_and_fetch(kh[0], v.view(c.kv_heads, c.head_dim))
+        group = c.heads // c.kv_heads
+        kf = keys.float().repeat_interleave(group, dim=0)                  # (H, L, D)
+        vf = values.float().repeat_interleave(group, dim=0)
+        scores = torch.matmul(kf, qh[0].float().unsqueeze(-1)).squeeze(-1) * c.head_dim ** -0.5
+        out = torch.matmul(torch.softmax(scores, dim=-1).unsqueeze(1), vf).squeeze(1)  # (H, D)
+        return out.reshape(1, c.heads * c.head_dim).to(torch.bfloat16)
+
+    def head(self, h: torch.Tensor) -> torch.Tensor:
+        """Final norm and the tied head: fp32 logits (vocab,)."""
+        e = self.embed_tokens
+        x = _rms_norm(h, self.norm, self.config.eps)
+        return _native.qmv(e.weight, e.scales, e.biases, x, out_dtype=torch.float32)[0]
+
+    def step(self, token: int, caches: list[KVCache]) -> torch.Tensor:
+        from .paired import paired_forward
+        return paired_forward(self, [token], [caches], share=False)[0]

@@ -22,3 +22,26 @@ def bf16_bits(t: torch.Tensor) -> np.ndarray:
 def announce(*parts) -> None:
     """Name the case before a GPU step, flushed, so a failure can be placed."""
     print("[gpu case]", *parts, flush=True)
+
+
+def oracle_decoder(do, orc, weights):
+    """The decode oracle's Model for a `decode.DecoderWeights` on the GPU: every projection
+    and the tied embedding dequantised to float64 by the oracle, norms widened from bf16."""
+    import numpy as np
+
+    def vals(t):
+        return t.float().cpu().numpy().astype(np.float64)
+
+    def deq(q):
+        w, s, b = (t.cpu() for t in q)
+        return orc.dequant_f32(w.numpy().view(np.uint32), s.view(torch.int16).numpy().view(np.uint16),
+                               b.view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+
+    c = weights.config
+    layers = [do.Layer(wq=deq(L["q"]), wk=deq(L["k"]), wv=deq(L["v"]), wo=deq(L["o"]),
+                       wg=deq(L["gate"]), wu=deq(L["up"]), wd=deq(L["down"]),
+                       input_norm=vals(L["input_norm"]), post_norm=vals(L["post_norm"]),
+                       q_norm=vals(L["q_norm"]), k_norm=vals(L["k_norm"]))
+              for L in weights.layers]
+    return do.Model(layers=layers, embed=deq(weights.embed), norm=vals(weights.norm),
+                    heads=c.heads, kv_heads=c.kv_heads, eps=c.eps, theta=c.theta)

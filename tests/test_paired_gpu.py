@@ -1,0 +1,90 @@
+"""GPU parity of the paired decode step (paired.paired_forward) and its scheduler, on a
+2-layer decoder with the layer shapes that put projections on the shared kernels: hidden
+3840 (q/k/v and gate/up take the shared K=3840 sweep), heads 32 x 128 (o is K=4096) and
+intermediate 15360 (down is K=15360: both aligned).
+
+Bars: two requests stepped together give the same logit bits with the sweeps shared, with
+them separate, and each request stepped alone (the shared kernels' results depend only on
+their own row); every step within max|logit - ref| / max|ref| <= 1e-2 of the decode oracle
+with the same bf16 rounding points (the decode step's bar); the scheduler's token streams
+are the same with and without sharing.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests.conftest import gpu_available
+from tests.gpu_util import announce, oracle_decoder
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+
+CAPACITY = 16
+
+
+@pytest.fixture(scope="module")
+def env():
+    from ironmule_amd import _native
+    from ironmule_amd.decode import Decoder, DecoderConfig, random_weights
+    from oracle import decode_oracle as do
+    from oracle import oracle as orc
+    code, arch, _ = _native.device_check()
+    assert code == 0, f"device {arch} is not supported"
+    orc.lib()
+    cfg = DecoderConfig(hidden=3840, layers=2, heads=32, kv_heads=8, head_dim=128,
+                        intermediate=15360, vocab=512, eps=1e-6, theta=1e6)
+    weights = random_weights(cfg, "cuda", seed=77)
+    return Decoder(weights), oracle_decoder(do, orc, weights), do
+
+
+def _rel(got, ref):
+    return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+def test_paired_step_matches_solo_steps_and_the_oracle(env):
+    from ironmule_amd.paired import paired_forward
+    model, omodel, do = env
+    shared = [model.make_caches(CAPACITY) for _ in range(2)]
+    apart = [model.make_caches(CAPACITY) for _ in range(2)]
+    solo = [model.make_caches(CAPACITY) for _ in range(2)]
+    keys = [np.zeros((2, 8, CAPACITY, 128)) for _ in range(2)]
+    values = [np.zeros_like(k) for k in keys]
+    tokens = [5, 300]
+    for step in range(3):
+        announce("paired step", step, tokens)
+        a = paired_forward(model, tokens, shared, share=True, share_aligned=True)
+        b = paired_forward(model, tokens, apart, share=False, share_aligned=True)
+        c = [model.step(t, caches) for t, caches in zip(tokens, solo)]
+        torch.cuda.synchronize()
+        ref = do.decode_step(omodel, keys, values, tokens, [0, 1], [step, step], round_bf16=True)
+        for r in range(2):
+            assert torch.equal(a[r], b[r]) and torch.equal(a[r], c[r]), (step, r)
+            got = a[r].cpu().numpy().astype(np.float64)
+            assert _rel(got, ref[r]) <= 1e-2, (step, r, _rel(got, ref[r]))
+        tokens = [int(torch.argmax(x)) for x in a]
+
+
+def test_scheduler_streams_agree_with_and_without_sharing(env):
+    from ironmule_amd.paired import PairedGroupedExecutor, Session
+    model, _, _ = env
+    streams = {}
+    for share in (True, False):
+        ex = PairedGroupedExecutor(model, share=share, share_aligned=share)
+        sessions = [Session(rid=str(i), tokens=[t], max_tokens=4, state=model.make_caches(CAPACITY))
+                    for i, t in enumerate([7, 411])]
+        announce("paired scheduler", share)
+        ex.run(sessions, CAPACITY)
+        assert ex.paired_steps == 3 and ex.solo_steps == 0
+        streams[share] = [s.tokens for s in sessions]
+    assert streams[True] == streams[False]
+    # a third request with its own capacity steps alone, the other two still pair
+    ex = PairedGroupedExecutor(model, share=True)
+    sessions = [Session(rid="a", tokens=[7], max_tokens=3, state=model.make_caches(CAPACITY)),
+                Session(rid="b", tokens=[411], max_tokens=3, state=model.make_caches(CAPACITY)),
+                Session(rid="c", tokens=[9], max_tokens=2, state=model.make_caches(8), capacity=8)]
+    ex.run(sessions, CAPACITY)
+    assert [s.tokens[:2] for s in sessions[:2]] == [t[:2] for t in streams[True]]
+    assert ex.solo_steps >= 1

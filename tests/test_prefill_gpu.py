@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from tests.conftest import gpu_available
-from tests.gpu_util import announce
+from tests.gpu_util import announce, oracle_decoder
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
@@ -37,21 +37,6 @@ def _vals(t):
     return t.float().cpu().numpy().astype(np.float64)
 
 
-def _oracle_model(torch, do, orc, weights):
-    def deq(q):
-        w, s, b = (t.cpu() for t in q)
-        return orc.dequant_f32(w.numpy().view(np.uint32), s.view(torch.int16).numpy().view(np.uint16),
-                               b.view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
-    c = weights.config
-    layers = [do.Layer(wq=deq(L["q"]), wk=deq(L["k"]), wv=deq(L["v"]), wo=deq(L["o"]),
-                       wg=deq(L["gate"]), wu=deq(L["up"]), wd=deq(L["down"]),
-                       input_norm=_vals(L["input_norm"]), post_norm=_vals(L["post_norm"]),
-                       q_norm=_vals(L["q_norm"]), k_norm=_vals(L["k_norm"]))
-              for L in weights.layers]
-    return do.Model(layers=layers, embed=deq(weights.embed), norm=_vals(weights.norm),
-                    heads=c.heads, kv_heads=c.kv_heads, eps=c.eps, theta=c.theta)
-
-
 def _rel(got, ref):
     return float(np.abs(got - ref).max() / np.abs(ref).max())
 
@@ -70,7 +55,7 @@ def test_prefill_matches_the_oracle_decoded_token_by_token(env, count):
     tokens = np.random.default_rng(count).integers(0, cfg.vocab, count).tolist()
     got = prefill(weights, state, tokens, slot).cpu().numpy().astype(np.float64)
 
-    model = _oracle_model(torch, do, orc, weights)
+    model = oracle_decoder(do, orc, weights)
     keys = [np.zeros((slots, cfg.kv_heads, cap, cfg.head_dim)) for _ in range(cfg.layers)]
     values = [np.zeros_like(k) for k in keys]
     for pos, tok in enumerate(tokens):
