@@ -74,6 +74,7 @@ constexpr size_t kSlotLds = 64 * 1024;  // LDS for those rows
 constexpr int kSbWords = 256;           // per wavefront: the span's scale halves, then at kBiasArea its bias halves
 constexpr int kBiasArea = 512;          // byte offset of the bias halves in the area
 constexpr int kDepth = 2;                // tiles in flight per wavefront (independent stages)
+constexpr int kShards = 16;              // claim counters (independent stages)
 
 // LDS bytes of one staged x row of K values: C = K/32 chunks of 80 bytes each, the
 // chunk's four words in pair order (64 bytes), its sum and -128 times its sum (8 bytes)
@@ -115,8 +116,13 @@ struct SArgs {
   uint32_t* counters;  // kSubs lines per stage
   uint32_t* status;
   const int32_t* run_site;  // independent stages: (stage << 2) | problem of each run's first tile
+  uint32_t* claim;          // independent stages: kShards claim counters, kLine words apart
   int32_t nstages, total, waves, sb_off;  // sb_off: LDS byte offset of the scale/bias areas
-  int32_t nslots, run, pad1[2];            // run: tiles per run (independent stages)
+  int32_t nslots, run;                     // run: tiles per static run (independent stages)
+  int32_t static_runs, runs;               // runs [0, static_runs) are dealt, the rest claimed
+  int32_t dyn_run, shards;                 // tiles per claimed run; claim counters in use
+  int32_t shard_lo[kShards + 1];           // shard s claims runs [shard_lo[s], shard_lo[s + 1])
+  int32_t shard_waves[kShards];            // wavefronts that claim from shard s
   XSlot slot[kMaxSlots];
 };
 
@@ -367,9 +373,29 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
 // (V wavefronts), so at any moment the device streams one compact window of the weights,
 // and a wavefront resolves a problem's descriptors once per run rather than once per
 // tile.  R (16 or a little more) is chosen so that the runs split the program evenly over
-// the wavefronts.  Its cursors only move forward.  kDepth tiles are in flight: the loads of a
-// wavefront's tile k + kDepth are issued as soon as its tile k has been computed.
+// the wavefronts.  Dealt runs cover whole rounds of the program's first tiles; the rest is
+// cut into runs of dyn_run tiles that the wavefronts claim one at a time from a counter
+// (an atomic add), so that the wavefronts that stream faster take more of them and all
+// finish together (measured on MI355X: with every run dealt, the last wavefronts of a
+// 20-layer launch ended 35 us after the median one; claiming the last 25% in runs of 8
+// tiles took that launch from 5.83 to 6.13 TB/s, while runs of 4 or 16 tiles and a 12%
+// share gained less).  The claimed runs are split between
+// `shards` counters, each on its own line (one counter serialises its atomic adds: 16K
+// claims on one counter cost a 20-layer launch 100 us); workgroup b claims from shard
+// (b / 8) % shards, so every shard is served by workgroups of all eight XCDs.  Each
+// wavefront makes exactly one claim past its shard's last run, so a shard's last claim is
+// number (its runs + its wavefronts - 1); the wavefront that receives it returns the
+// counter to zero for the next launch.  Its cursors only move forward.  kDepth tiles are in flight: the loads of a wavefront's tile
+// k + kDepth are issued as soon as its tile k has been computed; the load cursor claims the
+// runs and the compute cursor, kDepth tiles behind, takes them from a two-entry queue.
 constexpr int kRunTarget = 16;
+#ifndef IMQ_STREAM_DYN_RUN
+#define IMQ_STREAM_DYN_RUN 8
+#endif
+#ifndef IMQ_STREAM_DYN_PERCENT
+#define IMQ_STREAM_DYN_PERCENT 25
+#endif
+static_assert(IMQ_STREAM_DYN_RUN > kDepth, "a claimed run is longer than the cursors' distance");
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
   extern __shared__ uint4 smem_raw[];
@@ -378,17 +404,49 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int v = blockIdx.x * kWaves + wave;
   const int V = a.waves, total = a.total, R = a.run;
+  const int Rs = a.static_runs, Rend = a.runs, R2 = a.dyn_run;
   uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
   const uint32_t magic = in_vgpr(kMagic);
-  // a position in this wavefront's sequence of tiles: run r (global), tile t of the run
+  // a position in this wavefront's sequence of tiles: run r (global), tile t of the run; a
+  // run at or past Rend starts past the last tile
   struct Pos {
     int r, t;
   };
-  auto tile = [&](const Pos& p) { return p.r * R + p.t; };
-  auto step = [&](Pos& p) {
-    if (++p.t == R) {
-      p.t = 0;
+  auto start_of = [&](int r) { return r < Rs ? r * R : (r < Rend ? Rs * R + (r - Rs) * R2 : total); };
+  auto length_of = [&](int r) { return r < Rs ? R : R2; };
+  auto tile = [&](const Pos& p) { return start_of(p.r) + p.t; };
+  int qa = 0, qb = 0, qn = 0;  // runs the load cursor claimed that the compute cursor has not reached
+  const int shard = (blockIdx.x >> 3) % a.shards;
+  uint32_t* ctr = a.claim + shard * kLine;
+  const int lo = a.shard_lo[shard], count = a.shard_lo[shard + 1] - lo;
+  const uint32_t last_claim = (uint32_t)(count + a.shard_waves[shard] - 1);
+  auto claim = [&]() {
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old == last_claim && lane == 0) st_sc1(ctr, 0u);
+    return (int)old < count ? lo + (int)old : Rend;
+  };
+  auto step_load = [&](Pos& p) {
+    if (++p.t < length_of(p.r)) return;
+    p.t = 0;
+    if (p.r + V < Rs || Rs == Rend) {
+      p.r += V;  // the next dealt run (or, with nothing to claim, past the end)
+    } else if (p.r < Rend) {
+      p.r = claim();
+      if (qn == 0) qa = p.r; else qb = p.r;
+      ++qn;
+    }
+  };
+  auto step_compute = [&](Pos& p) {
+    if (++p.t < length_of(p.r)) return;
+    p.t = 0;
+    if (p.r + V < Rs || Rs == Rend) {
       p.r += V;
+    } else if (p.r < Rend) {
+      p.r = qa;
+      qa = qb;
+      --qn;
     }
   };
 
@@ -414,7 +472,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     const int g = tile(lpos);
     if (g < total) move(ls, lp, lc, g, lpos.r);
     load_site(lc, g, g < total, lane, t);
-    step(lpos);
+    step_load(lpos);
   };
 #pragma unroll
   for (int d = 0; d < kDepth; ++d) issue(T[d]);
@@ -435,7 +493,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
       const bool in = gd < total;
       move(cs, cp, cc, in ? gd : g0, in ? cpos.r : p0.r);
       compute_site(cc, in ? gd : g0, lane, T[d], smem, sbw, magic, in);
-      step(cpos);
+      step_compute(cpos);
       issue(T[d]);
     }
   }
@@ -681,8 +739,9 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
   p->lds = (size_t)p->args.sb_off + (size_t)kWaves * kSbWords * 4;
   const int nstages = (int)p->stages.size();
   p->counter_words = p->chained ? (int64_t)nstages * kSubs * kLine : 0;
-  if (hipMalloc(&p->d_words, (size_t)(p->counter_words + 1) * 4) != hipSuccess ||
-      hipMemset(p->d_words, 0, (size_t)(p->counter_words + 1) * 4) != hipSuccess) {
+  // the counters, the status word, and (each on a line of its own) the claim counters
+  const size_t words = (size_t)(p->counter_words + kLine + kShards * kLine);
+  if (hipMalloc(&p->d_words, words * 4) != hipSuccess || hipMemset(p->d_words, 0, words * 4) != hipSuccess) {
     free_stream(p);
     return fail(IMQ_ELAUNCH, "hipMalloc of the stream counters failed");
   }
@@ -712,6 +771,7 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
   p->grid = grid;
   p->args.counters = p->d_words;
   p->args.status = p->d_words + p->counter_words;
+  p->args.claim = p->d_words + p->counter_words + kLine;
   p->args.nstages = nstages;
   p->args.total = tiles;
   p->args.waves = grid * kWaves;
@@ -723,11 +783,33 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
     const int rounds = std::max(1, tiles / (V * kRunTarget));
     const int R = (tiles + V * rounds - 1) / (V * rounds);
     p->args.run = R;
-    const int nruns = (tiles + R - 1) / R;
+    // whole rounds dealt, the last IMQ_STREAM_DYN_PERCENT of the rounds (at least one, when
+    // there are two or more) claimed in runs of IMQ_STREAM_DYN_RUN tiles
+    int dealt = rounds;
+    if (rounds >= 2 && IMQ_STREAM_DYN_PERCENT > 0) {
+      const int claimed = std::max(1, (rounds * IMQ_STREAM_DYN_PERCENT + 50) / 100);
+      dealt = rounds - std::min(claimed, rounds - 1);
+    }
+    int static_runs = (tiles + R - 1) / R, nruns = static_runs, R2 = IMQ_STREAM_DYN_RUN;
+    if (dealt < rounds) {
+      static_runs = V * dealt;
+      nruns = static_runs + (tiles - static_runs * R + R2 - 1) / R2;
+    }
+    p->args.static_runs = static_runs;
+    p->args.runs = nruns;
+    p->args.dyn_run = R2;
+    // shards of the claimed runs: as many as there are groups of 8 workgroups (up to
+    // kShards), each with an equal share of the runs and the count of its wavefronts
+    const int shards = std::max(1, std::min(kShards, grid / 8));
+    p->args.shards = shards;
+    for (int k = 0; k <= shards; ++k)
+      p->args.shard_lo[k] = static_runs + (int)((int64_t)(nruns - static_runs) * k / shards);
+    for (int k = 0; k < shards; ++k) p->args.shard_waves[k] = 0;
+    for (int b = 0; b < grid; ++b) p->args.shard_waves[(b / 8) % shards] += kWaves;
     std::vector<int32_t> runs((size_t)nruns);
     int si = 0, pi = 0;
     for (int r = 0; r < nruns; ++r) {
-      const int g = r * R;
+      const int g = r < static_runs ? r * R : static_runs * R + (r - static_runs) * R2;
       while (g >= p->stages[si].first + p->stages[si].p[pi].tile_end) {
         if (pi + 1 < p->stages[si].nprob) {
           ++pi;
