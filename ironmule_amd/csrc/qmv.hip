@@ -12,14 +12,17 @@
 // The matching x values are therefore used in the pair order (x0,x4) (x1,x5) (x2,x6)
 // (x3,x7) of each word.  The offset is removed with the group's sum of x:
 //     s * sum (128+q) x  +  (b - 128 s) * sum x.
+// The MFMA kernels place q in mantissa bits 3..6 of bf16 1.0 instead (the value 1 + q/16,
+// same pair order): 16 s * sum (1 + q/16) x + (b - 16 s) * sum x, whose fp32 sums carry
+// terms near |x| rather than 128 |x| (an MFMA sum starts from zero, not from the offset).
 //
 // Kernels sharing that arithmetic:
 //   * qmv_m1_kernel / qmv_m1c_kernel / qmv_rows_kernel (one or two rows): v_dot2_f32_bf16
 //     chains, x staged once per workgroup in LDS already in pair order, each chain
 //     started at -128 * sum(x);
-//   * qmv_mma_kernel (3 to 32 rows): v_mfma_f32_32x32x16_bf16 with the activation rows
+//   * the MFMA kernels (3 to 32 rows): v_mfma_f32_32x32x16_bf16 with the activation rows
 //     as the A operand and 32 weight rows as the B operand, four MFMAs per group of 64,
-//     and four more against a ones operand that yield sum(x) per group.
+//     and the group's sums of x from MFMAs against a ones operand or prepared with x.
 //
 // Layout in HBM is the reference's own (row-major w (N, K/8) uint32, s and b (N, K/64)
 // bf16), so a caller passes its buffers unchanged.  One launch may serve up to
@@ -555,9 +558,22 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, t);
 }
 
-__device__ __forceinline__ bf16x8_t unpack_word(uint32_t u, uint32_t magic) {
-  u32x4_t t = {nibble_pair(u, 0, magic), nibble_pair(u, 1, magic), nibble_pair(u, 2, magic),
-               nibble_pair(u, 3, magic)};
+// The MFMA kernels' weight operand.  Word u's nibble pair (p, p + 4) as the bf16 pair
+// (1 + q_p/16, 1 + q_{p+4}/16), exact: with s v x summed for v = 1 + q/16, a group's
+// sum (s q + b) x = 16 s sum v x + (b - 16 s) sum x, and the fp32 sum of v x carries
+// terms within 2x of |x|, so its rounding stays near that of the direct sum (a 128 + q
+// operand would carry terms 128x larger into the same fp32 accumulator).
+// `one` must be in_vgpr(kNibOne).
+constexpr uint32_t kNibOne = 0x3f803f80u;   // bf16 pair (1.0, 1.0)
+constexpr uint32_t kNibMask = 0x00780078u;  // mantissa bits 3..6 of each half
+template <int P>
+__device__ __forceinline__ uint32_t nib16(uint32_t u, uint32_t one) {
+  const uint32_t t = P == 0 ? (u << 3) : (u >> (4 * P - 3));
+  return (t & kNibMask) | one;
+}
+
+__device__ __forceinline__ bf16x8_t unpack16(uint32_t u, uint32_t one) {
+  u32x4_t t = {nib16<0>(u, one), nib16<1>(u, one), nib16<2>(u, one), nib16<3>(u, one)};
   return __builtin_bit_cast(bf16x8_t, t);
 }
 
@@ -566,14 +582,14 @@ __device__ __forceinline__ bf16x8_t unpack_word(uint32_t u, uint32_t magic) {
 // A wavefront computes a 32 (activation rows) x 32 (weight rows) tile of y over its share
 // of the groups with v_mfma_f32_32x32x16_bf16, x as the A operand and the weights as the
 // B operand.  For a group of 64 values, lane (r = lane % 32, h = lane / 32) holds
-//   * 16 bytes of weight row r, words 4h .. 4h+3: word 4h+s (as nibble_pair bf16 pairs)
+//   * 16 bytes of weight row r, words 4h .. 4h+3: word 4h+s (as unpack16 bf16 pairs)
 //     is the lane's B operand of k-step s;
 //   * 64 bytes of activation row r, x[32h .. 32h+32): its piece s in pair order is the
 //     lane's A operand of k-step s.
 // So both operands come from one contiguous load each.  The output lane (n = lane % 32,
 // h) holds rows m = 8(i/4) + 4h + i%4 (i < 16) of column n, so a lane's scale and bias are
 // scalars.  Per group
-//     acc += s * P + (b - 128 s) * P1,
+//     acc += 16 s * P + (b - 16 s) * P1,
 // P1 being the four k-steps against a ones operand (the row sums of x over the group).
 // Rows m >= M read row M-1 and are never stored.
 //
@@ -629,7 +645,7 @@ __device__ __forceinline__ void mma_load(MmaStage<NT, GS>& st, __amdgpu_buffer_r
 
 template <int NT, int GS>
 __device__ __forceinline__ void mma_compute(const MmaStage<NT, GS>& st, int g, int g1,
-                                            f32x16_t (&acc)[NT], uint32_t magic) {
+                                            f32x16_t (&acc)[NT], uint32_t one) {
   const u32x4_t ones_u = {kOnes, kOnes, kOnes, kOnes};
   const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
   const f32x16_t zero = {};
@@ -649,11 +665,12 @@ __device__ __forceinline__ void mma_compute(const MmaStage<NT, GS>& st, int g, i
       f32x16_t p = zero;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], unpack_word(wd[s], magic), p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], unpack16(wd[s], one), p, 0, 0, 0);
       const float sc = bf16_bits_to_f32(st.s[i][t]);
-      const float c = fmaf(-128.0f, sc, bf16_bits_to_f32(st.b[i][t]));
+      const float c = fmaf(-16.0f, sc, bf16_bits_to_f32(st.b[i][t]));
+      const float s16 = 16.0f * sc;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(sc, p[e], fmaf(c, p1[e], acc[t][e]));
+      for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(s16, p[e], fmaf(c, p1[e], acc[t][e]));
     }
   }
 }
@@ -747,7 +764,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, h = lane >> 5;
-  const uint32_t magic = in_vgpr(kMagic);
+  const uint32_t one = in_vgpr(kNibOne);
 
   // this workgroup's groups, and this wavefront's quarter of them
   const int gs0 = (G * split) / splits, gs1 = (G * (split + 1)) / splits;
@@ -773,10 +790,10 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
   mma_load<NT, kMmaStage>(sa, wrsrc, srsrc, brsrc, woff, sboff, xr, g0, g1 > g0 ? g1 : g0 + 1);
   for (int g = g0; g < g1; g += 2 * kMmaStage) {
     mma_load<NT, kMmaStage>(sb, wrsrc, srsrc, brsrc, woff, sboff, xr, g + kMmaStage, g1);
-    mma_compute<NT, kMmaStage>(sa, g, g1, acc, magic);
+    mma_compute<NT, kMmaStage>(sa, g, g1, acc, one);
     if (g + kMmaStage >= g1) break;
     mma_load<NT, kMmaStage>(sa, wrsrc, srsrc, brsrc, woff, sboff, xr, g + 2 * kMmaStage, g1);
-    mma_compute<NT, kMmaStage>(sb, g + kMmaStage, g1, acc, magic);
+    mma_compute<NT, kMmaStage>(sb, g + kMmaStage, g1, acc, one);
   }
 
   // add the four quarters in order: waves 1..3 park theirs, wave 0 adds
@@ -811,8 +828,8 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
 // barrier on each side.  Rows m >= M read row M-1 and are never stored; groups past a
 // K-range read zero (buffer offsets past the end).  The bias term is one fp32 MFMA
 // (v_mfma_f32_32x32x2_f32) per pair of groups: A = the two groups' row sums of x, B = the
-// two groups' c = b - 128 s per weight row.  Requires K % 256 == 0 and x rows at
-// x + m * ldx (no row-pointer table).
+// two groups' c = b - 16 s per weight row; the weights enter the MFMAs as 1 + q/16.
+// Requires K % 256 == 0 and x rows at x + m * ldx (no row-pointer table).
 namespace staged {
 constexpr int kWN = 2, kWK = 2;                   // wavefronts along N and along K
 constexpr int kRows = 32 * kWN;                   // weight rows per workgroup
@@ -848,7 +865,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int wn = wave % kWN, wk = wave / kWN;
   const int r = lane & 31, h = lane >> 5;
-  const uint32_t magic = in_vgpr(kMagic);
+  const uint32_t one = in_vgpr(kNibOne);
 
   // the split's groups (whole stages), then the two K-ranges of whole stages
   const int gs0 = (G * split) / splits / 4 * 4;
@@ -951,13 +968,14 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
       f32x16_t pp = zero;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        pp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[s], unpack_word(wd[s], magic), pp, 0, 0, 0);
+        pp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[s], unpack16(wd[s], one), pp, 0, 0, 0);
       const uint32_t sw = gi < 2 ? s2.x : s2.y, bw = gi < 2 ? b2.x : b2.y;
       const float sc = __uint_as_float((gi & 1) ? (sw & 0xffff0000u) : (sw << 16));
       const float bb = __uint_as_float((gi & 1) ? (bw & 0xffff0000u) : (bw << 16));
-      const float cg = fmaf(-128.0f, sc, bb);
+      const float cg = fmaf(-16.0f, sc, bb);
+      const float s16 = 16.0f * sc;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = fmaf(sc, pp[e], acc[e]);
+      for (int e = 0; e < 16; ++e) acc[e] = fmaf(s16, pp[e], acc[e]);
       if (gi & 1)  // lanes h = 0 / 1 carry the pair's first / second group
         accb = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? p1[0] : spair, h ? cg : cpair, accb, 0, 0, 0);
       else {
@@ -1000,9 +1018,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
 //     sum (s q + b) x  =  16 s * sum v x  +  (b - 16 s) * sum x,
 // the first term from two bf16 MFMAs per (m-block, n-block) and one fp32 multiply-add
 // per output, the second from one v_mfma_f32_16x16x4_f32 per block of four groups (A =
-// the rows' sums of x over the four groups, B = b - 16 s per weight row).  Against the
-// 128 + q form the offset term is 8x smaller next to the signal, and so is the fp32
-// rounding it brings.
+// the rows' sums of x over the four groups, B = b - 16 s per weight row).
 //
 // Per tile every wavefront parks its partial in LDS and the workgroup adds them in
 // wavefront order (the same bits on every run).  Each tile's scales and biases are staged
@@ -1016,8 +1032,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
 // scales read as zero).  Requires K % 256 == 0 and K <= 4096.
 namespace xs {
 constexpr int kRows = 32;                 // weight rows per tile (two 16-row n-blocks)
-constexpr uint32_t kOne = 0x3f803f80u;    // bf16 pair (1.0, 1.0)
-constexpr uint32_t kQMask = 0x00780078u;  // mantissa bits 3..6 of each half
+constexpr uint32_t kOne = kNibOne;
 template <int MB>
 struct Shape {
   static constexpr int kWaves = MB == 1 ? 16 : 8;   // wavefronts per workgroup
@@ -1054,19 +1069,6 @@ struct XsArgs {
   int32_t y_f32;
   int32_t scs;        // LDS row stride of the staged scales/biases (odd, >= every Gs)
 };
-
-// Word u's nibble pair (p, p + 4) as the bf16 pair (1 + q_p/16, 1 + q_{p+4}/16).
-// `one` must be in_vgpr(xs::kOne).
-template <int P>
-__device__ __forceinline__ uint32_t nib16(uint32_t u, uint32_t one) {
-  const uint32_t t = P == 0 ? (u << 3) : (u >> (4 * P - 3));
-  return (t & xs::kQMask) | one;
-}
-
-__device__ __forceinline__ bf16x8_t unpack16(uint32_t u, uint32_t one) {
-  u32x4_t t = {nib16<0>(u, one), nib16<1>(u, one), nib16<2>(u, one), nib16<3>(u, one)};
-  return __builtin_bit_cast(bf16x8_t, t);
-}
 
 // Stores issued from inline assembly, so the compiler's wait-count model does not see
 // them.  Inside a loop that keeps loads in flight from one iteration to the next, a store
@@ -1335,42 +1337,49 @@ __global__ __launch_bounds__(64 * xs::Shape<MB>::kWaves) void qmv_xs_kernel(XsAr
   }
 }
 
-// ------------------------------ MFMA kernel fed by direct-to-LDS weight loads (M >= 3)
+// ------------------------------ MFMA kernel fed by direct-to-LDS weight loads (M >= 5)
 //
-// For launches with about one 64-row weight tile per CU (K = 3840 x 15360, the decoder
-// layer's gate/up): every workgroup owns 64 weight rows (two 32 x 32 MFMA tiles) over the
-// whole K, and each of its W wavefronts owns GMAX consecutive groups of them, so each
-// weight byte and each activation byte reaches a workgroup once.
+// Every workgroup owns 64 weight rows (two 32 x 32 MFMA tiles) over a K-range of whole
+// groups (the whole K, or one of SPLITS ranges of four-group multiples), and each of its W
+// wavefronts owns GMAX consecutive groups of that range, so each weight byte and each
+// activation byte reaches a workgroup once.
 //   * Activations come prepared by xprep_kernel (once per distinct x of the launch): for
 //     each group g and k-step t the 64 lanes' 16-byte A operands of
 //     v_mfma_f32_32x32x16_bf16 are one contiguous KiB (lane (m, kb) holds x[m][64 g +
 //     8 (4 kb + t) ..+8] in pair order, rows m >= M zero), followed by every group's 32
 //     row sums in fp32.  A wavefront loads them straight into registers with whole-line
-//     loads, two groups ahead of its use.
+//     loads, IMQ_DMA_XDEPTH groups ahead of their use.
 //   * Weights go from memory to LDS by the buffer loads' LDS path (16 bytes a lane): an
 //     instruction moves 8 rows x 128 bytes (four groups of a row: whole lines), lane l to
 //     LDS byte 16 l, piece c of row r stored at slot c ^ ((r >> 1) & 7) so that the reads
-//     in MFMA-operand order are free of bank conflicts.  Each wavefront issues every weight
-//     load of its groups at the start, one LDS array per four groups, so that the compiler's
-//     wait for a group's weights counts only the loads before them.
-//   * The workgroup's scales and biases (64 rows x K/64 groups, one contiguous block of
-//     each array) go to LDS the same way, 4 bytes a lane, first of all; one barrier
+//     in MFMA-operand order are free of bank conflicts.  One LDS array per four groups: the
+//     first four groups' weights are loaded at the start, the next four while the first
+//     group is computed, so that a wavefront is not held at issue by loads it needs late
+//     (every wavefront of a CU issuing its whole range at once kept the CU's first
+//     computation waiting for most of the launch's traffic).
+//   * The workgroup's scales and biases (64 rows x the range's groups, one contiguous block
+//     of each array) go to LDS the same way, 4 bytes a lane, first of all; one barrier
 //     publishes them.
 // Per group: P = sum_k v x from four bf16 MFMAs (v = 1 + q/16, exact), acc += 16 s * P; per
 // pair of groups one v_mfma_f32_32x32x2_f32 adds (b - 16 s) * sum x.  Groups past a
 // wavefront's range are not computed (their loads read valid bytes or zeros).  At the end
-// the wavefronts' accumulators are added in wavefront order (K order) through LDS and the
-// workgroup writes its 64 rows of y.  Requires K % 256 == 0, K <= 4096 and x rows 16-byte
-// aligned.
+// the wavefronts' accumulators are added in wavefront order (K order) through LDS.  Without
+// splits the workgroup writes its 64 rows of y.  With splits it writes an fp32 partial of
+// them, and the last split of the tile to finish (a counter per tile in the caller's
+// workspace) adds the partials in split order, writes y and returns the counter to zero
+// (the same bits whatever order the splits finish in; partials and counters through sc1
+// accesses, coherent across the XCDs' L2 caches).  Requires K % 256 == 0, a range of at
+// most 64 groups and x rows 16-byte aligned.
 #ifndef IMQ_DMA_XDEPTH
-#define IMQ_DMA_XDEPTH 8
+#define IMQ_DMA_XDEPTH 2
 #endif
 namespace dm {
 constexpr int kRows = 64;                  // weight rows per workgroup
 constexpr int kChunkBytes = kRows * 128;   // a wavefront's four groups of the 64 rows
 constexpr int kXrGroup = 4096;             // prepared x per group
 constexpr int kXsGroup = 32 * 4;           // row sums per group
-constexpr int kMaxGroups = 64;             // K <= 4096
+constexpr int kMaxGroups = 64;             // groups of a workgroup's K-range
+constexpr int kMaxSplits = 16;             // K-ranges of a tile
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 // s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9 encoding)
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
@@ -1406,9 +1415,15 @@ __global__ __launch_bounds__(256) void xprep_kernel(XprepArgs a) {
 
 struct DmaArgs {
   const char* xr[kMaxProblems];  // problem i's prepared x
+  float* partial;                // split partials: problem i at partial + i * pstride
+  uint32_t* counters;            // per (problem, tile) arrival counters, zero between calls
+  int64_t pstride;
+  int32_t splits;                // K-ranges per tile (1: no partials)
+  int32_t range;                 // groups per K-range (a multiple of 4)
+  int32_t tiles_max;             // counters per problem
 };
 
-template <int W, int GMAX>
+template <int W, int GMAX, bool SPLIT>
 __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d) {
   constexpr int NC = GMAX / 4;  // LDS arrays of four groups per wavefront
   static_assert(NC == 1 || NC == 2, "GMAX is 4 or 8");
@@ -1416,18 +1431,24 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   __shared__ __attribute__((aligned(16))) char wb0[W * dm::kChunkBytes];
   __shared__ __attribute__((aligned(16))) char wb1[NC > 1 ? W * dm::kChunkBytes : 16];
   __shared__ __attribute__((aligned(16))) uint32_t sbl[dm::kRows * W * GMAX];
+  __shared__ int last;
   const int pi = blockIdx.y;
   const Problem& P = a.p[pi];
   const int N = P.N, K = P.K, M = a.M, G = K >> 6;
-  const int row0 = blockIdx.x * dm::kRows;
+  const int splits = SPLIT ? d.splits : 1;
+  const int tile = SPLIT ? (int)blockIdx.x / splits : (int)blockIdx.x;
+  const int split = SPLIT ? (int)blockIdx.x - tile * splits : 0;
+  const int row0 = tile * dm::kRows;
   if (row0 >= N) return;  // past this problem's tiles
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 31, kb = lane >> 5;
 
-  // this wavefront's groups [g0, g0 + nw) of [gs0, gs1) = [0, G)
-  const int gs0 = 0, gs1 = G, Gs = G;
-  const int g0 = wave * GMAX;
+  // this workgroup's K-range [gs0, gs1) and this wavefront's groups [g0, g0 + nw) of it
+  const int gs0 = SPLIT ? split * d.range : 0;
+  const int gs1 = SPLIT ? min(G, gs0 + d.range) : G;
+  const int Gs = gs1 - gs0;
+  const int g0 = gs0 + wave * GMAX;
   const int nw = __builtin_amdgcn_readfirstlane(min(GMAX, max(0, gs1 - g0)));
 
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(P.w, (uint32_t)N * (uint32_t)(K >> 1));
@@ -1437,8 +1458,8 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   const uint32_t xs_base = (uint32_t)G * dm::kXrGroup;
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(d.xr[pi], xs_base + (uint32_t)G * dm::kXsGroup);
 
-  // 1. scales, then biases, of rows [row0, row0 + 64): Gs instructions of 64 dwords, dword
-  //    dd of an array at LDS dword array * 32 Gs + dd
+  // 1. scales, then biases, of rows [row0, row0 + 64) over the range: Gs instructions of 64
+  //    dwords, dword dd of an array at LDS dword array * 32 Gs + dd
   {
     const int hp = Gs >> 1;  // dwords per row and array
     for (int i = wave; i < Gs; i += W) {
@@ -1490,11 +1511,10 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   load_w(wb0, 0);
 #pragma unroll
   for (int gi = 0; gi < XD; ++gi) load_x(xq[gi], gi);
-  if (NC > 1) load_w(wb1, 1);
   __builtin_amdgcn_sched_barrier(0);
   // this wavefront's scales and biases have landed (the weight and x loads issued after
   // them may not have); past the barrier every wavefront's have
-  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(8 * NC + 4 * XD + (XD + 1) / 2));
+  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(8 + 4 * XD + (XD + 1) / 2));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
@@ -1502,10 +1522,11 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   const f32x16_t zero = {};
   f32x16_t acc[2] = {zero, zero}, accb[2] = {zero, zero};
   uint32_t sp[2] = {0u, 0u}, bp[2] = {0u, 0u};
-  const int gl0 = g0 - gs0;  // this wavefront's first group within the split
+  const int gl0 = g0 - gs0;  // this wavefront's first group within the range
 #pragma unroll
   for (int gi = 0; gi < GMAX; ++gi) {
     if (gi + XD < GMAX) load_x(xq[gi + XD], gi + XD);
+    if (NC > 1 && gi == 1) load_w(wb1, 1);  // the next four groups, behind the first x
     if (gi < nw) {
       const char* wb = (gi >> 2) ? wb1 : wb0;
       const XG& xg = xq[gi];
@@ -1555,14 +1576,73 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
 #pragma unroll
     for (int e = 0; e < 16; ++e) red[((wave * 2 + t) * 16 + e) * 64 + lane] = acc[t][e];
   __syncthreads();
+  // thread (wave, nl) adds rows m = wave, wave + W, ... of tile row nl; every LDS read before
+  // the first store
+  constexpr int MI = (32 + W - 1) / W;
   const int nl = tid & 63, t = nl >> 5, jn = nl & 31, n = row0 + nl;
-  for (int m = wave; m < M; m += W) {
+  float sums[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int m = min(wave + i * W, 31);
     const int h = (m >> 2) & 1, e = 4 * (m >> 3) + (m & 3);
     float v = 0.0f;
 #pragma unroll
     for (int w2 = 0; w2 < W; ++w2) v += red[((w2 * 2 + t) * 16 + e) * 64 + jn + 32 * h];
-    if (n < N) store_y(a, P, m, n, v);
+    sums[i] = v;
   }
+  if (!SPLIT) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = wave + i * W;
+      if (m < M && n < N) store_y(a, P, m, n, sums[i]);
+    }
+    return;
+  }
+  // split: park the partial, count the tile's arrivals; the last one adds them in order
+  const __amdgpu_buffer_rsrc_t prs =
+      buffer_rsrc(d.partial + pi * d.pstride, (uint32_t)((int64_t)splits * M * N * 4));
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int m = wave + i * W;
+    if (m < M && n < N)
+      store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(sums[i]));
+  }
+  wait_vmem();
+  __syncthreads();
+  uint32_t* cnt = d.counters + (int64_t)pi * d.tiles_max + tile;
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (uint32_t)(splits - 1);
+  __syncthreads();
+  if (!last) return;
+  // four partials of each output in flight at a time, added in split order
+  const uint32_t step = (uint32_t)(M * N * 4);
+  float tot[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) tot[i] = 0.0f;
+  for (int q0 = 0; q0 < splits; q0 += 4) {
+    float v[MI][4];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = wave + i * W;
+      const bool in = m < M && n < N;
+      const uint32_t o = (uint32_t)((m * N + n) * 4) + (uint32_t)q0 * step;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[i][q] = __uint_as_float(load_b32_sc1(prs, in && q0 + q < splits ? o + q * step : kPastBuffer));
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q0 + q < splits) tot[i] += v[i][q];
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int m = wave + i * W;
+    if (m < M && n < N) store_y(a, P, m, n, tot[i]);
+  }
+  if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
 }
 
 // ------------------------------------------------------------------ dequantise
@@ -2092,32 +2172,28 @@ hipError_t launch_xs(const XsArgs& x, const XsPlan& pl, hipStream_t stream) {
   }
 }
 
-// The direct-to-LDS kernel's plan: 64-row tiles over the whole K (K <= 4096), GMAX = 4
-// groups per wavefront for K <= 2048 (W = 2..8 wavefronts), else 8.  Each distinct x of the
-// launch is prepared once (xprep_kernel) into the workspace after the counter region.
-// Taken when the launch has IMQ_DMA_MIN_TILES to one tile per CU and M >= IMQ_DMA_MIN_ROWS:
-// measured on MI355X it is then ahead of the staged kernel (K = 3840 x 15360 at M = 32:
-// 17.8 against 19.4 us a call, the prepare kernel included; one 9728 x 2560 weight: 15.4
-// against about 17), while launches of fewer tiles (the q/k/v, o and down projections, which
-// the staged kernel splits over the K groups), of more tiles than CUs (a workgroup's LDS
-// holds one per CU, so the surplus runs as a second round: the 2 x 9728 x 2560 gate/up launch
-// of the batch-32 decode step lost 6 us) and M <= 4 (the few-row VALU tiles) are faster
-// elsewhere.  Not applicable: a pointer table, M > 32, K % 256 != 0, K > 4096, x rows not
-// 16-byte aligned, or offsets past 2 GiB.
+// The direct-to-LDS kernel's plan.  64-row tiles; the groups of a tile split into K-ranges
+// (multiples of four groups, at most 64) so that the launch has about DMA_WG_PER_CU
+// workgroups per CU, GMAX = 4 groups per wavefront for ranges up to 32 groups, else 8, and
+// W = range / GMAX wavefronts.  Each distinct x of the launch is prepared once
+// (xprep_kernel) into the workspace after the counter region; the split partials follow.
+// Not applicable: a pointer table, M outside [3, 32], K % 256 != 0, problems of different K
+// with splits, x rows not 16-byte aligned, offsets past 2 GiB, or more tile counters than
+// the counter region holds.
 #ifndef IMQ_DMA_MIN_ROWS
 #define IMQ_DMA_MIN_ROWS 5
-#endif
-#ifndef IMQ_DMA_MIN_TILES
-#define IMQ_DMA_MIN_TILES 128
 #endif
 
 struct DmaPlan {
   int waves = 0;
   int gmax = 0;
-  int grid_x = 0;
+  int grid_x = 0;          // tiles of the largest problem
+  int splits = 1;
+  int range = 0;           // groups per K-range
   int nx = 0;
   int groups_max = 0;      // largest K / 64 of the launch
   size_t x_stride = 0;     // workspace bytes per prepared x
+  size_t pstride = 0;      // partial floats per problem
   size_t bytes = 0;        // workspace the plan uses
   int xi[kMaxProblems];    // problem -> its prepared x
   const uint16_t* x[kMaxProblems];
@@ -2125,13 +2201,15 @@ struct DmaPlan {
   int32_t kx[kMaxProblems];
 };
 
+int dma_splits(int tiles, int groups, int cu_count);
+
 bool plan_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
   if (a.table || a.M < 3 || a.M > 32 || a.count < 1 || a.count > kMaxProblems) return false;
-  int tiles = 0, grid_x = 0, gmax = 0;
+  int tiles = 0, grid_x = 0, gmax = 0, gmin = 1 << 30, nmax = 0;
   pl->nx = 0;
   for (int i = 0; i < a.count; ++i) {
     const Problem& P = a.p[i];
-    if (P.K % 256 != 0 || P.K / 64 > dm::kMaxGroups || P.N < 1) return false;
+    if (P.K % 256 != 0 || P.N < 1) return false;
     if ((int64_t)P.N * (P.K / 2) >= ((int64_t)1 << 31)) return false;
     if (P.ldx % 8 != 0 || !imq_rt::aligned(P.x, 16)) return false;
     if (((int64_t)(a.M - 1) * P.ldy + P.N) * 4 >= ((int64_t)1 << 31)) return false;
@@ -2148,22 +2226,68 @@ bool plan_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
     tiles += t;
     grid_x = t > grid_x ? t : grid_x;
     gmax = P.K / 64 > gmax ? P.K / 64 : gmax;
+    gmin = P.K / 64 < gmin ? P.K / 64 : gmin;
+    nmax = P.N > nmax ? P.N : nmax;
   }
-  if (tiles < IMQ_DMA_MIN_TILES || tiles > cu_count) return false;
-  pl->gmax = gmax <= 32 ? 4 : 8;
-  int w = (gmax + pl->gmax - 1) / pl->gmax;
-  pl->waves = w <= 2 ? 2 : (w + 1) / 2 * 2;  // instantiated: 2, 4, 6, 8
+  int splits = dma_splits(tiles, gmax, cu_count);
+  if (splits == 0 || (splits > 1 && gmin != gmax)) return false;  // one range layout for all
+  int range = (gmax + splits - 1) / splits;
+  range = (range + 3) / 4 * 4;
+  if (range > dm::kMaxGroups) return false;
+  splits = (gmax + range - 1) / range;
+  if (splits > dm::kMaxSplits) return false;
+  if ((size_t)a.count * grid_x * 4 > kCounterBytes) return false;
+  if (splits > 1 && ((int64_t)splits * a.M * nmax) * 4 >= ((int64_t)1 << 31)) return false;
+  pl->splits = splits;
+  pl->range = range;
+  pl->gmax = range <= 32 ? 4 : 8;
+  const int w = (range + pl->gmax - 1) / pl->gmax;
+  pl->waves = w <= 2 ? 2 : w <= 6 ? w : 8;  // instantiated: 2, 3, 4, 5, 6, 8
   pl->grid_x = grid_x;
   pl->groups_max = gmax;
   pl->x_stride = ((size_t)gmax * (dm::kXrGroup + dm::kXsGroup) + 255) / 256 * 256;
-  pl->bytes = kCounterBytes + (size_t)pl->nx * pl->x_stride;
+  pl->pstride = splits > 1 ? (size_t)splits * a.M * nmax : 0;
+  pl->bytes = kCounterBytes + (size_t)pl->nx * pl->x_stride + (size_t)a.count * pl->pstride * sizeof(float);
   return true;
+}
+
+// K-ranges per tile, 0 to decline.  Measured on MI355X at M = 32 (one call, the prepare
+// kernel included, against the other kernels' best): K = 3840 x 15360, 240 tiles, no split
+// 16.3 us against 19.3; the q/k/v projections of a 2560-wide decoder layer (96 tiles) in two
+// ranges 12.8 against 13.8; its o projection (K = 4096, 40 tiles) in four 12.0 against 12.3
+// and its down projection (K = 9728) in six 14.7 against 15.3.  More ranges than about
+// three quarters of a workgroup per CU lost (each split adds a partial round trip), ranges
+// under 12 groups lost (K = 2560 x 2560: 11.4 at best against 11.1), and so did launches of
+// more tiles than CUs (the 2 x 9728 x 2560 gate/up launch: 21.3 at best against 19.9).
+int dma_splits(int tiles, int groups, int cu_count) {
+  if (tiles > cu_count) return 0;
+  int s = (3 * cu_count + 2 * tiles) / (4 * tiles);
+  s = s < 1 ? 1 : s;
+  if (s == 1) return tiles >= cu_count / 2 ? 1 : 0;
+  const int range = ((groups + s - 1) / s + 3) / 4 * 4;
+  return range >= 12 ? s : 0;
 }
 
 template <int W, int GMAX>
 hipError_t launch_dma_w(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl, hipStream_t stream) {
-  hipLaunchKernelGGL((qmv_dma_kernel<W, GMAX>), dim3(pl.grid_x, a.count), dim3(64 * W), 0, stream, a, d);
+  if (pl.splits > 1)
+    hipLaunchKernelGGL((qmv_dma_kernel<W, GMAX, true>), dim3(pl.grid_x * pl.splits, a.count), dim3(64 * W), 0,
+                       stream, a, d);
+  else
+    hipLaunchKernelGGL((qmv_dma_kernel<W, GMAX, false>), dim3(pl.grid_x, a.count), dim3(64 * W), 0, stream, a, d);
   return hipGetLastError();
+}
+
+template <int GMAX>
+hipError_t launch_dma_g(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl, hipStream_t stream) {
+  switch (pl.waves) {
+    case 2: return launch_dma_w<2, GMAX>(a, d, pl, stream);
+    case 3: return launch_dma_w<3, GMAX>(a, d, pl, stream);
+    case 4: return launch_dma_w<4, GMAX>(a, d, pl, stream);
+    case 5: return launch_dma_w<5, GMAX>(a, d, pl, stream);
+    case 6: return launch_dma_w<6, GMAX>(a, d, pl, stream);
+    default: return launch_dma_w<8, GMAX>(a, d, pl, stream);
+  }
 }
 
 hipError_t launch_dma(const LaunchArgs& a, const DmaPlan& pl, void* ws, hipStream_t stream) {
@@ -2184,20 +2308,13 @@ hipError_t launch_dma(const LaunchArgs& a, const DmaPlan& pl, void* ws, hipStrea
   DmaArgs d;
   memset(&d, 0, sizeof(d));
   for (int i = 0; i < a.count; ++i) d.xr[i] = xp.dst[pl.xi[i]];
-  if (pl.gmax == 4) {
-    switch (pl.waves) {
-      case 2: return launch_dma_w<2, 4>(a, d, pl, stream);
-      case 4: return launch_dma_w<4, 4>(a, d, pl, stream);
-      case 6: return launch_dma_w<6, 4>(a, d, pl, stream);
-      default: return launch_dma_w<8, 4>(a, d, pl, stream);
-    }
-  }
-  switch (pl.waves) {
-    case 2: return launch_dma_w<2, 8>(a, d, pl, stream);
-    case 4: return launch_dma_w<4, 8>(a, d, pl, stream);
-    case 6: return launch_dma_w<6, 8>(a, d, pl, stream);
-    default: return launch_dma_w<8, 8>(a, d, pl, stream);
-  }
+  d.counters = reinterpret_cast<uint32_t*>(base);
+  d.partial = reinterpret_cast<float*>(base + kCounterBytes + (size_t)pl.nx * pl.x_stride);
+  d.pstride = (int64_t)pl.pstride;
+  d.splits = pl.splits;
+  d.range = pl.range;
+  d.tiles_max = pl.grid_x;
+  return pl.gmax == 4 ? launch_dma_g<4>(a, d, pl, stream) : launch_dma_g<8>(a, d, pl, stream);
 }
 
 #ifndef IMQ_XS_MIN_ROWS

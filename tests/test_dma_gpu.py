@@ -1,15 +1,20 @@
 """GPU parity of the direct-to-LDS MFMA kernel (qmv_dma_kernel, with its activation
 preparation xprep_kernel), through the C ABI.
 
-The launch plan takes it for M >= 5 when the launch has from 128 tiles of 64 weight rows
-(8192 rows over all its weights) to one tile per CU (256 on MI355X) and every K is a multiple
-of 256 up to 4096.  The shapes below cover its
-variants: K = 3840 x 15360 (8 groups per wavefront, eight wavefronts, the last one with four
-groups), K = 512 with a ragged last tile (four groups per wavefront, two wavefronts), K = 256
-(the second wavefront has no groups), K = 4096 (eight full wavefronts), K = 2304 (a part-full
-and an idle wavefront), two weights sharing one x and two weights with their own x.  Bars are
-the oracle's (check_bf16 and the literal bar / check_f32) on sampled rows, which include the
-ragged last tile; repeated calls give the same bits.
+The launch plan takes it for M >= 5 when the launch has at most one tile of 64 weight rows
+per CU (256 on MI355X) and every K is a multiple of 256: whole-K tiles when there are more
+than 192 tiles, else the groups of each tile split into K-ranges of at least 12 groups
+(four-group multiples, at most 64) toward about 192 workgroups, the last range of a tile
+adding the others' fp32 partials in range order.  The shapes below cover its variants:
+K = 3840 x 15360 (8 groups per wavefront, eight wavefronts, the last one with four groups),
+K = 512 with a ragged last tile (four groups per wavefront, two wavefronts), K = 256 (the
+second wavefront has no groups), K = 4096 (two ranges of 32 groups), K = 2304 (a part-full
+and an idle wavefront), two weights sharing one x and two weights with their own x (two
+ranges each), the q/k/v projections of a 2560-wide layer in one launch (two ranges), a
+4096-deep weight in four ranges, a 9728-deep one in five (the last shorter) and a 3328-deep
+one whose last range has four groups.  Bars are the oracle's (check_bf16 and the literal bar
+/ check_f32) on sampled rows, which include the ragged last tile; repeated calls give the
+same bits (the split counters return to zero).
 """
 
 from __future__ import annotations
@@ -85,13 +90,49 @@ def test_two_weights_share_one_x(native, oracle):
 
 
 def test_two_weights_with_their_own_x(native, oracle):
-    """Two 4096 x 1024 weights (64 tiles each), each with its own 9 activation rows: two
-    prepared x in the workspace."""
+    """Two 4096 x 2048 weights (64 tiles each, two K-ranges), each with its own 9 activation
+    rows: two prepared x in the workspace."""
     m = 9
-    prs = [oracle.synthetic(4096, 1024, m, seed=oracle.SEED_BASE + 860 + i) for i in range(2)]
+    prs = [oracle.synthetic(4096, 2048, m, seed=oracle.SEED_BASE + 860 + i) for i in range(2)]
     dev = [to_device(pr) for pr in prs]
     announce("dma two x", m)
     outs = native.qmv_grouped([(w, s, b) for (w, s, b, _) in dev], [x for (*_, x) in dev])
     torch.cuda.synchronize()
     for pr, y in zip(prs, outs):
         _check(oracle, pr, y, _rows(4096, 37))
+
+
+@pytest.mark.parametrize("m", [32, 7])
+def test_split_qkv_projections_in_one_launch(native, oracle, m):
+    """q (4096 rows), k and v (1024 each) of a 2560-wide layer: 96 tiles in two K-ranges of
+    20 groups, one prepared x."""
+    shapes = [(4096, 2560), (1024, 2560), (1024, 2560)]
+    prs = [oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 870 + i) for i, (n, k) in enumerate(shapes)]
+    prs = [prs[0]] + [oracle.Problem(p.w, p.s, p.b, prs[0].x, 0) for p in prs[1:]]
+    dev = [to_device(pr) for pr in prs]
+    x = dev[0][3]
+    announce("dma split q/k/v", m)
+    weights = [(w, s, b) for (w, s, b, _) in dev]
+    outs = native.qmv_grouped(weights, [x, x, x])
+    again = native.qmv_grouped(weights, [x, x, x])
+    torch.cuda.synchronize()
+    for (n, _), pr, y, y2 in zip(shapes, prs, outs, again):
+        _check(oracle, pr, y, _rows(n, 41))
+        assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("n,k,m,out_f32", [
+    (2600, 4096, 32, True), (2600, 4096, 5, False),
+    (2560, 9728, 32, False), (2560, 9728, 32, True),
+    (3000, 3328, 19, False),
+])
+def test_split_ranges_match_oracle(native, oracle, n, k, m, out_f32):
+    pr = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 880 + m + k // 64)
+    w, s, b, x = to_device(pr)
+    announce("dma split", n, k, m, out_f32)
+    dtype = torch.float32 if out_f32 else torch.bfloat16
+    y = native.qmv(w, s, b, x, out_dtype=dtype)
+    y2 = native.qmv(w, s, b, x, out_dtype=dtype)
+    torch.cuda.synchronize()
+    _check(oracle, pr, y, _rows(n, 53), out_f32)
+    assert torch.equal(y, y2)

@@ -1,10 +1,10 @@
 """GPU parity of the staged MFMA kernel (qmv_mma_staged_kernel, M >= 3), through the C ABI.
 
 The launch plan takes it when every K is a multiple of 256, x rows are strided (no row
-pointer table) and either the launch has 77 to 127 tiles of 64 weight rows (from 128 tiles
-with K <= 4096 and M >= 5 the direct-to-LDS kernel takes over), or K >= 4096 and a split
-workspace is given.  The shapes below are chosen to meet those conditions (or,
-for the fallback case, to miss exactly one).  Bars are the oracle's (oracle.check_bf16 /
+pointer table), the direct-to-LDS kernel declines the launch (M < 5, more tiles of 64 weight
+rows than CUs, or K-ranges that would be shorter than 12 groups) and either the launch has
+at least 77 tiles, or K >= 4096 and a split workspace is given.  The shapes below are chosen
+to meet those conditions (or, for the fallback case, to miss exactly one).  Bars are the oracle's (oracle.check_bf16 /
 check_f32): bf16 outputs within 1 bf16 ulp of the exactly computed product plus the fp32
 summation allowance; split launches also repeat their bits call after call.
 """
@@ -76,10 +76,11 @@ def test_staged_split_repeats_bit_identical(native, oracle, m, n):
 
 
 def test_staged_grouped_problems(native, oracle):
-    """Two weights of 4100 rows sharing one x (65 + 65 tiles, ragged) and a third with its
-    own x and K, one launch; each output meets the oracle."""
+    """Two weights of 8200 rows sharing one x (129 + 129 tiles, ragged) and a third with its
+    own x and K, one launch (268 tiles: more than the direct-to-LDS kernel takes); each
+    output meets the oracle."""
     m = 7
-    shapes = [(4100, 1024), (4100, 1024), (640, 2048)]
+    shapes = [(8200, 1024), (8200, 1024), (640, 2048)]
     prs = [oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 540 + i)
            for i, (n, k) in enumerate(shapes)]
     dev = [to_device(p) for p in prs]
@@ -93,11 +94,11 @@ def test_staged_grouped_problems(native, oracle):
 
 def test_staged_fp32_output(native, oracle):
     import torch
-    pr = oracle.synthetic(8256, 768, 32, seed=oracle.SEED_BASE + 560)
+    pr = oracle.synthetic(16448, 768, 32, seed=oracle.SEED_BASE + 560)  # 257 tiles
     w, s, b, x = to_device(pr)
     announce("staged fp32")
     y = native.qmv(w, s, b, x, out_dtype=torch.float32)
-    _check(oracle, pr, y, _rows(8256, 13), out_f32=True)
+    _check(oracle, pr, y, _rows(16448, 29), out_f32=True)
 
 
 def test_staged_strided_rows_through_the_abi(native, oracle):

@@ -80,12 +80,14 @@ def test_noalloc_matches_workspace_entry_twice(native, oracle):
 
 
 def test_noalloc_prepared_x_twice(native, oracle):
-    """Launches of the direct-to-LDS kernel, whose prepared activations go to the scratch:
-    K = 3840 x 15360 at 8 rows, then a smaller call (8192 x 1024, 16 rows), both
+    """Launches of the direct-to-LDS kernel, whose prepared activations and split partials
+    go to the scratch: 2560 x 9728 at 32 rows (five K-ranges), then a smaller call (4096 x
+    2048, 16 rows, three ranges), then K = 3840 x 15360 at 8 rows (whole-K tiles), each
     bit-identical to imq_qmv_grouped_ws."""
-    first = _case(native, oracle, [(15360, 3840)], 8, oracle.SEED_BASE + 940)
-    second = _case(native, oracle, [(8192, 1024)], 16, oracle.SEED_BASE + 950)
-    assert first > second > 0
+    first = _case(native, oracle, [(2560, 9728)], 32, oracle.SEED_BASE + 940)
+    second = _case(native, oracle, [(4096, 2048)], 16, oracle.SEED_BASE + 950)
+    third = _case(native, oracle, [(15360, 3840)], 8, oracle.SEED_BASE + 960)
+    assert first > second > third > 0
 
 
 def test_noalloc_without_split(native, oracle):
