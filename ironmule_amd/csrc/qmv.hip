@@ -22,7 +22,7 @@
 //     started at -128 * sum(x);
 //   * the MFMA kernels (3 to 32 rows): v_mfma_f32_32x32x16_bf16 with the activation rows
 //     as the A operand and 32 weight rows as the B operand, four MFMAs per group of 64,
-//     and the group's sums of x from MFMAs against a ones operand or prepared with x.
+//     and the group's sums of x from MFMAs against a ones operand or dot2 against (1, 1).
 //
 // Layout in HBM is the reference's own (row-major w (N, K/8) uint32, s and b (N, K/64)
 // bf16), so a caller passes its buffers unchanged.  One launch may serve up to
@@ -1343,17 +1343,16 @@ __global__ __launch_bounds__(64 * xs::Shape<MB>::kWaves) void qmv_xs_kernel(XsAr
 // groups (the whole K, or one of SPLITS ranges of four-group multiples), and each of its W
 // wavefronts owns GMAX consecutive groups of that range, so each weight byte and each
 // activation byte reaches a workgroup once.
-//   * Activations come prepared by xprep_kernel (once per distinct x of the launch): for
-//     each group g and k-step t the 64 lanes' 16-byte A operands of
-//     v_mfma_f32_32x32x16_bf16 are one contiguous KiB (lane (m, kb) holds x[m][64 g +
-//     8 (4 kb + t) ..+8] in pair order, rows m >= M zero), followed by every group's 32
-//     row sums in fp32.  A wavefront loads them straight into registers with whole-line
-//     loads, IMQ_DMA_XDEPTH groups ahead of their use.
+//   * Activations: lane (m, kb) of a wavefront loads the 64 bytes x[m][64 g + 32 kb ..+32]
+//     of each of its groups g (four 16-byte loads, IMQ_DMA_XDEPTH groups ahead of their
+//     use; rows m >= M read zeros), which in pair order are its A operands of the group's
+//     four k-steps of v_mfma_f32_32x32x16_bf16.  The group's row sums come from the same
+//     registers (sixteen dot2 against (1, 1) and one exchange with lane m + 32).
 //   * Weights go from memory to LDS by the buffer loads' LDS path (16 bytes a lane): an
 //     instruction moves 8 rows x 128 bytes (four groups of a row: whole lines), lane l to
 //     LDS byte 16 l, piece c of row r stored at slot c ^ ((r >> 1) & 7) so that the reads
 //     in MFMA-operand order are free of bank conflicts.  One LDS array per four groups: the
-//     first four groups' weights are loaded at the start, the next four while the first
+//     first four groups' weights are loaded at the start, the next four while the second
 //     group is computed, so that a wavefront is not held at issue by loads it needs late
 //     (every wavefront of a CU issuing its whole range at once kept the CU's first
 //     computation waiting for most of the launch's traffic).
@@ -1376,8 +1375,6 @@ __global__ __launch_bounds__(64 * xs::Shape<MB>::kWaves) void qmv_xs_kernel(XsAr
 namespace dm {
 constexpr int kRows = 64;                  // weight rows per workgroup
 constexpr int kChunkBytes = kRows * 128;   // a wavefront's four groups of the 64 rows
-constexpr int kXrGroup = 4096;             // prepared x per group
-constexpr int kXsGroup = 32 * 4;           // row sums per group
 constexpr int kMaxGroups = 64;             // groups of a workgroup's K-range
 constexpr int kMaxSplits = 16;             // K-ranges of a tile
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
@@ -1385,36 +1382,7 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 }  // namespace dm
 
-struct XprepArgs {
-  const uint16_t* x[kMaxProblems];
-  int64_t ldx[kMaxProblems];
-  char* dst[kMaxProblems];
-  int32_t K[kMaxProblems];
-  int32_t count;
-  int32_t M;
-};
-
-// One workgroup per (group, distinct x): thread (m, c) moves the 16 bytes x[m][64 g + 8 c ..]
-// to their A-operand slot in pair order, and the eight threads of a row add its sum.
-__global__ __launch_bounds__(256) void xprep_kernel(XprepArgs a) {
-  const int xi = blockIdx.y, g = blockIdx.x;
-  const int K = a.K[xi];
-  if (g >= K / 64) return;
-  const int tid = threadIdx.x, m = tid >> 3, c = tid & 7;
-  uint4 v = make_uint4(0u, 0u, 0u, 0u);
-  if (m < a.M) v = *reinterpret_cast<const uint4*>(a.x[xi] + m * a.ldx[xi] + 64 * g + 8 * c);
-  float sum = sum8(v);
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
-  sum += __shfl_xor(sum, 4);
-  char* d = a.dst[xi];
-  *reinterpret_cast<uint4*>(d + (size_t)(g * 4 + (c & 3)) * 1024 + (m + 32 * (c >> 2)) * 16) =
-      pair_order(v);
-  if (c == 0) reinterpret_cast<float*>(d + (size_t)(K / 64) * dm::kXrGroup)[g * 32 + m] = sum;
-}
-
 struct DmaArgs {
-  const char* xr[kMaxProblems];  // problem i's prepared x
   float* partial;                // split partials: problem i at partial + i * pstride
   uint32_t* counters;            // per (problem, tile) arrival counters, zero between calls
   int64_t pstride;
@@ -1455,8 +1423,9 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
   const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.s, sb_bytes);
   const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(P.b, sb_bytes);
-  const uint32_t xs_base = (uint32_t)G * dm::kXrGroup;
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(d.xr[pi], xs_base + (uint32_t)G * dm::kXsGroup);
+  const __amdgpu_buffer_rsrc_t xrs =
+      buffer_rsrc(P.x, (uint32_t)(((int64_t)(M - 1) * P.ldx + K) * 2));
+  const uint32_t xrow = j < M ? (uint32_t)j * (uint32_t)P.ldx * 2u + 64u * (uint32_t)kb : kPastBuffer;
 
   // 1. scales, then biases, of rows [row0, row0 + 64) over the range: Gs instructions of 64
   //    dwords, dword dd of an array at LDS dword array * 32 Gs + dd
@@ -1488,22 +1457,16 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
           0, 0, kNt);
     }
   };
-  // 3. prepared x of group gi (4 operands) and, for an even gi, the pair's row sums
+  // 3. this lane's 64 bytes of x for group gi (rows m >= M and groups past the range:
+  //    zeros, no traffic)
   struct XG {
     uint4 v[4];
-    float sum;
   };
   auto load_x = [&](XG& xg, int gi) {
     const int g = g0 + gi;
-    const uint32_t dead = g < gs1 ? 0u : kPastBuffer;
+    const uint32_t off = g < gs1 ? xrow + 128u * (uint32_t)g : kPastBuffer;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      xg.v[t] = load_b128(xrs, ((uint32_t)(g * 4 + t) * 1024u + 16u * (uint32_t)lane) | dead);
-    if ((gi & 1) == 0) {
-      const uint32_t dsum = g + kb < gs1 ? 0u : kPastBuffer;
-      xg.sum = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-          xrs, (xs_base + 4u * (uint32_t)((g + kb) * 32 + j)) | dsum, 0, 0));
-    }
+    for (int t = 0; t < 4; ++t) xg.v[t] = load_b128(xrs, off + 16u * (uint32_t)t);
   };
 
   XG xq[GMAX];
@@ -1514,25 +1477,34 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   __builtin_amdgcn_sched_barrier(0);
   // this wavefront's scales and biases have landed (the weight and x loads issued after
   // them may not have); past the barrier every wavefront's have
-  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(8 + 4 * XD + (XD + 1) / 2));
+  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(8 + 4 * XD));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
-  const uint32_t one = in_vgpr(xs::kOne);
+  const uint32_t one = in_vgpr(kNibOne);
   const f32x16_t zero = {};
   f32x16_t acc[2] = {zero, zero}, accb[2] = {zero, zero};
   uint32_t sp[2] = {0u, 0u}, bp[2] = {0u, 0u};
+  float sum_even = 0.0f;  // row j's sum of x over the pair's first group
   const int gl0 = g0 - gs0;  // this wavefront's first group within the range
 #pragma unroll
   for (int gi = 0; gi < GMAX; ++gi) {
     if (gi + XD < GMAX) load_x(xq[gi + XD], gi + XD);
-    if (NC > 1 && gi == 1) load_w(wb1, 1);  // the next four groups, behind the first x
+    if (NC > 1 && gi == 1) load_w(wb1, 1);  // the next four groups, behind the second x
     if (gi < nw) {
       const char* wb = (gi >> 2) ? wb1 : wb0;
       const XG& xg = xq[gi];
       bf16x8_t xa[4];
+      float half = 0.0f;  // this lane's 32 values of row j
 #pragma unroll
-      for (int t = 0; t < 4; ++t) xa[t] = __builtin_bit_cast(bf16x8_t, xg.v[t]);
+      for (int t = 0; t < 4; ++t) {
+        xa[t] = as_bf16x8(pair_order(xg.v[t]));
+        half = dot2(xg.v[t].x, one, half);
+        half = dot2(xg.v[t].y, one, half);
+        half = dot2(xg.v[t].z, one, half);
+        half = dot2(xg.v[t].w, one, half);
+      }
+      const float gsum = half + __shfl_xor(half, 32);  // row j over the whole group
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int r = 32 * t + j;
@@ -1552,15 +1524,19 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
         const float s16 = 16.0f * __uint_as_float((gi & 1) ? (sp[t] & 0xffff0000u) : (sp[t] << 16));
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(s16, p[e], acc[t][e]);
-        // the pair's offset term once its second group is done (or at an unpaired last one)
+        // the pair's offset term once its second group is done (or at an unpaired last
+        // one): A = the rows' sums (lanes kb = 0 / 1: the pair's first / second group),
+        // B = b - 16 s of the same groups per weight row
         if ((gi & 1) || gi + 1 == nw) {
           const uint32_t sw = kb ? (sp[t] & 0xffff0000u) : (sp[t] << 16);
           const uint32_t bw = kb ? (bp[t] & 0xffff0000u) : (bp[t] << 16);
           float cg = fmaf(-16.0f, __uint_as_float(sw), __uint_as_float(bw));
           cg = (kb && !(gi & 1)) ? 0.0f : cg;
-          accb[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xq[gi & ~1].sum, cg, accb[t], 0, 0, 0);
+          const float xs = (gi & 1) ? (kb ? gsum : sum_even) : gsum;
+          accb[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs, cg, accb[t], 0, 0, 0);
         }
       }
+      sum_even = gsum;
     }
   }
   acc[0] += accb[0];
@@ -2173,13 +2149,12 @@ hipError_t launch_xs(const XsArgs& x, const XsPlan& pl, hipStream_t stream) {
 }
 
 // The direct-to-LDS kernel's plan.  64-row tiles; the groups of a tile split into K-ranges
-// (multiples of four groups, at most 64) so that the launch has about DMA_WG_PER_CU
-// workgroups per CU, GMAX = 4 groups per wavefront for ranges up to 32 groups, else 8, and
-// W = range / GMAX wavefronts.  Each distinct x of the launch is prepared once
-// (xprep_kernel) into the workspace after the counter region; the split partials follow.
-// Not applicable: a pointer table, M outside [3, 32], K % 256 != 0, problems of different K
-// with splits, x rows not 16-byte aligned, offsets past 2 GiB, or more tile counters than
-// the counter region holds.
+// (multiples of four groups, at most 64) so that the launch has about three quarters of a
+// workgroup per CU (dma_splits), GMAX = 4 groups per wavefront for ranges up to 32 groups,
+// else 8, and W = range / GMAX wavefronts.  The workspace holds the split counters and
+// partials (none without splits).  Not applicable: a pointer table, M outside [3, 32],
+// K % 256 != 0, problems of different K with splits, x rows not 16-byte aligned, offsets
+// past 2 GiB, or more tile counters than the counter region holds.
 #ifndef IMQ_DMA_MIN_ROWS
 #define IMQ_DMA_MIN_ROWS 5
 #endif
@@ -2190,15 +2165,8 @@ struct DmaPlan {
   int grid_x = 0;          // tiles of the largest problem
   int splits = 1;
   int range = 0;           // groups per K-range
-  int nx = 0;
-  int groups_max = 0;      // largest K / 64 of the launch
-  size_t x_stride = 0;     // workspace bytes per prepared x
   size_t pstride = 0;      // partial floats per problem
   size_t bytes = 0;        // workspace the plan uses
-  int xi[kMaxProblems];    // problem -> its prepared x
-  const uint16_t* x[kMaxProblems];
-  int64_t ldx[kMaxProblems];
-  int32_t kx[kMaxProblems];
 };
 
 int dma_splits(int tiles, int groups, int cu_count);
@@ -2206,22 +2174,13 @@ int dma_splits(int tiles, int groups, int cu_count);
 bool plan_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
   if (a.table || a.M < 3 || a.M > 32 || a.count < 1 || a.count > kMaxProblems) return false;
   int tiles = 0, grid_x = 0, gmax = 0, gmin = 1 << 30, nmax = 0;
-  pl->nx = 0;
   for (int i = 0; i < a.count; ++i) {
     const Problem& P = a.p[i];
     if (P.K % 256 != 0 || P.N < 1) return false;
     if ((int64_t)P.N * (P.K / 2) >= ((int64_t)1 << 31)) return false;
     if (P.ldx % 8 != 0 || !imq_rt::aligned(P.x, 16)) return false;
+    if (((int64_t)(a.M - 1) * P.ldx + P.K) * 2 >= ((int64_t)1 << 31)) return false;
     if (((int64_t)(a.M - 1) * P.ldy + P.N) * 4 >= ((int64_t)1 << 31)) return false;
-    int k = 0;
-    while (k < pl->nx && !(pl->x[k] == P.x && pl->ldx[k] == P.ldx && pl->kx[k] == P.K)) ++k;
-    if (k == pl->nx) {
-      pl->x[k] = P.x;
-      pl->ldx[k] = P.ldx;
-      pl->kx[k] = P.K;
-      ++pl->nx;
-    }
-    pl->xi[i] = k;
     const int t = (P.N + dm::kRows - 1) / dm::kRows;
     tiles += t;
     grid_x = t > grid_x ? t : grid_x;
@@ -2244,10 +2203,8 @@ bool plan_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
   const int w = (range + pl->gmax - 1) / pl->gmax;
   pl->waves = w <= 2 ? 2 : w <= 6 ? w : 8;  // instantiated: 2, 3, 4, 5, 6, 8
   pl->grid_x = grid_x;
-  pl->groups_max = gmax;
-  pl->x_stride = ((size_t)gmax * (dm::kXrGroup + dm::kXsGroup) + 255) / 256 * 256;
   pl->pstride = splits > 1 ? (size_t)splits * a.M * nmax : 0;
-  pl->bytes = kCounterBytes + (size_t)pl->nx * pl->x_stride + (size_t)a.count * pl->pstride * sizeof(float);
+  pl->bytes = splits > 1 ? kCounterBytes + (size_t)a.count * pl->pstride * sizeof(float) : 0;
   return true;
 }
 
@@ -2291,25 +2248,13 @@ hipError_t launch_dma_g(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl
 }
 
 hipError_t launch_dma(const LaunchArgs& a, const DmaPlan& pl, void* ws, hipStream_t stream) {
-  char* base = static_cast<char*>(ws);
-  XprepArgs xp;
-  memset(&xp, 0, sizeof(xp));
-  for (int k = 0; k < pl.nx; ++k) {
-    xp.x[k] = pl.x[k];
-    xp.ldx[k] = pl.ldx[k];
-    xp.K[k] = pl.kx[k];
-    xp.dst[k] = base + kCounterBytes + (size_t)k * pl.x_stride;
-  }
-  xp.count = pl.nx;
-  xp.M = a.M;
-  hipLaunchKernelGGL(xprep_kernel, dim3(pl.groups_max, pl.nx), dim3(256), 0, stream, xp);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   DmaArgs d;
   memset(&d, 0, sizeof(d));
-  for (int i = 0; i < a.count; ++i) d.xr[i] = xp.dst[pl.xi[i]];
-  d.counters = reinterpret_cast<uint32_t*>(base);
-  d.partial = reinterpret_cast<float*>(base + kCounterBytes + (size_t)pl.nx * pl.x_stride);
+  if (pl.splits > 1) {
+    char* base = static_cast<char*>(ws);
+    d.counters = reinterpret_cast<uint32_t*>(base);
+    d.partial = reinterpret_cast<float*>(base + kCounterBytes);
+  }
   d.pstride = (int64_t)pl.pstride;
   d.splits = pl.splits;
   d.range = pl.range;
@@ -2369,7 +2314,8 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* w
   DmaPlan dp;
   if (M >= IMQ_XS_MIN_ROWS && !big && plan_xs(a, dev->cu_count, &xa, &xp)) {
     e = launch_xs(xa, xp, stream);
-  } else if (M >= IMQ_DMA_MIN_ROWS && ws && plan_dma(a, dev->cu_count, &dp) && dp.bytes <= ws_bytes) {
+  } else if (M >= IMQ_DMA_MIN_ROWS && plan_dma(a, dev->cu_count, &dp) &&
+             (dp.bytes == 0 || (ws && dp.bytes <= ws_bytes))) {
     e = launch_dma(a, dp, ws, stream);
   } else if (M == 1 && plan_m1(a, &m1)) {
     e = launch_m1_for(a, m1, stream);

@@ -8,8 +8,10 @@ continuous-batched requests, each with its own KV slot and position:
     per layer:
         x = rms_norm(h)                        imq_add_rmsnorm (adds the previous delta)
         q, k, v = x @ W.T                      imq_qmv_grouped (one launch, three weights)
-        q, k = rope(norm(q)), rope(norm(k))    imq_qk_norm_rope (+ the KV write)
-        o = attention(q, KV[slot][:pos+1])     imq_attention_decode
+        q, k = rope(norm(q)), rope(norm(k))    imq_attention_fused: one launch for the q/k
+        o = attention(q, KV[slot][:pos+1])     norm + rotary, the KV write and the attention
+                                               (the bits of imq_qk_norm_rope followed by
+                                               imq_attention_decode)
         h += o @ Wo.T                          imq_qmv, added by the next imq_add_rmsnorm
         x = rms_norm(h)
         g, u = x @ Wg.T, x @ Wu.T              imq_qmv_grouped
@@ -133,7 +135,6 @@ class DecodeState:
         self.q = torch.empty((batch, c.heads * c.head_dim), **bf)
         self.k = torch.empty((batch, c.kv_heads * c.head_dim), **bf)
         self.v = torch.empty((batch, c.kv_heads * c.head_dim), **bf)
-        self.q_rot = torch.empty((batch, c.heads * c.head_dim), **bf)
         self.attn = torch.empty((batch, c.heads * c.head_dim), **bf)
         self.delta = torch.empty((batch, c.hidden), **bf)
         self.gate = torch.empty((batch, c.intermediate), **bf)
@@ -170,16 +171,11 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
         n.add_rmsnorm(s.h, layer["input_norm"], s.x, c.eps, delta=delta, stream=stream)
         n.qmv_grouped([layer["q"], layer["k"], layer["v"]], [s.x, s.x, s.x],
                       outs=[s.q, s.k, s.v], stream=stream)
-        if s.batch == 1:  # one launch (the decode programs' attention stage, same bits)
-            n.attention_fused(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
-                              s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len, c.theta,
-                              c.eps, s.workspace, s.attn_counters, stream=stream)
-        else:  # three launches: measured faster than the fused form at batch 32
-            n.qk_norm_rope(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
-                           s.slot_ids, s.q_rot, s.k_pool[i], s.v_pool[i], c.theta, c.eps,
-                           stream=stream)
-            n.attention_decode(s.q_rot, s.k_pool[i], s.v_pool[i], s.lengths, s.slot_ids, s.attn,
-                               s.max_len, c.head_dim ** -0.5, s.workspace, stream=stream)
+        # one launch (the decode programs' attention stage, the same bits as qk_norm_rope
+        # followed by attention_decode)
+        n.attention_fused(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
+                          s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len, c.theta,
+                          c.eps, s.workspace, s.attn_counters, stream=stream)
         n.qmv(*layer["o"], s.attn, out=s.delta, stream=stream)
         n.add_rmsnorm(s.h, layer["post_norm"], s.x, c.eps, delta=s.delta, stream=stream)
         n.qmv_grouped([layer["gate"], layer["up"]], [s.x, s.x], outs=[s.gate, s.up], stream=stream)

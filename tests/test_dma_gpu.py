@@ -1,5 +1,4 @@
-"""GPU parity of the direct-to-LDS MFMA kernel (qmv_dma_kernel, with its activation
-preparation xprep_kernel), through the C ABI.
+"""GPU parity of the direct-to-LDS MFMA kernel (qmv_dma_kernel), through the C ABI.
 
 The launch plan takes it for M >= 5 when the launch has at most one tile of 64 weight rows
 per CU (256 on MI355X) and every K is a multiple of 256: whole-K tiles when there are more
@@ -73,8 +72,7 @@ def test_single_weight_matches_oracle(native, oracle, n, k, m, out_f32):
 
 
 def test_two_weights_share_one_x(native, oracle):
-    """Two 6144 x 2560 weights (96 tiles each), one x of 32 rows (prepared once), one
-    launch."""
+    """Two 6144 x 2560 weights (96 tiles each), one x of 32 rows, one launch."""
     m, n, k = 32, 6144, 2560
     pg = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 850)
     pu = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 851)
@@ -91,7 +89,7 @@ def test_two_weights_share_one_x(native, oracle):
 
 def test_two_weights_with_their_own_x(native, oracle):
     """Two 4096 x 2048 weights (64 tiles each, two K-ranges), each with its own 9 activation
-    rows: two prepared x in the workspace."""
+    rows."""
     m = 9
     prs = [oracle.synthetic(4096, 2048, m, seed=oracle.SEED_BASE + 860 + i) for i in range(2)]
     dev = [to_device(pr) for pr in prs]
@@ -105,7 +103,7 @@ def test_two_weights_with_their_own_x(native, oracle):
 @pytest.mark.parametrize("m", [32, 7])
 def test_split_qkv_projections_in_one_launch(native, oracle, m):
     """q (4096 rows), k and v (1024 each) of a 2560-wide layer: 96 tiles in two K-ranges of
-    20 groups, one prepared x."""
+    20 groups, one x."""
     shapes = [(4096, 2560), (1024, 2560), (1024, 2560)]
     prs = [oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 870 + i) for i, (n, k) in enumerate(shapes)]
     prs = [prs[0]] + [oracle.Problem(p.w, p.s, p.b, prs[0].x, 0) for p in prs[1:]]
