@@ -2208,21 +2208,24 @@ bool plan_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
   return true;
 }
 
-// K-ranges per tile, 0 to decline.  Measured on MI355X at M = 32 (one call, the prepare
-// kernel included, against the other kernels' best): K = 3840 x 15360, 240 tiles, no split
-// 16.3 us against 19.3; the q/k/v projections of a 2560-wide decoder layer (96 tiles) in two
-// ranges 12.8 against 13.8; its o projection (K = 4096, 40 tiles) in four 12.0 against 12.3
-// and its down projection (K = 9728) in six 14.7 against 15.3.  More ranges than about
-// three quarters of a workgroup per CU lost (each split adds a partial round trip), ranges
-// under 12 groups lost (K = 2560 x 2560: 11.4 at best against 11.1), and so did launches of
-// more tiles than CUs (the 2 x 9728 x 2560 gate/up launch: 21.3 at best against 19.9).
+// K-ranges per tile, 0 to decline.  Measured on MI355X at M = 32 (one call, against the
+// other kernels' best): launches of more than half a tile per CU run whole-K tiles (K =
+// 3840 x 15360, 240 tiles: 16.3 us against 19.5; any split lost); smaller ones split into
+// ranges of at most 28 groups and into at least 0.6 workgroups per CU: the q/k/v
+// projections of a 2560-wide decoder layer (96 tiles) in two ranges 11.4 us against 14.0,
+// its o projection (K = 4096, 40 tiles) in four 10.1 against 12.4, its down projection (K =
+// 9728) in six 12.6 against 15.5, K = 2560 x 2560 in four 10.0 against 11.2.  Launches of
+// more tiles than CUs stay with the staged kernel (the 2 x 9728 x 2560 gate/up launch: 21.3
+// at best against 19.9), and so do splits into ranges under 8 groups.
 int dma_splits(int tiles, int groups, int cu_count) {
   if (tiles > cu_count) return 0;
-  int s = (3 * cu_count + 2 * tiles) / (4 * tiles);
-  s = s < 1 ? 1 : s;
-  if (s == 1) return tiles >= cu_count / 2 ? 1 : 0;
+  if (2 * tiles > cu_count) return (groups + dm::kMaxGroups - 1) / dm::kMaxGroups;
+  const int by_range = (groups + 27) / 28;
+  const int by_count = (6 * cu_count + 5 * tiles) / (10 * tiles);
+  const int s = by_range > by_count ? by_range : by_count;
+  if (s <= 1) return 1;
   const int range = ((groups + s - 1) / s + 3) / 4 * 4;
-  return range >= 12 ? s : 0;
+  return range >= 8 ? s : 0;
 }
 
 template <int W, int GMAX>

@@ -2,18 +2,19 @@
 
 The launch plan takes it for M >= 5 when the launch has at most one tile of 64 weight rows
 per CU (256 on MI355X) and every K is a multiple of 256: whole-K tiles when there are more
-than 192 tiles, else the groups of each tile split into K-ranges of at least 12 groups
-(four-group multiples, at most 64) toward about 192 workgroups, the last range of a tile
-adding the others' fp32 partials in range order.  The shapes below cover its variants:
-K = 3840 x 15360 (8 groups per wavefront, eight wavefronts, the last one with four groups),
-K = 512 with a ragged last tile (four groups per wavefront, two wavefronts), K = 256 (the
-second wavefront has no groups), K = 4096 (two ranges of 32 groups), K = 2304 (a part-full
-and an idle wavefront), two weights sharing one x and two weights with their own x (two
-ranges each), the q/k/v projections of a 2560-wide layer in one launch (two ranges), a
-4096-deep weight in four ranges, a 9728-deep one in five (the last shorter) and a 3328-deep
-one whose last range has four groups.  Bars are the oracle's (check_bf16 and the literal bar
-/ check_f32) on sampled rows, which include the ragged last tile; repeated calls give the
-same bits (the split counters return to zero).
+tiles than half the CUs, else the groups of each tile split into K-ranges (four-group
+multiples of at most 28 groups, at least 8) toward at least 0.6 workgroups per CU, the last
+range of a tile adding the others' fp32 partials in range order.  The shapes below cover its
+variants: K = 3840 x 15360 (8 groups per wavefront, eight wavefronts, the last one with four
+groups), K = 512 with a ragged last tile (four groups per wavefront, two wavefronts), K = 256
+(the second wavefront has no groups), K = 4096 x 8192 (three ranges, the last shorter),
+K = 2304 (a part-full and an idle wavefront), two weights sharing one x and two weights with
+their own x (two ranges each), the q/k/v projections of a 2560-wide layer in one launch
+(two ranges), a 4096-deep weight in four ranges, a 9728-deep one in six (the last with 12
+groups), a 3328-deep one in three and K = 2560 x 2560 in four (the last with four groups),
+and x rows strided inside a wider buffer.  Bars are the oracle's (check_bf16 and the literal
+bar / check_f32) on sampled rows, which include the ragged last tile; repeated calls give
+the same bits (the split counters return to zero).
 """
 
 from __future__ import annotations
@@ -122,7 +123,7 @@ def test_split_qkv_projections_in_one_launch(native, oracle, m):
 @pytest.mark.parametrize("n,k,m,out_f32", [
     (2600, 4096, 32, True), (2600, 4096, 5, False),
     (2560, 9728, 32, False), (2560, 9728, 32, True),
-    (3000, 3328, 19, False),
+    (3000, 3328, 19, False), (2560, 2560, 32, False),
 ])
 def test_split_ranges_match_oracle(native, oracle, n, k, m, out_f32):
     pr = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 880 + m + k // 64)
@@ -134,3 +135,20 @@ def test_split_ranges_match_oracle(native, oracle, n, k, m, out_f32):
     torch.cuda.synchronize()
     _check(oracle, pr, y, _rows(n, 53), out_f32)
     assert torch.equal(y, y2)
+
+
+def test_strided_rows_through_the_abi(native, oracle):
+    """imq_qmv with ldx > K (x rows inside a wider buffer) and ldy > N, 128 whole-K tiles."""
+    n, k, m = 8192, 256, 9
+    pr = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 890)
+    w, s, b, x = to_device(pr)
+    wide = torch.zeros((m, k + 64), dtype=torch.bfloat16, device="cuda")
+    wide[:, :k] = x
+    y = torch.zeros((m, n + 8), dtype=torch.bfloat16, device="cuda")
+    announce("dma strided")
+    native._check(native.lib().imq_qmv(
+        native._ptr(w), native._ptr(s), native._ptr(b), native._ptr(wide), k + 64,
+        native._ptr(y), n + 8, m, n, k, 64, 4, 0, native._stream(None)))
+    torch.cuda.synchronize()
+    _check(oracle, pr, y[:, :n].contiguous(), _rows(n, 17))
+    assert not y[:, n:].any()  # columns past N untouched

@@ -102,9 +102,9 @@ def test_staged_fp32_output(native, oracle):
 
 
 def test_staged_strided_rows_through_the_abi(native, oracle):
-    """imq_qmv with ldx > K (x rows inside a wider buffer) and ldy > N."""
+    """imq_qmv with ldx > K (x rows inside a wider buffer) and ldy > N (257 tiles)."""
     import torch
-    n, k, m = 8192, 256, 9
+    n, k, m = 16448, 256, 9
     pr = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 570)
     w, s, b, x = to_device(pr)
     wide = torch.zeros((m, k + 64), dtype=torch.bfloat16, device="cuda")
