@@ -568,7 +568,11 @@ constexpr uint32_t kNibOne = 0x3f803f80u;   // bf16 pair (1.0, 1.0)
 constexpr uint32_t kNibMask = 0x00780078u;  // mantissa bits 3..6 of each half
 template <int P>
 __device__ __forceinline__ uint32_t nib16(uint32_t u, uint32_t one) {
-  const uint32_t t = P == 0 ? (u << 3) : (u >> (4 * P - 3));
+  uint32_t t;
+  if constexpr (P == 0)
+    t = u << 3;
+  else
+    t = u >> (4 * P - 3);
   return (t & kNibMask) | one;
 }
 
@@ -2159,6 +2163,7 @@ hipError_t launch_xs(const XsArgs& x, const XsPlan& pl, hipStream_t stream) {
 #define IMQ_DMA_MIN_ROWS 5
 #endif
 
+
 struct DmaPlan {
   int waves = 0;
   int gmax = 0;
@@ -2228,6 +2233,15 @@ int dma_splits(int tiles, int groups, int cu_count) {
   return range >= 8 ? s : 0;
 }
 
+// The launches the direct-to-LDS kernel takes: from IMQ_DMA_MIN_ROWS rows any it plans,
+// and from 3 rows those of whole-K tiles, where the few-row VALU tile is slower (K = 3840 x
+// 15360: 16.3 us at M = 4 against about 13 us here) while it stays ahead on smaller
+// launches (K = 2560 x 2560 at M = 4: 5.9 us against about 10).
+bool take_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
+  if (a.M < 3 || !plan_dma(a, cu_count, pl)) return false;
+  return a.M >= IMQ_DMA_MIN_ROWS || pl->splits == 1;
+}
+
 template <int W, int GMAX>
 hipError_t launch_dma_w(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl, hipStream_t stream) {
   if (pl.splits > 1)
@@ -2276,7 +2290,7 @@ size_t wanted_workspace(const LaunchArgs& a, int cu_count) {
   XsPlan xp;
   if (a.M >= IMQ_XS_MIN_ROWS && plan_xs(a, cu_count, &x, &xp)) return 0;
   DmaPlan dp;
-  if (a.M >= IMQ_DMA_MIN_ROWS && plan_dma(a, cu_count, &dp)) return dp.bytes;
+  if (take_dma(a, cu_count, &dp)) return dp.bytes;
   return plan_mma(a, (size_t)1 << 40, cu_count).bytes;
 }
 
@@ -2317,7 +2331,7 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* w
   DmaPlan dp;
   if (M >= IMQ_XS_MIN_ROWS && !big && plan_xs(a, dev->cu_count, &xa, &xp)) {
     e = launch_xs(xa, xp, stream);
-  } else if (M >= IMQ_DMA_MIN_ROWS && plan_dma(a, dev->cu_count, &dp) &&
+  } else if (take_dma(a, dev->cu_count, &dp) &&
              (dp.bytes == 0 || (ws && dp.bytes <= ws_bytes))) {
     e = launch_dma(a, dp, ws, stream);
   } else if (M == 1 && plan_m1(a, &m1)) {

@@ -1,7 +1,7 @@
 """GPU parity of the direct-to-LDS MFMA kernel (qmv_dma_kernel), through the C ABI.
 
-The launch plan takes it for M >= 5 when the launch has at most one tile of 64 weight rows
-per CU (256 on MI355X) and every K is a multiple of 256: whole-K tiles when there are more
+The launch plan takes it for M >= 5 (M >= 3 with whole-K tiles) when the launch has at most
+one tile of 64 weight rows per CU (256 on MI355X) and every K is a multiple of 256: whole-K tiles when there are more
 tiles than half the CUs, else the groups of each tile split into K-ranges (four-group
 multiples of at most 28 groups, at least 8) toward at least 0.6 workgroups per CU, the last
 range of a tile adding the others' fp32 partials in range order.  The shapes below cover its
@@ -53,6 +53,7 @@ def _check(oracle, pr, y, rows, out_f32=False):
 
 
 @pytest.mark.parametrize("n,k,m,out_f32", [
+    (15360, 3840, 3, False), (15360, 3840, 4, True),
     (15360, 3840, 5, False), (15360, 3840, 8, False), (15360, 3840, 31, False),
     (15360, 3840, 32, False), (15360, 3840, 32, True),
     (8200, 512, 5, False), (8200, 512, 32, True),
