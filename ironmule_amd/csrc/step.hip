@@ -450,6 +450,12 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
 
 constexpr int kMergeBatch = 16;  // splits whose partials a merge loads at once
 constexpr uint32_t kNegZeroPair = 0x80008000u;  // the bf16 pair (-0, -0)
+// 64-key chunks of K and V in flight per task (registers).  At 32 requests x 8 KV heads x
+// 512 keys (768 tasks of three chunks) one measured 21.9 us a launch, two 25.2 and three
+// 35.5 (fewer resident workgroups, and no gain from the deeper prefetch).
+#ifndef IMQ_ATTN_RING
+#define IMQ_ATTN_RING 1
+#endif
 
 struct AttnLds {
   uint4 kv[kChunk][17];  // K rows (padded), or V as uint32 [64][64]
@@ -470,7 +476,7 @@ __device__ __forceinline__ uint16_t ld16_sc1(const uint16_t* base, uint32_t byte
   return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(base, bytes), off, 0, kSc1);
 }
 
-template <typename SRef>
+template <bool kStaged, typename SRef>
 __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs& a, uint4* smem) {
   AttnLds& L = *reinterpret_cast<AttnLds*>(smem);
   const int splits = S.splits, Hkv = S.Hkv, Hq = S.Hq, G = Hq / Hkv;
@@ -493,9 +499,10 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   uint32_t(*vt)[kD / 2] = reinterpret_cast<uint32_t(*)[kD / 2]>(&L.kv[0][0]);
 
   // Chunk rows as raw buffer loads: rows past `last` read row last-1 (in the slot; never
-  // used), a split with nothing to do reads past the buffer (zeros, no traffic).  The
-  // row of the new key is read too (whatever the pool holds there) and replaced by the
-  // new key when staged.
+  // used), chunks at or past `last` read past the buffer (zeros, no traffic).  The row of
+  // the new key is read too (whatever the pool holds there) and replaced by the new key
+  // when staged.  kRing chunks of K and V are in flight in registers: the next one is
+  // issued into a chunk's registers as soon as they are staged in LDS.
   const uint32_t pool_bytes = (uint32_t)(((size_t)(slot_ok ? slot : 0) * Hkv + kvh + 1) * S.capacity * kD * 2);
   const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(S.k_pool, pool_bytes);
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(S.v_pool, pool_bytes);
@@ -503,44 +510,69 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   auto chunk_off = [&](int start, int i) -> uint32_t {
     const int p = tid + kThreads * i;
     const int t = start + (p >> 4) < last ? start + (p >> 4) : last - 1;
-    return first < last ? (uint32_t)((base + (size_t)t * kD) * 2) + 16u * (p & 15) : kPastBuffer;
+    return start < last ? (uint32_t)((base + (size_t)t * kD) * 2) + 16u * (p & 15) : kPastBuffer;
   };
-  uint4 k0 = load_b128(krs, chunk_off(first, 0)), k1 = load_b128(krs, chunk_off(first, 1));
-  uint4 k2 = load_b128(krs, chunk_off(first, 2)), k3 = load_b128(krs, chunk_off(first, 3));
-  if (!a.staged && !wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
-  // the first chunk's values: in flight while q and the new key are rotated
-  uint4 v0 = load_b128(vrs, chunk_off(first, 0)), v1 = load_b128(vrs, chunk_off(first, 1));
-  uint4 v2 = load_b128(vrs, chunk_off(first, 2)), v3 = load_b128(vrs, chunk_off(first, 3));
+  constexpr int kRing = IMQ_ATTN_RING;
+  uint4 kr[kRing][4], vr[kRing][4];
+  auto issue_k = [&](uint4 (&r)[4], int start) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = load_b128(krs, chunk_off(start, i));
+  };
+  auto issue_v = [&](uint4 (&r)[4], int start) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = load_b128(vrs, chunk_off(start, i));
+  };
+  auto issue_ring = [&]() {
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) {
+      issue_k(kr[d], first + d * kChunk);
+      issue_v(vr[d], first + d * kChunk);
+    }
+  };
 
-  // Rotated q heads (wavefront per head) and, on wavefront 0, the new key and value.  Every
-  // element load is issued first, so their round trips overlap each other and the chunk's.
+  // q of the task's heads (a wavefront per head), the new key and value and the norm
+  // weights.  A staged launch reads them first (its inputs are complete; loads return in
+  // issue order, so the rotation below waits only for these) and then puts the chunks in
+  // flight; the persistent form puts the chunks in flight, waits for its input stage and
+  // reads them through sc1.
+  if (!kStaged) {
+    issue_ring();
+    if (!wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
+  }
   const float eps = S.eps;
   const uint32_t qbytes = (uint32_t)(b + 1) * Hq * kD * 2u;
   const uint32_t kvbytes = (uint32_t)(b + 1) * Hkv * kD * 2u;
   const uint32_t kvoff = (uint32_t)((b * Hkv + kvh) * kD) * 2u;
+  auto ld16 = [&](const uint16_t* p, uint32_t bytes, uint32_t off) -> uint32_t {
+    return kStaged ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p, bytes), off, 0, 0)
+                   : (uint32_t)ld16_sc1(p, bytes, off);
+  };
   uint32_t qx[2][2], kx[2] = {0u, 0u}, vx[2] = {0u, 0u};
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int g = wave + 4 * r;
     const uint32_t off = (uint32_t)((b * Hq + kvh * G + (g < G ? g : 0)) * kD) * 2u;
-    qx[r][0] = g < G ? ld16_sc1(S.q, qbytes, off + 2u * lane) : 0u;
-    qx[r][1] = g < G ? ld16_sc1(S.q, qbytes, off + 2u * (lane + 64)) : 0u;
+    qx[r][0] = g < G ? ld16(S.q, qbytes, off + 2u * lane) : 0u;
+    qx[r][1] = g < G ? ld16(S.q, qbytes, off + 2u * (lane + 64)) : 0u;
   }
   if (wave == 0) {
-    kx[0] = ld16_sc1(S.k, kvbytes, kvoff + 2u * lane);
-    kx[1] = ld16_sc1(S.k, kvbytes, kvoff + 2u * (lane + 64));
-    vx[0] = ld16_sc1(S.v, kvbytes, kvoff + 2u * lane);
-    vx[1] = ld16_sc1(S.v, kvbytes, kvoff + 2u * (lane + 64));
+    kx[0] = ld16(S.k, kvbytes, kvoff + 2u * lane);
+    kx[1] = ld16(S.k, kvbytes, kvoff + 2u * (lane + 64));
+    vx[0] = ld16(S.v, kvbytes, kvoff + 2u * lane);
+    vx[1] = ld16(S.v, kvbytes, kvoff + 2u * (lane + 64));
   }
+  const float qn0 = bf(S.q_norm[lane]), qn1 = bf(S.q_norm[lane + 64]);
+  const float kn0 = bf(S.k_norm[lane]), kn1 = bf(S.k_norm[lane + 64]);
+  if (kStaged) issue_ring();
   const float inv_freq = exp2f(-(float)lane * (S.log2_theta / 64.0f));
   float sn, cs;
   sincosf((float)pos * inv_freq, &sn, &cs);
-  auto rotate = [&](uint32_t h0, uint32_t h1, const uint16_t* nw, uint16_t* dst) {
+  auto rotate = [&](uint32_t h0, uint32_t h1, float nw0, float nw1, uint16_t* dst) {
     float x0 = bf(h0), x1 = bf(h1);
     const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
     const float inv = 1.0f / sqrtf(ss / (float)kD + eps);
-    x0 = bf(to_bf(x0 * inv * bf(nw[lane])));
-    x1 = bf(to_bf(x1 * inv * bf(nw[lane + 64])));
+    x0 = bf(to_bf(x0 * inv * nw0));
+    x1 = bf(to_bf(x1 * inv * nw1));
     const float r0 = x0 * cs - x1 * sn;
     const float r1 = x0 * sn + x1 * cs;
     dst[lane] = to_bf(r0);
@@ -549,12 +581,12 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int g = wave + 4 * r;
-    if (g < G) rotate(qx[r][0], qx[r][1], S.q_norm, reinterpret_cast<uint16_t*>(L.qs[g]));
+    if (g < G) rotate(qx[r][0], qx[r][1], qn0, qn1, reinterpret_cast<uint16_t*>(L.qs[g]));
   }
   if (wave == 0) {
     uint16_t* kn = reinterpret_cast<uint16_t*>(L.knew);
     uint16_t* vn = reinterpret_cast<uint16_t*>(L.vnew);
-    rotate(kx[0], kx[1], S.k_norm, kn);
+    rotate(kx[0], kx[1], kn0, kn1, kn);
     vn[lane] = (uint16_t)vx[0];
     vn[lane + 64] = (uint16_t)vx[1];
     if (s == writer) {  // this step's key and value into the pools (read by later launches)
@@ -588,25 +620,23 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   float mc[2], lc[2];
   const uint4* kn4 = reinterpret_cast<const uint4*>(L.knew);
   const uint4* vn4 = reinterpret_cast<const uint4*>(L.vnew);
-  for (int start = first; start < last; start += kChunk) {
+  for (int base_start = first; base_start < last; base_start += kRing * kChunk) {
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) {
+    const int start = base_start + d * kChunk;
+    if (start >= last) break;
     const int count = min(kChunk, last - start);
     __syncthreads();  // the previous chunk's V readers are done
     {
-      const uint4 kr[4] = {k0, k1, k2, k3};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = tid + kThreads * i;
         const int row = p >> 4, col = p & 15;
-        L.kv[row][col] = select4(start + row == newrow ? ~0u : 0u, kn4[col], kr[i]);
+        L.kv[row][col] = select4(start + row == newrow ? ~0u : 0u, kn4[col], kr[d][i]);
       }
     }
     __syncthreads();
-    if (start + kChunk < last) {
-      k0 = load_b128(krs, chunk_off(start + kChunk, 0));
-      k1 = load_b128(krs, chunk_off(start + kChunk, 1));
-      k2 = load_b128(krs, chunk_off(start + kChunk, 2));
-      k3 = load_b128(krs, chunk_off(start + kChunk, 3));
-    }
+    if (start + kRing * kChunk < last) issue_k(kr[d], start + kRing * kChunk);
     // q is re-read from LDS every chunk (an opaque zero offset keeps the compiler from
     // holding a head's 16 q vectors in registers across the chunk loop)
     int qoff = 0;
@@ -618,16 +648,16 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
         const uint4* qv = reinterpret_cast<const uint4*>(L.qs[g]) + qoff;
         float sc = -INFINITY;
         if (lane < count) {
-          float d = 0.0f;
+          float dq = 0.0f;
 #pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
             const uint4 qa = qv[jj], kk = L.kv[lane][jj];
-            d = dot2(qa.x, kk.x, d);
-            d = dot2(qa.y, kk.y, d);
-            d = dot2(qa.z, kk.z, d);
-            d = dot2(qa.w, kk.w, d);
+            dq = dot2(qa.x, kk.x, dq);
+            dq = dot2(qa.y, kk.y, dq);
+            dq = dot2(qa.z, kk.z, dq);
+            dq = dot2(qa.w, kk.w, dq);
           }
-          sc = d * S.scale;
+          sc = dq * S.scale;
         }
         mc[r] = wave_max(sc);
         const float p = lane < count ? expf(sc - mc[r]) : 0.0f;
@@ -637,25 +667,19 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     }
     __syncthreads();  // the K readers are done: V takes the region
     {
-      const uint4 vr[4] = {v0, v1, v2, v3};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = tid + kThreads * i;
         const int row = p >> 4, col = p & 15;
         // rows past the chunk's keys hold -0 (weight +0, so they add -0: no change)
-        const uint4 v = select4(start + row == newrow ? ~0u : 0u, vn4[col], vr[i]);
+        const uint4 v = select4(start + row == newrow ? ~0u : 0u, vn4[col], vr[d][i]);
         const uint32_t z = start + row < last ? 0u : kNegZeroPair, keep = start + row < last ? ~0u : 0u;
         *reinterpret_cast<uint4*>(&vt[row][col * 4]) =
             make_uint4((v.x & keep) | z, (v.y & keep) | z, (v.z & keep) | z, (v.w & keep) | z);
       }
     }
     __syncthreads();
-    if (start + kChunk < last) {
-      v0 = load_b128(vrs, chunk_off(start + kChunk, 0));
-      v1 = load_b128(vrs, chunk_off(start + kChunk, 1));
-      v2 = load_b128(vrs, chunk_off(start + kChunk, 2));
-      v3 = load_b128(vrs, chunk_off(start + kChunk, 3));
-    }
+    if (start + kRing * kChunk < last) issue_v(vr[d], start + kRing * kChunk);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int g = wave + 4 * r;
@@ -676,6 +700,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
         M[r] = mn;
       }
     }
+  }
   }
 
   // this split's partial, then the last split of (b, kvh) merges them in split order
@@ -797,7 +822,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
 __device__ __forceinline__ bool run_task(StageRef S, int task, const StepArgs& a, uint4* smem) {
   bool good = false;
   if (S.kind == kKindAttention) {
-    good = attention_task<StageRef>(S, task, a, smem);
+    good = attention_task<false, StageRef>(S, task, a, smem);
   } else {
     switch (S.xsrc * 16 + S.epi * 4 + S.shape) {
       IMQ_QMV_SHAPES_X2(kXVector, kEpiBf16)
@@ -840,7 +865,7 @@ __global__ __launch_bounds__(kThreads) void qmv_stage_kernel(const Stage S, Step
 
 __global__ __launch_bounds__(kThreads) void attention_stage_kernel(const Stage S, StepArgs a) {
   extern __shared__ uint4 smem[];
-  attention_task<const Stage&>(S, blockIdx.x, a, smem);
+  attention_task<true, const Stage&>(S, blockIdx.x, a, smem);
 }
 
 #undef IMQ_QMV_SHAPES_X2
