@@ -95,6 +95,23 @@ IMQ_API int32_t imq_qmv(const uint32_t* w, const uint16_t* scales, const uint16_
                 int32_t K, int32_t group_size, int32_t bits, int32_t y_dtype, void* stream);
 
 /*
+ * The gate and up projections of a SwiGLU MLP and their product, one launch:
+ *   act[m][n] = bf16(silu(g) * u),  g = bf16(sum_k x[m][k] W_gate[n][k]),
+ *                                   u = bf16(sum_k x[m][k] W_up[n][k]),
+ * the bits of imq_qmv_grouped over (gate, up) at the same M followed by imq_silu_mul.
+ * gate and up are N x K weights of the format above sharing x (M rows, `ldx` apart); act
+ * rows are `ld_act` apart.  5 <= M <= 32 and K % 256 == 0, else IMQ_EUNSUPPORTED (the caller
+ * makes the two launches).  Replaces the fused gate/up launch and the SwiGLU that follows it:
+ *   ironmule/fast.py:186-215             fuse_projections (gate and up in one launch)
+ *   ironmule/dense_plan.py:374-375       silu(gate) * up
+ */
+IMQ_API int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate,
+                const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
+                const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
+                int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                int32_t bits, void* stream);
+
+/*
  * The same product for `count` separate activation vectors xs[i] (each (1, K)) and
  * separate outputs ys[i] (each (1, N)), one weight sweep for all of them.
  *

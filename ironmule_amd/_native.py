@@ -105,6 +105,8 @@ _SIGNATURES = {
                             ctypes.c_size_t, _P], _I32),
     "imq_qmv_grouped_noalloc": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, _I32, _P],
                                 _I32),
+    "imq_qmv_gate_up_silu": ([_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32,
+                              _I32, _P], _I32),
     "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_gather_qmv": ([_P, _P, _P, _I32, _P, _I64, _I32, _P, _I32, _P, _I64, _I32, _I32, _I32,
                         _I32, _I32, _P], _I32),
@@ -527,6 +529,26 @@ def attention_decode(q, k_pool, v_pool, lengths, slots, out, max_len: int, scale
                                       _ptr(slots), _ptr(out), b, hq, hkv, capacity, num_slots,
                                       int(max_len), float(scale), _ptr(workspace),
                                       _stream(stream)))
+    return out
+
+
+def gate_up_silu(gate: tuple[torch.Tensor, torch.Tensor, torch.Tensor],
+                 up: tuple[torch.Tensor, torch.Tensor, torch.Tensor], x: torch.Tensor,
+                 out: torch.Tensor, stream=None) -> torch.Tensor:
+    """out (M, N) bf16 = silu(bf16(x @ gate.T)) * bf16(x @ up.T), one launch; the bits of
+    qmv_grouped over (gate, up) and silu_mul.  5 <= M <= 32, K a multiple of 256
+    (NativeError with the unsupported code otherwise)."""
+    n, k = check_weights(*gate)
+    if check_weights(*up) != (n, k):
+        raise ValueError("gate and up must have the same shape")
+    _require(x, torch.bfloat16, "x")
+    _require(out, torch.bfloat16, "out")
+    if x.dim() != 2 or int(x.shape[1]) != k or tuple(out.shape) != (int(x.shape[0]), n):
+        raise ValueError(f"x must be (M, {k}) and out (M, {n})")
+    m = int(x.shape[0])
+    _check(lib().imq_qmv_gate_up_silu(_ptr(gate[0]), _ptr(gate[1]), _ptr(gate[2]), _ptr(up[0]),
+                                      _ptr(up[1]), _ptr(up[2]), _ptr(x), k, _ptr(out), n, m, n, k,
+                                      GROUP_SIZE, BITS, _stream(stream)))
     return out
 
 

@@ -850,7 +850,12 @@ static_assert(kWK * kRows * 2 == kThreads, "one scale or bias piece per thread")
 static_assert(kStage >= kWN * 64 * 64, "the K-range reduction reuses the stage");
 }  // namespace staged
 
-template <bool PARTIAL>
+// PAIR: the gate/up form.  p[0] is the gate weight, p[1] the up weight (same x, N and K);
+// workgroup i computes gate rows [32 i, 32 i + 32) on its N-wavefront 0 and the same up rows
+// on N-wavefront 1, and writes act[m][n] = bf16(silu(bf16(gate)) * bf16(up)) to p[0].y
+// (row stride p[0].ldy): silu_mul_kernel's expression on the values the grouped launch
+// and its bf16 outputs would give, bit for bit (the rows' sums run the same way).
+template <bool PARTIAL, bool PAIR = false>
 __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, int splits,
                                                                   float* __restrict__ partial,
                                                                   int64_t pstride,
@@ -862,8 +867,11 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   const int pi = blockIdx.y / splits, split = blockIdx.y - pi * splits;
   const Problem& P = a.p[pi];
   const int K = P.K, N = P.N, M = a.M;
-  const int row0 = blockIdx.x * kRows;
-  if (row0 >= N) return;  // past this problem's tiles
+  // a tile's row slot r (0..63) is weight row row0 + r, or (PAIR) row rp0 + r % 32 of the
+  // gate (r < 32) or up (r >= 32) weight
+  const int row0 = PAIR ? 0 : blockIdx.x * kRows;
+  const int rp0 = blockIdx.x * 32;
+  if ((PAIR ? rp0 : row0) >= N) return;  // past this problem's tiles
   const int G = K >> 6, W = K >> 3;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -887,8 +895,16 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
   const __amdgpu_buffer_rsrc_t srsrc = buffer_rsrc(P.s, sb_bytes);
   const __amdgpu_buffer_rsrc_t brsrc = buffer_rsrc(P.b, sb_bytes);
+  const Problem& Pu = a.p[PAIR ? 1 : 0];
+  const __amdgpu_buffer_rsrc_t wrsrc_u = buffer_rsrc(Pu.w, (uint32_t)N * (uint32_t)W * 4u);
+  const __amdgpu_buffer_rsrc_t srsrc_u = buffer_rsrc(Pu.s, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc_u = buffer_rsrc(Pu.b, sb_bytes);
   const __amdgpu_buffer_rsrc_t xrsrc =
       buffer_rsrc(P.x, (uint32_t)((M - 1) * P.ldx * 2 + K * 2));
+  auto slot_row = [&](int r) {  // weight row of tile slot r, clamped to the weight
+    const int n = PAIR ? rp0 + (r & 31) : row0 + r;
+    return n < N ? n : N - 1;
+  };
 
   // Staging.  x piece i of a thread: K-range i / kXPK, row (tid >> 5) + 8 (i % kXPK), piece
   // tid & 31 of the row's 512 bytes.  Weight piece i: row slot (tid >> 3) + 32 i (row =
@@ -901,7 +917,8 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   const uint32_t wdst0 = (uint32_t)((tid >> 3) * kWRow + 16 * wp);
   const int sb_is_b = __builtin_amdgcn_readfirstlane(tid / (kWK * kRows));
   const int sb_rem = tid % (kWK * kRows), sb_k = sb_rem / kRows;
-  const int sb_n = row0 + sb_rem % kRows < N ? row0 + sb_rem % kRows : N - 1;
+  const int sb_n = slot_row(sb_rem % kRows);
+  const bool sb_up = PAIR && sb_rem % kRows >= 32;  // per lane: the up weight's row
   const uint32_t sb_src = (uint32_t)sb_n * (uint32_t)G * 2u;
   const uint32_t sb_dst = (uint32_t)(kWBytes + kXBytes + sb_rem * 16 + 8 * sb_is_b);
 
@@ -918,15 +935,24 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
 #pragma unroll
     for (int i = 0; i < kWP; ++i) {
       const int slot = (tid >> 3) + 32 * i, k = slot / kRows;
-      const int n = row0 + slot % kRows < N ? row0 + slot % kRows : N - 1;
+      const int n = slot_row(slot % kRows);
       const int g = klo[k] + (wp >> 1) + 4 * st;
       const uint32_t off = (uint32_t)n * (uint32_t)W * 4u + 16u * (wp & 1) + 32u * (uint32_t)g;
-      wreg[i] = load_b128_nt(wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
+      // slot % kRows < 32 exactly for even i: the weight is uniform per instruction
+      wreg[i] = load_b128_nt(PAIR && (i & 1) ? wrsrc_u : wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
     }
     const int g = klo[sb_k] + 4 * st;
     const uint32_t off = (sb_src + 2u * (uint32_t)g) | ((uint32_t)(g >= khi[sb_k]) << 31);
-    sbreg = __builtin_bit_cast(u32x2_t,
-                               __builtin_amdgcn_raw_buffer_load_b64(sb_is_b ? brsrc : srsrc, off, 0, 0));
+    if (PAIR) {  // gate and up rows share the wavefront: each lane reads from one of them
+      const u32x2_t sg = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+          sb_is_b ? brsrc : srsrc, sb_up ? kPastBuffer : off, 0, 0));
+      const u32x2_t su = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+          sb_is_b ? brsrc_u : srsrc_u, sb_up ? off : kPastBuffer, 0, 0));
+      sbreg = u32x2_t{sg[0] | su[0], sg[1] | su[1]};
+    } else {
+      sbreg = __builtin_bit_cast(u32x2_t,
+                                 __builtin_amdgcn_raw_buffer_load_b64(sb_is_b ? brsrc : srsrc, off, 0, 0));
+    }
   };
   auto store = [&]() {
 #pragma unroll
@@ -997,6 +1023,27 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   if (wk > 0) red[wn * 64 + lane] = acc;
   __syncthreads();
   if (wk == 0) acc += red[wn * 64 + lane];
+  if (PAIR) {
+    // the up tile's values to the gate wavefront, which writes SiLU(gate) * up
+    __syncthreads();  // every wavefront is done with the K-range sums in LDS
+    if (wk == 0 && wn == 1) red[lane] = acc;
+    __syncthreads();
+    if (wk == 0 && wn == 0) {
+      const f32x16_t up = red[lane];
+      const int n = rp0 + r;
+      uint16_t* act = static_cast<uint16_t*>(P.y);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M && n < N) {
+          const float g0 = bf16_bits_to_f32(f32_to_bf16_bits(acc[e]));
+          const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(up[e]));
+          act[(size_t)m * P.ldy + n] = f32_to_bf16_bits(g0 / (1.0f + expf(-g0)) * u0);
+        }
+      }
+    }
+    return;
+  }
   f32x16_t tiles[1] = {acc};
   finish_tiles<1, PARTIAL, kMaxSplitsStaged>(a, P, pi, split, splits, partial, pstride, counters,
                                              tiles_max, tiles,
@@ -2403,6 +2450,35 @@ int32_t imq_qmv(const uint32_t* w, const uint16_t* scales, const uint16_t* biase
   a.M = M;
   a.y_f32 = (y_dtype == IMQ_F32);
   return launch(a, dev, static_cast<hipStream_t>(stream));
+}
+
+int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate,
+                             const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
+                             const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
+                             int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                             int32_t bits, void* stream) {
+  int32_t code = check_format(N, K, group_size, bits);
+  if (code != IMQ_OK) return code;
+  if ((code = check_weights(w_gate, s_gate, b_gate)) != IMQ_OK) return code;
+  if ((code = check_weights(w_up, s_up, b_up)) != IMQ_OK) return code;
+  if ((code = check_rows(x, ldx, act, ld_act, M, N, K, IMQ_BF16)) != IMQ_OK) return code;
+  if (M < 5 || K % 256 != 0)
+    return fail(IMQ_EUNSUPPORTED, "the fused gate/up launch takes 5 to 32 rows and K a multiple of 256");
+  if ((int64_t)N * (K / 2) >= ((int64_t)1 << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= ((int64_t)1 << 31))
+    return fail(IMQ_EUNSUPPORTED, "a weight or activation of 2 GiB or more exceeds the kernel's offsets");
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
+  LaunchArgs a;
+  memset(&a, 0, sizeof(a));
+  a.p[0] = Problem{w_gate, s_gate, b_gate, x, act, ldx, ld_act, N, K, 0, 0, 0, 0};
+  a.p[1] = Problem{w_up, s_up, b_up, x, nullptr, ldx, ld_act, N, K, 0, 0, 0, 0};
+  a.count = 2;
+  a.M = M;
+  hipLaunchKernelGGL((qmv_mma_staged_kernel<false, true>), dim3((N + 31) / 32, 1), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), a, 1, nullptr, (int64_t)0, nullptr, 0);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("gate/up launch failed: ") + hipGetErrorString(e));
+  return ok();
 }
 
 int32_t imq_qmv_multi(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

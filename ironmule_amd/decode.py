@@ -14,8 +14,9 @@ continuous-batched requests, each with its own KV slot and position:
                                                imq_attention_decode)
         h += o @ Wo.T                          imq_qmv, added by the next imq_add_rmsnorm
         x = rms_norm(h)
-        g, u = x @ Wg.T, x @ Wu.T              imq_qmv_grouped
-        h += (silu(g) * u) @ Wd.T              imq_silu_mul, imq_qmv
+        g, u = x @ Wg.T, x @ Wu.T              imq_qmv_gate_up_silu (from 5 requests: one
+        h += (silu(g) * u) @ Wd.T              launch), else imq_qmv_grouped + imq_silu_mul;
+                                               imq_qmv
     logits = rms_norm(h) @ E.T                 imq_add_rmsnorm, imq_qmv (fp32, tied head)
 
 All buffers are allocated once per (model, batch size) in `DecodeState`; a step only
@@ -178,8 +179,12 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
                           c.eps, s.workspace, s.attn_counters, stream=stream)
         n.qmv(*layer["o"], s.attn, out=s.delta, stream=stream)
         n.add_rmsnorm(s.h, layer["post_norm"], s.x, c.eps, delta=s.delta, stream=stream)
-        n.qmv_grouped([layer["gate"], layer["up"]], [s.x, s.x], outs=[s.gate, s.up], stream=stream)
-        n.silu_mul(s.gate, s.up, s.act, stream=stream)
+        if s.batch >= 5:  # gate, up and SiLU * up in one launch (the same bits)
+            n.gate_up_silu(layer["gate"], layer["up"], s.x, s.act, stream=stream)
+        else:
+            n.qmv_grouped([layer["gate"], layer["up"]], [s.x, s.x], outs=[s.gate, s.up],
+                          stream=stream)
+            n.silu_mul(s.gate, s.up, s.act, stream=stream)
         n.qmv(*layer["down"], s.act, out=s.delta, stream=stream)
         delta = s.delta
     n.add_rmsnorm(s.h, weights.norm, s.x, c.eps, delta=delta, stream=stream)
