@@ -1024,22 +1024,23 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   __syncthreads();
   if (wk == 0) acc += red[wn * 64 + lane];
   if (PAIR) {
-    // the up tile's values to the gate wavefront, which writes SiLU(gate) * up
+    // the gate and up tiles to LDS as [tile][e][lane], then every thread writes four of the
+    // 32 x 32 SiLU(gate) * up values
+    float* tiles2 = reinterpret_cast<float*>(lds);
     __syncthreads();  // every wavefront is done with the K-range sums in LDS
-    if (wk == 0 && wn == 1) red[lane] = acc;
-    __syncthreads();
-    if (wk == 0 && wn == 0) {
-      const f32x16_t up = red[lane];
-      const int n = rp0 + r;
-      uint16_t* act = static_cast<uint16_t*>(P.y);
+    if (wk == 0)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = 8 * (e >> 2) + 4 * h + (e & 3);
-        if (m < M && n < N) {
-          const float g0 = bf16_bits_to_f32(f32_to_bf16_bits(acc[e]));
-          const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(up[e]));
-          act[(size_t)m * P.ldy + n] = f32_to_bf16_bits(g0 / (1.0f + expf(-g0)) * u0);
-        }
+      for (int e = 0; e < 16; ++e) tiles2[(wn * 16 + e) * 64 + lane] = acc[e];
+    __syncthreads();
+    uint16_t* act = static_cast<uint16_t*>(P.y);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int idx = tid + kThreads * q, e = idx >> 6, l = idx & 63;
+      const int m = 8 * (e >> 2) + 4 * (l >> 5) + (e & 3), n = rp0 + (l & 31);
+      if (m < M && n < N) {
+        const float g0 = bf16_bits_to_f32(f32_to_bf16_bits(tiles2[e * 64 + l]));
+        const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(tiles2[(16 + e) * 64 + l]));
+        act[(size_t)m * P.ldy + n] = f32_to_bf16_bits(g0 / (1.0f + expf(-g0)) * u0);
       }
     }
     return;
