@@ -180,16 +180,24 @@ __device__ __forceinline__ uint4 load_b128_nt(__amdgpu_buffer_rsrc_t rsrc, uint3
 
 // ------------------------------------------------------------------ wavefront sums
 
+// Sum (max) over the wavefront, in every lane: each 16-lane row by DPP, then the four row
+// results read from lanes 0, 16, 32 and 48 and combined as (r0 + r1) + (r2 + r3).  No LDS
+// round trips (a __shfl_xor butterfly costs six of them in a chain).
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v = row16_sum(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 // ------------------------------------------------ device-coherent accesses (sc1)
