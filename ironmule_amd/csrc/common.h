@@ -180,6 +180,17 @@ __device__ __forceinline__ uint4 load_b128_nt(__amdgpu_buffer_rsrc_t rsrc, uint3
 
 // ------------------------------------------------------------------ wavefront sums
 
+// v plus the value of lane l ^ 16 (l ^ 32) in every lane l, by the lane-swap instructions
+// (no LDS round trip); the same sums as v + __shfl_xor(v, 16 / 32).
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
 // Sum (max) over the wavefront, in every lane: each 16-lane row by DPP, then the four row
 // results read from lanes 0, 16, 32 and 48 and combined as (r0 + r1) + (r2 + r3).  No LDS
 // round trips (a __shfl_xor butterfly costs six of them in a chain).

@@ -233,8 +233,8 @@ __global__ __launch_bounds__(kThreads) void qmv_rows_kernel(LaunchArgs a) {
         if (i < W) {  // the four words of a chunk are four aligned lanes (W % 4 == 0)
           xq[(m * 4 + (i & 3)) * C + (i >> 2)] = pair_order(xs[m][t]);
           float part = sum8(xs[m][t]);
-          part += __shfl_xor(part, 1);
-          part += __shfl_xor(part, 2);
+          part += dpp<0xB1>(part);  // lane ^ 1
+          part += dpp<0x4E>(part);  // lane ^ 2
           if ((i & 3) == 0) sx[m * C + (i >> 2)] = part;
         }
       }
@@ -257,8 +257,8 @@ __global__ __launch_bounds__(kThreads) void qmv_rows_kernel(LaunchArgs a) {
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     float v = row16_sum(acc[m]);
-    if (sh >= 5) v += __shfl_xor(v, 16);
-    if (sh >= 6) v += __shfl_xor(v, 32);
+    if (sh >= 5) v = add_xor16(v);
+    if (sh >= 6) v = add_xor32(v);
     if (j == 0 && row < N) store_y(a, P, m, row, v);
   }
 }
@@ -366,8 +366,8 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
       const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
       xq[(m * 4 + (i & 3)) * CP + (i >> 2)] = pair_order(xs[m][t]);
       float part = sum8(xs[m][t]);
-      part += __shfl_xor(part, 1);
-      part += __shfl_xor(part, 2);
+      part += dpp<0xB1>(part);  // lane ^ 1
+      part += dpp<0x4E>(part);  // lane ^ 2
       if ((i & 3) == 0) sx[m * CP + (i >> 2)] = part;
     }
   }
@@ -407,8 +407,8 @@ __device__ __forceinline__ void m1_tile(const uint32_t* wp, const uint16_t* sp, 
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     float v = row16_sum(acc[m]);
-    if (sh >= 5) v += __shfl_xor(v, 16);
-    if (sh >= 6) v += __shfl_xor(v, 32);
+    if (sh >= 5) v = add_xor16(v);
+    if (sh >= 6) v = add_xor32(v);
     if (j == 0 && row < N) {
       if (yf32)
         static_cast<float*>(yps[m])[row] = v;
@@ -1282,8 +1282,8 @@ __global__ __launch_bounds__(64 * xs::Shape<MB>::kWaves) void qmv_xs_kernel(XsAr
           part = dot2(v.w, ones, part);
           xa[mb][g][p] = as_bf16x8(pair_order(v));
         }
-        part += __shfl_xor(part, 16);
-        part += __shfl_xor(part, 32);  // the row's sum over the group, in every kb lane
+        part = add_xor16(part);
+        part = add_xor32(part);  // the row's sum over the group, in every kb lane
         if (kb == (g & 3)) sxa[mb][g >> 2] = part;
       }
       __builtin_amdgcn_sched_barrier(0);  // group by group: the raw x dies as it is converted
@@ -1556,7 +1556,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
         half = dot2(xg.v[t].z, one, half);
         half = dot2(xg.v[t].w, one, half);
       }
-      const float gsum = half + __shfl_xor(half, 32);  // row j over the whole group
+      const float gsum = add_xor32(half);  // row j over the whole group
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int r = 32 * t + j;

@@ -382,8 +382,8 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
     const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
     xq[(i & 3) * CP + (i >> 2)] = pair_order(xs[t]);
     float part = sum8(xs[t]);
-    part += __shfl_xor(part, 1);
-    part += __shfl_xor(part, 2);
+    part += dpp<0xB1>(part);  // lane ^ 1
+    part += dpp<0x4E>(part);  // lane ^ 2
     if ((i & 3) == 0) sx[i >> 2] = part;
   }
   const int sbase = kPair && tid >= 128 ? 4 * G : 0;  // dword offset of the up rows' span
@@ -415,8 +415,8 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
     }
   }
   float v = row16_sum(acc);
-  if (sh >= 5) v += __shfl_xor(v, 16);
-  if (sh >= 6) v += __shfl_xor(v, 32);
+  if (sh >= 5) v = add_xor16(v);
+  if (sh >= 6) v = add_xor32(v);
 
   if (EPI == kEpiBf16) {
     if (owner) store_b16_sc1(buffer_rsrc(S.p[qi].y, (uint32_t)N * 2u), 2u * row, to_bf(v));

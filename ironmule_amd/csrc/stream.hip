@@ -357,8 +357,8 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
   for (int t = 0; t < kXr; ++t) {
     const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
     float part = sum8(xs[t]);
-    part += __shfl_xor(part, 1);
-    part += __shfl_xor(part, 2);
+    part += dpp<0xB1>(part);  // lane ^ 1
+    part += dpp<0x4E>(part);  // lane ^ 2
     if (i < W) {
       char* chunk = dst + (size_t)kXChunk * (i >> 2);
       reinterpret_cast<uint4*>(chunk)[i & 3] = pair_order(xs[t]);
