@@ -44,6 +44,16 @@ IMQ_API int32_t imq_embed(const uint32_t* w, const uint16_t* scales, const uint1
                           const int32_t* tokens, float* h, int32_t B, int32_t vocab, int32_t dim,
                           void* stream);
 
+/* The first half of an RMSNorm folded into the projection that follows it: if delta is
+ * non-NULL, h += delta (bf16) first; then out = bf16(h * weight) (not normalised) and
+ * ssq[b * ld] = sum of h[b][:]^2, the one partial sum per row that imq_qmv_norm or
+ * imq_qmv_gate_up_silu_norm (ironmule_qmv.h, imq_norm_in with tiles = 1) turns into the row's
+ * 1/rms.  ssq 16-byte aligned, ld a multiple of 4; dim <= 8192.
+ * Replaces the input RMSNorm of the first layer, ironmule/dense_plan.py:348. */
+IMQ_API int32_t imq_rmsnorm_prescale(float* h, const uint16_t* delta, const uint16_t* weight,
+                                     uint16_t* out, float* ssq, int32_t ld, int32_t B, int32_t dim,
+                                     void* stream);
+
 /* If delta is non-NULL, h += delta (bf16) first; then out = bf16(h * rsqrt(mean(h^2) + eps)
  * * weight), per row of dim values (dim <= 8192).
  * Replaces mx.fast.rms_norm(h, weight, eps) and the residual adds `h = h + ...`

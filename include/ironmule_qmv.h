@@ -112,6 +112,69 @@ IMQ_API int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_g
                 int32_t bits, void* stream);
 
 /*
+ * An RMSNorm folded into the projections around it (decode glue).  With
+ * inv_m = 1 / sqrt(sum_n h[m][n]^2 / dim + eps), rms_norm(h) W^T = inv * ((h * w) W^T) row by
+ * row, so the kernel that produces the residual stream h writes x' = bf16(h * w) and per
+ * 64-column tile of h each row's partial sum of squares, and the projection that reads x'
+ * scales its output rows by inv: the RMSNorm needs no launch of its own.  The rounding
+ * points differ from bf16(bf16(h * inv) * w) by the place of one bf16 rounding.
+ * Replaces the RMSNorm launches between the projections of the reference's decode step,
+ * ironmule/dense_plan.py:348 and 359 (the input and post-attention norms).
+ */
+typedef struct imq_norm_in {
+  const float* ssq;  /* row m's partial sums at ssq[m * ld + t], t < tiles; 16-byte aligned */
+  int32_t tiles;     /* 1..64 partials per row, added in a fixed order */
+  int32_t ld;        /* a multiple of 4, >= tiles */
+  int32_t dim;       /* h's row length, the mean's divisor */
+  float eps;
+} imq_norm_in;
+
+typedef struct imq_residual_out {
+  float* h;                /* (M, N) fp32 residual rows, ldh apart: h += bf16(y) */
+  int64_t ldh;
+  const uint16_t* weight;  /* (N) bf16 weight of the next RMSNorm; NULL: update h only */
+  uint16_t* x;             /* (M, N) bf16 x' = bf16(h * weight), rows ldx apart */
+  int64_t ldx;
+  float* ssq;              /* NULL, or (M, ld): ssq[m * ld + t] = sum of h[m][n]^2 over
+                            * the 64 columns n of tile t, t < ceil(N / 64) */
+  int32_t ld;              /* a multiple of 4, >= ceil(N / 64) */
+} imq_residual_out;
+
+/* Bytes of workspace imq_qmv_norm needs for these problems at M rows (zero-filled before
+ * its first use, left ready by every call, as for imq_qmv_grouped_ws). */
+IMQ_API size_t imq_qmv_norm_workspace(const imq_problem* problems, int32_t count, int32_t M);
+
+/*
+ * imq_qmv_grouped_ws (bf16 outputs) with the RMSNorm of the inputs and/or the residual add
+ * of the output folded in.  `in` (or NULL): every output row m is scaled by inv_m before
+ * rounding, x being x' (the x rows of every problem).  `out` (or NULL; one problem only):
+ * instead of writing y, h[m][n] += bf16(y[m][n]) (the bits a bf16 y added to h in fp32
+ * gives), then x'[m][n] = bf16(h * weight[n]) and the per-tile sums of squares of the new
+ * h for the next RMSNorm; the problem's y may be NULL.  x, y, h, x' and ssq must not
+ * overlap.  M 1..32, K % 256 == 0; workspace of imq_qmv_norm_workspace bytes.  Same bits on
+ * every call.  Replaces the projections of the reference's decode step together with the
+ * RMSNorm before them and the residual add after them, ironmule/dense_plan.py:348-361.
+ */
+IMQ_API int32_t imq_qmv_norm(const imq_problem* problems, int32_t count, int32_t M,
+                             int32_t group_size, int32_t bits, const imq_norm_in* in,
+                             const imq_residual_out* out, float* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
+ * imq_qmv_gate_up_silu on x' rows with the input RMSNorm folded in (`in` non-NULL):
+ *   act[m][n] = bf16(silu(g) * u),  g = bf16(inv_m * sum_k x'[m][k] W_gate[n][k]),
+ *                                   u = bf16(inv_m * sum_k x'[m][k] W_up[n][k]).
+ * Same shapes and limits as imq_qmv_gate_up_silu.  Replaces the post-attention RMSNorm,
+ * the fused gate/up launch and the SwiGLU, ironmule/dense_plan.py:359-360 and
+ * ironmule/fast.py:186-215.
+ */
+IMQ_API int32_t imq_qmv_gate_up_silu_norm(const uint32_t* w_gate, const uint16_t* s_gate,
+                const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
+                const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
+                int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                int32_t bits, const imq_norm_in* in, void* stream);
+
+/*
  * The same product for `count` separate activation vectors xs[i] (each (1, K)) and
  * separate outputs ys[i] (each (1, N)), one weight sweep for all of them.
  *
@@ -177,16 +240,6 @@ IMQ_API int32_t imq_qmv_grouped_noalloc(const imq_problem* problems, int32_t cou
                                         int32_t group_size, int32_t bits, int32_t y_dtype,
                                         void* stream);
 
-/*
- * out[n][k] = scales[n][k/64] * q[n][k] + biases[n][k/64] as fp32 (bit-exact:
- * scale*q is exact in fp32, so only the add rounds), or that fp32 value rounded
- * to bf16 / fp16 (nearest even) per out_dtype.  out is (N, K) contiguous.
- *
- * Replaces mx.dequantize on the path:
- *   ironmule/cuda_native.py:177-179      prefill: dequantise (fp16) then GEMM
- *   ironmule/cuda_native.py:265-266      probe reference: dequantise with fp32 scales
- *   ironmule/numeric_plans.py:462-464    the `dequantize` plan's fp32 weights
- */
 /* MoE gather: for each of `pairs` (token, expert) pairs p, the one-row product
  *   y[p] = x[p / rows_per_x] W[idx[p]]^T
  * where w, scales and biases hold `experts` stacked weights ((E, N, K/8) words and
@@ -203,6 +256,16 @@ IMQ_API int32_t imq_gather_qmv(const uint32_t* w, const uint16_t* scales, const 
                                int32_t K, int32_t group_size, int32_t bits, int32_t y_dtype,
                                void* stream);
 
+/*
+ * out[n][k] = scales[n][k/64] * q[n][k] + biases[n][k/64] as fp32 (bit-exact:
+ * scale*q is exact in fp32, so only the add rounds), or that fp32 value rounded
+ * to bf16 / fp16 (nearest even) per out_dtype.  out is (N, K) contiguous.
+ *
+ * Replaces mx.dequantize on the path:
+ *   ironmule/cuda_native.py:177-179      prefill: dequantise (fp16) then GEMM
+ *   ironmule/cuda_native.py:265-266      probe reference: dequantise with fp32 scales
+ *   ironmule/numeric_plans.py:462-464    the `dequantize` plan's fp32 weights
+ */
 IMQ_API int32_t imq_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     void* out, int32_t out_dtype, int32_t N, int32_t K, int32_t group_size,
                     int32_t bits, void* stream);

@@ -63,6 +63,19 @@ class Problem(ctypes.Structure):
                 ("y", _P), ("ldy", _I64), ("N", _I32), ("K", _I32)]
 
 
+class NormIn(ctypes.Structure):
+    """imq_norm_in: per-row partial sums of squares from which a projection scales its rows."""
+
+    _fields_ = [("ssq", _P), ("tiles", _I32), ("ld", _I32), ("dim", _I32), ("eps", ctypes.c_float)]
+
+
+class ResidualOut(ctypes.Structure):
+    """imq_residual_out: h += bf16(y), x' = bf16(h * weight) and the tiles' sums of squares."""
+
+    _fields_ = [("h", _P), ("ldh", _I64), ("weight", _P), ("x", _P), ("ldx", _I64), ("ssq", _P),
+                ("ld", _I32)]
+
+
 class QWeight(ctypes.Structure):
     """imq_qweight: packed words, bf16 scales, bf16 biases."""
 
@@ -107,6 +120,12 @@ _SIGNATURES = {
                                 _I32),
     "imq_qmv_gate_up_silu": ([_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32,
                               _I32, _P], _I32),
+    "imq_qmv_norm_workspace": ([ctypes.POINTER(Problem), _I32, _I32], ctypes.c_size_t),
+    "imq_qmv_norm": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, ctypes.POINTER(NormIn),
+                      ctypes.POINTER(ResidualOut), _P, ctypes.c_size_t, _P], _I32),
+    "imq_qmv_gate_up_silu_norm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32,
+                                   _I32, _I32, ctypes.POINTER(NormIn), _P], _I32),
+    "imq_rmsnorm_prescale": ([_P, _P, _P, _P, _P, _I32, _I32, _I32, _P], _I32),
     "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_gather_qmv": ([_P, _P, _P, _I32, _P, _I64, _I32, _P, _I32, _P, _I64, _I32, _I32, _I32,
                         _I32, _I32, _P], _I32),
@@ -549,6 +568,128 @@ def gate_up_silu(gate: tuple[torch.Tensor, torch.Tensor, torch.Tensor],
     _check(lib().imq_qmv_gate_up_silu(_ptr(gate[0]), _ptr(gate[1]), _ptr(gate[2]), _ptr(up[0]),
                                       _ptr(up[1]), _ptr(up[2]), _ptr(x), k, _ptr(out), n, m, n, k,
                                       GROUP_SIZE, BITS, _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------- RMSNorm folded into projections
+
+class NormStats:
+    """Per-row partial sums of squares of a residual stream h: `ssq` (rows, ld) fp32 with
+    `tiles` partials per row, the input of a projection that folds in the RMSNorm
+    (imq_norm_in).  The producer fills `tiles` of them: one for rmsnorm_prescale, one per
+    64 columns of h for qmv_norm's residual epilogue."""
+
+    def __init__(self, rows: int, dim: int, device) -> None:
+        self.dim = dim
+        tiles = -(-dim // 64)
+        self.ld = -(-tiles // 4) * 4
+        self.ssq = torch.zeros((rows, self.ld), dtype=torch.float32, device=device)
+        self.tiles = 1
+
+    def norm_in(self, eps: float) -> NormIn:
+        return NormIn(self.ssq.data_ptr(), self.tiles, self.ld, self.dim, float(eps))
+
+
+def rmsnorm_prescale(h: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, stats: NormStats,
+                     delta: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """h += delta (if given); out = bf16(h * weight) unnormalised, and one sum of squares per
+    row into `stats` (the RMSNorm finished by the projection that reads `out`)."""
+    _require(h, torch.float32, "h")
+    _require(weight, torch.bfloat16, "weight")
+    _require(out, torch.bfloat16, "out")
+    b, dim = h.shape
+    if delta is not None:
+        _require(delta, torch.bfloat16, "delta")
+        if delta.numel() != h.numel():
+            raise ValueError("delta must match h")
+    if out.numel() != h.numel() or weight.numel() != dim or stats.dim != dim or stats.ssq.shape[0] < b:
+        raise ValueError("out must match h, weight and stats its row length")
+    _check(lib().imq_rmsnorm_prescale(_ptr(h), _ptr(delta) if delta is not None else None,
+                                      _ptr(weight), _ptr(out), _ptr(stats.ssq), stats.ld, b, dim,
+                                      _stream(stream)))
+    stats.tiles = 1
+    return out
+
+
+def qmv_norm(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]], x: torch.Tensor,
+             outs: list[torch.Tensor] | None = None, norm_in: NormStats | None = None,
+             eps: float = 1e-6, residual: torch.Tensor | None = None,
+             next_norm: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
+             stats_out: NormStats | None = None, stream=None):
+    """Projections of one bf16 activation x (M, K) with the RMSNorm folded in (imq_qmv_norm).
+
+    norm_in: x is x' = bf16(h * w) and every output row is scaled by 1/rms(h) from these
+    statistics.  residual (one weight): no output is written; instead residual (M, N fp32)
+    += bf16(y), x_out = bf16(residual * next_norm) and stats_out gets the per-tile sums of
+    squares of the new residual.  Returns the bf16 outputs (none with a residual)."""
+    count = len(weights)
+    if not 1 <= count <= MAX_PROBLEMS:
+        raise ValueError(f"1 to {MAX_PROBLEMS} weights")
+    _require(x, torch.bfloat16, "x")
+    if x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous (M, K) tensor")
+    m = int(x.shape[0])
+    if not 1 <= m <= MAX_ROWS:
+        raise ValueError(f"the qmv kernels take 1 to {MAX_ROWS} rows, got {m}")
+    if residual is not None and (count != 1 or outs is not None):
+        raise ValueError("a residual epilogue takes one weight and writes no output")
+    probs = (Problem * count)()
+    result = []
+    for i, (w, s, b) in enumerate(weights):
+        n, k = check_weights(w, s, b)
+        if int(x.shape[1]) != k:
+            raise ValueError(f"weight {i} takes K = {k}, x has {int(x.shape[1])}")
+        y = None
+        if residual is None:
+            y = outs[i] if outs is not None else torch.empty((m, n), dtype=torch.bfloat16, device=w.device)
+            if tuple(y.shape) != (m, n) or y.dtype != torch.bfloat16 or not y.is_contiguous():
+                raise ValueError(f"output {i} must be a contiguous ({m}, {n}) bf16 tensor")
+            result.append(y)
+        probs[i] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), k,
+                           y.data_ptr() if y is not None else None, n, n, k)
+    nin = norm_in.norm_in(eps) if norm_in is not None else None
+    rout = None
+    if residual is not None:
+        n = int(weights[0][0].shape[0])
+        _require(residual, torch.float32, "residual")
+        if tuple(residual.shape) != (m, n) or not residual.is_contiguous():
+            raise ValueError(f"residual must be a contiguous ({m}, {n}) fp32 tensor")
+        if next_norm is not None:
+            _require(next_norm, torch.bfloat16, "next_norm")
+            if x_out is None or tuple(x_out.shape) != (m, n) or x_out.dtype != torch.bfloat16:
+                raise ValueError(f"x_out must be a ({m}, {n}) bf16 tensor")
+        rout = ResidualOut(residual.data_ptr(), n, next_norm.data_ptr() if next_norm is not None else None,
+                           x_out.data_ptr() if next_norm is not None else None, n,
+                           stats_out.ssq.data_ptr() if stats_out is not None else None,
+                           stats_out.ld if stats_out is not None else 0)
+    nbytes = int(lib().imq_qmv_norm_workspace(probs, count, m))
+    ws = _workspace(nbytes, weights[0][0].device, stream) if nbytes else None
+    _check(lib().imq_qmv_norm(probs, count, m, GROUP_SIZE, BITS,
+                              ctypes.byref(nin) if nin is not None else None,
+                              ctypes.byref(rout) if rout is not None else None,
+                              _ptr(ws) if ws is not None else None, ws.numel() * 4 if ws is not None else 0,
+                              _stream(stream)))
+    if stats_out is not None:
+        stats_out.tiles = -(-int(weights[0][0].shape[0]) // 64)
+    return result
+
+
+def gate_up_silu_norm(gate, up, x: torch.Tensor, out: torch.Tensor, norm_in: NormStats,
+                      eps: float, stream=None) -> torch.Tensor:
+    """gate_up_silu on x' = bf16(h * w) with the RMSNorm folded in: the gate and up rows are
+    scaled by 1/rms(h) from `norm_in` before the SwiGLU."""
+    n, k = check_weights(*gate)
+    if check_weights(*up) != (n, k):
+        raise ValueError("gate and up must have the same shape")
+    _require(x, torch.bfloat16, "x")
+    _require(out, torch.bfloat16, "out")
+    if x.dim() != 2 or int(x.shape[1]) != k or tuple(out.shape) != (int(x.shape[0]), n):
+        raise ValueError(f"x must be (M, {k}) and out (M, {n})")
+    m = int(x.shape[0])
+    nin = norm_in.norm_in(eps)
+    _check(lib().imq_qmv_gate_up_silu_norm(_ptr(gate[0]), _ptr(gate[1]), _ptr(gate[2]), _ptr(up[0]),
+                                           _ptr(up[1]), _ptr(up[2]), _ptr(x), k, _ptr(out), n, m, n,
+                                           k, GROUP_SIZE, BITS, ctypes.byref(nin), _stream(stream)))
     return out
 
 

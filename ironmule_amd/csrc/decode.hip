@@ -71,12 +71,17 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t* __restr
 // value and masked), so the row costs one memory round trip.  The sum of squares is added
 // per thread, then over each wavefront (butterfly), then over the four wavefronts in
 // order, so the result does not depend on scheduling.
-template <int VPT>
+//
+// PRE (the RMSNorm folded into the next projection): out = bf16(h * weight), unnormalised,
+// and ssq[row * ld] = the row's sum of squares, from which that projection scales its
+// output rows.
+template <int VPT, bool PRE = false>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(float* __restrict__ h,
                                                                const uint16_t* __restrict__ delta,
                                                                const uint16_t* __restrict__ weight,
                                                                uint16_t* __restrict__ out, int dim,
-                                                               float eps) {
+                                                               float eps, float* __restrict__ ssq = nullptr,
+                                                               int ld = 0) {
   __shared__ float red[kThreads / 64];
   const int row = blockIdx.x, tid = threadIdx.x;
   float* hr = h + (size_t)row * dim;
@@ -104,12 +109,13 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(float* __restrict
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   const float total = (red[0] + red[1]) + (red[2] + red[3]);
-  const float inv = 1.0f / sqrtf(total / (float)dim + eps);
+  const float inv = PRE ? 1.0f : 1.0f / sqrtf(total / (float)dim + eps);
+  if (PRE && tid == 0) ssq[(size_t)row * ld] = total;
   uint16_t* orow = out + (size_t)row * dim;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int idx = tid + kThreads * i;
-    if (idx < dim) orow[idx] = to_bf(v[i] * inv * bf(wv[i]));
+    if (idx < dim) orow[idx] = to_bf(PRE ? v[i] * bf(wv[i]) : v[i] * inv * bf(wv[i]));
   }
 }
 
@@ -476,6 +482,26 @@ int32_t imq_add_rmsnorm(float* h, const uint16_t* delta, const uint16_t* weight,
   else
     hipLaunchKernelGGL(add_rmsnorm_kernel<kNormVpt>, dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, eps);
   return launched("add_rmsnorm");
+}
+
+int32_t imq_rmsnorm_prescale(float* h, const uint16_t* delta, const uint16_t* weight, uint16_t* out,
+                             float* ssq, int32_t ld, int32_t B, int32_t dim, void* stream) {
+  if (!h || !weight || !out || !ssq) return fail(IMQ_EINVAL, "null pointer");
+  if (B < 1 || dim < 1 || dim > kMaxNormDim) return fail(IMQ_EINVAL, "B >= 1 and 1 <= dim <= 8192");
+  if (ld < 4 || ld % 4 || !aligned(ssq, 16)) return fail(IMQ_EINVAL, "ssq must be 16-byte aligned, ld a multiple of 4");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int vpt = (dim + kThreads - 1) / kThreads;
+  if (vpt <= 4)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<4, true>), dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, 0.0f, ssq, ld);
+  else if (vpt <= 10)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<10, true>), dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, 0.0f, ssq, ld);
+  else if (vpt <= 16)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<16, true>), dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, 0.0f, ssq, ld);
+  else
+    hipLaunchKernelGGL((add_rmsnorm_kernel<kNormVpt, true>), dim3(B), dim3(kThreads), 0, st, h, delta, weight, out, dim, 0.0f, ssq, ld);
+  return launched("rmsnorm_prescale");
 }
 
 int32_t imq_qk_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v,

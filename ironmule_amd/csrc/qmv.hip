@@ -99,6 +99,55 @@ __device__ __forceinline__ void store_y(const LaunchArgs& a, const Problem& P, i
   }
 }
 
+// ------------------------------------------------- an RMSNorm folded into projections
+//
+// rms_norm(h) W^T = inv (h * w) W^T per row, inv = 1 / sqrt(sum(h^2) / dim + eps): the
+// kernel that produces h writes x' = bf16(h * w) and, per 64-column tile of h, the row's
+// partial sum of squares; the kernel that consumes x' scales its product rows by inv.  No
+// launch of its own and no round trip through a normalised copy of h.
+struct NormIn {
+  const float* ssq;  // row m's partials at ssq[m * ld + t], t < tiles (nullptr: off)
+  int32_t tiles;     // 1 .. kNormMaxTiles
+  int32_t ld;        // a multiple of 4, >= tiles
+  int32_t dim;
+  float eps;
+};
+struct ResidualOut {
+  float* h;            // h[m][n] += bf16(y[m][n]), rows ldh apart (nullptr: off)
+  int64_t ldh;
+  const uint16_t* w;   // the next RMSNorm's weight (nullptr: h only)
+  uint16_t* x;         // x'[m][n] = bf16(h[m][n] * w[n]), rows ldx apart
+  int64_t ldx;
+  float* ssq;          // ssq[m * ld + tile] = sum over the tile's columns of h^2 (nullptr: none)
+  int32_t ld;
+  int32_t pad;
+};
+constexpr int kNormMaxTiles = 64;
+constexpr int kNormSlots = IMQ_MAX_ROWS * kNormMaxTiles / 4;  // (row, four partials) pairs
+
+// One b128 of the partials of pair p = (row p % 32, partials 4 (p / 32) ..): the offset to
+// load, or past the buffer (zeros, no traffic) for pairs past the rows or the partials.
+__device__ __forceinline__ uint32_t norm_pair_offset(const NormIn& ni, int M, int p) {
+  const int m = p & 31, j = p >> 5;
+  return m < M && 4 * j < ni.tiles ? (uint32_t)(m * ni.ld + 4 * j) * 4u : kPastBuffer;
+}
+
+// The four partials of pair p, added in order, those past `tiles` as zeros.
+__device__ __forceinline__ float norm_pair_sum(const NormIn& ni, int p, uint4 v) {
+  const int t0 = 4 * (p >> 5);
+  const float a = __uint_as_float(v.x), b = t0 + 1 < ni.tiles ? __uint_as_float(v.y) : 0.0f;
+  const float c = t0 + 2 < ni.tiles ? __uint_as_float(v.z) : 0.0f;
+  const float d = t0 + 3 < ni.tiles ? __uint_as_float(v.w) : 0.0f;
+  return ((a + b) + c) + d;
+}
+
+// inv of row m from the pair sums in LDS (sums[j][m]), added in pair order.
+__device__ __forceinline__ float norm_row_inv(const NormIn& ni, const float (*sums)[32], int m) {
+  float ss = 0.0f;
+  for (int j = 0; 4 * j < ni.tiles; ++j) ss += sums[j][m];
+  return 1.0f / sqrtf(ss / (float)ni.dim + ni.eps);
+}
+
 // ----------------------------------------------------------- VALU kernel (few rows)
 //
 // One workgroup per tile of weight rows of one problem (no persistent loop: the
@@ -860,9 +909,11 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
                                                                   float* __restrict__ partial,
                                                                   int64_t pstride,
                                                                   uint32_t* __restrict__ counters,
-                                                                  int tiles_max) {
+                                                                  int tiles_max, NormIn ni) {
   using namespace staged;
   __shared__ __attribute__((aligned(16))) char lds[kStage];
+  __shared__ float nsum[PAIR ? kNormMaxTiles / 4 : 1][32];  // input norm: pair sums [j][row]
+  __shared__ float ninv[32];                                // input norm: 1/rms per row
   __shared__ int last;
   const int pi = blockIdx.y / splits, split = blockIdx.y - pi * splits;
   const Problem& P = a.p[pi];
@@ -973,7 +1024,23 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   const uint32_t wrd = (uint32_t)(wk * kRows * kWRow + wrow * kWRow + 16 * h);
   const uint32_t sbrd = (uint32_t)(kWBytes + kXBytes + (wk * kRows + wrow) * 16);
 
+  // the input norm's partial sums (gate/up form): two b128 per thread cover 32 rows x
+  // kNormMaxTiles partials; their sums are published by the stage loop's barriers
+  const bool norm_in = PAIR && ni.ssq != nullptr;  // uniform
+  uint4 nq[kNormSlots / kThreads];
+  if (norm_in) {
+    const __amdgpu_buffer_rsrc_t qrs = buffer_rsrc(ni.ssq, (uint32_t)(M * ni.ld * 4));
+#pragma unroll
+    for (int r = 0; r < kNormSlots / kThreads; ++r) nq[r] = load_b128(qrs, norm_pair_offset(ni, M, tid + kThreads * r));
+  }
   fetch(0);
+  if (norm_in) {
+#pragma unroll
+    for (int r = 0; r < kNormSlots / kThreads; ++r) {
+      const int p = tid + kThreads * r;
+      nsum[PAIR ? p >> 5 : 0][p & 31] = norm_pair_sum(ni, p, nq[r]);
+    }
+  }
   for (int st = 0; st < nst; ++st) {
     __builtin_amdgcn_sched_barrier(0);
     store();
@@ -1025,8 +1092,9 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   if (wk == 0) acc += red[wn * 64 + lane];
   if (PAIR) {
     // the gate and up tiles to LDS as [tile][e][lane], then every thread writes four of the
-    // 32 x 32 SiLU(gate) * up values
+    // 32 x 32 SiLU(gate) * up values (with an input norm, of the rows scaled by 1/rms)
     float* tiles2 = reinterpret_cast<float*>(lds);
+    if (norm_in && tid < 32) ninv[tid] = norm_row_inv(ni, nsum, tid);
     __syncthreads();  // every wavefront is done with the K-range sums in LDS
     if (wk == 0)
 #pragma unroll
@@ -1038,8 +1106,10 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
       const int idx = tid + kThreads * q, e = idx >> 6, l = idx & 63;
       const int m = 8 * (e >> 2) + 4 * (l >> 5) + (e & 3), n = rp0 + (l & 31);
       if (m < M && n < N) {
-        const float g0 = bf16_bits_to_f32(f32_to_bf16_bits(tiles2[e * 64 + l]));
-        const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(tiles2[(16 + e) * 64 + l]));
+        const float sc = norm_in ? ninv[m] : 1.0f;
+        const float gs = tiles2[e * 64 + l], us = tiles2[(16 + e) * 64 + l];
+        const float g0 = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? gs * sc : gs));
+        const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? us * sc : us));
         act[(size_t)m * P.ldy + n] = f32_to_bf16_bits(g0 / (1.0f + expf(-g0)) * u0);
       }
     }
@@ -1441,6 +1511,8 @@ struct DmaArgs {
   int32_t splits;                // K-ranges per tile (1: no partials)
   int32_t range;                 // groups per K-range (a multiple of 4)
   int32_t tiles_max;             // counters per problem
+  NormIn nin;                    // input rows scaled by 1/rms (nin.ssq == nullptr: off)
+  ResidualOut res;               // residual epilogue instead of y (res.h == nullptr: off)
 };
 
 template <int W, int GMAX, bool SPLIT>
@@ -1451,6 +1523,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   __shared__ __attribute__((aligned(16))) char wb0[W * dm::kChunkBytes];
   __shared__ __attribute__((aligned(16))) char wb1[NC > 1 ? W * dm::kChunkBytes : 16];
   __shared__ __attribute__((aligned(16))) uint32_t sbl[dm::kRows * W * GMAX];
+  __shared__ float nsum[kNormMaxTiles / 4][32];  // input norm: pair sums [j][row]
   __shared__ int last;
   const int pi = blockIdx.y;
   const Problem& P = a.p[pi];
@@ -1478,6 +1551,20 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   const __amdgpu_buffer_rsrc_t xrs =
       buffer_rsrc(P.x, (uint32_t)(((int64_t)(M - 1) * P.ldx + K) * 2));
   const uint32_t xrow = j < M ? (uint32_t)j * (uint32_t)P.ldx * 2u + 64u * (uint32_t)kb : kPastBuffer;
+
+  // 0. the input norm's partial sums of squares, before every other load (the first wait
+  //    below then covers them): NQ b128 per thread cover 32 rows x kNormMaxTiles partials
+  constexpr int NQ = (kNormSlots + 64 * W - 1) / (64 * W);
+  const bool norm_in = d.nin.ssq != nullptr;  // uniform
+  uint4 nq[NQ];
+  if (norm_in) {
+    const __amdgpu_buffer_rsrc_t qrs = buffer_rsrc(d.nin.ssq, (uint32_t)(M * d.nin.ld * 4));
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      const int p = tid + 64 * W * r;
+      nq[r] = load_b128(qrs, p < kNormSlots ? norm_pair_offset(d.nin, M, p) : kPastBuffer);
+    }
+  }
 
   // 1. scales, then biases, of rows [row0, row0 + 64) over the range: Gs instructions of 64
   //    dwords, dword dd of an array at LDS dword array * 32 Gs + dd
@@ -1598,6 +1685,13 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   // [tile][e][lane] floats (a wavefront without groups never waited for its weight loads
   // into that slice: wait for them first)
   wait_vmem();
+  if (norm_in) {  // the input norm's pair sums, published by the barrier below
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      const int p = tid + 64 * W * r;
+      if (p < kNormSlots) nsum[p >> 5][p & 31] = norm_pair_sum(d.nin, p, nq[r]);
+    }
+  }
   float* red = reinterpret_cast<float*>(wb0);
 #pragma unroll
   for (int t = 0; t < 2; ++t)
@@ -1618,12 +1712,44 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
     for (int w2 = 0; w2 < W; ++w2) v += red[((w2 * 2 + t) * 16 + e) * 64 + jn + 32 * h];
     sums[i] = v;
   }
-  if (!SPLIT) {
+  // The outputs of this thread: y[m][n] for m = wave + i W (uniform across the wavefront),
+  // scaled by the row's 1/rms with an input norm; with a residual epilogue y is not stored:
+  // h += bf16(y), x' = bf16(h * w) and the tile's sums of squares of h per row instead.
+  const bool res = d.res.h != nullptr;  // uniform
+  auto finish = [&](const float (&v)[MI], const float (&hv)[MI], float wn) {
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int m = wave + i * W;
-      if (m < M && n < N) store_y(a, P, m, n, sums[i]);
+      if (m >= M) break;
+      const float y = norm_in ? v[i] * norm_row_inv(d.nin, nsum, m) : v[i];
+      if (!res) {
+        if (n < N) store_y(a, P, m, n, y);
+        continue;
+      }
+      const float hn = hv[i] + bf16_bits_to_f32(f32_to_bf16_bits(y));
+      if (n < N) {
+        d.res.h[(size_t)m * d.res.ldh + n] = hn;
+        if (d.res.w) d.res.x[(size_t)m * d.res.ldx + n] = f32_to_bf16_bits(hn * wn);
+      }
+      if (d.res.ssq) {
+        const float ss = wave_sum(n < N ? hn * hn : 0.0f);
+        if (lane == 0) d.res.ssq[m * d.res.ld + tile] = ss;
+      }
     }
+  };
+  // h and the norm weight of this thread's outputs (residual epilogue)
+  float hv[MI] = {}, wn = 0.0f;
+  auto load_res = [&]() {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = wave + i * W;
+      hv[i] = m < M && n < N ? d.res.h[(size_t)m * d.res.ldh + n] : 0.0f;
+    }
+    wn = d.res.w && n < N ? bf16_bits_to_f32(d.res.w[n]) : 0.0f;
+  };
+  if (!SPLIT) {
+    if (res) load_res();
+    finish(sums, hv, wn);
     return;
   }
   // split: park the partial, count the tile's arrivals; the last one adds them in order
@@ -1643,6 +1769,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
            (uint32_t)(splits - 1);
   __syncthreads();
   if (!last) return;
+  if (res) load_res();  // in flight with the partials
   // four partials of each output in flight at a time, added in split order
   const uint32_t step = (uint32_t)(M * N * 4);
   float tot[MI];
@@ -1665,11 +1792,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
       for (int q = 0; q < 4; ++q)
         if (q0 + q < splits) tot[i] += v[i][q];
   }
-#pragma unroll
-  for (int i = 0; i < MI; ++i) {
-    const int m = wave + i * W;
-    if (m < M && n < N) store_y(a, P, m, n, tot[i]);
-  }
+  finish(tot, hv, wn);
   if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
 }
 
@@ -2082,13 +2205,13 @@ hipError_t launch_mma(const LaunchArgs& a, const MmaPlan& pl, void* ws, hipStrea
   if (pl.staged) {
     if (pl.splits == 1) {
       hipLaunchKernelGGL((qmv_mma_staged_kernel<false>), dim3(pl.grid_x, a.count), dim3(kThreads),
-                         0, stream, a, 1, nullptr, (int64_t)0, nullptr, 0);
+                         0, stream, a, 1, nullptr, (int64_t)0, nullptr, 0, NormIn{});
     } else {
       uint32_t* counters = static_cast<uint32_t*>(ws);
       float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
       hipLaunchKernelGGL((qmv_mma_staged_kernel<true>), dim3(pl.grid_x, a.count * pl.splits),
                          dim3(kThreads), 0, stream, a, pl.splits, partial, pl.pstride, counters,
-                         pl.grid_x);
+                         pl.grid_x, NormIn{});
     }
     return hipGetLastError();
   }
@@ -2261,6 +2384,42 @@ bool plan_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
   return true;
 }
 
+// The direct-to-LDS plan for the fused-norm calls, which only this kernel serves: the
+// usual plan where it applies, else whole-K tiles (or the fewest K-ranges of at most 64
+// groups) at any M from 1 and any tile count.
+bool plan_dma_norm(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
+  if (a.M >= 3 && plan_dma(a, cu_count, pl)) return true;
+  if (a.table || a.M < 1 || a.M > 32 || a.count < 1 || a.count > kMaxProblems) return false;
+  int grid_x = 0, gmax = 0, gmin = 1 << 30, nmax = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const Problem& P = a.p[i];
+    if (P.K % 256 != 0 || P.N < 1) return false;
+    if ((int64_t)P.N * (P.K / 2) >= ((int64_t)1 << 31)) return false;
+    if (P.ldx % 8 != 0 || !imq_rt::aligned(P.x, 16)) return false;
+    if (((int64_t)(a.M - 1) * P.ldx + P.K) * 2 >= ((int64_t)1 << 31)) return false;
+    const int t = (P.N + dm::kRows - 1) / dm::kRows;
+    grid_x = t > grid_x ? t : grid_x;
+    gmax = P.K / 64 > gmax ? P.K / 64 : gmax;
+    gmin = P.K / 64 < gmin ? P.K / 64 : gmin;
+    nmax = P.N > nmax ? P.N : nmax;
+  }
+  int splits = (gmax + dm::kMaxGroups - 1) / dm::kMaxGroups;
+  if (splits > 1 && gmin != gmax) return false;
+  int range = ((gmax + splits - 1) / splits + 3) / 4 * 4;
+  splits = (gmax + range - 1) / range;
+  if (splits > dm::kMaxSplits || (size_t)a.count * grid_x * 4 > kCounterBytes) return false;
+  if (splits > 1 && ((int64_t)splits * a.M * nmax) * 4 >= ((int64_t)1 << 31)) return false;
+  pl->splits = splits;
+  pl->range = range;
+  pl->gmax = range <= 32 ? 4 : 8;
+  const int w = (range + pl->gmax - 1) / pl->gmax;
+  pl->waves = w <= 2 ? 2 : w <= 6 ? w : 8;
+  pl->grid_x = grid_x;
+  pl->pstride = splits > 1 ? (size_t)splits * a.M * nmax : 0;
+  pl->bytes = splits > 1 ? kCounterBytes + (size_t)a.count * pl->pstride * sizeof(float) : 0;
+  return true;
+}
+
 // K-ranges per tile, 0 to decline.  Measured on MI355X at M = 32 (one call, against the
 // other kernels' best): launches of more than half a tile per CU run whole-K tiles (K =
 // 3840 x 15360, 240 tiles: 16.3 us against 19.5; any split lost); smaller ones split into
@@ -2312,9 +2471,12 @@ hipError_t launch_dma_g(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl
   }
 }
 
-hipError_t launch_dma(const LaunchArgs& a, const DmaPlan& pl, void* ws, hipStream_t stream) {
+hipError_t launch_dma(const LaunchArgs& a, const DmaPlan& pl, void* ws, hipStream_t stream,
+                      const NormIn* nin = nullptr, const ResidualOut* res = nullptr) {
   DmaArgs d;
   memset(&d, 0, sizeof(d));
+  if (nin) d.nin = *nin;
+  if (res) d.res = *res;
   if (pl.splits > 1) {
     char* base = static_cast<char*>(ws);
     d.counters = reinterpret_cast<uint32_t*>(base);
@@ -2451,35 +2613,6 @@ int32_t imq_qmv(const uint32_t* w, const uint16_t* scales, const uint16_t* biase
   a.M = M;
   a.y_f32 = (y_dtype == IMQ_F32);
   return launch(a, dev, static_cast<hipStream_t>(stream));
-}
-
-int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate,
-                             const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
-                             const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
-                             int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
-                             int32_t bits, void* stream) {
-  int32_t code = check_format(N, K, group_size, bits);
-  if (code != IMQ_OK) return code;
-  if ((code = check_weights(w_gate, s_gate, b_gate)) != IMQ_OK) return code;
-  if ((code = check_weights(w_up, s_up, b_up)) != IMQ_OK) return code;
-  if ((code = check_rows(x, ldx, act, ld_act, M, N, K, IMQ_BF16)) != IMQ_OK) return code;
-  if (M < 5 || K % 256 != 0)
-    return fail(IMQ_EUNSUPPORTED, "the fused gate/up launch takes 5 to 32 rows and K a multiple of 256");
-  if ((int64_t)N * (K / 2) >= ((int64_t)1 << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= ((int64_t)1 << 31))
-    return fail(IMQ_EUNSUPPORTED, "a weight or activation of 2 GiB or more exceeds the kernel's offsets");
-  const DeviceInfo* dev = current_device(&code);
-  if (!dev) return code;
-  LaunchArgs a;
-  memset(&a, 0, sizeof(a));
-  a.p[0] = Problem{w_gate, s_gate, b_gate, x, act, ldx, ld_act, N, K, 0, 0, 0, 0};
-  a.p[1] = Problem{w_up, s_up, b_up, x, nullptr, ldx, ld_act, N, K, 0, 0, 0, 0};
-  a.count = 2;
-  a.M = M;
-  hipLaunchKernelGGL((qmv_mma_staged_kernel<false, true>), dim3((N + 31) / 32, 1), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), a, 1, nullptr, (int64_t)0, nullptr, 0);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("gate/up launch failed: ") + hipGetErrorString(e));
-  return ok();
 }
 
 int32_t imq_qmv_multi(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
@@ -2701,5 +2834,164 @@ int32_t imq_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* b
 }
 
 int32_t imq_last_error(char* buf, size_t len) { return imq_rt::last_error(buf, len); }
+
+}  // extern "C"
+
+// ============================================ the RMSNorm folded into projections
+
+namespace {
+
+int32_t check_norm_in(const imq_norm_in* in) {
+  if (!in->ssq || !aligned(in->ssq, 16)) return fail(IMQ_EINVAL, "norm ssq must be non-null and 16-byte aligned");
+  if (in->tiles < 1 || in->tiles > kNormMaxTiles)
+    return fail(IMQ_EUNSUPPORTED, "norm partials per row must be 1..64");
+  if (in->ld < in->tiles || in->ld % 4) return fail(IMQ_EINVAL, "norm ld must be a multiple of 4 and >= tiles");
+  if (in->dim < 1 || !(in->eps >= 0.0f)) return fail(IMQ_EINVAL, "norm dim must be >= 1 and eps >= 0");
+  if ((int64_t)IMQ_MAX_ROWS * in->ld * 4 >= ((int64_t)1 << 31)) return fail(IMQ_EINVAL, "norm ld too large");
+  return IMQ_OK;
+}
+
+NormIn to_norm_in(const imq_norm_in* in) {
+  NormIn n;
+  memset(&n, 0, sizeof(n));
+  if (in) n = NormIn{in->ssq, in->tiles, in->ld, in->dim, in->eps};
+  return n;
+}
+
+// Validates a fused-norm call into `a`, the plan `pl` and the device arguments.
+int32_t build_norm(LaunchArgs& a, DmaPlan* pl, NormIn* nin, ResidualOut* res,
+                   const imq_problem* problems, int32_t count, int32_t M, int32_t group_size,
+                   int32_t bits, const imq_norm_in* in, const imq_residual_out* out,
+                   const DeviceInfo** dev) {
+  if (!problems) return fail(IMQ_EINVAL, "problems must be non-null");
+  if (count < 1 || count > IMQ_MAX_PROBLEMS) return fail(IMQ_EINVAL, "count must be 1..IMQ_MAX_PROBLEMS");
+  if (out && count != 1) return fail(IMQ_EINVAL, "a residual epilogue takes one problem");
+  imq_problem probs[IMQ_MAX_PROBLEMS];
+  for (int i = 0; i < count; ++i) probs[i] = problems[i];
+  if (out) {  // y is not written: validate the rows against the residual rows instead
+    if (!out->h || !aligned(out->h, 4)) return fail(IMQ_EINVAL, "residual h must be non-null and 4-byte aligned");
+    if (M > 1 && out->ldh < probs[0].N) return fail(IMQ_EINVAL, "residual ldh must be >= N");
+    probs[0].y = out->h;
+    probs[0].ldy = out->ldh;
+  }
+  int32_t code = build_grouped(a, probs, count, M, group_size, bits, IMQ_BF16);
+  if (code != IMQ_OK) return code;
+  memset(nin, 0, sizeof(*nin));
+  memset(res, 0, sizeof(*res));
+  if (in) {
+    if ((code = check_norm_in(in)) != IMQ_OK) return code;
+    *nin = to_norm_in(in);
+  }
+  if (out) {
+    const int N = probs[0].N, tiles = (N + 63) / 64;
+    if (out->weight) {
+      if (!aligned(out->weight, 2) || !out->x || !aligned(out->x, 2))
+        return fail(IMQ_EINVAL, "norm weight and x' must be non-null and 2-byte aligned");
+      if (M > 1 && out->ldx < N) return fail(IMQ_EINVAL, "x' ldx must be >= N");
+    }
+    if (out->ssq && (!aligned(out->ssq, 4) || out->ld < tiles || out->ld % 4))
+      return fail(IMQ_EINVAL, "residual ssq must be 4-byte aligned with ld >= ceil(N / 64), a multiple of 4");
+    *res = ResidualOut{out->h, M > 1 ? out->ldh : N, out->weight, out->x, M > 1 ? out->ldx : N,
+                       out->ssq, out->ld, 0};
+  }
+  *dev = current_device(&code);
+  if (!*dev) return code;
+  if (!plan_dma_norm(a, (*dev)->cu_count, pl))
+    return fail(IMQ_EUNSUPPORTED, "the fused-norm projections need K % 256 == 0, 16-byte aligned x rows "
+                                  "(ldx a multiple of 8), one K per call when K-ranges split and "
+                                  "offsets under 2 GiB");
+  return IMQ_OK;
+}
+
+int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint16_t* b_gate,
+                     const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
+                     const uint16_t* x, int64_t ldx, uint16_t* act, int64_t ld_act, int32_t M,
+                     int32_t N, int32_t K, int32_t group_size, int32_t bits, const imq_norm_in* in,
+                     void* stream) {
+  int32_t code = check_format(N, K, group_size, bits);
+  if (code != IMQ_OK) return code;
+  if ((code = check_weights(w_gate, s_gate, b_gate)) != IMQ_OK) return code;
+  if ((code = check_weights(w_up, s_up, b_up)) != IMQ_OK) return code;
+  if ((code = check_rows(x, ldx, act, ld_act, M, N, K, IMQ_BF16)) != IMQ_OK) return code;
+  if (in && (code = check_norm_in(in)) != IMQ_OK) return code;
+  if (M < 5 || K % 256 != 0)
+    return fail(IMQ_EUNSUPPORTED, "the fused gate/up launch takes 5 to 32 rows and K a multiple of 256");
+  if ((int64_t)N * (K / 2) >= ((int64_t)1 << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= ((int64_t)1 << 31))
+    return fail(IMQ_EUNSUPPORTED, "a weight or activation of 2 GiB or more exceeds the kernel's offsets");
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return code;
+  LaunchArgs a;
+  memset(&a, 0, sizeof(a));
+  a.p[0] = Problem{w_gate, s_gate, b_gate, x, act, ldx, ld_act, N, K, 0, 0, 0, 0};
+  a.p[1] = Problem{w_up, s_up, b_up, x, nullptr, ldx, ld_act, N, K, 0, 0, 0, 0};
+  a.count = 2;
+  a.M = M;
+  hipLaunchKernelGGL((qmv_mma_staged_kernel<false, true>), dim3((N + 31) / 32, 1), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), a, 1, nullptr, (int64_t)0, nullptr, 0, to_norm_in(in));
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("gate/up launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t imq_qmv_norm_workspace(const imq_problem* problems, int32_t count, int32_t M) {
+  if (!problems || count < 1 || count > IMQ_MAX_PROBLEMS || M < 1 || M > IMQ_MAX_ROWS) return 0;
+  int32_t code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return 0;
+  LaunchArgs a;
+  memset(&a, 0, sizeof(a));
+  for (int i = 0; i < count; ++i) {
+    if (problems[i].N < 1 || problems[i].K < 64 || problems[i].K % 64) return 0;
+    a.p[i].N = problems[i].N;
+    a.p[i].K = problems[i].K;
+    a.p[i].x = problems[i].x;
+    a.p[i].ldx = M > 1 ? problems[i].ldx : problems[i].K;
+  }
+  a.count = count;
+  a.M = M;
+  DmaPlan pl;
+  return plan_dma_norm(a, dev->cu_count, &pl) ? pl.bytes : 0;
+}
+
+int32_t imq_qmv_norm(const imq_problem* problems, int32_t count, int32_t M, int32_t group_size,
+                     int32_t bits, const imq_norm_in* in, const imq_residual_out* out,
+                     float* workspace, size_t workspace_bytes, void* stream) {
+  LaunchArgs a;
+  DmaPlan pl;
+  NormIn nin;
+  ResidualOut res;
+  const DeviceInfo* dev = nullptr;
+  int32_t code = build_norm(a, &pl, &nin, &res, problems, count, M, group_size, bits, in, out, &dev);
+  if (code != IMQ_OK) return code;
+  if (pl.bytes > 0 && (!workspace || !aligned(workspace, 16) || workspace_bytes < pl.bytes))
+    return fail(IMQ_EINVAL, "this call needs a 16-byte aligned workspace of imq_qmv_norm_workspace bytes (" +
+                                std::to_string(pl.bytes) + ")");
+  const hipError_t e = launch_dma(a, pl, workspace, static_cast<hipStream_t>(stream), &nin, &res);
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused-norm qmv launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate,
+                             const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
+                             const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
+                             int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                             int32_t bits, void* stream) {
+  return gate_up_silu(w_gate, s_gate, b_gate, w_up, s_up, b_up, x, ldx, act, ld_act, M, N, K, group_size,
+                      bits, nullptr, stream);
+}
+
+int32_t imq_qmv_gate_up_silu_norm(const uint32_t* w_gate, const uint16_t* s_gate,
+                                  const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
+                                  const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
+                                  int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                                  int32_t bits, const imq_norm_in* in, void* stream) {
+  if (!in) return fail(IMQ_EINVAL, "in must be non-null (imq_qmv_gate_up_silu takes no norm)");
+  return gate_up_silu(w_gate, s_gate, b_gate, w_up, s_up, b_up, x, ldx, act, ld_act, M, N, K, group_size,
+                      bits, in, stream);
+}
 
 }  // extern "C"

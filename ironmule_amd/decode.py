@@ -142,6 +142,10 @@ class DecodeState:
         self.up = torch.empty((batch, c.intermediate), **bf)
         self.act = torch.empty((batch, c.intermediate), **bf)
         self.logits = torch.empty((batch, c.vocab), dtype=torch.float32, device=device)
+        # the residual stream's per-row sums of squares for the RMSNorms folded into the
+        # projections (batches of FUSED_NORM_ROWS or more)
+        self.stats_in = _native.NormStats(batch, c.hidden, device)
+        self.stats_post = _native.NormStats(batch, c.hidden, device)
         self.workspace = torch.empty(_native.attention_workspace(batch, c.heads, self.max_len),
                                      dtype=torch.float32, device=device)
         self.attn_counters = torch.zeros(batch * c.kv_heads, dtype=torch.int32, device=device)
@@ -161,9 +165,14 @@ class DecodeState:
         self.lengths.copy_(pos + 1)
 
 
+FUSED_NORM_ROWS = 5  # from this batch the RMSNorms run inside the projections
+
+
 def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> torch.Tensor:
     """Launches one decode step for the requests in `state` (tokens, slots, positions set
     by `set_requests`); returns state.logits (B, vocab) fp32, written on `stream`."""
+    if state.batch >= FUSED_NORM_ROWS:
+        return _decode_step_fused_norms(weights, state, stream)
     c, s = weights.config, state
     n = _native
     n.embed(*weights.embed, s.tokens, s.h, stream=stream)
@@ -188,6 +197,47 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
         n.qmv(*layer["down"], s.act, out=s.delta, stream=stream)
         delta = s.delta
     n.add_rmsnorm(s.h, weights.norm, s.x, c.eps, delta=delta, stream=stream)
+    n.qmv(*weights.embed, s.x, out=s.logits, stream=stream)
+    return s.logits
+
+
+def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream=None) -> torch.Tensor:
+    """decode_step with every RMSNorm but the last folded into the launches around it, five
+    launches per layer:
+
+        x' = bf16(h * w_in), stats                 imq_rmsnorm_prescale (first layer only)
+        per layer:
+            q, k, v = inv * (x' @ W.T)             imq_qmv_norm (norm_in: the stats)
+            attention                              imq_attention_fused
+            h += o @ Wo.T; x' = bf16(h * w_post)   imq_qmv_norm (residual epilogue: h, x'
+                                                   and the per-tile sums of squares)
+            act = silu(inv * g) * (inv * u)        imq_qmv_gate_up_silu_norm
+            h += act @ Wd.T; x' = bf16(h * w_in')  imq_qmv_norm (residual epilogue; the last
+                                                   layer updates h only)
+        logits = rms_norm(h) @ E.T                 imq_add_rmsnorm, imq_qmv
+
+    inv is each row's 1 / rms(h), so inv * (x' W^T) is rms_norm(h) W^T up to the place of one
+    bf16 rounding (x' is rounded before the scaling instead of after it)."""
+    c, s = weights.config, state
+    n = _native
+    n.embed(*weights.embed, s.tokens, s.h, stream=stream)
+    n.rmsnorm_prescale(s.h, weights.layers[0]["input_norm"], s.x, s.stats_in, stream=stream)
+    for i, layer in enumerate(weights.layers):
+        n.qmv_norm([layer["q"], layer["k"], layer["v"]], s.x, outs=[s.q, s.k, s.v],
+                   norm_in=s.stats_in, eps=c.eps, stream=stream)
+        n.attention_fused(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
+                          s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len, c.theta,
+                          c.eps, s.workspace, s.attn_counters, stream=stream)
+        n.qmv_norm([layer["o"]], s.attn, residual=s.h, next_norm=layer["post_norm"], x_out=s.x,
+                   stats_out=s.stats_post, stream=stream)
+        n.gate_up_silu_norm(layer["gate"], layer["up"], s.x, s.act, s.stats_post, c.eps,
+                            stream=stream)
+        last = i + 1 == len(weights.layers)
+        n.qmv_norm([layer["down"]], s.act, residual=s.h,
+                   next_norm=None if last else weights.layers[i + 1]["input_norm"],
+                   x_out=None if last else s.x, stats_out=None if last else s.stats_in,
+                   stream=stream)
+    n.add_rmsnorm(s.h, weights.norm, s.x, c.eps, stream=stream)
     n.qmv(*weights.embed, s.x, out=s.logits, stream=stream)
     return s.logits
 

@@ -295,13 +295,17 @@ def _oracle_model(torch, do, orc, weights):
                     heads=c.heads, kv_heads=c.kv_heads, eps=c.eps, theta=c.theta)
 
 
-def test_decode_step_matches_oracle(env):
+@pytest.mark.parametrize("batch", [3, 6])
+def test_decode_step_matches_oracle(env, batch):
+    """B = 3 runs the per-kernel step with RMSNorm launches; B = 6 the step with the
+    RMSNorms folded into the projections (decode.FUSED_NORM_ROWS)."""
     torch, n, do, orc = env
-    from ironmule_amd.decode import DecodeState, decode_step, random_weights
-    announce("decode step, small decoder, B=3")
+    from ironmule_amd.decode import FUSED_NORM_ROWS, DecodeState, decode_step, random_weights
+    assert (batch >= FUSED_NORM_ROWS) == (batch == 6)
+    announce("decode step, small decoder", batch)
     cfg = _tiny()
     weights = random_weights(cfg, "cuda", seed=5)
-    state = DecodeState(cfg, batch=3, slots=4, capacity=80, max_len=80, device="cuda")
+    state = DecodeState(cfg, batch=batch, slots=max(4, batch), capacity=80, max_len=80, device="cuda")
     for kp, vp in zip(state.k_pool, state.v_pool):  # a synthetic context in every slot
         kp.copy_(torch.randn(kp.shape, device="cuda").to(torch.bfloat16))
         vp.copy_(torch.randn(vp.shape, device="cuda").to(torch.bfloat16))
@@ -309,6 +313,8 @@ def test_decode_step_matches_oracle(env):
     values = [_vals(vp) for vp in state.v_pool]
     model = _oracle_model(torch, do, orc, weights)
     tokens, slots, positions = [5, 511, 200], [3, 0, 1], [64, 0, 79]
+    if batch == 6:
+        tokens, slots, positions = tokens + [7, 300, 42], slots + [2, 5, 4], positions + [1, 33, 63]
     for step in range(2):  # a second step reads the keys the first one wrote
         state.set_requests(tokens, slots, positions)
         logits = decode_step(weights, state)
@@ -318,7 +324,7 @@ def test_decode_step_matches_oracle(env):
         rel = np.abs(got - ref).max() / np.abs(ref).max()
         assert rel <= 1e-2, (step, rel)
         for i in range(cfg.layers):
-            for r in range(3):
+            for r in range(batch):
                 kg = _vals(state.k_pool[i])[slots[r], :, positions[r]]
                 kr = keys[i][slots[r], :, positions[r]]
                 assert np.abs(kg - kr).max() <= 0.05 * np.abs(kr).max(), (step, i, r)

@@ -1,0 +1,226 @@
+"""GPU parity of the RMSNorm folded into the projections (imq_rmsnorm_prescale,
+imq_qmv_norm, imq_qmv_gate_up_silu_norm), through the C ABI.
+
+rms_norm(h) W^T = inv * ((h * w) W^T) row by row, inv = 1 / sqrt(sum h^2 / dim + eps): the
+producer writes x' = bf16(h * w) and partial sums of squares, the consumer scales its rows.
+
+* prescale: x' = bf16(h * w) and h += delta bit-exact against torch, the row's sum of
+  squares within fp32 rounding of the float64 sum.
+* input norm with partials whose sum makes inv exactly 1/2: every output is half the plain
+  projection's, bit for bit (the scaling by a power of two commutes with the rounding), at
+  the decode shapes (q/k/v, o and down at 5 and 32 rows) and for the gate/up launch against
+  silu_mul of the halved grouped outputs.
+* input norm with random partials: within the oracle's bf16 bar of inv * (x' W^T), inv from
+  the float64 sum (plus 2^-18 relative for the fp32 sum of up to 64 partials).
+* residual epilogue: h_new = h + bf16(y) bit-exact with y the plain projection's output, x' =
+  bf16(h_new * w) bit-exact, the per-tile sums of squares within fp32 rounding; h only
+  without a weight; a small forced plan (K = 512, 8 rows, whole-K tiles) against the oracle.
+* refusals: a residual epilogue over two weights, partial counts outside 1..64, ld not a
+  multiple of 4.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests.conftest import gpu_available
+from tests.gpu_util import announce, bf16_bits, to_device
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+
+
+@pytest.fixture(scope="module")
+def native():
+    from ironmule_amd import _native
+    code, arch, _ = _native.device_check()
+    assert code == 0, f"device {arch} is not supported"
+    return _native
+
+
+def _stats(native, rows, dim, tiles, values):
+    """NormStats over `rows` rows with `tiles` partials per row set to `values` (rows, tiles)."""
+    st = native.NormStats(rows, dim, "cuda")
+    if tiles > st.ld:
+        st.ld = -(-tiles // 4) * 4
+        st.ssq = torch.zeros((rows, st.ld), dtype=torch.float32, device="cuda")
+    st.ssq.zero_()
+    st.ssq[:, :tiles] = torch.as_tensor(np.asarray(values, np.float32), device="cuda")
+    st.tiles = tiles
+    return st
+
+
+def _weights(oracle, shapes, m, seed):
+    probs = [oracle.synthetic(n, k, m, seed=seed + i) for i, (n, k) in enumerate(shapes)]
+    x = probs[0].x
+    probs = [oracle.Problem(p.w, p.s, p.b, x, 0) for p in probs]
+    dev = [to_device(p) for p in probs]
+    return probs, [d[:3] for d in dev], dev[0][3]
+
+
+def test_prescale(native):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    for b, dim, with_delta in ((1, 2560, False), (32, 2560, True), (5, 320, True)):
+        announce("rmsnorm prescale", b, dim, with_delta)
+        h = torch.randn((b, dim), device="cuda", generator=g) * 3
+        w = (torch.rand(dim, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+        delta = torch.randn((b, dim), device="cuda", generator=g).to(torch.bfloat16) if with_delta else None
+        h0 = h.clone()
+        out = torch.empty((b, dim), dtype=torch.bfloat16, device="cuda")
+        st = native.NormStats(b, dim, "cuda")
+        native.rmsnorm_prescale(h, w, out, st, delta=delta)
+        torch.cuda.synchronize()
+        hn = h0 + delta.float() if with_delta else h0
+        assert torch.equal(h, hn)
+        assert torch.equal(out, (hn * w.float()).to(torch.bfloat16))
+        ss = (hn.double() ** 2).sum(dim=1)
+        assert st.tiles == 1
+        assert torch.allclose(st.ssq[:, 0].double(), ss, rtol=2e-6, atol=0)
+
+
+# Partials summing to exactly 4 * dim: inv = 1 / sqrt(4) = 1/2 with eps = 0.
+def _half_stats(native, m, dim, tiles):
+    return _stats(native, m, dim, tiles, np.full((m, tiles), 4.0 * dim / tiles))
+
+
+@pytest.mark.parametrize("shapes,m", [
+    ([(4096, 2560), (1024, 2560), (1024, 2560)], 32),
+    ([(4096, 2560), (1024, 2560), (1024, 2560)], 5),
+    ([(2560, 4096)], 32), ([(2560, 9728)], 32), ([(2560, 9728)], 7),
+])
+def test_input_norm_halves_the_plain_projection(native, oracle, shapes, m):
+    _, weights, x = _weights(oracle, shapes, m, oracle.SEED_BASE + 2000 + m)
+    announce("input norm = plain / 2", shapes, m)
+    plain = native.qmv_grouped(weights, [x] * len(weights))
+    st = _half_stats(native, m, 2560, 40)
+    got = native.qmv_norm(weights, x, norm_in=st, eps=0.0)
+    again = native.qmv_norm(weights, x, norm_in=st, eps=0.0)
+    torch.cuda.synchronize()
+    for p, y, y2 in zip(plain, got, again):
+        assert torch.equal(y, (p.float() * 0.5).to(torch.bfloat16))
+        assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("shapes,m,tiles", [
+    ([(4096, 2560), (1024, 2560), (1024, 2560)], 32, 40),
+    ([(2560, 4096)], 6, 1), ([(1000, 512)], 8, 64), ([(2560, 9728)], 32, 13),
+    ([(640, 2560)], 1, 40),
+])
+def test_input_norm_matches_oracle(native, oracle, shapes, m, tiles):
+    probs, weights, x = _weights(oracle, shapes, m, oracle.SEED_BASE + 2100 + m)
+    rng = np.random.default_rng(2100 + m + tiles)
+    dim, eps = 2560, 1e-6
+    vals = rng.uniform(0.5, 3.0, size=(m, tiles)).astype(np.float32) * dim / tiles
+    st = _stats(native, m, dim, tiles, vals)
+    announce("input norm vs oracle", shapes, m, tiles)
+    got = native.qmv_norm(weights, x, norm_in=st, eps=eps)
+    torch.cuda.synchronize()
+    inv = 1.0 / np.sqrt(vals.astype(np.float64).sum(axis=1) / dim + eps)
+    for pr, y in zip(probs, got):
+        ref, mag = oracle.qmv_f64(pr.w, pr.s, pr.b, pr.x)
+        ref = ref * inv[:, None]
+        v = oracle.check_bf16(bf16_bits(y), ref, mag * inv[:, None] + 4.0 * np.abs(ref))
+        assert v.ok, v.detail
+
+
+@pytest.mark.parametrize("n,k,m", [(9728, 2560, 32), (9728, 2560, 5), (1000, 512, 9)])
+def test_gate_up_norm_halves(native, oracle, n, k, m):
+    pg = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 2200 + m)
+    pu = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 2201 + m)
+    pu = oracle.Problem(pu.w, pu.s, pu.b, pg.x, 0)
+    dg, du = to_device(pg), to_device(pu)
+    gate, up, x = dg[:3], du[:3], dg[3]
+    announce("gate/up norm = silu(g/2) * u/2", n, k, m)
+    st = _half_stats(native, m, 2560, 40)
+    out = native.gate_up_silu_norm(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"),
+                                   st, 0.0)
+    plain = native.gate_up_silu(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"))
+    torch.cuda.synchronize()
+    if (n, k) == (9728, 2560):  # grouped launch on the staged kernel: the same row sums
+        g, u = native.qmv_grouped([gate, up], [x, x])
+        ref = native.silu_mul((g.float() * 0.5).to(torch.bfloat16), (u.float() * 0.5).to(torch.bfloat16),
+                              torch.empty_like(g))
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+    # against the oracle: each projection within one bf16 ulp (plus the summation
+    # allowance) of its exact value, then SiLU (slope <= 1.1) and one more rounding
+    g64, mg = oracle.qmv_f64(pg.w, pg.s, pg.b, pg.x)
+    u64, mu = oracle.qmv_f64(pu.w, pu.s, pu.b, pu.x)
+    g64, u64, mg, mu = g64 / 2, u64 / 2, mg / 2, mu / 2
+    eg = oracle.bf16_ulp(g64) + 2.0 ** -20 * mg
+    eu = oracle.bf16_ulp(u64) + 2.0 ** -20 * mu
+    sg = g64 / (1.0 + np.exp(-g64))
+    ref = sg * u64
+    got = oracle.bf16_to_f32(bf16_bits(out)).astype(np.float64)
+    bound = oracle.bf16_ulp(ref) + 1.1 * eg * (np.abs(u64) + eu) + np.abs(sg) * eu
+    assert (np.abs(got - ref) <= bound).all(), float(np.max(np.abs(got - ref) / bound))
+    assert not torch.equal(out, plain)  # the scaling took effect
+
+
+@pytest.mark.parametrize("n,k,m", [(2560, 4096, 32), (2560, 9728, 32), (2560, 4096, 5)])
+def test_residual_epilogue(native, oracle, n, k, m):
+    probs, weights, x = _weights(oracle, [(n, k)], m, oracle.SEED_BASE + 2300 + m)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2300 + m)
+    h = torch.randn((m, n), device="cuda", generator=g) * 4
+    w = (torch.rand(n, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+    announce("residual epilogue", n, k, m)
+    (y,) = native.qmv_grouped(weights, [x])
+    h1 = h.clone()
+    xo = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    st = native.NormStats(m, n, "cuda")
+    out = native.qmv_norm(weights, x, residual=h1, next_norm=w, x_out=xo, stats_out=st)
+    h2 = h.clone()
+    native.qmv_norm(weights, x, residual=h2)  # h only
+    torch.cuda.synchronize()
+    assert out == []
+    hn = h + y.float()
+    assert torch.equal(h1, hn)
+    assert torch.equal(h2, hn)
+    assert torch.equal(xo, (hn * w.float()).to(torch.bfloat16))
+    tiles = n // 64
+    assert st.tiles == tiles
+    ss = (hn.double() ** 2).reshape(m, tiles, 64).sum(dim=2)
+    assert torch.allclose(st.ssq[:, :tiles].double(), ss, rtol=2e-6, atol=0)
+
+
+def test_residual_epilogue_forced_plan_matches_oracle(native, oracle):
+    n, k, m = 256, 512, 8  # the usual plan would not take the direct-to-LDS kernel here
+    probs, weights, x = _weights(oracle, [(n, k)], m, oracle.SEED_BASE + 2400)
+    h = torch.zeros((m, n), device="cuda")
+    w = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+    xo = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    st = native.NormStats(m, n, "cuda")
+    announce("residual epilogue forced plan", n, k, m)
+    native.qmv_norm(weights, x, residual=h, next_norm=w, x_out=xo, stats_out=st)
+    torch.cuda.synchronize()
+    # h was zero: h_new = bf16(y) exactly, and x' = bf16(h_new * 1) = y
+    v, lit = oracle.check_bf16_both(bf16_bits(xo), probs[0].w, probs[0].s, probs[0].b, probs[0].x)
+    assert v.ok and lit.ok, (v.detail, lit.detail)
+    assert torch.equal(h, xo.float())
+
+
+def test_refusals(native, oracle):
+    from ironmule_amd._native import NativeError, NormIn, Problem, lib
+    import ctypes
+    _, weights, x = _weights(oracle, [(512, 512), (512, 512)], 8, oracle.SEED_BASE + 2500)
+    announce("fused norm refusals")
+    h = torch.zeros((8, 512), device="cuda")
+    with pytest.raises(ValueError):
+        native.qmv_norm(weights, x, residual=h)
+    for tiles, ld in ((0, 4), (65, 68), (5, 6)):
+        st = native.NormStats(8, 512, "cuda")
+        nin = NormIn(st.ssq.data_ptr(), tiles, ld, 512, 1e-6)
+        probs = (Problem * 1)()
+        y = torch.empty((8, 512), dtype=torch.bfloat16, device="cuda")
+        w, s, b = weights[0]
+        probs[0] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), 512, y.data_ptr(), 512, 512, 512)
+        code = lib().imq_qmv_norm(probs, 1, 8, 64, 4, ctypes.byref(nin), None, None, 0, None)
+        assert code in (1, 2), (tiles, ld, code)
+    pr = oracle.synthetic(64, 320, 8, seed=oracle.SEED_BASE + 2501)  # K % 256 != 0
+    w3, s3, b3, x3 = to_device(pr)
+    with pytest.raises(NativeError):
+        native.qmv_norm([(w3, s3, b3)], x3, norm_in=native.NormStats(8, 512, "cuda"))
