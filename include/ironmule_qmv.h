@@ -160,6 +160,25 @@ IMQ_API int32_t imq_qmv_norm(const imq_problem* problems, int32_t count, int32_t
                              const imq_residual_out* out, float* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* K-ranges (output planes) imq_qmv_norm_planes splits these problems into at M rows; 0 if
+ * the call would be refused. */
+IMQ_API int32_t imq_qmv_norm_splits(const imq_problem* problems, int32_t count, int32_t M);
+
+/*
+ * imq_qmv_norm's input-norm form without the in-launch reduction of the K-ranges: each range
+ * writes its fp32 partial product (row-scaled by inv_m when `in` is given) as an output
+ * plane, and the reader of the result adds the planes in order (plane 0 first) and rounds:
+ *   problem i, plane s, row m, column n at planes[i * pstride + (s * M + m) * N_i + n].
+ * *splits receives the plane count (imq_qmv_norm_splits); pstride >= splits * M * max N_i.
+ * The problems' y are not written (may be NULL).  Same limits as imq_qmv_norm; no workspace.
+ * Replaces the same reference calls as imq_qmv_norm (the q/k/v projections of the decode
+ * step, ironmule/dense_plan.py:348-353), for a reader that adds the planes itself
+ * (imq_attention_fused_planes, ironmule_decode.h).
+ */
+IMQ_API int32_t imq_qmv_norm_planes(const imq_problem* problems, int32_t count, int32_t M,
+                                    int32_t group_size, int32_t bits, const imq_norm_in* in,
+                                    float* planes, int64_t pstride, int32_t* splits, void* stream);
+
 /*
  * imq_qmv_gate_up_silu on x' rows with the input RMSNorm folded in (`in` non-NULL):
  *   act[m][n] = bf16(silu(g) * u),  g = bf16(inv_m * sum_k x'[m][k] W_gate[n][k]),

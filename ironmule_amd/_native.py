@@ -123,6 +123,9 @@ _SIGNATURES = {
     "imq_qmv_norm_workspace": ([ctypes.POINTER(Problem), _I32, _I32], ctypes.c_size_t),
     "imq_qmv_norm": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, ctypes.POINTER(NormIn),
                       ctypes.POINTER(ResidualOut), _P, ctypes.c_size_t, _P], _I32),
+    "imq_qmv_norm_splits": ([ctypes.POINTER(Problem), _I32, _I32], _I32),
+    "imq_qmv_norm_planes": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, ctypes.POINTER(NormIn),
+                             _P, _I64, ctypes.POINTER(_I32), _P], _I32),
     "imq_qmv_gate_up_silu_norm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32,
                                    _I32, _I32, ctypes.POINTER(NormIn), _P], _I32),
     "imq_rmsnorm_prescale": ([_P, _P, _P, _P, _P, _I32, _I32, _I32, _P], _I32),
@@ -140,6 +143,9 @@ _SIGNATURES = {
                               ctypes.c_float, _P, _P], _I32),
     "imq_attention_fused": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                              _I32, _I32, ctypes.c_float, ctypes.c_float, _P, _P, _P], _I32),
+    "imq_attention_fused_planes": ([_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                    _I32, _I32, _I32, ctypes.c_float, ctypes.c_float, _P, _P, _P],
+                                   _I32),
     "imq_silu_mul": ([_P, _P, _P, _I64, _P], _I32),
     # persistent programs (include/ironmule_step.h)
     "imq_decode_program_create": ([ctypes.POINTER(StepDesc), ctypes.POINTER(_P)], _I32),
@@ -528,6 +534,81 @@ def attention_fused(q, k, v, q_norm, k_norm, positions, slots, k_pool, v_pool, o
                                      _ptr(out), b, hq, hkv, capacity, num_slots, int(max_len),
                                      float(theta), float(eps), _ptr(workspace), _ptr(counters),
                                      _stream(stream)))
+    return out
+
+
+class QkvPlanes:
+    """fp32 output planes of the q/k/v projections for `rows` requests (imq_qmv_norm_planes),
+    read and reduced by attention_fused_planes: problem i (q, k, v) at offset i * pstride."""
+
+    def __init__(self, rows: int, hq: int, hkv: int, device, max_planes: int = 4) -> None:
+        self.rows, self.hq, self.hkv = rows, hq, hkv
+        self.pstride = max_planes * rows * hq * 128
+        self.max_planes = max_planes
+        self.data = torch.empty(3 * self.pstride, dtype=torch.float32, device=device)
+        self.planes = 0
+
+    def view(self, i: int) -> torch.Tensor:
+        """(planes, rows, N_i) of problem i, for tests."""
+        width = (self.hq if i == 0 else self.hkv) * 128
+        base = i * self.pstride
+        return self.data[base:base + self.planes * self.rows * width].view(self.planes, self.rows, width)
+
+
+def qmv_norm_planes(weights, x: torch.Tensor, out: QkvPlanes, norm_in: NormStats | None = None,
+                    eps: float = 1e-6, stream=None) -> int:
+    """The q, k and v projections of x' rows (with the RMSNorm folded in when `norm_in` is
+    given) as fp32 output planes, one per K-range of the plan, left for the reader to add
+    (imq_qmv_norm_planes); returns the plane count."""
+    if len(weights) != 3:
+        raise ValueError("q, k and v: three weights")
+    _require(x, torch.bfloat16, "x")
+    m = int(x.shape[0])
+    if x.dim() != 2 or not x.is_contiguous() or m != out.rows:
+        raise ValueError("x must be a contiguous (rows, K) tensor of the planes' rows")
+    probs = (Problem * 3)()
+    for i, (w, s, b) in enumerate(weights):
+        n, k = check_weights(w, s, b)
+        if int(x.shape[1]) != k or n != (out.hq if i == 0 else out.hkv) * 128:
+            raise ValueError(f"weight {i} does not match x or the planes' head counts")
+        probs[i] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), k, None, n, n, k)
+    nin = norm_in.norm_in(eps) if norm_in is not None else None
+    splits = _I32(0)
+    if int(lib().imq_qmv_norm_splits(probs, 3, m)) > out.max_planes:
+        raise ValueError("the plan splits into more planes than the buffer holds")
+    _check(lib().imq_qmv_norm_planes(probs, 3, m, GROUP_SIZE, BITS,
+                                     ctypes.byref(nin) if nin is not None else None,
+                                     _ptr(out.data), out.pstride, ctypes.byref(splits), _stream(stream)))
+    out.planes = int(splits.value)
+    return out.planes
+
+
+def attention_fused_planes(qkv: QkvPlanes, q_norm, k_norm, positions, slots, k_pool, v_pool, out,
+                           max_len: int, theta: float, eps: float, workspace: torch.Tensor,
+                           counters: torch.Tensor, stream=None) -> torch.Tensor:
+    """attention_fused reading q, k and v as the planes of qmv_norm_planes (each value the
+    sum of its planes in order, rounded to bf16)."""
+    for name, t in (("q_norm", q_norm), ("k_norm", k_norm), ("k_pool", k_pool), ("v_pool", v_pool),
+                    ("out", out)):
+        _require(t, torch.bfloat16, name)
+    _require(positions, torch.int32, "positions")
+    _require(slots, torch.int32, "slots")
+    _require(workspace, torch.float32, "workspace")
+    _require(counters, torch.int32, "counters")
+    num_slots, hkv, capacity, d = k_pool.shape
+    b = int(positions.numel())
+    if (d != 128 or v_pool.shape != k_pool.shape or hkv != qkv.hkv or b != qkv.rows
+            or out.numel() != b * qkv.hq * d or slots.numel() != b or qkv.planes < 1):
+        raise ValueError("inconsistent planes/pool/out shapes (head dim 128)")
+    if workspace.numel() < attention_workspace(b, qkv.hq, max_len):
+        raise ValueError("workspace too small")
+    if counters.numel() < b * hkv:
+        raise ValueError("counters too small")
+    _check(lib().imq_attention_fused_planes(_ptr(qkv.data), qkv.pstride, qkv.planes, _ptr(q_norm),
+                                            _ptr(k_norm), _ptr(positions), _ptr(slots), _ptr(k_pool),
+                                            _ptr(v_pool), _ptr(out), b, qkv.hq, hkv, capacity, num_slots,
+                                            int(max_len), float(theta), float(eps), _ptr(workspace),
+                                            _ptr(counters), _stream(stream)))
     return out
 
 

@@ -33,6 +33,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -1513,6 +1514,8 @@ struct DmaArgs {
   int32_t tiles_max;             // counters per problem
   NormIn nin;                    // input rows scaled by 1/rms (nin.ssq == nullptr: off)
   ResidualOut res;               // residual epilogue instead of y (res.h == nullptr: off)
+  int32_t planes;                // 1: every K-range's partial is an output plane (no y)
+  int32_t pad;
 };
 
 template <int W, int GMAX, bool SPLIT>
@@ -1747,20 +1750,25 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
     }
     wn = d.res.w && n < N ? bf16_bits_to_f32(d.res.w[n]) : 0.0f;
   };
-  if (!SPLIT) {
+  if (!SPLIT && !d.planes) {
     if (res) load_res();
     finish(sums, hv, wn);
     return;
   }
-  // split: park the partial, count the tile's arrivals; the last one adds them in order
+  // split: park the partial, count the tile's arrivals; the last one adds them in order.
+  // As output planes (d.planes): each range's partial, scaled by the rows' 1/rms, is the
+  // output, and the reader adds the planes in range order.
   const __amdgpu_buffer_rsrc_t prs =
       buffer_rsrc(d.partial + pi * d.pstride, (uint32_t)((int64_t)splits * M * N * 4));
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     const int m = wave + i * W;
-    if (m < M && n < N)
-      store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(sums[i]));
+    if (m < M && n < N) {
+      const float v = d.planes && norm_in ? sums[i] * norm_row_inv(d.nin, nsum, m) : sums[i];
+      store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(v));
+    }
   }
+  if (d.planes) return;
   wait_vmem();
   __syncthreads();
   uint32_t* cnt = d.counters + (int64_t)pi * d.tiles_max + tile;
@@ -2472,17 +2480,21 @@ hipError_t launch_dma_g(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl
 }
 
 hipError_t launch_dma(const LaunchArgs& a, const DmaPlan& pl, void* ws, hipStream_t stream,
-                      const NormIn* nin = nullptr, const ResidualOut* res = nullptr) {
+                      const NormIn* nin = nullptr, const ResidualOut* res = nullptr,
+                      float* planes = nullptr, int64_t plane_pstride = 0) {
   DmaArgs d;
   memset(&d, 0, sizeof(d));
   if (nin) d.nin = *nin;
   if (res) d.res = *res;
-  if (pl.splits > 1) {
+  if (planes) {  // the partials are the outputs: no counters, no workspace
+    d.partial = planes;
+    d.planes = 1;
+  } else if (pl.splits > 1) {
     char* base = static_cast<char*>(ws);
     d.counters = reinterpret_cast<uint32_t*>(base);
     d.partial = reinterpret_cast<float*>(base + kCounterBytes);
   }
-  d.pstride = (int64_t)pl.pstride;
+  d.pstride = planes ? plane_pstride : (int64_t)pl.pstride;
   d.splits = pl.splits;
   d.range = pl.range;
   d.tiles_max = pl.grid_x;
@@ -2971,6 +2983,57 @@ int32_t imq_qmv_norm(const imq_problem* problems, int32_t count, int32_t M, int3
     return fail(IMQ_EINVAL, "this call needs a 16-byte aligned workspace of imq_qmv_norm_workspace bytes (" +
                                 std::to_string(pl.bytes) + ")");
   const hipError_t e = launch_dma(a, pl, workspace, static_cast<hipStream_t>(stream), &nin, &res);
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused-norm qmv launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+int32_t imq_qmv_norm_splits(const imq_problem* problems, int32_t count, int32_t M) {
+  if (!problems || count < 1 || count > IMQ_MAX_PROBLEMS || M < 1 || M > IMQ_MAX_ROWS) return 0;
+  int32_t code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return 0;
+  LaunchArgs a;
+  memset(&a, 0, sizeof(a));
+  for (int i = 0; i < count; ++i) {
+    if (problems[i].N < 1 || problems[i].K < 64 || problems[i].K % 64) return 0;
+    a.p[i].N = problems[i].N;
+    a.p[i].K = problems[i].K;
+    a.p[i].x = problems[i].x;
+    a.p[i].ldx = M > 1 ? problems[i].ldx : problems[i].K;
+  }
+  a.count = count;
+  a.M = M;
+  DmaPlan pl;
+  return plan_dma_norm(a, dev->cu_count, &pl) ? pl.splits : 0;
+}
+
+int32_t imq_qmv_norm_planes(const imq_problem* problems, int32_t count, int32_t M,
+                            int32_t group_size, int32_t bits, const imq_norm_in* in, float* planes,
+                            int64_t pstride, int32_t* splits, void* stream) {
+  if (!planes || !aligned(planes, 4) || !splits) return fail(IMQ_EINVAL, "planes and splits must be non-null");
+  if (!problems) return fail(IMQ_EINVAL, "problems must be non-null");
+  // the problems' y are not written: validate against the planes
+  imq_problem probs[IMQ_MAX_PROBLEMS];
+  if (count < 1 || count > IMQ_MAX_PROBLEMS) return fail(IMQ_EINVAL, "count must be 1..IMQ_MAX_PROBLEMS");
+  for (int i = 0; i < count; ++i) {
+    probs[i] = problems[i];
+    probs[i].y = planes;
+    probs[i].ldy = problems[i].N;
+  }
+  LaunchArgs a;
+  DmaPlan pl;
+  NormIn nin;
+  ResidualOut res;
+  const DeviceInfo* dev = nullptr;
+  int32_t code = build_norm(a, &pl, &nin, &res, probs, count, M, group_size, bits, in, nullptr, &dev);
+  if (code != IMQ_OK) return code;
+  int64_t need = 0;
+  for (int i = 0; i < count; ++i) need = std::max(need, (int64_t)pl.splits * M * probs[i].N);
+  if (pstride < need) return fail(IMQ_EINVAL, "pstride must hold every plane of the widest problem (" +
+                                                  std::to_string(need) + " floats)");
+  if (((int64_t)count * pstride) * 4 >= ((int64_t)1 << 31)) return fail(IMQ_EUNSUPPORTED, "planes of 2 GiB or more");
+  *splits = pl.splits;
+  const hipError_t e = launch_dma(a, pl, nullptr, static_cast<hipStream_t>(stream), &nin, &res, planes, pstride);
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused-norm qmv launch failed: ") + hipGetErrorString(e));
   return ok();
 }

@@ -101,7 +101,14 @@ struct Stage {
   float* ml;
   uint32_t* combine;  // one counter per (request, KV head)
   int32_t Hq, Hkv, capacity, num_slots, max_len, splits, cps, pad3;
+  // q, k and v as fp32 output planes of a split projection instead (staged launches only):
+  // problem i (q, k, v), plane s, request b at qkv + i * qkv_pstride + (s * qkv_rows + b) * N_i
+  const float* qkv;
+  int64_t qkv_pstride;
+  int32_t qkv_splits, qkv_rows;
 };
+
+constexpr int kMaxQkvPlanes = 4;
 
 struct StepArgs {
   uint32_t* done;
@@ -548,18 +555,52 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
                    : (uint32_t)ld16_sc1(p, bytes, off);
   };
   uint32_t qx[2][2], kx[2] = {0u, 0u}, vx[2] = {0u, 0u};
+  if (kStaged && S.qkv != nullptr) {
+    // the planes of element `elem` of problem `pi` (width nw) for request b, added in plane
+    // order from zero and rounded to bf16: every plane's load issued before the first add
+    const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(S.qkv, (uint32_t)(3 * S.qkv_pstride * 4));
+    const int np = S.qkv_splits, rows = S.qkv_rows;
+    auto planes = [&](int pi, int nw, int elem) -> uint32_t {
+      float v[kMaxQkvPlanes];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int g = wave + 4 * r;
-    const uint32_t off = (uint32_t)((b * Hq + kvh * G + (g < G ? g : 0)) * kD) * 2u;
-    qx[r][0] = g < G ? ld16(S.q, qbytes, off + 2u * lane) : 0u;
-    qx[r][1] = g < G ? ld16(S.q, qbytes, off + 2u * (lane + 64)) : 0u;
-  }
-  if (wave == 0) {
-    kx[0] = ld16(S.k, kvbytes, kvoff + 2u * lane);
-    kx[1] = ld16(S.k, kvbytes, kvoff + 2u * (lane + 64));
-    vx[0] = ld16(S.v, kvbytes, kvoff + 2u * lane);
-    vx[1] = ld16(S.v, kvbytes, kvoff + 2u * (lane + 64));
+      for (int sp = 0; sp < kMaxQkvPlanes; ++sp) {
+        const uint32_t off = (uint32_t)(pi * S.qkv_pstride + (int64_t)(sp * rows + b) * nw + elem) * 4u;
+        v[sp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, sp < np ? off : kPastBuffer, 0, 0));
+      }
+      float t = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp < kMaxQkvPlanes; ++sp)
+        if (sp < np) t += v[sp];
+      return to_bf(t);
+    };
+    const int nq = Hq * kD, nkv = Hkv * kD;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int g = wave + 4 * r;
+      const int e0 = (kvh * G + (g < G ? g : 0)) * kD;
+      qx[r][0] = g < G ? planes(0, nq, e0 + lane) : 0u;
+      qx[r][1] = g < G ? planes(0, nq, e0 + lane + 64) : 0u;
+    }
+    if (wave == 0) {
+      kx[0] = planes(1, nkv, kvh * kD + lane);
+      kx[1] = planes(1, nkv, kvh * kD + lane + 64);
+      vx[0] = planes(2, nkv, kvh * kD + lane);
+      vx[1] = planes(2, nkv, kvh * kD + lane + 64);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int g = wave + 4 * r;
+      const uint32_t off = (uint32_t)((b * Hq + kvh * G + (g < G ? g : 0)) * kD) * 2u;
+      qx[r][0] = g < G ? ld16(S.q, qbytes, off + 2u * lane) : 0u;
+      qx[r][1] = g < G ? ld16(S.q, qbytes, off + 2u * (lane + 64)) : 0u;
+    }
+    if (wave == 0) {
+      kx[0] = ld16(S.k, kvbytes, kvoff + 2u * lane);
+      kx[1] = ld16(S.k, kvbytes, kvoff + 2u * (lane + 64));
+      vx[0] = ld16(S.v, kvbytes, kvoff + 2u * lane);
+      vx[1] = ld16(S.v, kvbytes, kvoff + 2u * (lane + 64));
+    }
   }
   const float qn0 = bf(S.q_norm[lane]), qn1 = bf(S.q_norm[lane + 64]);
   const float kn0 = bf(S.k_norm[lane]), kn1 = bf(S.k_norm[lane + 64]);
@@ -1050,25 +1091,26 @@ void attention_split(int B, int Hkv, int span, int* splits, int* cps) {
   attention_splits(B, Hkv, span, splits, cps);
 }
 
-}  // namespace
-
-extern "C" {
-
-int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* planes,
+                        int64_t pstride, int32_t nplanes,
                             const uint16_t* q_norm, const uint16_t* k_norm,
                             const int32_t* positions, const int32_t* slots, uint16_t* k_pool,
                             uint16_t* v_pool, uint16_t* out, int32_t B, int32_t Hq, int32_t Hkv,
                             int32_t capacity, int32_t num_slots, int32_t max_len, float theta,
                             float eps, float* workspace, uint32_t* counters, void* stream) {
-  if (!q || !k || !v || !q_norm || !k_norm || !positions || !slots || !k_pool || !v_pool || !out ||
-      !workspace || !counters)
+  if ((planes ? false : (!q || !k || !v)) || !q_norm || !k_norm || !positions || !slots || !k_pool ||
+      !v_pool || !out || !workspace || !counters)
     return fail(IMQ_EINVAL, "null pointer");
+  if (planes && (nplanes < 1 || nplanes > kMaxQkvPlanes || !aligned(planes, 4) ||
+                 pstride < (int64_t)nplanes * B * (Hq > Hkv ? Hq : Hkv) * kD ||
+                 3 * pstride * 4 >= ((int64_t)1 << 31)))
+    return fail(IMQ_EINVAL, "q/k/v planes: 1 to 4 planes, 4-byte aligned, pstride >= planes * B * Hq * 128, under 2 GiB");
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || Hq / Hkv > 8)
     return fail(IMQ_EINVAL, "bad head counts (Hq a multiple of Hkv, at most 8 query heads per KV head)");
   if (capacity < 1 || num_slots < 1 || max_len < 1 || !(theta > 0.0f) || !(eps >= 0.0f))
     return fail(IMQ_EINVAL, "bad capacity, slot count, max_len, theta or eps");
   // the same layout requirements as imq_attention_decode, whose attention this computes
-  if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(workspace, 16))
+  if ((!planes && !aligned(q, 16)) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(workspace, 16))
     return fail(IMQ_EINVAL, "q, pools and workspace must be 16-byte aligned");
   if (!aligned(counters, 4)) return fail(IMQ_EINVAL, "counters must be 4-byte aligned");
   if (B > 65535 || Hkv > 65535 || Hq > 65535)
@@ -1108,6 +1150,10 @@ int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t
   A.max_len = span;
   A.splits = splits;
   A.cps = cps;
+  A.qkv = planes;
+  A.qkv_pstride = pstride;
+  A.qkv_splits = planes ? nplanes : 0;
+  A.qkv_rows = B;
   StepArgs a;
   memset(&a, 0, sizeof(a));
   a.ntasks = A.count;
@@ -1118,6 +1164,32 @@ int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused attention launch: ") + hipGetErrorString(e));
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            const uint16_t* q_norm, const uint16_t* k_norm,
+                            const int32_t* positions, const int32_t* slots, uint16_t* k_pool,
+                            uint16_t* v_pool, uint16_t* out, int32_t B, int32_t Hq, int32_t Hkv,
+                            int32_t capacity, int32_t num_slots, int32_t max_len, float theta,
+                            float eps, float* workspace, uint32_t* counters, void* stream) {
+  return attention_fused(q, k, v, nullptr, 0, 0, q_norm, k_norm, positions, slots, k_pool, v_pool, out, B,
+                         Hq, Hkv, capacity, num_slots, max_len, theta, eps, workspace, counters, stream);
+}
+
+int32_t imq_attention_fused_planes(const float* planes, int64_t pstride, int32_t nplanes,
+                                   const uint16_t* q_norm, const uint16_t* k_norm,
+                                   const int32_t* positions, const int32_t* slots, uint16_t* k_pool,
+                                   uint16_t* v_pool, uint16_t* out, int32_t B, int32_t Hq, int32_t Hkv,
+                                   int32_t capacity, int32_t num_slots, int32_t max_len, float theta,
+                                   float eps, float* workspace, uint32_t* counters, void* stream) {
+  if (!planes) return fail(IMQ_EINVAL, "planes must be non-null");
+  return attention_fused(nullptr, nullptr, nullptr, planes, pstride, nplanes, q_norm, k_norm, positions,
+                         slots, k_pool, v_pool, out, B, Hq, Hkv, capacity, num_slots, max_len, theta, eps,
+                         workspace, counters, stream);
 }
 
 int32_t imq_qmv_program_create(const imq_qmv_stage* stages, int32_t count, imq_program** out) {

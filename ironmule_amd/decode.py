@@ -146,6 +146,7 @@ class DecodeState:
         # projections (batches of FUSED_NORM_ROWS or more)
         self.stats_in = _native.NormStats(batch, c.hidden, device)
         self.stats_post = _native.NormStats(batch, c.hidden, device)
+        self.qkv_planes = _native.QkvPlanes(batch, c.heads, c.kv_heads, device)
         self.workspace = torch.empty(_native.attention_workspace(batch, c.heads, self.max_len),
                                      dtype=torch.float32, device=device)
         self.attn_counters = torch.zeros(batch * c.kv_heads, dtype=torch.int32, device=device)
@@ -207,8 +208,10 @@ def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream
 
         x' = bf16(h * w_in), stats                 imq_rmsnorm_prescale (first layer only)
         per layer:
-            q, k, v = inv * (x' @ W.T)             imq_qmv_norm (norm_in: the stats)
-            attention                              imq_attention_fused
+            q, k, v = inv * (x' @ W.T)             imq_qmv_norm_planes (norm_in: the stats;
+                                                   the K-ranges' partials as output planes)
+            attention                              imq_attention_fused_planes (adds the
+                                                   planes as it reads q, k and v)
             h += o @ Wo.T; x' = bf16(h * w_post)   imq_qmv_norm (residual epilogue: h, x'
                                                    and the per-tile sums of squares)
             act = silu(inv * g) * (inv * u)        imq_qmv_gate_up_silu_norm
@@ -223,11 +226,11 @@ def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream
     n.embed(*weights.embed, s.tokens, s.h, stream=stream)
     n.rmsnorm_prescale(s.h, weights.layers[0]["input_norm"], s.x, s.stats_in, stream=stream)
     for i, layer in enumerate(weights.layers):
-        n.qmv_norm([layer["q"], layer["k"], layer["v"]], s.x, outs=[s.q, s.k, s.v],
-                   norm_in=s.stats_in, eps=c.eps, stream=stream)
-        n.attention_fused(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
-                          s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len, c.theta,
-                          c.eps, s.workspace, s.attn_counters, stream=stream)
+        n.qmv_norm_planes([layer["q"], layer["k"], layer["v"]], s.x, s.qkv_planes,
+                          norm_in=s.stats_in, eps=c.eps, stream=stream)
+        n.attention_fused_planes(s.qkv_planes, layer["q_norm"], layer["k_norm"], s.positions,
+                                 s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len,
+                                 c.theta, c.eps, s.workspace, s.attn_counters, stream=stream)
         n.qmv_norm([layer["o"]], s.attn, residual=s.h, next_norm=layer["post_norm"], x_out=s.x,
                    stats_out=s.stats_post, stream=stream)
         n.gate_up_silu_norm(layer["gate"], layer["up"], s.x, s.act, s.stats_post, c.eps,

@@ -224,3 +224,60 @@ def test_refusals(native, oracle):
     w3, s3, b3, x3 = to_device(pr)
     with pytest.raises(NativeError):
         native.qmv_norm([(w3, s3, b3)], x3, norm_in=native.NormStats(8, 512, "cuda"))
+
+
+@pytest.mark.parametrize("m", [32, 5, 1])
+def test_qkv_planes(native, oracle, m):
+    """imq_qmv_norm_planes: the planes added in order equal the in-launch reduction (inv = 1/2
+    exactly: half the plain projection, bit for bit, where that takes the same kernel; the
+    oracle's bar at one row); then imq_attention_fused_planes gives
+    the bits imq_attention_fused gives on those q/k/v rows, outputs and KV pools alike."""
+    shapes = [(4096, 2560), (1024, 2560), (1024, 2560)]
+    probs, weights, x = _weights(oracle, shapes, m, oracle.SEED_BASE + 2600 + m)
+    announce("q/k/v planes", m)
+    st = _half_stats(native, m, 2560, 40)
+    planes = native.QkvPlanes(m, 32, 8, "cuda")
+    count = native.qmv_norm_planes(weights, x, planes, norm_in=st, eps=0.0)
+    plain = native.qmv_grouped(weights, [x] * 3)
+    torch.cuda.synchronize()
+    assert 1 <= count <= 4
+    rows = []
+    for i in range(3):
+        pl = planes.view(i)
+        tot = torch.zeros_like(pl[0])
+        for s in range(count):
+            tot = tot + pl[s]
+        got = tot.to(torch.bfloat16)
+        if m >= 5:  # the plain launch takes the same kernel and plan from 5 rows
+            assert torch.equal(got, (plain[i].float() * 0.5).to(torch.bfloat16)), i
+        else:  # one row takes the one-row VALU tile: the oracle's bar instead
+            ref, mag = oracle.qmv_f64(probs[i].w, probs[i].s, probs[i].b, probs[i].x)
+            v = oracle.check_bf16(bf16_bits(got), ref * 0.5, mag * 0.5)
+            assert v.ok, (i, v.detail)
+        rows.append(got)
+    # the attention launch on the planes against the launch on the bf16 rows
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2600 + m)
+    slots_n, cap = max(m, 2), 96
+    pools = [torch.randn((slots_n, 8, cap, 128), device="cuda", generator=g).to(torch.bfloat16) for _ in range(2)]
+    qn = (torch.rand(128, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+    kn = (torch.rand(128, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+    positions = torch.tensor([(7 * i + 3) % cap for i in range(m)], dtype=torch.int32, device="cuda")
+    slots = torch.arange(m, dtype=torch.int32, device="cuda") % slots_n
+    ws = torch.empty(native.attention_workspace(m, 32, cap), dtype=torch.float32, device="cuda")
+    outs, kps, vps = [], [], []
+    for use_planes in (False, True):
+        kp, vp = pools[0].clone(), pools[1].clone()
+        out = torch.empty((m, 32 * 128), dtype=torch.bfloat16, device="cuda")
+        cnt = torch.zeros(m * 8, dtype=torch.int32, device="cuda")
+        if use_planes:
+            native.attention_fused_planes(planes, qn, kn, positions, slots, kp, vp, out, cap, 1e6, 1e-6, ws, cnt)
+        else:
+            native.attention_fused(rows[0], rows[1], rows[2], qn, kn, positions, slots, kp, vp, out, cap,
+                                   1e6, 1e-6, ws, cnt)
+        torch.cuda.synchronize()
+        outs.append(out)
+        kps.append(kp)
+        vps.append(vp)
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(kps[0], kps[1]) and torch.equal(vps[0], vps[1])
