@@ -318,8 +318,8 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
     """Full synthetic Qwen3-4B decode step (36 layers of 4-bit projections + the 151,936-
     token tied head, GQA attention over a 512-token KV context per request), as one HIP
     graph per batch size; returns tokens/s and the weight + KV bytes per step."""
-    from ironmule_amd.decode import (DecodeState, DecoderConfig, PersistentDecode, decode_step,
-                                     random_weights)
+    from ironmule_amd.decode import (FUSED_NORM_ROWS, DecodeState, DecoderConfig, PersistentDecode,
+                                     decode_step, random_weights)
 
     cfg = DecoderConfig()
     weights = random_weights(cfg, device, seed=seed)
@@ -334,8 +334,13 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
         state.set_requests(torch.randint(0, cfg.vocab, (b,), generator=gen, device=device).tolist(),
                            list(range(b)), [CONTEXT] * b)
         stream = torch.cuda.Stream(device=device)
+        # launches per step: the embedding, the layers, the final norm and the head; from
+        # FUSED_NORM_ROWS requests the RMSNorms run inside the projections (five launches per
+        # layer and one more for the first layer's input norm), below it nine per layer
+        per_layer = 5 if b >= FUSED_NORM_ROWS else (7 if b >= 5 else 8)
+        extra = 4 if b >= FUSED_NORM_ROWS else 3
         paths = {"per_kernel": (lambda: decode_step(weights, state, stream=stream),
-                                2 + cfg.layers * 9)}
+                                extra + cfg.layers * per_layer)}
         if b == 1:
             staged = PersistentDecode(weights, state, staged=True)
             paths["staged_program"] = (lambda: staged.step(stream), 2 + cfg.layers * 5)
