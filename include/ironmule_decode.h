@@ -3,7 +3,7 @@
  * launches of a Qwen3-style decoder on MI355X (gfx950), in libironmule_qmv.so.
  *
  * One decode step of B requests (each its own KV slot and position), as the reference
- * composes it (ironmule/dense_plan.py:351-376, ironmule/dense_cpu.py:188-220):
+ * composes it (ironmule/dense_plan.py:337-363, ironmule/dense_cpu.py:188-220):
  *   h = embed(tokens)
  *   per layer: x = rms_norm(h) ; q,k,v = qmv(x) ; q,k = rope(rms_norm_head(q,k)) ;
  *              KV[slot][pos] = k,v ; o = attention(q, KV[slot][:pos+1]) ;
@@ -20,7 +20,7 @@
  *   h         fp32 (B, dim): the residual stream
  *   bf16      activations (B, dim) and heads (B, H, 128)
  *   KV pool   bf16 (slots, kv_heads, capacity, 128) per layer, the reference's pool layout
- *             (dense_plan.py:294-299, rows = (slot * kv_heads + head) * capacity + position)
+ *             (dense_plan.py:297-301, rows = (slot * kv_heads + head) * capacity + position)
  */
 #ifndef IRONMULE_DECODE_H
 #define IRONMULE_DECODE_H
@@ -39,7 +39,7 @@ extern "C" {
 /* h[b][:] = dequantised embedding row tokens[b] (4-bit, group 64, bf16 scales/biases, the
  * qmv weight format), as fp32.  Tokens outside [0, vocab) are refused by the kernel:
  * their rows are written as NaN.
- * Replaces trunk.embed_tokens(tokens) (ironmule/dense_plan.py:357; dense_cpu.py:200). */
+ * Replaces trunk.embed_tokens(tokens) (ironmule/dense_plan.py:343; dense_cpu.py:200). */
 IMQ_API int32_t imq_embed(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                           const int32_t* tokens, float* h, int32_t B, int32_t vocab, int32_t dim,
                           void* stream);
@@ -57,7 +57,7 @@ IMQ_API int32_t imq_rmsnorm_prescale(float* h, const uint16_t* delta, const uint
 /* If delta is non-NULL, h += delta (bf16) first; then out = bf16(h * rsqrt(mean(h^2) + eps)
  * * weight), per row of dim values (dim <= 8192).
  * Replaces mx.fast.rms_norm(h, weight, eps) and the residual adds `h = h + ...`
- * (ironmule/dense_plan.py:362, 373-376). */
+ * (ironmule/dense_plan.py:348, 358-359, 362). */
 IMQ_API int32_t imq_add_rmsnorm(float* h, const uint16_t* delta, const uint16_t* weight,
                                 uint16_t* out, int32_t B, int32_t dim, float eps, void* stream);
 
@@ -67,7 +67,7 @@ IMQ_API int32_t imq_add_rmsnorm(float* h, const uint16_t* delta, const uint16_t*
  * the untouched v go to the KV pools (num_slots slots of `capacity` positions) at
  * (slots[b], head, positions[b]).  A request whose position is not in [0, capacity) or
  * whose slot is not in [0, num_slots) is refused: nothing is written for it.
- * Replaces q_norm/k_norm + _rope + the KV write (ironmule/dense_plan.py:363-372, 378-383). */
+ * Replaces q_norm/k_norm + _rope + the KV write (ironmule/dense_plan.py:349-356, 365-371). */
 IMQ_API int32_t imq_qk_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                  const uint16_t* q_norm, const uint16_t* k_norm,
                                  const int32_t* positions, const int32_t* slots, uint16_t* q_out,
@@ -86,7 +86,7 @@ IMQ_API size_t imq_attention_workspace(int32_t B, int32_t Hq, int32_t max_len);
  * several workgroups (whole 64-key chunks each, enough splits to fill the GPU); a second
  * launch merges the splits in split order, so the result does not depend on scheduling.
  * Calls that share `workspace` must not overlap.
- * Replaces fa2 (ironmule/dense_plan.py:250-278): the FA2_PARTIAL / FA2_COMBINE pair. */
+ * Replaces fa2 (ironmule/dense_plan.py:258-274): the FA2_PARTIAL / FA2_COMBINE pair. */
 IMQ_API int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool,
                                      const uint16_t* v_pool, const int32_t* lengths,
                                      const int32_t* slots, uint16_t* out, int32_t B, int32_t Hq,
@@ -134,7 +134,7 @@ IMQ_API int32_t imq_attention_fused_planes(const float* planes, int64_t pstride,
                                            float* workspace, uint32_t* counters, void* stream);
 
 /* out = bf16(silu(gate) * up), silu(g) = g / (1 + exp(-g)), n elements.
- * Replaces swiglu(gate, up) (ironmule/dense_plan.py:374-375; nn.silu in dense_cpu.py:216). */
+ * Replaces swiglu(gate, up) (ironmule/dense_plan.py:360; nn.silu in dense_cpu.py:216). */
 IMQ_API int32_t imq_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
                              void* stream);
 

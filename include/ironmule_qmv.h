@@ -103,7 +103,7 @@ IMQ_API int32_t imq_qmv(const uint32_t* w, const uint16_t* scales, const uint16_
  * rows are `ld_act` apart.  5 <= M <= 32 and K % 256 == 0, else IMQ_EUNSUPPORTED (the caller
  * makes the two launches).  Replaces the fused gate/up launch and the SwiGLU that follows it:
  *   ironmule/fast.py:186-215             fuse_projections (gate and up in one launch)
- *   ironmule/dense_plan.py:374-375       silu(gate) * up
+ *   ironmule/dense_plan.py:360            silu(gate) * up
  */
 IMQ_API int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate,
                 const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,

@@ -9,7 +9,7 @@
  * then waits for its input stage, so the weight stream of later stages keeps HBM busy
  * while the activations of earlier ones are still being produced.  This replaces the
  * per-kernel launches of a decode step (the reference issues one kernel per projection
- * and per attention piece: ironmule/dense_plan.py:351-383, cuda_native.py:155-168).
+ * and per attention piece: ironmule/dense_plan.py:337-363, cuda_native.py:155-168).
  *
  * Contract:
  *   * Creation validates shapes, plans the tasks and allocates the program's device
@@ -68,7 +68,7 @@ typedef struct {
  * with the same rounding points as the per-kernel path (ironmule_decode.h).  A request
  * whose slot is outside [0, num_slots) or whose position is outside [0, capacity) gets
  * no KV write and zeros from attention.
- * Replaces DensePlan.forward's decode step (ironmule/dense_plan.py:351-383;
+ * Replaces DensePlan.forward's decode step (ironmule/dense_plan.py:337-363;
  * ironmule/dense_cpu.py:188-220) for one request. */
 typedef struct {
   int32_t layers, batch, hidden, heads, kv_heads, intermediate, vocab;

@@ -1,6 +1,6 @@
 """One decode step of a Qwen3-style decoder whose projections are 4-bit qmv on MI355X.
 
-Mirrors the reference's decode composition (ironmule/dense_plan.py:351-383,
+Mirrors the reference's decode composition (ironmule/dense_plan.py:337-363,
 `DensePlan.forward`; ironmule/dense_cpu.py:188-220, `CpuDensePlan.forward`) over B
 continuous-batched requests, each with its own KV slot and position:
 
@@ -116,7 +116,7 @@ class DecodeState:
     """KV pools and every activation buffer of a decode step for `batch` rows.
 
     The pools are (slots, kv_heads, capacity, 128) bf16 per layer, the reference's pool
-    layout (ironmule/dense_plan.py:294-299).  `max_len` bounds the lengths a step may
+    layout (ironmule/dense_plan.py:297-301).  `max_len` bounds the lengths a step may
     attend over (it sizes the attention workspace and grid)."""
 
     def __init__(self, config: DecoderConfig, batch: int, slots: int, capacity: int,

@@ -3,7 +3,7 @@
 Only `tests/`, `__graft_entry__.smoke()` and the CPU-baseline leg of `bench.py` may use
 this module, and only as the checker.  It restates, in numpy float64, the reference's
 decode step for a Qwen3-style decoder (ironmule/dense_cpu.py:188-220, `CpuDensePlan.
-forward`; ironmule/dense_plan.py:351-383, `DensePlan.forward` and `_rope`):
+forward`; ironmule/dense_plan.py:337-371, `DensePlan.forward` and `_rope`):
 
     h = embed(tokens)                                         (fp32 residual stream)
     per layer:
@@ -49,7 +49,7 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 
 def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
     """x * rsqrt(mean(x^2) + eps) * weight over the last axis (mx.fast.rms_norm,
-    ironmule/dense_plan.py:362, 364-367)."""
+    ironmule/dense_plan.py:348-352, 359, 362)."""
     x = np.asarray(x, dtype=np.float64)
     inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
     return x * inv * np.asarray(weight, dtype=np.float64)
@@ -58,7 +58,7 @@ def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
 def rope(x: np.ndarray, positions: np.ndarray, theta: float) -> np.ndarray:
     """Non-interleaved rotary embedding over the last axis (D = 128): pair (i, i + D/2)
     turns by pos * theta^(-2i / D) (mx.fast.rope(..., traditional=False, base=theta,
-    scale=1.0, offset=pos), ironmule/dense_plan.py:378-383).  x is (B, H, D), positions (B,)."""
+    scale=1.0, offset=pos), ironmule/dense_plan.py:365-371).  x is (B, H, D), positions (B,)."""
     x = np.asarray(x, dtype=np.float64)
     half = x.shape[-1] // 2
     inv_freq = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / x.shape[-1])
@@ -82,7 +82,7 @@ def attention(q: np.ndarray, keys: np.ndarray, values: np.ndarray, scale: float)
 
 
 def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
-    """silu(gate) * up, silu(g) = g / (1 + exp(-g)) (swiglu, ironmule/dense_plan.py:374-375)."""
+    """silu(gate) * up, silu(g) = g / (1 + exp(-g)) (swiglu, ironmule/dense_plan.py:360)."""
     g = np.asarray(gate, np.float64)
     return g / (1.0 + np.exp(-g)) * np.asarray(up, np.float64)
 
