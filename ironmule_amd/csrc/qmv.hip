@@ -1720,10 +1720,12 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   // h += bf16(y), x' = bf16(h * w) and the tile's sums of squares of h per row instead.
   const bool res = d.res.h != nullptr;  // uniform
   auto finish = [&](const float (&v)[MI], const float (&hv)[MI], float wn) {
+    float sq[MI];  // the new h squared (residual epilogue), 0 outside the rows and columns
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int m = wave + i * W;
-      if (m >= M) break;
+      sq[i] = 0.0f;
+      if (m >= M) continue;
       const float y = norm_in ? v[i] * norm_row_inv(d.nin, nsum, m) : v[i];
       if (!res) {
         if (n < N) store_y(a, P, m, n, y);
@@ -1733,10 +1735,20 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
       if (n < N) {
         d.res.h[(size_t)m * d.res.ldh + n] = hn;
         if (d.res.w) d.res.x[(size_t)m * d.res.ldx + n] = f32_to_bf16_bits(hn * wn);
+        sq[i] = hn * hn;
       }
-      if (d.res.ssq) {
-        const float ss = wave_sum(n < N ? hn * hn : 0.0f);
-        if (lane == 0) d.res.ssq[m * d.res.ld + tile] = ss;
+    }
+    if (res && d.res.ssq) {
+      // the rows' sums over the tile's 64 columns: the DPP stages of all rows first (their
+      // chains interleave), then each row's four 16-lane sums, as wave_sum adds them
+#pragma unroll
+      for (int i = 0; i < MI; ++i) sq[i] = row16_sum(sq[i]);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = wave + i * W;
+        const float ss = (lane_value(sq[i], 0) + lane_value(sq[i], 16)) +
+                         (lane_value(sq[i], 32) + lane_value(sq[i], 48));
+        if (m < M && lane == 0) d.res.ssq[m * d.res.ld + tile] = ss;
       }
     }
   };
