@@ -884,6 +884,9 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
 // (v_mfma_f32_32x32x2_f32) per pair of groups: A = the two groups' row sums of x, B = the
 // two groups' c = b - 16 s per weight row; the weights enter the MFMAs as 1 + q/16.
 // Requires K % 256 == 0 and x rows at x + m * ldx (no row-pointer table).
+#ifndef IMQ_STAGED_DEPTH
+#define IMQ_STAGED_DEPTH 2
+#endif
 namespace staged {
 constexpr int kWN = 2, kWK = 2;                   // wavefronts along N and along K
 constexpr int kRows = 32 * kWN;                   // weight rows per workgroup
@@ -974,9 +977,16 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   const uint32_t sb_src = (uint32_t)sb_n * (uint32_t)G * 2u;
   const uint32_t sb_dst = (uint32_t)(kWBytes + kXBytes + sb_rem * 16 + 8 * sb_is_b);
 
-  uint4 wreg[kWP], xreg[kXP];
-  u32x2_t sbreg;
-  auto fetch = [&](int st) {
+  // A stage's loads in registers: x one stage ahead (from L2), the weights, scales and
+  // biases IMQ_STAGED_DEPTH stages ahead (from HBM) in DEPTH register sets.  Each stage
+  // issues the next x before the weights DEPTH ahead: loads return in issue order, so the
+  // wait for the next stage's x never waits for those weights.
+  struct WRegs {
+    uint4 w[kWP];
+    u32x2_t sb;
+  };
+  uint4 xreg[kXP];
+  auto fetch_x = [&](int st) {
 #pragma unroll
     for (int i = 0; i < kXP; ++i) {
       const int k = i / kXPK, m = (tid >> 5) + 8 * (i % kXPK);
@@ -984,6 +994,8 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
       const uint32_t off = (uint32_t)(m < M ? m : M - 1) * ldx2 + 16u * (xp & 7) + 128u * (uint32_t)g;
       xreg[i] = load_b128(xrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
     }
+  };
+  auto fetch_w = [&](WRegs& R, int st) {
 #pragma unroll
     for (int i = 0; i < kWP; ++i) {
       const int slot = (tid >> 3) + 32 * i, k = slot / kRows;
@@ -991,7 +1003,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
       const int g = klo[k] + (wp >> 1) + 4 * st;
       const uint32_t off = (uint32_t)n * (uint32_t)W * 4u + 16u * (wp & 1) + 32u * (uint32_t)g;
       // slot % kRows < 32 exactly for even i: the weight is uniform per instruction
-      wreg[i] = load_b128_nt(PAIR && (i & 1) ? wrsrc_u : wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
+      R.w[i] = load_b128_nt(PAIR && (i & 1) ? wrsrc_u : wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
     }
     const int g = klo[sb_k] + 4 * st;
     const uint32_t off = (sb_src + 2u * (uint32_t)g) | ((uint32_t)(g >= khi[sb_k]) << 31);
@@ -1000,20 +1012,20 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
           sb_is_b ? brsrc : srsrc, sb_up ? kPastBuffer : off, 0, 0));
       const u32x2_t su = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
           sb_is_b ? brsrc_u : srsrc_u, sb_up ? off : kPastBuffer, 0, 0));
-      sbreg = u32x2_t{sg[0] | su[0], sg[1] | su[1]};
+      R.sb = u32x2_t{sg[0] | su[0], sg[1] | su[1]};
     } else {
-      sbreg = __builtin_bit_cast(u32x2_t,
+      R.sb = __builtin_bit_cast(u32x2_t,
                                  __builtin_amdgcn_raw_buffer_load_b64(sb_is_b ? brsrc : srsrc, off, 0, 0));
     }
   };
-  auto store = [&]() {
+  auto store = [&](const WRegs& R) {
 #pragma unroll
     for (int i = 0; i < kXP; ++i)
       *reinterpret_cast<uint4*>(lds + xdst0 + (i / kXPK) * 32 * kXRow + 8 * (i % kXPK) * kXRow) =
           pair_order(xreg[i]);
 #pragma unroll
-    for (int i = 0; i < kWP; ++i) *reinterpret_cast<uint4*>(lds + wdst0 + 32 * i * kWRow) = wreg[i];
-    *reinterpret_cast<u32x2_t*>(lds + sb_dst) = sbreg;
+    for (int i = 0; i < kWP; ++i) *reinterpret_cast<uint4*>(lds + wdst0 + 32 * i * kWRow) = R.w[i];
+    *reinterpret_cast<u32x2_t*>(lds + sb_dst) = R.sb;
   };
 
   f32x16_t acc = {}, accb = {};
@@ -1034,7 +1046,12 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
 #pragma unroll
     for (int r = 0; r < kNormSlots / kThreads; ++r) nq[r] = load_b128(qrs, norm_pair_offset(ni, M, tid + kThreads * r));
   }
-  fetch(0);
+  constexpr int DEPTH = IMQ_STAGED_DEPTH;
+  static_assert(DEPTH == 1 || DEPTH == 2, "one or two stages in flight");
+  WRegs ra, rb;
+  fetch_w(ra, 0);
+  fetch_x(0);
+  if (DEPTH > 1) fetch_w(rb, 1);
   if (norm_in) {
 #pragma unroll
     for (int r = 0; r < kNormSlots / kThreads; ++r) {
@@ -1042,12 +1059,16 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
       nsum[PAIR ? p >> 5 : 0][p & 31] = norm_pair_sum(ni, p, nq[r]);
     }
   }
-  for (int st = 0; st < nst; ++st) {
+  // one stage: its registers to LDS, the next x and the weights DEPTH ahead into the same
+  // registers (past the last stage every offset is past its buffer: no traffic), then the
+  // stage's MFMAs
+  auto stage = [&](WRegs& R, int st) {
     __builtin_amdgcn_sched_barrier(0);
-    store();
+    store(R);
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    fetch(st + 1);  // past the last stage every offset is past its buffer: no traffic
+    fetch_x(st + 1);
+    fetch_w(R, st + DEPTH);
     __builtin_amdgcn_sched_barrier(0);
     const u32x2_t s2 = *reinterpret_cast<const u32x2_t*>(lds + sbrd);
     const u32x2_t b2 = *reinterpret_cast<const u32x2_t*>(lds + sbrd + 8);
@@ -1083,6 +1104,10 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
     }
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();  // every wavefront is done with this stage
+  };
+  for (int st = 0; st < nst; st += DEPTH) {
+    stage(ra, st);
+    if (DEPTH > 1 && st + 1 < nst) stage(rb, st + 1);
   }
   acc += accb;
 
