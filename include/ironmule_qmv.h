@@ -179,19 +179,28 @@ IMQ_API int32_t imq_qmv_norm_planes(const imq_problem* problems, int32_t count, 
                                     int32_t group_size, int32_t bits, const imq_norm_in* in,
                                     float* planes, int64_t pstride, int32_t* splits, void* stream);
 
+/* Bytes of workspace imq_qmv_gate_up_silu_norm uses at these shapes (0: none): when the
+ * launch's 32-row tiles make more than one round over the CUs, the tiles of the last,
+ * partial round are cut into K-parts that occupy the CUs the whole tiles leave free. */
+IMQ_API size_t imq_qmv_gate_up_silu_norm_workspace(int32_t M, int32_t N, int32_t K);
+
 /*
  * imq_qmv_gate_up_silu on x' rows with the input RMSNorm folded in (`in` non-NULL):
  *   act[m][n] = bf16(silu(g) * u),  g = bf16(inv_m * sum_k x'[m][k] W_gate[n][k]),
  *                                   u = bf16(inv_m * sum_k x'[m][k] W_up[n][k]).
- * Same shapes and limits as imq_qmv_gate_up_silu.  Replaces the post-attention RMSNorm,
- * the fused gate/up launch and the SwiGLU, ironmule/dense_plan.py:359-360 and
- * ironmule/fast.py:186-215.
+ * Same shapes and limits as imq_qmv_gate_up_silu.  With a workspace of
+ * imq_qmv_gate_up_silu_norm_workspace bytes (zero-filled before its first use and left
+ * ready by every call; calls sharing one must not overlap) the last round's tiles are cut
+ * into K-parts whose sums are added in part order; with none (NULL, 0 bytes) every tile is
+ * whole.  Replaces the post-attention RMSNorm, the fused gate/up launch and the SwiGLU,
+ * ironmule/dense_plan.py:359-360 and ironmule/fast.py:186-215.
  */
 IMQ_API int32_t imq_qmv_gate_up_silu_norm(const uint32_t* w_gate, const uint16_t* s_gate,
                 const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
                 const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
                 int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
-                int32_t bits, const imq_norm_in* in, void* stream);
+                int32_t bits, const imq_norm_in* in, float* workspace, size_t workspace_bytes,
+                void* stream);
 
 /*
  * The same product for `count` separate activation vectors xs[i] (each (1, K)) and

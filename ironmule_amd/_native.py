@@ -126,8 +126,10 @@ _SIGNATURES = {
     "imq_qmv_norm_splits": ([ctypes.POINTER(Problem), _I32, _I32], _I32),
     "imq_qmv_norm_planes": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, ctypes.POINTER(NormIn),
                              _P, _I64, ctypes.POINTER(_I32), _P], _I32),
+    "imq_qmv_gate_up_silu_norm_workspace": ([_I32, _I32, _I32], ctypes.c_size_t),
     "imq_qmv_gate_up_silu_norm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32,
-                                   _I32, _I32, ctypes.POINTER(NormIn), _P], _I32),
+                                   _I32, _I32, ctypes.POINTER(NormIn), _P, ctypes.c_size_t, _P],
+                                  _I32),
     "imq_rmsnorm_prescale": ([_P, _P, _P, _P, _P, _I32, _I32, _I32, _P], _I32),
     "imq_dequant": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P], _I32),
     "imq_gather_qmv": ([_P, _P, _P, _I32, _P, _I64, _I32, _P, _I32, _P, _I64, _I32, _I32, _I32,
@@ -756,9 +758,10 @@ def qmv_norm(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]], x: 
 
 
 def gate_up_silu_norm(gate, up, x: torch.Tensor, out: torch.Tensor, norm_in: NormStats,
-                      eps: float, stream=None) -> torch.Tensor:
+                      eps: float, stream=None, split_tail: bool = True) -> torch.Tensor:
     """gate_up_silu on x' = bf16(h * w) with the RMSNorm folded in: the gate and up rows are
-    scaled by 1/rms(h) from `norm_in` before the SwiGLU."""
+    scaled by 1/rms(h) from `norm_in` before the SwiGLU.  With `split_tail` the tiles of the
+    launch's last, partial round over the CUs run as K-parts (this stream's workspace)."""
     n, k = check_weights(*gate)
     if check_weights(*up) != (n, k):
         raise ValueError("gate and up must have the same shape")
@@ -768,9 +771,13 @@ def gate_up_silu_norm(gate, up, x: torch.Tensor, out: torch.Tensor, norm_in: Nor
         raise ValueError(f"x must be (M, {k}) and out (M, {n})")
     m = int(x.shape[0])
     nin = norm_in.norm_in(eps)
+    nbytes = int(lib().imq_qmv_gate_up_silu_norm_workspace(m, n, k)) if split_tail else 0
+    ws = _workspace(nbytes, gate[0].device, stream) if nbytes else None
     _check(lib().imq_qmv_gate_up_silu_norm(_ptr(gate[0]), _ptr(gate[1]), _ptr(gate[2]), _ptr(up[0]),
                                            _ptr(up[1]), _ptr(up[2]), _ptr(x), k, _ptr(out), n, m, n,
-                                           k, GROUP_SIZE, BITS, ctypes.byref(nin), _stream(stream)))
+                                           k, GROUP_SIZE, BITS, ctypes.byref(nin),
+                                           _ptr(ws) if ws is not None else None,
+                                           ws.numel() * 4 if ws is not None else 0, _stream(stream)))
     return out
 
 

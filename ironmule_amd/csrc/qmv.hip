@@ -888,6 +888,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
 #define IMQ_STAGED_DEPTH 2
 #endif
 namespace staged {
+constexpr int kMaxPairParts = 4;  // K-parts of a gate/up tile of the last round
 constexpr int kWN = 2, kWK = 2;                   // wavefronts along N and along K
 constexpr int kRows = 32 * kWN;                   // weight rows per workgroup
 constexpr int kWRow = 144, kXRow = 528;           // LDS row strides (bytes)
@@ -919,13 +920,26 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   __shared__ float nsum[PAIR ? kNormMaxTiles / 4 : 1][32];  // input norm: pair sums [j][row]
   __shared__ float ninv[32];                                // input norm: 1/rms per row
   __shared__ int last;
-  const int pi = blockIdx.y / splits, split = blockIdx.y - pi * splits;
+  // PAIR: the first `tiles_max` workgroups take whole tiles; with `splits` > 1 every later
+  // tile (the launch's last, partial round over the CUs) is cut into `splits` K-parts, one
+  // workgroup each, whose last part to finish adds them (the launch then ends after about
+  // one tile per CU instead of two on some); `partial` and `counters` hold the parts
+  int tile_p = blockIdx.x, part = 0, parts = 1;
+  if (PAIR && splits > 1 && (int)blockIdx.x >= tiles_max) {
+    const int q = blockIdx.x - tiles_max;
+    tile_p = tiles_max + q / splits;
+    part = q - (q / splits) * splits;
+    parts = splits;
+  }
+  const int pi = PAIR ? 0 : blockIdx.y / splits;
+  const int split = PAIR ? part : blockIdx.y - pi * splits;
+  const int nsplit = PAIR ? parts : splits;
   const Problem& P = a.p[pi];
   const int K = P.K, N = P.N, M = a.M;
   // a tile's row slot r (0..63) is weight row row0 + r, or (PAIR) row rp0 + r % 32 of the
   // gate (r < 32) or up (r >= 32) weight
   const int row0 = PAIR ? 0 : blockIdx.x * kRows;
-  const int rp0 = blockIdx.x * 32;
+  const int rp0 = tile_p * 32;
   if ((PAIR ? rp0 : row0) >= N) return;  // past this problem's tiles
   const int G = K >> 6, W = K >> 3;
   const int tid = threadIdx.x;
@@ -935,8 +949,8 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
   const uint32_t one = in_vgpr(kNibOne);
 
   // the split's groups (whole stages), then the two K-ranges of whole stages
-  const int gs0 = (G * split) / splits / 4 * 4;
-  const int gs1 = split + 1 == splits ? G : (G * (split + 1)) / splits / 4 * 4;
+  const int gs0 = (G * split) / nsplit / 4 * 4;
+  const int gs1 = split + 1 == nsplit ? G : (G * (split + 1)) / nsplit / 4 * 4;
   const int span = ((gs1 - gs0 + kWK - 1) / kWK + 3) / 4 * 4;
   const int nst = span / 4;
   int klo[kWK], khi[kWK];
@@ -1126,6 +1140,54 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
 #pragma unroll
       for (int e = 0; e < 16; ++e) tiles2[(wn * 16 + e) * 64 + lane] = acc[e];
     __syncthreads();
+    float gsum[4], usum[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int idx = tid + kThreads * q;
+      gsum[q] = tiles2[idx];
+      usum[q] = tiles2[1024 + idx];
+    }
+    if (parts > 1) {
+      // a K-part: park its gate and up sums ([16][64] floats each), count the tile's parts;
+      // the last adds them in part order (sc1 accesses, coherent across the XCDs' L2s)
+      const int tt = tile_p - tiles_max;
+      const __amdgpu_buffer_rsrc_t prs =
+          buffer_rsrc(partial + (int64_t)tt * parts * 2048, (uint32_t)(parts * 2048 * 4));
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int idx = tid + kThreads * q;
+        store_b32_sc1(prs, (uint32_t)((part * 2048 + idx) * 4), __float_as_uint(tiles2[idx]));
+      }
+      wait_vmem();
+      __syncthreads();
+      uint32_t* cnt = counters + tt;
+      if (tid == 0)
+        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(parts - 1);
+      __syncthreads();
+      if (!last) return;
+      float gp[kMaxPairParts][4], up[kMaxPairParts][4];  // every part's load in flight
+#pragma unroll
+      for (int sp = 0; sp < kMaxPairParts; ++sp)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int idx = tid + kThreads * q;
+          const uint32_t o = (uint32_t)((sp * 2048 + idx) * 4);
+          gp[sp][q] = __uint_as_float(load_b32_sc1(prs, sp < parts ? o : kPastBuffer));
+          up[sp][q] = __uint_as_float(load_b32_sc1(prs, sp < parts ? o + 4096u : kPastBuffer));
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        gsum[q] = usum[q] = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < kMaxPairParts; ++sp)
+          if (sp < parts) {
+            gsum[q] += gp[sp][q];
+            usum[q] += up[sp][q];
+          }
+      }
+      if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
+    }
     uint16_t* act = static_cast<uint16_t*>(P.y);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -1133,7 +1195,7 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
       const int m = 8 * (e >> 2) + 4 * (l >> 5) + (e & 3), n = rp0 + (l & 31);
       if (m < M && n < N) {
         const float sc = norm_in ? ninv[m] : 1.0f;
-        const float gs = tiles2[e * 64 + l], us = tiles2[(16 + e) * 64 + l];
+        const float gs = gsum[q], us = usum[q];
         const float g0 = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? gs * sc : gs));
         const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? us * sc : us));
         act[(size_t)m * P.ldy + n] = f32_to_bf16_bits(g0 / (1.0f + expf(-g0)) * u0);
@@ -2952,11 +3014,31 @@ int32_t build_norm(LaunchArgs& a, DmaPlan* pl, NormIn* nin, ResidualOut* res,
   return IMQ_OK;
 }
 
+// The gate/up launch's plan: whole tiles of 32 gate and 32 up rows, and with a workspace the
+// tiles past the last whole round over the CUs cut into K-parts (0 parts: none).
+struct PairPlan {
+  int whole = 0, tail = 0, parts = 1;
+  size_t bytes = 0;
+};
+PairPlan plan_pair(int N, int K, int cu_count) {
+  PairPlan pl;
+  const int T = (N + 31) / 32;
+  pl.whole = T;
+  const int r = T > cu_count ? T % cu_count : 0;
+  if (r > 0 && K / 64 >= 4 * staged::kMaxPairParts) {
+    pl.whole = T - r;
+    pl.tail = r;
+    pl.parts = staged::kMaxPairParts;
+    pl.bytes = kCounterBytes + (size_t)r * pl.parts * 2048 * sizeof(float);
+  }
+  return pl;
+}
+
 int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint16_t* b_gate,
                      const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
                      const uint16_t* x, int64_t ldx, uint16_t* act, int64_t ld_act, int32_t M,
                      int32_t N, int32_t K, int32_t group_size, int32_t bits, const imq_norm_in* in,
-                     void* stream) {
+                     void* stream, float* workspace = nullptr, size_t workspace_bytes = 0) {
   int32_t code = check_format(N, K, group_size, bits);
   if (code != IMQ_OK) return code;
   if ((code = check_weights(w_gate, s_gate, b_gate)) != IMQ_OK) return code;
@@ -2975,8 +3057,14 @@ int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint1
   a.p[1] = Problem{w_up, s_up, b_up, x, nullptr, ldx, ld_act, N, K, 0, 0, 0, 0};
   a.count = 2;
   a.M = M;
-  hipLaunchKernelGGL((qmv_mma_staged_kernel<false, true>), dim3((N + 31) / 32, 1), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), a, 1, nullptr, (int64_t)0, nullptr, 0, to_norm_in(in));
+  PairPlan pl = plan_pair(N, K, dev->cu_count);
+  if (pl.parts > 1 && (!workspace || workspace_bytes < pl.bytes)) pl = PairPlan{(N + 31) / 32, 0, 1, 0};
+  if (pl.parts > 1 && !aligned(workspace, 16)) return fail(IMQ_EINVAL, "workspace must be 16-byte aligned");
+  char* ws = reinterpret_cast<char*>(workspace);
+  hipLaunchKernelGGL((qmv_mma_staged_kernel<false, true>), dim3(pl.whole + pl.tail * pl.parts, 1),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), a, pl.parts,
+                     pl.parts > 1 ? reinterpret_cast<float*>(ws + kCounterBytes) : nullptr, (int64_t)0,
+                     pl.parts > 1 ? reinterpret_cast<uint32_t*>(ws) : nullptr, pl.whole, to_norm_in(in));
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("gate/up launch failed: ") + hipGetErrorString(e));
   return ok();
@@ -3084,14 +3172,23 @@ int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate,
                       bits, nullptr, stream);
 }
 
+size_t imq_qmv_gate_up_silu_norm_workspace(int32_t M, int32_t N, int32_t K) {
+  if (M < 5 || M > IMQ_MAX_ROWS || N < 1 || K < 256 || K % 256) return 0;
+  int32_t code;
+  const DeviceInfo* dev = current_device(&code);
+  if (!dev) return 0;
+  return plan_pair(N, K, dev->cu_count).bytes;
+}
+
 int32_t imq_qmv_gate_up_silu_norm(const uint32_t* w_gate, const uint16_t* s_gate,
                                   const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
                                   const uint16_t* b_up, const uint16_t* x, int64_t ldx, uint16_t* act,
                                   int64_t ld_act, int32_t M, int32_t N, int32_t K, int32_t group_size,
-                                  int32_t bits, const imq_norm_in* in, void* stream) {
+                                  int32_t bits, const imq_norm_in* in, float* workspace,
+                                  size_t workspace_bytes, void* stream) {
   if (!in) return fail(IMQ_EINVAL, "in must be non-null (imq_qmv_gate_up_silu takes no norm)");
   return gate_up_silu(w_gate, s_gate, b_gate, w_up, s_up, b_up, x, ldx, act, ld_act, M, N, K, group_size,
-                      bits, in, stream);
+                      bits, in, stream, workspace, workspace_bytes);
 }
 
 }  // extern "C"

@@ -126,7 +126,7 @@ def test_input_norm_matches_oracle(native, oracle, shapes, m, tiles):
         assert v.ok, v.detail
 
 
-@pytest.mark.parametrize("n,k,m", [(9728, 2560, 32), (9728, 2560, 5), (1000, 512, 9)])
+@pytest.mark.parametrize("n,k,m", [(9728, 2560, 32), (9728, 2560, 5), (1000, 512, 9), (16416, 1024, 8)])
 def test_gate_up_norm_halves(native, oracle, n, k, m):
     pg = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 2200 + m)
     pu = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 2201 + m)
@@ -137,16 +137,27 @@ def test_gate_up_norm_halves(native, oracle, n, k, m):
     st = _half_stats(native, m, 2560, 40)
     out = native.gate_up_silu_norm(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"),
                                    st, 0.0)
+    whole = native.gate_up_silu_norm(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"),
+                                     st, 0.0, split_tail=False)
+    again = native.gate_up_silu_norm(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"),
+                                     st, 0.0)
     plain = native.gate_up_silu(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"))
     torch.cuda.synchronize()
+    assert torch.equal(out, again)  # the K-parts add in a fixed order
+    # the tiles of whole rounds over the CUs are whole tiles either way: the same bits
+    cus = native.device_check()[2]
+    tiles = -(-n // 32)
+    cut = 32 * (tiles - tiles % cus) if tiles > cus else n
+    assert torch.equal(out[:, :cut], whole[:, :cut])
     if (n, k) == (9728, 2560):  # grouped launch on the staged kernel: the same row sums
         g, u = native.qmv_grouped([gate, up], [x, x])
         ref = native.silu_mul((g.float() * 0.5).to(torch.bfloat16), (u.float() * 0.5).to(torch.bfloat16),
                               torch.empty_like(g))
         torch.cuda.synchronize()
-        assert torch.equal(out, ref)
-    # against the oracle: each projection within one bf16 ulp (plus the summation
-    # allowance) of its exact value, then SiLU (slope <= 1.1) and one more rounding
+        assert torch.equal(whole, ref)
+    # against the oracle (every column, the K-parts of the last round's tiles included):
+    # each projection within one bf16 ulp (plus the summation allowance) of its exact value,
+    # then SiLU (slope <= 1.1) and one more rounding
     g64, mg = oracle.qmv_f64(pg.w, pg.s, pg.b, pg.x)
     u64, mu = oracle.qmv_f64(pu.w, pu.s, pu.b, pu.x)
     g64, u64, mg, mu = g64 / 2, u64 / 2, mg / 2, mu / 2
@@ -154,9 +165,10 @@ def test_gate_up_norm_halves(native, oracle, n, k, m):
     eu = oracle.bf16_ulp(u64) + 2.0 ** -20 * mu
     sg = g64 / (1.0 + np.exp(-g64))
     ref = sg * u64
-    got = oracle.bf16_to_f32(bf16_bits(out)).astype(np.float64)
     bound = oracle.bf16_ulp(ref) + 1.1 * eg * (np.abs(u64) + eu) + np.abs(sg) * eu
-    assert (np.abs(got - ref) <= bound).all(), float(np.max(np.abs(got - ref) / bound))
+    for t in (out, whole):
+        got = oracle.bf16_to_f32(bf16_bits(t)).astype(np.float64)
+        assert (np.abs(got - ref) <= bound).all(), float(np.max(np.abs(got - ref) / bound))
     assert not torch.equal(out, plain)  # the scaling took effect
 
 
