@@ -878,8 +878,9 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_kernel(LaunchArgs a, int spl
 //   * x: 2 x 32 rows x 512 B, stored in pair order, 528-byte LDS rows;
 //   * scales and biases: 2 x 64 rows x 8 B each.
 // (The row paddings make the MFMA-layout reads conflict-free.)  A stage's loads are issued
-// into registers before the previous stage is computed and written to LDS after it, one
-// barrier on each side.  Rows m >= M read row M-1 and are never stored; groups past a
+// into registers ahead of it (x one stage ahead, weights, scales and biases two) and
+// written to LDS after the previous stage is computed, one barrier on each side.  Rows
+// m >= M read row M-1 and are never stored; groups past a
 // K-range read zero (buffer offsets past the end).  The bias term is one fp32 MFMA
 // (v_mfma_f32_32x32x2_f32) per pair of groups: A = the two groups' row sums of x, B = the
 // two groups' c = b - 16 s per weight row; the weights enter the MFMAs as 1 + q/16.
