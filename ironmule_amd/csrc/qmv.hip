@@ -1904,6 +1904,267 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
 }
 
+// ------------------------------------------- MFMA kernel over 256-row bands (M >= 16)
+//
+// The direct-to-LDS kernel's 64-row workgroup reads, at 32 activation rows, twice as many
+// activation bytes as weight bytes (x: 64 bytes per K column, the 64 rows' weights 36).
+// Where that kernel would split K anyway, or declines (more 64-row tiles than CUs), the
+// activation bytes are cut by a wider tile.  Here a workgroup of eight wavefronts
+// owns a band of 256 weight rows (wavefront w: rows 32 w .. 32 w + 31, one 32 x 32 MFMA
+// tile) over a K-range of at most 16 groups, so that the range's x is read once for 256
+// rows (x: 64 bytes per K column against 144 of weights), and the bands' K-ranges are
+// split toward one workgroup per CU.
+//   * x: the range's activations go memory -> LDS by the buffer loads' LDS path, 16 bytes
+//     a lane, in MFMA A-operand order (slot [group][k-step][lane] holds x[m][64 g + 32 kb
+//     + 8 t ..+8] for lane (m, kb)); rows m >= M read row M - 1 (never stored).  After one
+//     barrier each thread (group, row) puts its eight slots in pair order and writes the
+//     row's group sum, so the per-group activation work is done once per workgroup instead
+//     of once per wavefront.
+//   * Weights: per wavefront, chunks of four groups of its 32 rows (whole 128-byte lines,
+//     the direct-to-LDS kernel's swizzled slots) in a two-buffer ring: chunks 0 and 1 at
+//     the start, chunk q + 2 once chunk q is read.
+//   * Scales and biases of the band's rows over the range: LDS, 4 bytes a lane, with x.
+// Per group (the direct-to-LDS kernel's arithmetic): P = sum_k v x from four bf16 MFMAs (v =
+// 1 + q/16, exact), acc += 16 s P; per pair of groups one v_mfma_f32_32x32x2_f32 adds (b -
+// 16 s) sum x.  A wavefront's tile needs no other wavefront's sums.  Without splits it
+// writes its rows of y; with splits an fp32 partial, and the last split of the band to
+// finish (a counter per band in the caller's workspace) adds the partials in split order
+// (the same bits whatever order the splits finish in; partials and counters through sc1
+// accesses).  Requires K % 256 == 0, ranges of four-group multiples and x rows 16-byte
+// aligned.  Measured at M = 32 on MI355X (against the kernel the plan took before): 19456 x
+// 2560 18.7 us (20.2, staged), 8192 x 4096 20.3 (21.6, direct-to-LDS in three ranges),
+// 50000 x 1024 14.2 (21.8); at K = 3840 x 15360 20.5 against the direct-to-LDS kernel's
+// whole-K tiles' 16.5 (the last split's serial add of three 32 KB partials costs some
+// 4.5 us), so whole-K direct-to-LDS plans keep precedence.  Weights loaded straight into
+// registers (16 bytes a lane, the whole range in flight) measured 20-40% slower than the
+// whole-line LDS loads.
+namespace bd {
+constexpr int kWaves = 8;
+constexpr int kRows = 32 * kWaves;       // weight rows per workgroup
+constexpr int kMaxGroups = 16;           // groups of a K-range
+constexpr int kChunkBytes = 32 * 128;    // four groups of a wavefront's 32 rows
+constexpr int kMaxSplits = 16;
+}  // namespace bd
+
+template <bool SPLIT>
+__global__ __launch_bounds__(64 * bd::kWaves) void qmv_band_kernel(LaunchArgs a, DmaArgs d) {
+  __shared__ __attribute__((aligned(16))) uint4 xl[bd::kMaxGroups * 4 * 64];
+  __shared__ __attribute__((aligned(16))) char wb[bd::kWaves * 2 * bd::kChunkBytes];
+  __shared__ __attribute__((aligned(16))) uint32_t sbl[bd::kRows * bd::kMaxGroups];
+  __shared__ float xsum[bd::kMaxGroups][32];
+  __shared__ int last;
+  const int pi = blockIdx.y;
+  const Problem& P = a.p[pi];
+  const int N = P.N, K = P.K, M = a.M, G = K >> 6;
+  const int splits = SPLIT ? d.splits : 1;
+  const int band = SPLIT ? (int)blockIdx.x / splits : (int)blockIdx.x;
+  const int split = SPLIT ? (int)blockIdx.x - band * splits : 0;
+  const int row0 = band * bd::kRows;
+  if (row0 >= N) return;  // past this problem's bands
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, kb = lane >> 5;
+  const int gs0 = SPLIT ? split * d.range : 0;
+  const int gs1 = SPLIT ? min(G, gs0 + d.range) : G;
+  const int Gs = __builtin_amdgcn_readfirstlane(gs1 - gs0);  // a multiple of four, <= 16
+  const int nq = Gs >> 2;                                     // chunks of four groups
+  const int hp = Gs >> 1;                                     // scale dwords per row
+  const int wrow0 = row0 + 32 * wave;
+
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(P.w, (uint32_t)N * (uint32_t)(K >> 1));
+  const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.s, sb_bytes);
+  const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(P.b, sb_bytes);
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)(((int64_t)(M - 1) * P.ldx + K) * 2));
+
+  __builtin_amdgcn_sched_barrier(0);
+  // 1. x of the range: instruction i = 4 gl + t, lane l -> slot i * 64 + l
+  {
+    const uint32_t xro = (uint32_t)min(j, M - 1) * (uint32_t)P.ldx * 2u + 64u * (uint32_t)kb;
+    for (int i = wave; i < 4 * Gs; i += bd::kWaves) {
+      const uint32_t off = xro + 128u * (uint32_t)(gs0 + (i >> 2)) + 16u * (uint32_t)(i & 3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrs, (__attribute__((address_space(3))) void*)(xl + i * 64), 16, off, 0, 0, 0);
+    }
+  }
+  // 2. scales, then biases: 4 hp instructions of 64 dwords per array; dword dd of an array
+  //    (row dd / hp, pair dd % hp of the range's groups) at LDS dword array * 256 hp + dd
+  {
+    const int per = 4 * hp;
+    for (int i = wave; i < 2 * per; i += bd::kWaves) {
+      const int arr = i >= per ? 1 : 0;
+      const int ii = i - arr * per;
+      const int dd = ii * 64 + lane;
+      const int r = dd / hp, pr = dd - r * hp;
+      const int row = row0 + r < N ? row0 + r : N - 1;
+      const uint32_t off = (uint32_t)row * (uint32_t)G * 2u + 2u * (uint32_t)gs0 + 4u * (uint32_t)pr;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          arr ? brs : srs, (__attribute__((address_space(3))) void*)(sbl + arr * bd::kRows * hp + ii * 64),
+          4, off, 0, 0, 0);
+    }
+  }
+  // 3. weights: chunk q of this wavefront's rows into its buffer q & 1, 4 instructions of
+  //    8 rows x 128 bytes
+  char* const wbuf = wb + wave * 2 * bd::kChunkBytes;
+  auto load_w = [&](int q) {
+#pragma unroll
+    for (int i8 = 0; i8 < 4; ++i8) {
+      const int r = 8 * i8 + (lane >> 3);
+      const int c = (lane & 7) ^ dm::swz(r);
+      int gg = gs0 + 4 * q + (c >> 1);
+      gg = gg < gs1 ? gg : gs1 - 1;
+      const int row = wrow0 + r < N ? wrow0 + r : N - 1;
+      const uint32_t off = (uint32_t)row * (uint32_t)(K >> 1) + 32u * (uint32_t)gg + 16u * (uint32_t)(c & 1);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wrs, (__attribute__((address_space(3))) void*)(wbuf + (q & 1) * bd::kChunkBytes + i8 * 1024), 16, off,
+          0, 0, kNt);
+    }
+  };
+  __builtin_amdgcn_sched_barrier(0);
+  load_w(0);
+  if (nq > 1) load_w(1);
+  __builtin_amdgcn_sched_barrier(0);
+  // this wavefront's x, scales and biases have landed (its weight loads, issued after
+  // them, may not have); past the barrier every wavefront's have
+  if (nq > 1)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. x in pair order and the rows' group sums: thread (group g, row m)
+  const uint32_t one = in_vgpr(kNibOne);
+  {
+    const int g = tid >> 5, m = tid & 31;
+    if (g < Gs) {
+      uint4 v[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[4 * h + t] = xl[(4 * g + t) * 64 + 32 * h + m];
+      float half[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint4 u = v[4 * h + t];
+          half[h] = dot2(u.x, one, half[h]);
+          half[h] = dot2(u.y, one, half[h]);
+          half[h] = dot2(u.z, one, half[h]);
+          half[h] = dot2(u.w, one, half[h]);
+          xl[(4 * g + t) * 64 + 32 * h + m] = pair_order(u);
+        }
+      xsum[g][m] = half[0] + half[1];
+    }
+  }
+  __syncthreads();
+
+  // 5. the range's groups, four per chunk
+  const f32x16_t zero = {};
+  f32x16_t acc = zero, accb = zero;
+  const int rl = 32 * wave + j;  // this lane's weight row within the band
+#pragma unroll
+  for (int q = 0; q < bd::kMaxGroups / 4; ++q) {
+    if (q >= nq) break;
+    if (q + 1 < nq)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const char* buf = wbuf + (q & 1) * bd::kChunkBytes;
+    uint32_t sp = 0u, bp = 0u;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int gl = 4 * q + gq;
+      bf16x8_t xa[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xa[t] = as_bf16x8(xl[(4 * gl + t) * 64 + lane]);
+      if ((gq & 1) == 0) {
+        sp = sbl[rl * hp + (gl >> 1)];
+        bp = sbl[bd::kRows * hp + rl * hp + (gl >> 1)];
+      }
+      const int c = 2 * gq + kb;
+      const uint4 wv = *reinterpret_cast<const uint4*>(buf + (j >> 3) * 1024 + 16 * (8 * (j & 7) + (c ^ dm::swz(j))));
+      f32x16_t p = zero;
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[0], unpack16(wv.x, one), p, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[1], unpack16(wv.y, one), p, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[2], unpack16(wv.z, one), p, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[3], unpack16(wv.w, one), p, 0, 0, 0);
+      const float s16 = 16.0f * __uint_as_float((gq & 1) ? (sp & 0xffff0000u) : (sp << 16));
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = fmaf(s16, p[e], acc[e]);
+      if (gq & 1) {  // the pair's offset term: lanes kb = 0 / 1 take its first / second group
+        const uint32_t sw = kb ? (sp & 0xffff0000u) : (sp << 16);
+        const uint32_t bw = kb ? (bp & 0xffff0000u) : (bp << 16);
+        const float cg = fmaf(-16.0f, __uint_as_float(sw), __uint_as_float(bw));
+        accb = __builtin_amdgcn_mfma_f32_32x32x2f32(xsum[gl - 1 + kb][j], cg, accb, 0, 0, 0);
+      }
+    }
+    if (q + 2 < nq) {
+      // every read of this chunk's buffer has returned before the buffer is refilled
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(q + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  acc += accb;
+
+  // 6. lane (n = j, kb) holds y[m][wrow0 + j] for m = 8 (e / 4) + 4 kb + e % 4
+  const int n = wrow0 + j;
+  if (!SPLIT) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = 8 * (e >> 2) + 4 * kb + (e & 3);
+      if (m < M && n < N) store_y(a, P, m, n, acc[e]);
+    }
+    return;
+  }
+  const __amdgpu_buffer_rsrc_t prs =
+      buffer_rsrc(d.partial + pi * d.pstride, (uint32_t)((int64_t)splits * M * N * 4));
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int m = 8 * (e >> 2) + 4 * kb + (e & 3);
+    if (m < M && n < N) store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(acc[e]));
+  }
+  wait_vmem();
+  __syncthreads();
+  uint32_t* cnt = d.counters + (int64_t)pi * d.tiles_max + band;
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(splits - 1);
+  __syncthreads();
+  if (!last) return;
+  // four partials of each output in flight at a time, added in split order
+  const uint32_t step = (uint32_t)(M * N * 4);
+  float tot[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) tot[e] = 0.0f;
+  for (int q0 = 0; q0 < splits; q0 += 4) {
+    float v[16][4];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = 8 * (e >> 2) + 4 * kb + (e & 3);
+      const bool in = m < M && n < N;
+      const uint32_t o = (uint32_t)((m * N + n) * 4) + (uint32_t)q0 * step;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        v[e][s] = __uint_as_float(load_b32_sc1(prs, in && q0 + s < splits ? o + s * step : kPastBuffer));
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (q0 + s < splits) tot[e] += v[e][s];
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int m = 8 * (e >> 2) + 4 * kb + (e & 3);
+    if (m < M && n < N) store_y(a, P, m, n, tot[e]);
+  }
+  if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
+}
+
 // ------------------------------------------------------------------ dequantise
 //
 // One thread per packed word: eight outputs.  fp32 output is fl32(s*q + b), which is
@@ -2557,6 +2818,79 @@ bool take_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
   return a.M >= IMQ_DMA_MIN_ROWS || pl->splits == 1;
 }
 
+// The 256-row band kernel's plan: K-ranges of at most 16 groups (four-group multiples)
+// toward one workgroup per CU, and at least half a workgroup per CU.  Single-weight
+// launches only: grouped launches keep the staged and direct-to-LDS plans, whose bits the
+// fused gate/up entry (imq_qmv_gate_up_silu) reproduces.  Not applicable either: a pointer
+// table, M outside [IMQ_BAND_MIN_ROWS, 32], K % 256 != 0, x rows not 16-byte aligned,
+// offsets past 2 GiB, or more band counters than the counter region holds.
+#ifndef IMQ_BAND_MIN_ROWS
+#define IMQ_BAND_MIN_ROWS 16
+#endif
+
+struct BandPlan {
+  int grid_x = 0;      // bands of the largest problem
+  int splits = 1;
+  int range = 0;       // groups per K-range
+  size_t pstride = 0;  // partial floats per problem
+  size_t bytes = 0;    // workspace the plan uses
+};
+
+bool plan_band(const LaunchArgs& a, int cu_count, BandPlan* pl) {
+  if (a.table || a.M < IMQ_BAND_MIN_ROWS || a.M > 32 || a.count != 1) return false;
+  int bands = 0, grid_x = 0, gmax = 0, gmin = 1 << 30, nmax = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const Problem& P = a.p[i];
+    if (P.K % 256 != 0 || P.N < 1) return false;
+    if ((int64_t)P.N * (P.K / 2) >= ((int64_t)1 << 31)) return false;
+    if (P.ldx % 8 != 0 || !imq_rt::aligned(P.x, 16)) return false;
+    if (((int64_t)(a.M - 1) * P.ldx + P.K) * 2 >= ((int64_t)1 << 31)) return false;
+    if (((int64_t)(a.M - 1) * P.ldy + P.N) * 4 >= ((int64_t)1 << 31)) return false;
+    const int t = (P.N + bd::kRows - 1) / bd::kRows;
+    bands += t;
+    grid_x = t > grid_x ? t : grid_x;
+    gmax = P.K / 64 > gmax ? P.K / 64 : gmax;
+    gmin = P.K / 64 < gmin ? P.K / 64 : gmin;
+    nmax = P.N > nmax ? P.N : nmax;
+  }
+  int splits = (gmax + bd::kMaxGroups - 1) / bd::kMaxGroups;
+  const int by_count = (cu_count + bands / 2) / bands;
+  splits = by_count > splits ? by_count : splits;
+  int range = ((gmax + splits - 1) / splits + 3) / 4 * 4;
+  range = range < 8 ? (gmax < 8 ? gmax : 8) : range;
+  splits = (gmax + range - 1) / range;
+  if (2 * bands * splits < cu_count) return false;
+  if (splits > bd::kMaxSplits || (splits > 1 && gmin != gmax)) return false;
+  if ((size_t)a.count * grid_x * 4 > kCounterBytes) return false;
+  if (splits > 1 && ((int64_t)splits * a.M * nmax) * 4 >= ((int64_t)1 << 31)) return false;
+  pl->splits = splits;
+  pl->range = range;
+  pl->grid_x = grid_x;
+  pl->pstride = splits > 1 ? (size_t)splits * a.M * nmax : 0;
+  pl->bytes = splits > 1 ? kCounterBytes + (size_t)a.count * pl->pstride * sizeof(float) : 0;
+  return true;
+}
+
+hipError_t launch_band(const LaunchArgs& a, const BandPlan& pl, void* ws, hipStream_t stream) {
+  DmaArgs d;
+  memset(&d, 0, sizeof(d));
+  if (pl.splits > 1) {
+    char* base = static_cast<char*>(ws);
+    d.counters = reinterpret_cast<uint32_t*>(base);
+    d.partial = reinterpret_cast<float*>(base + kCounterBytes);
+  }
+  d.pstride = (int64_t)pl.pstride;
+  d.splits = pl.splits;
+  d.range = pl.range;
+  d.tiles_max = pl.grid_x;
+  if (pl.splits > 1)
+    hipLaunchKernelGGL((qmv_band_kernel<true>), dim3(pl.grid_x * pl.splits, a.count), dim3(64 * bd::kWaves), 0,
+                       stream, a, d);
+  else
+    hipLaunchKernelGGL((qmv_band_kernel<false>), dim3(pl.grid_x, a.count), dim3(64 * bd::kWaves), 0, stream, a, d);
+  return hipGetLastError();
+}
+
 template <int W, int GMAX>
 hipError_t launch_dma_w(const LaunchArgs& a, const DmaArgs& d, const DmaPlan& pl, hipStream_t stream) {
   if (pl.splits > 1)
@@ -2612,6 +2946,9 @@ size_t wanted_workspace(const LaunchArgs& a, int cu_count) {
   XsPlan xp;
   if (a.M >= IMQ_XS_MIN_ROWS && plan_xs(a, cu_count, &x, &xp)) return 0;
   DmaPlan dp;
+  if (take_dma(a, cu_count, &dp) && dp.splits == 1) return 0;
+  BandPlan bp;
+  if (plan_band(a, cu_count, &bp)) return bp.bytes;
   if (take_dma(a, cu_count, &dp)) return dp.bytes;
   return plan_mma(a, (size_t)1 << 40, cu_count).bytes;
 }
@@ -2651,8 +2988,13 @@ int32_t launch(LaunchArgs& a, const DeviceInfo* dev, hipStream_t stream, void* w
   for (int i = 0; i < a.count; ++i)
     big = big || (int64_t)a.p[i].N * (a.p[i].K / 2) >= ((int64_t)1 << 31);
   DmaPlan dp;
+  BandPlan bp;
   if (M >= IMQ_XS_MIN_ROWS && !big && plan_xs(a, dev->cu_count, &xa, &xp)) {
     e = launch_xs(xa, xp, stream);
+  } else if (take_dma(a, dev->cu_count, &dp) && dp.splits == 1) {
+    e = launch_dma(a, dp, ws, stream);
+  } else if (!big && plan_band(a, dev->cu_count, &bp) && (bp.bytes == 0 || (ws && bp.bytes <= ws_bytes))) {
+    e = launch_band(a, bp, ws, stream);
   } else if (take_dma(a, dev->cu_count, &dp) &&
              (dp.bytes == 0 || (ws && dp.bytes <= ws_bytes))) {
     e = launch_dma(a, dp, ws, stream);

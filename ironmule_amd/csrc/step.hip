@@ -744,6 +744,21 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   }
   }
 
+  if (used == 1) {
+    // the only split with keys: the merge of one partial is c / L with c = fma(a, 1, 0),
+    // L = fma(l, 1, 0) (exp(0) = 1), so it is written here with the same bits and no
+    // partial round trip
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int g = wave + 4 * r;
+      if (g < G) {
+        const float lx = Ls[r] + 0.0f;
+        const uint32_t o = (uint32_t)to_bf((a0[r] + 0.0f) / lx) | ((uint32_t)to_bf((a1[r] + 0.0f) / lx) << 16);
+        store_b32_sc1(buffer_rsrc(out, out_bytes), (uint32_t)((b * Hq + kvh * G + g) * kD + 2 * lane) * 2u, o);
+      }
+    }
+    return true;
+  }
   // this split's partial, then the last split of (b, kvh) merges them in split order
   const uint32_t part_bytes = (uint32_t)((b + 1) * Hq * splits) * kD * 4u;
   const uint32_t ml_bytes = (uint32_t)((b + 1) * Hq * splits) * 8u;
