@@ -526,7 +526,7 @@ def copy_calibration(torch, device) -> None:
 def _short(name: str) -> str:
     for marker in ("stream_chain_kernel", "stream_kernel", "qmv_stage_kernel", "attention_stage_kernel",
                    "step_kernel", "reset_kernel", "qmv_gather_kernel", "qmv_m1c_kernel", "qmv_m1_kernel", "qmv_rows_kernel",
-                   "qmv_mma_staged_kernel", "qmv_mma_kernel", "qmv_dma_kernel", "xprep_kernel",
+                   "qmv_mma_staged_kernel", "qmv_mma_kernel", "qmv_dma_kernel", "qmv_band_kernel", "xprep_kernel",
                    "qmv_xs_kernel", "qmv_mr_kernel", "clear_words_kernel",
                    "dequant_kernel", "embed_kernel", "add_rmsnorm_kernel", "qk_norm_rope_kernel",
                    "attention_partial_kernel", "attention_combine_kernel", "silu_mul_kernel"):
