@@ -1878,26 +1878,28 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   __syncthreads();
   if (!last) return;
   if (res) load_res();  // in flight with the partials
-  // four partials of each output in flight at a time, added in split order
+  // QB partials of each output in flight at a time (one round trip for up to eight ranges
+  // where a thread has at most four outputs), added in split order
+  constexpr int QB = MI <= 4 ? 8 : 4;
   const uint32_t step = (uint32_t)(M * N * 4);
   float tot[MI];
 #pragma unroll
   for (int i = 0; i < MI; ++i) tot[i] = 0.0f;
-  for (int q0 = 0; q0 < splits; q0 += 4) {
-    float v[MI][4];
+  for (int q0 = 0; q0 < splits; q0 += QB) {
+    float v[MI][QB];
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int m = wave + i * W;
       const bool in = m < M && n < N;
       const uint32_t o = (uint32_t)((m * N + n) * 4) + (uint32_t)q0 * step;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < QB; ++q)
         v[i][q] = __uint_as_float(load_b32_sc1(prs, in && q0 + q < splits ? o + q * step : kPastBuffer));
     }
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < QB; ++q)
         if (q0 + q < splits) tot[i] += v[i][q];
   }
   finish(tot, hv, wn);
