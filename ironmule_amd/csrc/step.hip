@@ -667,8 +667,16 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     const int start = base_start + d * kChunk;
     if (start >= last) break;
     const int count = min(kChunk, last - start);
+    // a chunk that holds neither the new key nor rows past `last` is stored as read
+    const bool plain = (newrow < start || newrow >= start + kChunk) && start + kChunk <= last;  // uniform
     __syncthreads();  // the previous chunk's V readers are done
-    {
+    if (plain) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = tid + kThreads * i;
+        L.kv[p >> 4][p & 15] = kr[d][i];
+      }
+    } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = tid + kThreads * i;
@@ -707,7 +715,13 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
       }
     }
     __syncthreads();  // the K readers are done: V takes the region
-    {
+    if (plain) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = tid + kThreads * i;
+        *reinterpret_cast<uint4*>(&vt[p >> 4][(p & 15) * 4]) = vr[d][i];
+      }
+    } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = tid + kThreads * i;
