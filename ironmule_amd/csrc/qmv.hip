@@ -1906,7 +1906,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
 }
 
-// ------------------------------------------- MFMA kernel over 256-row bands (M >= 16)
+// -------------------------------------------- MFMA kernel over 256-row bands (M >= 5)
 //
 // The direct-to-LDS kernel's 64-row workgroup reads, at 32 activation rows, twice as many
 // activation bytes as weight bytes (x: 64 bytes per K column, the 64 rows' weights 36).
@@ -2826,8 +2826,11 @@ bool take_dma(const LaunchArgs& a, int cu_count, DmaPlan* pl) {
 // fused gate/up entry (imq_qmv_gate_up_silu) reproduces.  Not applicable either: a pointer
 // table, M outside [IMQ_BAND_MIN_ROWS, 32], K % 256 != 0, x rows not 16-byte aligned,
 // offsets past 2 GiB, or more band counters than the counter region holds.
+// From 5 rows, as the direct-to-LDS kernel (measured at M = 5 / 8 / 12: 50000 x 1024 11.4 /
+// 11.5 / 12.0 us against 17.8 / 17.9 / 19.0, 19456 x 2560 15.5 / 15.6 / 16.3 against 17.7 /
+// 17.7 / 18.3, 8192 x 4096 16.1 / 16.1 / 17.2 against 17.7 / 18.0 / 18.5)
 #ifndef IMQ_BAND_MIN_ROWS
-#define IMQ_BAND_MIN_ROWS 16
+#define IMQ_BAND_MIN_ROWS 5
 #endif
 
 struct BandPlan {
