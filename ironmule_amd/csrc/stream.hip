@@ -50,6 +50,7 @@
 #include "../../include/ironmule_step.h"
 #include "common.h"
 #include "runtime.h"
+#include "stream_runs.h"
 
 namespace {
 
@@ -118,13 +119,11 @@ struct SArgs {
   const int32_t* run_site;  // independent stages: (stage << 2) | problem of each run's first tile
   uint32_t* claim;          // independent stages: kShards claim counters, kLine words apart
   int32_t nstages, total, waves, sb_off;  // sb_off: LDS byte offset of the scale/bias areas
-  int32_t nslots, run;                     // run: tiles per static run (independent stages)
-  int32_t static_runs, runs;               // runs [0, static_runs) are dealt, the rest claimed
-  int32_t dyn_run, shards;                 // tiles per claimed run; claim counters in use
-  int32_t shard_lo[kShards + 1];           // shard s claims runs [shard_lo[s], shard_lo[s + 1])
-  int32_t shard_waves[kShards];            // wavefronts that claim from shard s
+  int32_t nslots, pad;
+  imq_runs::ShardPlan runs;  // independent stages: dealt and claimed runs, claim shards
   XSlot slot[kMaxSlots];
 };
+static_assert(kShards == imq_runs::kMaxShards, "one claim counter line per shard");
 
 typedef const struct SStage __attribute__((address_space(4)))& StageRef;
 
@@ -374,20 +373,19 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
 // and a wavefront resolves a problem's descriptors once per run rather than once per
 // tile.  R (16 or a little more) is chosen so that the runs split the program evenly over
 // the wavefronts.  Dealt runs cover whole rounds of the program's first tiles; the rest is
-// cut into runs of dyn_run tiles that the wavefronts claim one at a time from a counter
-// (an atomic add), so that the wavefronts that stream faster take more of them and all
-// finish together (measured on MI355X: with every run dealt, the last wavefronts of a
-// 20-layer launch ended 35 us after the median one; claiming the last 25% in runs of 8
-// tiles took that launch from 5.83 to 6.13 TB/s, while runs of 4 or 16 tiles and a 12%
-// share gained less).  The claimed runs are split between
-// `shards` counters, each on its own line (one counter serialises its atomic adds: 16K
-// claims on one counter cost a 20-layer launch 100 us); workgroup b claims from shard
-// (b / 8) % shards, so every shard is served by workgroups of all eight XCDs.  Each
-// wavefront makes exactly one claim past its shard's last run, so a shard's last claim is
-// number (its runs + its wavefronts - 1); the wavefront that receives it returns the
-// counter to zero for the next launch.  Its cursors only move forward.  kDepth tiles are in flight: the loads of a wavefront's tile
-// k + kDepth are issued as soon as its tile k has been computed; the load cursor claims the
-// runs and the compute cursor, kDepth tiles behind, takes them from a two-entry queue.
+// cut into runs of dyn_run tiles (the last ending at the program's last tile) that the
+// wavefronts claim one at a time from a counter (an atomic add), so that the wavefronts
+// that stream faster take more of them and all finish together (measured on MI355X: with
+// every run dealt, the last wavefronts of a 20-layer launch ended 35 us after the median
+// one; claiming the last 25% in runs of 8 tiles took that launch from 5.83 to 6.13 TB/s,
+// while runs of 4 or 16 tiles and a 12% share gained less).  The claimed runs are split
+// between `shards` counters, each on its own line (one counter serialises its atomic adds:
+// 16K claims on one counter cost a 20-layer launch 100 us).  The plan, the claim count
+// that returns a shard's counter to zero and the two cursors' steps are in stream_runs.h,
+// which a host simulation of this protocol compiles as well.  kDepth tiles are in flight:
+// the loads of a wavefront's tile k + kDepth are issued as soon as its tile k has been
+// computed; the load cursor claims the runs and the compute cursor, kDepth tiles behind,
+// takes them from a two-entry queue.
 constexpr int kRunTarget = 16;
 #ifndef IMQ_STREAM_DYN_RUN
 #define IMQ_STREAM_DYN_RUN 8
@@ -403,52 +401,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int v = blockIdx.x * kWaves + wave;
-  const int V = a.waves, total = a.total, R = a.run;
-  const int Rs = a.static_runs, Rend = a.runs, R2 = a.dyn_run;
+  const imq_runs::RunPlan& P = a.runs.plan;
+  const int total = P.total;
   uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
   const uint32_t magic = in_vgpr(kMagic);
-  // a position in this wavefront's sequence of tiles: run r (global), tile t of the run; a
-  // run at or past Rend starts past the last tile
-  struct Pos {
-    int r, t;
-  };
-  auto start_of = [&](int r) { return r < Rs ? r * R : (r < Rend ? Rs * R + (r - Rs) * R2 : total); };
-  auto length_of = [&](int r) { return r < Rs ? R : R2; };
-  auto tile = [&](const Pos& p) { return start_of(p.r) + p.t; };
-  int qa = 0, qb = 0, qn = 0;  // runs the load cursor claimed that the compute cursor has not reached
-  const int shard = (blockIdx.x >> 3) % a.shards;
+  using imq_runs::Pos;
+  auto tile = [&](const Pos& p) { return imq_runs::tile_of(P, p); };
+  imq_runs::ClaimQueue cq;
+  const int shard = imq_runs::shard_of_group(blockIdx.x, a.runs.shards);
   uint32_t* ctr = a.claim + shard * kLine;
-  const int lo = a.shard_lo[shard], count = a.shard_lo[shard + 1] - lo;
-  const uint32_t last_claim = (uint32_t)(count + a.shard_waves[shard] - 1);
+  const int lo = a.runs.shard_lo[shard], count = a.runs.shard_lo[shard + 1] - lo;
+  const uint32_t last_claim = imq_runs::last_claim_of(count, a.runs.shard_waves[shard]);
   auto claim = [&]() {
     uint32_t old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old == last_claim && lane == 0) st_sc1(ctr, 0u);
-    return (int)old < count ? lo + (int)old : Rend;
+    return imq_runs::claimed_run(old, lo, count, P.runs);
   };
-  auto step_load = [&](Pos& p) {
-    if (++p.t < length_of(p.r)) return;
-    p.t = 0;
-    if (p.r + V < Rs || Rs == Rend) {
-      p.r += V;  // the next dealt run (or, with nothing to claim, past the end)
-    } else if (p.r < Rend) {
-      p.r = claim();
-      if (qn == 0) qa = p.r; else qb = p.r;
-      ++qn;
-    }
-  };
-  auto step_compute = [&](Pos& p) {
-    if (++p.t < length_of(p.r)) return;
-    p.t = 0;
-    if (p.r + V < Rs || Rs == Rend) {
-      p.r += V;
-    } else if (p.r < Rend) {
-      p.r = qa;
-      qa = qb;
-      --qn;
-    }
-  };
+  auto step_load = [&](Pos& p) { imq_runs::step_load(P, p, cq, claim); };
+  auto step_compute = [&](Pos& p) { imq_runs::step_compute(P, p, cq); };
 
   // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp); a cursor that
   // leaves its problem starts from the problem of its run's first tile (a table lookup)
@@ -776,40 +748,18 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
   p->args.total = tiles;
   p->args.waves = grid * kWaves;
   if (!p->chained) {
-    // runs of kRunTarget tiles or a little more, in whole rounds of one run per wavefront
-    // (the last round short by less than one tile per run), and the problem of the first
-    // tile of every run
-    const int V = grid * kWaves;
-    const int rounds = std::max(1, tiles / (V * kRunTarget));
-    const int R = (tiles + V * rounds - 1) / (V * rounds);
-    p->args.run = R;
-    // whole rounds dealt, the last IMQ_STREAM_DYN_PERCENT of the rounds (at least one, when
-    // there are two or more) claimed in runs of IMQ_STREAM_DYN_RUN tiles
-    int dealt = rounds;
-    if (rounds >= 2 && IMQ_STREAM_DYN_PERCENT > 0) {
-      const int claimed = std::max(1, (rounds * IMQ_STREAM_DYN_PERCENT + 50) / 100);
-      dealt = rounds - std::min(claimed, rounds - 1);
-    }
-    int static_runs = (tiles + R - 1) / R, nruns = static_runs, R2 = IMQ_STREAM_DYN_RUN;
-    if (dealt < rounds) {
-      static_runs = V * dealt;
-      nruns = static_runs + (tiles - static_runs * R + R2 - 1) / R2;
-    }
-    p->args.static_runs = static_runs;
-    p->args.runs = nruns;
-    p->args.dyn_run = R2;
-    // shards of the claimed runs: as many as there are groups of 8 workgroups (up to
-    // kShards), each with an equal share of the runs and the count of its wavefronts
-    const int shards = std::max(1, std::min(kShards, grid / 8));
-    p->args.shards = shards;
-    for (int k = 0; k <= shards; ++k)
-      p->args.shard_lo[k] = static_runs + (int)((int64_t)(nruns - static_runs) * k / shards);
-    for (int k = 0; k < shards; ++k) p->args.shard_waves[k] = 0;
-    for (int b = 0; b < grid; ++b) p->args.shard_waves[(b / 8) % shards] += kWaves;
+    // runs of kRunTarget tiles or a little more, in whole rounds of one run per wavefront,
+    // the last IMQ_STREAM_DYN_PERCENT of the rounds claimed in runs of IMQ_STREAM_DYN_RUN
+    // tiles from as many shards as there are groups of 8 workgroups (up to kShards); and
+    // the problem of the first tile of every run
+    p->args.runs = imq_runs::plan_runs(tiles, grid, kWaves, kRunTarget, IMQ_STREAM_DYN_RUN,
+                                       IMQ_STREAM_DYN_PERCENT);
+    const imq_runs::RunPlan& P = p->args.runs.plan;
+    const int nruns = P.runs;
     std::vector<int32_t> runs((size_t)nruns);
     int si = 0, pi = 0;
     for (int r = 0; r < nruns; ++r) {
-      const int g = r < static_runs ? r * R : static_runs * R + (r - static_runs) * R2;
+      const int g = P.start_of(r);
       while (g >= p->stages[si].first + p->stages[si].p[pi].tile_end) {
         if (pi + 1 < p->stages[si].nprob) {
           ++pi;

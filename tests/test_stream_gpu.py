@@ -81,6 +81,28 @@ def test_independent_layer_stages(env, workgroups):
     prog.close()
 
 
+@pytest.mark.parametrize("n_rows,workgroups", [(5000, 1), (5000, 3), (3001, 2), (5000, 9)])
+def test_short_last_claimed_run_repeated_launches(env, n_rows, workgroups):
+    """One stage whose last claimed run is shorter than the others (5000 rows at K = 2560
+    are 1250 tiles: at one workgroup the claimed tail is 2 tiles past a multiple of 8),
+    launched eight times on the same claim counters: every launch's output equals the
+    per-kernel call.  A counter left behind by one launch would make the next skip runs."""
+    torch, n, orc = env
+    announce("stream short last run", n_rows, workgroups)
+    x = _row(torch, 2560, 5)
+    ws = [_weight(orc, n_rows, 2560, 77)]
+    ys = [torch.empty(n_rows, dtype=torch.bfloat16, device="cuda")]
+    stages = [(ws, x, ys, False)]
+    prog = n.stream_program(stages, workgroups=workgroups)
+    assert prog.info()["workgroups"] == workgroups
+    for run in range(8):
+        ys[0].fill_(9.0)
+        prog.launch()
+        torch.cuda.synchronize()
+        _check_stages(torch, n, stages, run)
+    prog.close()
+
+
 def test_independent_ragged_shapes_and_the_oracle(env):
     """Small K (64, 192, 320), N not a multiple of any tile, one weight per stage and
     three per stage; one output is also checked against the oracle's fp64 product."""
