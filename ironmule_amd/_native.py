@@ -287,6 +287,11 @@ def qmv(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, x: torch.Te
 
 
 _workspaces: dict = {}
+# Every workspace a (device, stream) outgrew.  A HIP graph captured on that stream before
+# the growth still holds the old pointer, so the old buffer is never released: a replay
+# keeps reading and writing memory that is still its own, and its split counters are
+# still zero (every call returns them to zero).
+_retired: list = []
 
 
 def _workspace_key(device, stream) -> tuple[int, int]:
@@ -300,20 +305,27 @@ def _workspace_key(device, stream) -> tuple[int, int]:
     return index, int(stream.cuda_stream)
 
 
+def _zeroed(words: int, index: int, stream) -> torch.Tensor:
+    """A zero-filled fp32 tensor of `words` on device `index`, allocated and filled on
+    `stream` (so the fill is ordered before the launch that uses it)."""
+    s = stream if stream is not None else torch.cuda.current_stream(index)
+    with torch.cuda.stream(s):
+        return torch.zeros(words, dtype=torch.float32, device=torch.device("cuda", index))
+
+
 def _workspace(nbytes: int, device, stream) -> torch.Tensor:
     """A zero-filled fp32 workspace of at least nbytes for (device, stream), kept for later
     calls: the library's split counters must be zero before a workspace's first use and
     every call leaves them at zero, so one workspace serves every call on that stream
-    (calls on one stream never overlap).  It is allocated and filled on that stream, so
-    the fill is ordered before the launch that uses it; a replaced smaller workspace is
-    released only after the work already queued on the stream."""
+    (calls on one stream never overlap).  A call that needs more gets a new, larger one;
+    the smaller one is kept alive in `_retired` for the graphs that may hold it."""
     index, handle = _workspace_key(device, stream)
     key = (index, handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
-        s = stream if stream is not None else torch.cuda.current_stream(index)
-        with torch.cuda.stream(s):
-            ws = torch.zeros(-(-nbytes // 4), dtype=torch.float32, device=torch.device("cuda", index))
+        if ws is not None:
+            _retired.append(ws)
+        ws = _zeroed(-(-nbytes // 4), index, stream)
         _workspaces[key] = ws
     return ws
 

@@ -284,3 +284,48 @@ def test_split_calls_of_different_shapes_share_a_workspace(native, oracle):
             for a, b in zip(bits, first):
                 for x, y in zip(a, b):
                     assert np.array_equal(x, y), rnd
+
+
+def test_a_graph_keeps_its_workspace_after_the_stream_outgrows_it(native, oracle):
+    """Continuous batching's pattern: a graph of a batch-8 split launch is captured on a
+    stream, then a batch-32 launch on the same stream needs a larger workspace and a graph
+    of it is captured too.  The first graph's workspace must stay allocated: fresh tensors
+    filled with junk take whatever memory was freed, and five replays of each graph (with
+    eager work between them) still give their eager results' bits."""
+    import torch
+    n_rows, k = 2560, 4096
+    pr = oracle.synthetic(n_rows, k, 32, seed=oracle.SEED_BASE + 95)
+    w, s, b, x32 = to_device(pr)
+    x8 = x32[:8].contiguous()
+    stream = torch.cuda.Stream()
+    key = native._workspace_key(w.device, stream)
+    announce("graph workspace growth")
+    with torch.cuda.stream(stream):
+        want8 = native.qmv(w, s, b, x8, stream=stream)
+    torch.cuda.synchronize()
+    size8 = native._workspaces[key].numel()
+    retired = len(native._retired)
+    g8 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g8, stream=stream):
+        y8 = native.qmv(w, s, b, x8, stream=stream)
+    with torch.cuda.stream(stream):
+        want32 = native.qmv(w, s, b, x32, stream=stream)
+    torch.cuda.synchronize()
+    assert native._workspaces[key].numel() > size8 and len(native._retired) == retired + 1
+    g32 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g32, stream=stream):
+        y32 = native.qmv(w, s, b, x32, stream=stream)
+    torch.cuda.synchronize()
+    junk = [torch.full((size8,), -7.0e30, device="cuda") for _ in range(8)]
+    _check(oracle, pr, want32)
+    for rep in range(5):
+        with torch.cuda.stream(stream):
+            g8.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y8.view(torch.int16), want8.view(torch.int16)), rep
+        with torch.cuda.stream(stream):
+            g32.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y32.view(torch.int16), want32.view(torch.int16)), rep
+        junk.append(native.qmv(w, s, b, x8))
+    del junk
