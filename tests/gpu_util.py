@@ -24,9 +24,11 @@ def announce(*parts) -> None:
     print("[gpu case]", *parts, flush=True)
 
 
-def oracle_decoder(do, orc, weights):
+def oracle_decoder(do, orc, weights, lazy: bool = False):
     """The decode oracle's Model for a `decode.DecoderWeights` on the GPU: every projection
-    and the tied embedding dequantised to float64 by the oracle, norms widened from bf16."""
+    and the tied embedding dequantised to float64 by the oracle, norms widened from bf16.
+    With `lazy` the layers are dequantised one at a time as the oracle walks them (a
+    36-layer Qwen3-4B in float64 would take 32 GB at once)."""
     import numpy as np
 
     def vals(t):
@@ -37,11 +39,29 @@ def oracle_decoder(do, orc, weights):
         return orc.dequant_f32(w.numpy().view(np.uint32), s.view(torch.int16).numpy().view(np.uint16),
                                b.view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
 
+    def layer(L):
+        return do.Layer(wq=deq(L["q"]), wk=deq(L["k"]), wv=deq(L["v"]), wo=deq(L["o"]),
+                        wg=deq(L["gate"]), wu=deq(L["up"]), wd=deq(L["down"]),
+                        input_norm=vals(L["input_norm"]), post_norm=vals(L["post_norm"]),
+                        q_norm=vals(L["q_norm"]), k_norm=vals(L["k_norm"]))
+
+    class _Layers:
+        def __len__(self):
+            return len(weights.layers)
+
+        def __iter__(self):
+            for L in weights.layers:
+                yield layer(L)
+
     c = weights.config
-    layers = [do.Layer(wq=deq(L["q"]), wk=deq(L["k"]), wv=deq(L["v"]), wo=deq(L["o"]),
-                       wg=deq(L["gate"]), wu=deq(L["up"]), wd=deq(L["down"]),
-                       input_norm=vals(L["input_norm"]), post_norm=vals(L["post_norm"]),
-                       q_norm=vals(L["q_norm"]), k_norm=vals(L["k_norm"]))
-              for L in weights.layers]
+    layers = _Layers() if lazy else [layer(L) for L in weights.layers]
     return do.Model(layers=layers, embed=deq(weights.embed), norm=vals(weights.norm),
                     heads=c.heads, kv_heads=c.kv_heads, eps=c.eps, theta=c.theta)
+
+
+def logit_error(got, ref):
+    """max|got - ref| / max|ref| over one request's logits."""
+    import numpy as np
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max() / np.abs(ref).max())

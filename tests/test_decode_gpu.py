@@ -6,8 +6,9 @@ attention outputs within one bf16 ulp of the float64 reference plus a small abso
 allowance for cancellation; q/k after norm + rotation within two bf16 ulps of their
 pair's length (the rotation mixes two values that each carry one rounding); v and the
 KV placement exact.  The whole step (a small decoder: 2 layers, hidden 256, 4/2 heads)
-within max|logit - ref| / max|ref| <= 1e-2 of the oracle step with the same bf16
-rounding points (the reference's own probe tolerance, ironmule/cuda_native.py:253-268).
+within max|logit - ref| / max|ref| <= 2e-7 (RMSNorm launches) or 5e-4 (RMSNorms folded into
+the projections) of the oracle step with the same bf16 rounding points: about twice the
+observed values (the reference's own probe tolerance is 1e-2, ironmule/cuda_native.py:253-268).
 """
 
 from __future__ import annotations
@@ -322,7 +323,9 @@ def test_decode_step_matches_oracle(env, batch):
         ref = do.decode_step(model, keys, values, tokens, slots, positions, round_bf16=True)
         got = logits.cpu().numpy().astype(np.float64)
         rel = np.abs(got - ref).max() / np.abs(ref).max()
-        assert rel <= 1e-2, (step, rel)
+        print(f"[observed] small decoder batch {batch} step {step}: max|dlogit|/max|logit| = {rel:.3e}", flush=True)
+        # observed 8.6e-8 (batch 3, RMSNorm launches), 2.2e-4 (batch 6, folded RMSNorms)
+        assert rel <= (2e-7 if batch < FUSED_NORM_ROWS else 5e-4), (step, rel)
         for i in range(cfg.layers):
             for r in range(batch):
                 kg = _vals(state.k_pool[i])[slots[r], :, positions[r]]

@@ -5,7 +5,7 @@ intermediate 15360 (down is K=15360: both aligned).
 
 Bars: two requests stepped together give the same logit bits with the sweeps shared, with
 them separate, and each request stepped alone (the shared kernels' results depend only on
-their own row); every step within max|logit - ref| / max|ref| <= 1e-2 of the decode oracle
+their own row); every step within max|logit - ref| / max|ref| <= 1e-5 of the decode oracle
 with the same bf16 rounding points (the decode step's bar); the scheduler's token streams
 are the same with and without sharing.
 """
@@ -63,7 +63,8 @@ def test_paired_step_matches_solo_steps_and_the_oracle(env):
         for r in range(2):
             assert torch.equal(a[r], b[r]) and torch.equal(a[r], c[r]), (step, r)
             got = a[r].cpu().numpy().astype(np.float64)
-            assert _rel(got, ref[r]) <= 1e-2, (step, r, _rel(got, ref[r]))
+            print(f"[observed] paired step {step} row {r}: max|dlogit|/max|logit| = {_rel(got, ref[r]):.3e}", flush=True)
+            assert _rel(got, ref[r]) <= 1e-5, (step, r, _rel(got, ref[r]))  # observed <= 3.0e-6
         tokens = [int(torch.argmax(x)) for x in a]
 
 

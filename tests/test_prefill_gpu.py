@@ -2,7 +2,7 @@
 token at a time, on a small decoder (2 layers, hidden 256, 4/2 heads of 128).
 
 Bars (the decode step's): the last position's logits within max|logit - ref| / max|ref|
-<= 1e-2 of the oracle with the same bf16 rounding points; every key and value written to
+<= 5e-4 (1e-4 for the decode step after it) of the oracle with the same bf16 rounding points; every key and value written to
 the request's KV slot within 5% of that layer's largest oracle entry; nothing written to
 other slots; and a decode step continuing at position T meets the logit bar again.
 Prompts of 7 tokens take the qmv kernel, 40 and 96 tokens the fp16 dequantise + GEMM path.
@@ -60,7 +60,8 @@ def test_prefill_matches_the_oracle_decoded_token_by_token(env, count):
     values = [np.zeros_like(k) for k in keys]
     for pos, tok in enumerate(tokens):
         ref = do.decode_step(model, keys, values, [tok], [slot], [pos], round_bf16=True)[0]
-    assert _rel(got, ref) <= 1e-2, _rel(got, ref)
+    print(f"[observed] prefill last position: max|dlogit|/max|logit| = {_rel(got, ref):.3e}", flush=True)
+    assert _rel(got, ref) <= 5e-4, _rel(got, ref)  # observed 7.0e-8 .. 2.0e-4
     for i in range(cfg.layers):
         for pool, want in ((state.k_pool[i], keys[i]), (state.v_pool[i], values[i])):
             have = _vals(pool)
@@ -74,7 +75,8 @@ def test_prefill_matches_the_oracle_decoded_token_by_token(env, count):
     state.set_requests([nxt], [slot], [count])
     step = decode_step(weights, state)[0].cpu().numpy().astype(np.float64)
     ref2 = do.decode_step(model, keys, values, [nxt], [slot], [count], round_bf16=True)[0]
-    assert _rel(step, ref2) <= 1e-2, _rel(step, ref2)
+    print(f"[observed] decode step after prefill: max|dlogit|/max|logit| = {_rel(step, ref2):.3e}", flush=True)
+    assert _rel(step, ref2) <= 1e-4, _rel(step, ref2)  # observed 6.0e-8 .. 5.2e-5
 
 
 def test_prefill_rejects_bad_prompts(env):

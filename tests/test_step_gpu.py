@@ -157,7 +157,8 @@ def test_decode_program_tiny_against_the_oracle(env):
         assert not engine.failed()
         ref = do.decode_step(model, keys, values, [tok], [slot], [pos], round_bf16=True)
         rel = np.abs(got - ref).max() / np.abs(ref).max()
-        assert rel <= 1e-2, (step, rel)
+        print(f"[observed] persistent decode step {step}: max|dlogit|/max|logit| = {rel:.3e}", flush=True)
+        assert rel <= 2e-7, (step, rel)  # observed 6.0e-8
         tok, pos = int(np.argmax(got[0])), pos + 1
 
 
