@@ -61,11 +61,17 @@ using imq_rt::DeviceInfo;
 using imq_rt::fail;
 using imq_rt::ok;
 
-constexpr int kThreads = 256;
+#ifndef IMQ_STREAM_THREADS
+#define IMQ_STREAM_THREADS 768
+#endif
+// One workgroup of 12 wavefronts per CU: every distinct x of a program is loaded and
+// staged once per CU (with three workgroups of 4 wavefronts a CU read and staged it three
+// times, about as many bytes at the start of a launch as the first two tiles' weights).
+constexpr int kThreads = IMQ_STREAM_THREADS;
 constexpr int kWaves = kThreads / 64;
 constexpr int kNch = 5;                // 16-byte chunks per lane: m1_lane_shift gives <= 5 for K <= 10240
-constexpr int kXr = 5;                 // most x pieces of 8 values per thread: K <= 10240
-constexpr int kMaxK = kXr * kThreads * 8;
+constexpr int kMaxK = 10240;           // m1_lane_shift gives <= kNch chunks per lane up to here
+constexpr int kXr = (kMaxK + kThreads * 8 - 1) / (kThreads * 8);  // x pieces of 8 values per thread
 constexpr int kSubs = 16;              // completion counters per stage
 constexpr int kLine = 32;              // words per counter line
 constexpr int kMaxPolls = 1 << 22;
@@ -76,6 +82,10 @@ constexpr int kSbWords = 256;           // per wavefront: the span's scale halve
 constexpr int kBiasArea = 512;          // byte offset of the bias halves in the area
 constexpr int kDepth = 2;                // tiles in flight per wavefront (independent stages)
 constexpr int kShards = 16;              // claim counters (independent stages)
+#ifndef IMQ_STREAM_PRE_SLOTS
+#define IMQ_STREAM_PRE_SLOTS 3
+#endif
+constexpr int kPreSlots = IMQ_STREAM_PRE_SLOTS;  // x rows loaded ahead of the first weights
 
 // LDS bytes of one staged x row of K values: C = K/32 chunks of 80 bytes each, the
 // chunk's four words in pair order (64 bytes), its sum and -128 times its sum (8 bytes)
@@ -342,16 +352,19 @@ __device__ __forceinline__ void compute_site(const Site& c, int g, int lane, con
 
 // Stages the bf16 row x (K values) in LDS at `dst` in pair order with its chunk sums; the
 // whole workgroup takes part.  `live`: x was written earlier in this launch (sc1 loads).
-__device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, char* dst, int tid) {
+__device__ __forceinline__ void load_x(const uint16_t* x, int K, bool live, int tid, uint4 (&xs)[kXr]) {
   const int W = K >> 3;
   const __amdgpu_buffer_rsrc_t r = buffer_rsrc(x, (uint32_t)K * 2u);
-  uint4 xs[kXr];
 #pragma unroll
   for (int t = 0; t < kXr; ++t) {
     const int i = tid + kThreads * t;
     const uint32_t off = i < W ? 16u * i : kPastBuffer;
     xs[t] = live ? load_b128_sc1(r, off) : load_b128(r, off);
   }
+}
+
+__device__ __forceinline__ void store_x(const uint4 (&xs)[kXr], int K, char* dst, int tid) {
+  const int W = K >> 3;
 #pragma unroll
   for (int t = 0; t < kXr; ++t) {
     const int i = tid + kThreads * t;  // the four words of a chunk are four aligned lanes
@@ -364,6 +377,12 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
       if ((i & 3) == 0) reinterpret_cast<float2*>(chunk + 64)[0] = make_float2(part, -128.0f * part);
     }
   }
+}
+
+__device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, char* dst, int tid) {
+  uint4 xs[kXr];
+  load_x(x, K, live, tid, xs);
+  store_x(xs, K, dst, tid);
 }
 
 // ------------------------------------------------------------ independent stages
@@ -393,6 +412,14 @@ constexpr int kRunTarget = 16;
 #ifndef IMQ_STREAM_DYN_PERCENT
 #define IMQ_STREAM_DYN_PERCENT 25
 #endif
+#ifndef IMQ_STREAM_TAIL_RUN
+#define IMQ_STREAM_TAIL_RUN 2
+#endif
+#ifndef IMQ_STREAM_TAIL_PERCENT
+#define IMQ_STREAM_TAIL_PERCENT 30
+#endif
+// workgroups in a row that land on distinct XCDs (workgroup b runs on XCD b % 8)
+constexpr int kXcdSpread = 8;
 static_assert(IMQ_STREAM_DYN_RUN > kDepth, "a claimed run is longer than the cursors' distance");
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void stream_kernel(const SStage* __restrict__ st, SArgs a) {
@@ -406,21 +433,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
   const uint32_t magic = in_vgpr(kMagic);
   using imq_runs::Pos;
-  auto tile = [&](const Pos& p) { return imq_runs::tile_of(P, p); };
+  const int shard = imq_runs::shard_of_group(blockIdx.x, a.runs.shards, a.runs.spread);
+  const imq_runs::ShardRuns sh = a.runs.shard[shard];
+  auto tile = [&](const Pos& p) { return imq_runs::tile_of(P, sh, p); };
   imq_runs::ClaimQueue cq;
-  const int shard = imq_runs::shard_of_group(blockIdx.x, a.runs.shards);
   uint32_t* ctr = a.claim + shard * kLine;
-  const int lo = a.runs.shard_lo[shard], count = a.runs.shard_lo[shard + 1] - lo;
-  const uint32_t last_claim = imq_runs::last_claim_of(count, a.runs.shard_waves[shard]);
+  const uint32_t last_claim = imq_runs::last_claim_of(sh.count, a.runs.shard_waves[shard]);
   auto claim = [&]() {
     uint32_t old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old == last_claim && lane == 0) st_sc1(ctr, 0u);
-    return imq_runs::claimed_run(old, lo, count, P.runs);
+    return imq_runs::claimed_run(old, sh, P.runs);
   };
-  auto step_load = [&](Pos& p) { imq_runs::step_load(P, p, cq, claim); };
-  auto step_compute = [&](Pos& p) { imq_runs::step_compute(P, p, cq); };
+  auto step_load = [&](Pos& p) { imq_runs::step_load(P, sh, p, cq, claim); };
+  auto step_compute = [&](Pos& p) { imq_runs::step_compute(P, sh, p, cq); };
 
   // the load cursor (stage ls, problem lp) and the compute cursor (cs, cp); a cursor that
   // leaves its problem starts from the problem of its run's first tile (a table lookup)
@@ -446,9 +473,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     load_site(lc, g, g < total, lane, t);
     step_load(lpos);
   };
+  // x first: the loads of the first kPreSlots distinct x rows go ahead of the first tiles'
+  // weights (loads return in issue order, so staging x then waits for x alone), the rest
+  // after them
+  uint4 xs[kPreSlots > 0 ? kPreSlots : 1][kXr];
+#pragma unroll
+  for (int k = 0; k < kPreSlots; ++k)
+    load_x(a.slot[k].x, k < a.nslots ? a.slot[k].K : 0, false, tid, xs[k]);
 #pragma unroll
   for (int d = 0; d < kDepth; ++d) issue(T[d]);
-  for (int k = 0; k < a.nslots; ++k) stage_x(a.slot[k].x, a.slot[k].K, false, smem + a.slot[k].off, tid);
+#pragma unroll
+  for (int k = 0; k < kPreSlots; ++k)
+    if (k < a.nslots) store_x(xs[k], a.slot[k].K, smem + a.slot[k].off, tid);
+  for (int k = kPreSlots; k < a.nslots; ++k) stage_x(a.slot[k].x, a.slot[k].K, false, smem + a.slot[k].off, tid);
   lds_barrier();
 
   // Every pass runs all kDepth tiles with no exit in between, so that every path into the
@@ -749,17 +786,20 @@ int32_t imq_stream_create(const imq_qmv_stage* stages, int32_t count, int32_t wo
   p->args.waves = grid * kWaves;
   if (!p->chained) {
     // runs of kRunTarget tiles or a little more, in whole rounds of one run per wavefront,
-    // the last IMQ_STREAM_DYN_PERCENT of the rounds claimed in runs of IMQ_STREAM_DYN_RUN
-    // tiles from as many shards as there are groups of 8 workgroups (up to kShards); and
-    // the problem of the first tile of every run
-    p->args.runs = imq_runs::plan_runs(tiles, grid, kWaves, kRunTarget, IMQ_STREAM_DYN_RUN,
-                                       IMQ_STREAM_DYN_PERCENT);
-    const imq_runs::RunPlan& P = p->args.runs.plan;
+    // the last IMQ_STREAM_DYN_PERCENT of the rounds claimed from as many shards as there
+    // are groups of kXcdSpread workgroups (up to kShards), each shard's tiles in runs of
+    // IMQ_STREAM_DYN_RUN and its last IMQ_STREAM_TAIL_PERCENT in runs of
+    // IMQ_STREAM_TAIL_RUN; and the problem of the first tile of every run
+    const imq_runs::ShardPlan& plan = p->args.runs = imq_runs::plan_runs(
+        tiles, grid, kWaves, kRunTarget, IMQ_STREAM_DYN_RUN, IMQ_STREAM_DYN_PERCENT,
+        IMQ_STREAM_TAIL_RUN, IMQ_STREAM_TAIL_PERCENT, kXcdSpread);
+    const imq_runs::RunPlan& P = plan.plan;
     const int nruns = P.runs;
     std::vector<int32_t> runs((size_t)nruns);
-    int si = 0, pi = 0;
+    int si = 0, pi = 0, shard = 0;
     for (int r = 0; r < nruns; ++r) {
-      const int g = P.start_of(r);
+      while (r >= P.static_runs && r >= plan.shard[shard].lo + plan.shard[shard].count) ++shard;
+      const int g = P.start_of(r, plan.shard[shard]);
       while (g >= p->stages[si].first + p->stages[si].p[pi].tile_end) {
         if (pi + 1 < p->stages[si].nprob) {
           ++pi;

@@ -30,8 +30,8 @@ using namespace imq_runs;
 namespace {
 
 constexpr int kDepth = 2;    // tiles in flight per wavefront (stream.hip)
-constexpr int kWaves = 4;    // wavefronts per workgroup (stream.hip)
 constexpr int kRunTarget = 16;
+constexpr int kSpread = 8;
 
 struct Rng {
   uint64_t s;
@@ -44,9 +44,16 @@ struct Rng {
   int below(int n) { return (int)(next() % (uint64_t)n); }
 };
 
-// The run lengths before the fix: every claimed run dyn_run tiles long.
+// Run lengths that ignore where a shard's tiles end: every claimed run as long as its kind
+// (the rule that left counters behind when a last run was short).
 struct OldPlan : RunPlan {
-  int length_of(int r) const { return r < static_runs ? run : dyn_run; }
+  int length_of(int r, const ShardRuns& s) const {
+    return r < static_runs ? run : (r - s.lo < s.nlong ? dyn_run : tail_run);
+  }
+};
+
+struct Params {
+  int total, grid, waves_per_group, dyn_run, pct, tail_run, tail_pct;
 };
 
 enum State { kInit, kPassStart, kCompute, kIssue, kDone };
@@ -61,28 +68,28 @@ struct Wave {
 };
 
 template <class Plan>
-bool launch(const ShardPlan& sp, const Plan& P, int grid, std::vector<uint32_t>& ctr, Rng& rng,
+bool launch(const ShardPlan& sp, const Plan& P, const Params& pr, std::vector<uint32_t>& ctr, Rng& rng,
             char* why, size_t why_len) {
-  const int V = grid * kWaves;
+  const int V = pr.grid * pr.waves_per_group;
   std::vector<Wave> waves((size_t)V);
   for (int v = 0; v < V; ++v) {
     waves[(size_t)v].lpos = Pos{v, 0};
     waves[(size_t)v].cpos = Pos{v, 0};
-    waves[(size_t)v].shard = shard_of_group(v / kWaves, sp.shards);
+    waves[(size_t)v].shard = shard_of_group(v / pr.waves_per_group, sp.shards, sp.spread);
   }
   std::vector<int> computed((size_t)P.total, 0);
   int max_queue = 0;
   auto issue = [&](Wave& w) {
-    const int g = tile_of(P, w.lpos);
+    const ShardRuns& sh = sp.shard[w.shard];
+    const int g = tile_of(P, sh, w.lpos);
     w.loaded.push_back(g < P.total ? g : -1);
-    const int lo = sp.shard_lo[w.shard], count = sp.shard_lo[w.shard + 1] - lo;
-    const uint32_t last = last_claim_of(count, sp.shard_waves[w.shard]);
+    const uint32_t last = last_claim_of(sh.count, sp.shard_waves[w.shard]);
     auto claim = [&]() {
       const uint32_t old = ctr[(size_t)w.shard]++;
       if (old == last) ctr[(size_t)w.shard] = 0;
-      return claimed_run(old, lo, count, P.runs);
+      return claimed_run(old, sh, P.runs);
     };
-    step_load(P, w.lpos, w.cq, claim);
+    step_load(P, sh, w.lpos, w.cq, claim);
     if (w.cq.qn > max_queue) max_queue = w.cq.qn;
   };
   std::vector<int> live;
@@ -107,7 +114,7 @@ bool launch(const ShardPlan& sp, const Plan& P, int grid, std::vector<uint32_t>&
         if (++w.inits == kDepth) w.state = kPassStart;
         break;
       case kPassStart:
-        w.g0 = tile_of(P, w.cpos);
+        w.g0 = tile_of(P, sp.shard[w.shard], w.cpos);
         if (w.g0 >= P.total) {
           w.state = kDone;
         } else {
@@ -116,7 +123,7 @@ bool launch(const ShardPlan& sp, const Plan& P, int grid, std::vector<uint32_t>&
         }
         break;
       case kCompute: {
-        const int gd = tile_of(P, w.cpos);
+        const int gd = tile_of(P, sp.shard[w.shard], w.cpos);
         const int got = w.loaded.front();
         w.loaded.pop_front();
         if (gd < P.total) {
@@ -129,7 +136,7 @@ bool launch(const ShardPlan& sp, const Plan& P, int grid, std::vector<uint32_t>&
           snprintf(why, why_len, "loaded tile %d is dropped", got);
           return false;
         }
-        step_compute(P, w.cpos, w.cq);
+        step_compute(P, sp.shard[w.shard], w.cpos, w.cq);
         w.state = kIssue;
         break;
       }
@@ -168,13 +175,29 @@ bool launch(const ShardPlan& sp, const Plan& P, int grid, std::vector<uint32_t>&
 }
 
 template <class Plan>
-bool run_case(int total, int grid, int dyn_run, int pct, int launches, Rng& rng, char* why, size_t n) {
-  const ShardPlan sp = plan_runs(total, grid, kWaves, kRunTarget, dyn_run, pct);
+bool run_case(const Params& pr, int launches, Rng& rng, char* why, size_t n) {
+  const ShardPlan sp = plan_runs(pr.total, pr.grid, pr.waves_per_group, kRunTarget, pr.dyn_run, pr.pct,
+                                 pr.tail_run, pr.tail_pct, kSpread);
+  // the shards cover the claimed tiles, in order, and the runs are numbered in tile order
+  int next_lo = sp.plan.static_runs;
+  for (int s = 0; s < kMaxShards; ++s) {
+    const ShardRuns& sh = sp.shard[s];
+    if (sh.count == 0) continue;
+    if (sh.lo != next_lo || sp.plan.start_of(sh.lo, sh) != sh.t0) {
+      snprintf(why, n, "shard %d does not follow the previous one", s);
+      return false;
+    }
+    next_lo += sh.count;
+  }
+  if (next_lo != sp.plan.runs) {
+    snprintf(why, n, "the shards hold %d runs of %d", next_lo - sp.plan.static_runs, sp.plan.runs - sp.plan.static_runs);
+    return false;
+  }
   Plan P;
   static_cast<RunPlan&>(P) = sp.plan;
   std::vector<uint32_t> ctr((size_t)kMaxShards, 0);
   for (int l = 0; l < launches; ++l) {
-    if (!launch(sp, P, grid, ctr, rng, why, n)) {
+    if (!launch(sp, P, pr, ctr, rng, why, n)) {
       char tail[128];
       snprintf(tail, sizeof(tail), " (launch %d)", l + 1);
       strncat(why, tail, n - strlen(why) - 1);
@@ -199,30 +222,37 @@ int main(int argc, char** argv) {
   }
   Rng rng{(uint64_t)strtoull(argv[a], nullptr, 10) * 2654435761ull + 1};
   const int cases = atoi(argv[a + 1]), launches = atoi(argv[a + 2]);
-  // fixed cases first: one workgroup over 1250 tiles (a 5000-row, K = 2560 stage: the
-  // last claimed run is 2 tiles), then random tile counts and grids
+  // fixed cases first: one workgroup of 4 wavefronts over 1250 tiles (a 5000-row,
+  // K = 2560 stage: the last claimed run is 2 tiles), the 20- and 36-layer programs of
+  // the streaming engine's grid (256 workgroups of 12 wavefronts), then random cases
   struct Fixed {
-    int total, grid;
-  } fixed[] = {{1250, 1}, {20480, 1}, {20480, 37}, {1, 1}, {7, 3}, {64, 1}, {129, 2}, {1000, 8}};
+    int total, grid, waves;
+  } fixed[] = {{1250, 1, 4},       {20480, 1, 4}, {20480, 37, 4}, {1, 1, 4},  {7, 3, 4},
+               {64, 1, 4},         {129, 2, 4},   {1000, 8, 4},   {204800, 256, 12},
+               {368640, 256, 12},  {5000, 2, 12}};
   const int nfixed = (int)(sizeof(fixed) / sizeof(fixed[0]));
   char why[256];
   for (int c = 0; c < nfixed + cases; ++c) {
-    int total, grid;
+    Params pr;
     if (c < nfixed) {
-      total = fixed[c].total;
-      grid = fixed[c].grid;
+      pr = Params{fixed[c].total, fixed[c].grid, fixed[c].waves, 8, 25, 2, 30};
     } else {
-      grid = 1 + rng.below(rng.below(4) == 0 ? 300 : 40);
-      const int per = kWaves * grid * kRunTarget;
-      total = 1 + rng.below(per * (1 + rng.below(6)));
+      pr.waves_per_group = rng.below(2) == 0 ? 4 : 12;
+      pr.grid = 1 + rng.below(rng.below(4) == 0 ? 300 : 40);
+      const int per = pr.waves_per_group * pr.grid * kRunTarget;
+      pr.total = 1 + rng.below(per * (1 + rng.below(6)));
+      pr.dyn_run = 3 + rng.below(8);  // stream.hip: > kDepth
+      pr.pct = rng.below(3) == 0 ? 50 : 25;
+      pr.tail_run = 1 + rng.below(3);
+      const int tails[] = {0, 30, 100};
+      pr.tail_pct = tails[rng.below(3)];
     }
-    const int dyn_run = c < nfixed ? 8 : 3 + rng.below(8);  // stream.hip: 8, and > kDepth
-    const int pct = c < nfixed ? 25 : (rng.below(3) == 0 ? 50 : 25);
     why[0] = 0;
-    const bool good = old ? run_case<OldPlan>(total, grid, dyn_run, pct, launches, rng, why, sizeof(why))
-                          : run_case<RunPlan>(total, grid, dyn_run, pct, launches, rng, why, sizeof(why));
+    const bool good = old ? run_case<OldPlan>(pr, launches, rng, why, sizeof(why))
+                          : run_case<RunPlan>(pr, launches, rng, why, sizeof(why));
     if (!good) {
-      printf("FAIL total=%d grid=%d dyn_run=%d pct=%d: %s\n", total, grid, dyn_run, pct, why);
+      printf("FAIL total=%d grid=%d waves=%d dyn_run=%d pct=%d tail_run=%d tail_pct=%d: %s\n", pr.total,
+             pr.grid, pr.waves_per_group, pr.dyn_run, pr.pct, pr.tail_run, pr.tail_pct, why);
       return 1;
     }
   }
