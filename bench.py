@@ -648,6 +648,8 @@ def main() -> None:
                     help="skip the GEMV bandwidth probe (and with it the phase roofline)")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the full decode step and exit (a short program for profilers)")
+    ap.add_argument("--decode-batches", default="1,32", metavar="B[,B...]",
+                    help="with --decode-only: the batch sizes to time (and no prefill unless 1 is one)")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="time only the headline layer steps (a short program for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -678,8 +680,10 @@ def main() -> None:
     if args.copy_calibration:
         copy_calibration(torch, device)
     if args.decode_only:
-        print(json.dumps({"metric": "decode tokens/s (profiling run)", **bench_decode(torch, device=device)}),
-              flush=True)
+        batches = tuple(int(b) for b in args.decode_batches.split(","))
+        print(json.dumps({"metric": "decode tokens/s (profiling run)",
+                          **bench_decode(torch, batches=batches, device=device,
+                                         prefill_tokens=1 in batches)}), flush=True)
         return
     if args.only:
         parts = args.only.split(",")
