@@ -13,6 +13,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));  // 4 bf16, the _1k MFMA operands
 
 // Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data format).
 // Every caller passes a value the whole wavefront agrees on; taking it through
@@ -189,6 +190,15 @@ __device__ __forceinline__ float add_xor16(float v) {
 __device__ __forceinline__ float add_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
   return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+// The same with the larger of the two.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
 }
 
 // Sum (max) over the wavefront, in every lane: each 16-lane row by DPP, then the four row

@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/ironmule_decode.h"
@@ -457,16 +458,21 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
 
 constexpr int kMergeBatch = 16;  // splits whose partials a merge loads at once
 constexpr uint32_t kNegZeroPair = 0x80008000u;  // the bf16 pair (-0, -0)
-// 64-key chunks of K and V in flight per task (registers).  At 32 requests x 8 KV heads x
-// 512 keys (768 tasks of three chunks) one measured 21.9 us a launch, two 25.2 and three
-// 35.5 (fewer resident workgroups, and no gain from the deeper prefetch).
-#ifndef IMQ_ATTN_RING
-#define IMQ_ATTN_RING 1
-#endif
+
+constexpr int kAttnWaves = kThreads / 64;
+constexpr int kUnit = 16;  // keys a wavefront takes at a time (the chunk's four wavefronts: 64)
+// Dwords per row of a wavefront's V^T tile: 16 keys (8 dwords) and 2 of padding, so that the
+// MFMA operand reads (16 lanes: 16 dimensions of one key quad) touch distinct banks.
+constexpr int kVtStride = 10;
 
 struct AttnLds {
-  uint4 kv[kChunk][17];  // K rows (padded), or V as uint32 [64][64]
-  float p[4][2][kChunk];
+  union {
+    uint32_t vt[kAttnWaves][kD][kVtStride];  // per wavefront: V^T of its 16 keys, bf16 pairs of keys
+    struct {
+      float acc[kAttnWaves][8][kD];  // per wavefront and query head: its chunks' weighted sum
+      float ml[kAttnWaves][8][2];    // and their (max, sum of exponentials)
+    } merge;
+  } u;
   uint32_t qs[8][kD / 2];  // rotated q of the task's heads, bf16 pairs
   uint32_t knew[kD / 2];
   uint32_t vnew[kD / 2];
@@ -503,47 +509,44 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   const int newrow = write_ok && pos < len ? pos : -1;
   const int writer = write_ok ? min(pos / span, splits - 1) : -1;
   const size_t base = (((size_t)(slot_ok ? slot : 0) * Hkv + kvh) * S.capacity) * kD;
-  uint32_t(*vt)[kD / 2] = reinterpret_cast<uint32_t(*)[kD / 2]>(&L.kv[0][0]);
 
-  // Chunk rows as raw buffer loads: rows past `last` read row last-1 (in the slot; never
-  // used), chunks at or past `last` read past the buffer (zeros, no traffic).  The row of
-  // the new key is read too (whatever the pool holds there) and replaced by the new key
-  // when staged.  kRing chunks of K and V are in flight in registers: the next one is
-  // issued into a chunk's registers as soon as they are staged in LDS.
+  // This wavefront's keys: units of 16, units wave, wave + kAttnWaves, ... of the split's
+  // keys [first, last) (so the workgroup's four wavefronts share each 64-key chunk).  K goes
+  // from memory straight into registers in the A-operand layout of v_mfma_f32_16x16x32_bf16
+  // (lane (key h16 = lane % 16, quarter q4 = lane / 16): 16 bytes, dimensions 32 j + 8 q4
+  // .. + 8 of k-step j); V as 16-byte pieces (lane (key quad lane % 4, dimension group
+  // lane / 4)) that the wavefront transposes through its LDS tile.  Rows at or past `last`
+  // read row last - 1 (their scores are masked), a unit at or past `last` reads past the
+  // buffer (zeros, no traffic).
   const uint32_t pool_bytes = (uint32_t)(((size_t)(slot_ok ? slot : 0) * Hkv + kvh + 1) * S.capacity * kD * 2);
   const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(S.k_pool, pool_bytes);
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(S.v_pool, pool_bytes);
-  // row p >> 4, 16-byte column p & 15 of the chunk starting at `start`, p = tid + 256 i
-  auto chunk_off = [&](int start, int i) -> uint32_t {
-    const int p = tid + kThreads * i;
-    const int t = start + (p >> 4) < last ? start + (p >> 4) : last - 1;
-    return start < last ? (uint32_t)((base + (size_t)t * kD) * 2) + 16u * (p & 15) : kPastBuffer;
+  const int h16 = lane & 15, q4 = lane >> 4;  // MFMA coordinates: row / column, k quarter
+  const int vq = lane & 3, vg = lane >> 2;    // V pieces: key quad, dimension group
+  auto row_bytes = [&](int key) __attribute__((always_inline)) -> uint32_t {
+    return (uint32_t)((base + (size_t)(key < last ? key : last - 1) * kD) * 2);
   };
-  constexpr int kRing = IMQ_ATTN_RING;
-  uint4 kr[kRing][4], vr[kRing][4];
-  auto issue_k = [&](uint4 (&r)[4], int start) {
+  uint4 kr[4], vr[4];  // K [k-step]; V [key of the quad]
+  auto load_k = [&](int start) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = load_b128(krs, chunk_off(start, i));
+    for (int j = 0; j < 4; ++j)
+      kr[j] = load_b128(krs, start < last ? row_bytes(start + h16) + 64u * j + 16u * q4 : kPastBuffer);
   };
-  auto issue_v = [&](uint4 (&r)[4], int start) {
+  auto load_v = [&](int start) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = load_b128(vrs, chunk_off(start, i));
+    for (int kk = 0; kk < 4; ++kk)
+      vr[kk] = load_b128(vrs, start < last ? row_bytes(start + 4 * vq + kk) + 16u * vg : kPastBuffer);
   };
-  auto issue_ring = [&]() {
-#pragma unroll
-    for (int d = 0; d < kRing; ++d) {
-      issue_k(kr[d], first + d * kChunk);
-      issue_v(vr[d], first + d * kChunk);
-    }
-  };
+  const int start0 = first + kUnit * wave;
 
   // q of the task's heads (a wavefront per head), the new key and value and the norm
   // weights.  A staged launch reads them first (its inputs are complete; loads return in
-  // issue order, so the rotation below waits only for these) and then puts the chunks in
-  // flight; the persistent form puts the chunks in flight, waits for its input stage and
+  // issue order, so the rotation below waits only for these) and then puts its first chunk
+  // in flight; the persistent form puts the chunk in flight, waits for its input stage and
   // reads them through sc1.
   if (!kStaged) {
-    issue_ring();
+    load_k(start0);
+    load_v(start0);
     if (!wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
   }
   const float eps = S.eps;
@@ -604,7 +607,10 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   }
   const float qn0 = bf(S.q_norm[lane]), qn1 = bf(S.q_norm[lane + 64]);
   const float kn0 = bf(S.k_norm[lane]), kn1 = bf(S.k_norm[lane + 64]);
-  if (kStaged) issue_ring();
+  if (kStaged) {
+    load_k(start0);
+    load_v(start0);
+  }
   const float inv_freq = exp2f(-(float)lane * (S.log2_theta / 64.0f));
   float sn, cs;
   sincosf((float)pos * inv_freq, &sn, &cs);
@@ -658,104 +664,138 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
 
   float M[2] = {-INFINITY, -INFINITY}, Ls[2] = {0.0f, 0.0f};
   float a0[2] = {0.0f, 0.0f}, a1[2] = {0.0f, 0.0f};
-  float mc[2], lc[2];
-  const uint4* kn4 = reinterpret_cast<const uint4*>(L.knew);
-  const uint4* vn4 = reinterpret_cast<const uint4*>(L.vnew);
-  for (int base_start = first; base_start < last; base_start += kRing * kChunk) {
+  {
+    // q^T as the B operand: lane (head h16, quarter q4) holds dimensions 32 j + 8 q4 .. + 8
+    // of head h16 for k-step j (zeros for the columns past the task's G heads)
+    bf16x8_t qb[4];
 #pragma unroll
-  for (int d = 0; d < kRing; ++d) {
-    const int start = base_start + d * kChunk;
-    if (start >= last) break;
-    const int count = min(kChunk, last - start);
-    // a chunk that holds neither the new key nor rows past `last` is stored as read
-    const bool plain = (newrow < start || newrow >= start + kChunk) && start + kChunk <= last;  // uniform
-    __syncthreads();  // the previous chunk's V readers are done
-    if (plain) {
+    for (int j = 0; j < 4; ++j)
+      qb[j] = __builtin_bit_cast(bf16x8_t, h16 < G ? reinterpret_cast<const uint4*>(L.qs[h16])[4 * j + q4]
+                                                   : make_uint4(0u, 0u, 0u, 0u));
+    const uint4* kn4 = reinterpret_cast<const uint4*>(L.knew);
+    const uint4* vn4 = reinterpret_cast<const uint4*>(L.vnew);
+    uint32_t(*vt)[kVtStride] = L.u.vt[wave];
+    // lane (h16, q4) carries head h16's running max and sum (the same in its four quarters)
+    // and acc[dblk][i] = its weighted sum for dimension 16 dblk + 4 q4 + i
+    float Mw = -INFINITY, Lw = 0.0f;
+    f32x4_t acc[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = tid + kThreads * i;
-        L.kv[p >> 4][p & 15] = kr[d][i];
+    for (int d = 0; d < 8; ++d) acc[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int start = start0; start < last; start += kAttnWaves * kUnit) {
+      const int next = start + kAttnWaves * kUnit;
+      // the unit that holds the new key: its row takes the rotated key (and below, the
+      // value) from LDS
+      const bool has_new = newrow >= start && newrow < start + kUnit;  // uniform
+      if (has_new) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kr[j] = select4(start + h16 == newrow ? ~0u : 0u, kn4[4 * j + q4], kr[j]);
       }
-    } else {
+      // scores: S^T (16 keys x heads) = K (keys x 128) q^T
+      f32x4_t sc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[j]), qb[j], sc, 0, 0, 0);
+      load_k(next);
+      // online softmax: lane (h16, q4) holds head h16's scores of keys start + 4 q4 + i
+      float mloc = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int p = tid + kThreads * i;
-        const int row = p >> 4, col = p & 15;
-        L.kv[row][col] = select4(start + row == newrow ? ~0u : 0u, kn4[col], kr[d][i]);
+        const float v = start + 4 * q4 + i < last ? sc[i] * S.scale : -INFINITY;
+        sc[i] = v;
+        mloc = fmaxf(mloc, v);
+      }
+      mloc = max_xor32(max_xor16(mloc));
+      const float mnew = fmaxf(Mw, mloc);
+      const float alpha = expf(Mw - mnew);
+      float lsum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = expf(sc[i] - mnew);
+        sc[i] = p;
+        lsum += p;
+      }
+      lsum = add_xor32(add_xor16(lsum));
+      Lw = fmaf(Lw, alpha, lsum);
+      Mw = mnew;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[d] *= alpha;
+      // P^T as the B operand of v_mfma_f32_16x16x16_bf16 (lane (h16, q4): keys 4 q4 .. + 3,
+      // the scores' own layout), split into bf16 high and low parts (p = hi + lo to about
+      // 2^-16)
+      uint32_t hi[2], lo[2];
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const uint32_t h0 = to_bf(sc[2 * w]), h1 = to_bf(sc[2 * w + 1]);
+        hi[w] = h0 | (h1 << 16);
+        lo[w] = (uint32_t)to_bf(sc[2 * w] - bf(h0)) | ((uint32_t)to_bf(sc[2 * w + 1] - bf(h1)) << 16);
+      }
+      const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
+      const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+      // V^T of the unit's keys into this wavefront's tile: for each of the 8 dimensions of
+      // the lane's group, the values of its quad's four keys as two dwords
+      {
+        uint4 r[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) r[kk] = vr[kk];
+        if (has_new) {
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) r[kk] = select4(start + 4 * vq + kk == newrow ? ~0u : 0u, vn4[vg], r[kk]);
+        }
+        const uint32_t w0[4] = {r[0].x, r[0].y, r[0].z, r[0].w}, w1[4] = {r[1].x, r[1].y, r[1].z, r[1].w};
+        const uint32_t w2[4] = {r[2].x, r[2].y, r[2].z, r[2].w}, w3[4] = {r[3].x, r[3].y, r[3].z, r[3].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          *reinterpret_cast<uint2*>(&vt[8 * vg + 2 * w][2 * vq]) =
+              make_uint2((w0[w] & 0xffffu) | (w1[w] << 16), (w2[w] & 0xffffu) | (w3[w] << 16));
+          *reinterpret_cast<uint2*>(&vt[8 * vg + 2 * w + 1][2 * vq]) =
+              make_uint2((w0[w] >> 16) | (w1[w] & 0xffff0000u), (w2[w] >> 16) | (w3[w] & 0xffff0000u));
+        }
+      }
+      load_v(next);
+      // O^T (dims x heads) += V^T (dims x keys) P^T: lane (h16, q4) reads dimension
+      // 16 dblk + h16's keys 4 q4 .. + 3
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const s16x4_t av = __builtin_bit_cast(s16x4_t, *reinterpret_cast<const uint2*>(&vt[16 * d + h16][2 * q4]));
+        acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, phi, acc[d], 0, 0, 0);
+        acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, plo, acc[d], 0, 0, 0);
+      }
+    }
+    // the wavefronts' partials through LDS (the V^T tiles are done with), merged in
+    // wavefront order by the wavefront of each head
+    __syncthreads();
+    if (h16 < G) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+        *reinterpret_cast<f32x4_t*>(&L.u.merge.acc[wave][h16][16 * d + 4 * q4]) = acc[d];
+      if (q4 == 0) {
+        L.u.merge.ml[wave][h16][0] = Mw;
+        L.u.merge.ml[wave][h16][1] = Lw;
       }
     }
     __syncthreads();
-    if (start + kRing * kChunk < last) issue_k(kr[d], start + kRing * kChunk);
-    // q is re-read from LDS every chunk (an opaque zero offset keeps the compiler from
-    // holding a head's 16 q vectors in registers across the chunk loop)
-    int qoff = 0;
-    asm volatile("" : "+s"(qoff));
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int g = wave + 4 * r;
       if (g < G) {
-        const uint4* qv = reinterpret_cast<const uint4*>(L.qs[g]) + qoff;
-        float sc = -INFINITY;
-        if (lane < count) {
-          float dq = 0.0f;
+        float mx = -INFINITY;
 #pragma unroll
-          for (int jj = 0; jj < 16; ++jj) {
-            const uint4 qa = qv[jj], kk = L.kv[lane][jj];
-            dq = dot2(qa.x, kk.x, dq);
-            dq = dot2(qa.y, kk.y, dq);
-            dq = dot2(qa.z, kk.z, dq);
-            dq = dot2(qa.w, kk.w, dq);
-          }
-          sc = dq * S.scale;
+        for (int w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, L.u.merge.ml[w][g][0]);
+        float ls = 0.0f, c0 = 0.0f, c1 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+          const float e = expf(L.u.merge.ml[w][g][0] - mx);  // a wavefront without keys: 0
+          ls = fmaf(L.u.merge.ml[w][g][1], e, ls);
+          const float2 x = *reinterpret_cast<const float2*>(&L.u.merge.acc[w][g][2 * lane]);
+          c0 = fmaf(x.x, e, c0);
+          c1 = fmaf(x.y, e, c1);
         }
-        mc[r] = wave_max(sc);
-        const float p = lane < count ? expf(sc - mc[r]) : 0.0f;
-        lc[r] = wave_sum(p);
-        L.p[wave][r][lane] = p;
+        M[r] = mx;
+        Ls[r] = ls;
+        a0[r] = c0;
+        a1[r] = c1;
       }
     }
-    __syncthreads();  // the K readers are done: V takes the region
-    if (plain) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = tid + kThreads * i;
-        *reinterpret_cast<uint4*>(&vt[p >> 4][(p & 15) * 4]) = vr[d][i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = tid + kThreads * i;
-        const int row = p >> 4, col = p & 15;
-        // rows past the chunk's keys hold -0 (weight +0, so they add -0: no change)
-        const uint4 v = select4(start + row == newrow ? ~0u : 0u, vn4[col], vr[d][i]);
-        const uint32_t z = start + row < last ? 0u : kNegZeroPair, keep = start + row < last ? ~0u : 0u;
-        *reinterpret_cast<uint4*>(&vt[row][col * 4]) =
-            make_uint4((v.x & keep) | z, (v.y & keep) | z, (v.z & keep) | z, (v.w & keep) | z);
-      }
-    }
-    __syncthreads();
-    if (start + kRing * kChunk < last) issue_v(vr[d], start + kRing * kChunk);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int g = wave + 4 * r;
-      if (g < G) {
-        float c0 = 0.0f, c1 = 0.0f;
-#pragma unroll
-        for (int t = 0; t < kChunk; ++t) {  // t >= count: p = +0 times -0
-          const float pt = L.p[wave][r][t];
-          const uint32_t vd = vt[t][lane];
-          c0 = fmaf(pt, bf(vd & 0xffffu), c0);
-          c1 = fmaf(pt, bf(vd >> 16), c1);
-        }
-        const float mn = fmaxf(M[r], mc[r]);
-        const float eo = expf(M[r] - mn), ec = expf(mc[r] - mn);
-        Ls[r] = fmaf(Ls[r], eo, lc[r] * ec);
-        a0[r] = fmaf(a0[r], eo, c0 * ec);
-        a1[r] = fmaf(a1[r], eo, c1 * ec);
-        M[r] = mn;
-      }
-    }
-  }
   }
 
   if (used == 1) {
@@ -1113,10 +1153,10 @@ int32_t finish_program(imq_program* prog) {
   return ok();
 }
 
-// Attention splits: the per-kernel path's plan (attention_splits, common.h), so both
-// paths merge the same partials in the same order.
+// Attention splits: the per-kernel path's plan (attention_splits, common.h): a split's
+// chunks of 64 keys are shared by the workgroup's four wavefronts, 16 keys each.
 void attention_split(int B, int Hkv, int span, int* splits, int* cps) {
-  static_assert(kChunk == 64, "attention_splits counts 64-key chunks");
+  static_assert(kChunk == kAttnWaves * kUnit, "a chunk is one unit per wavefront");
   attention_splits(B, Hkv, span, splits, cps);
 }
 

@@ -178,19 +178,39 @@ def _fused_pair(torch, n, B, positions, slots, slots_n, hq=32, hkv=8, cap=700, m
     return (out_a, kp_a, vp_a), (out_b, kp_b, vp_b), fused, counters
 
 
+def _fused_against_oracle(a, b, positions, slots, slots_n, cap, hq=32, hkv=8):
+    """The fused call's KV pools equal the three-launch form's bit for bit, and its output
+    is within the attention bar of the oracle over the three-launch form's rotated q and
+    pools (zeros for an invalid request)."""
+    out_a, kp_a, vp_a = a
+    out_b, kp_b, vp_b = b
+    assert np.array_equal(bf16_bits(kp_a), bf16_bits(kp_b))
+    assert np.array_equal(bf16_bits(vp_a), bf16_bits(vp_b))
+    return _vals(out_b)
+
+
 @pytest.mark.parametrize("B,positions", [(1, [63]), (1, [64]), (1, [511]), (1, [699]),
                                          (3, [0, 127, 128]), (3, [64, 650, 5])])
-def test_attention_fused_equals_the_three_launch_form(env, B, positions):
-    """imq_attention_fused gives the bits of imq_qk_norm_rope + imq_attention_decode: the
-    attention output and both KV pools, with positions on both sides of the 64-key chunk
-    (split) boundaries, at the last row of the pools, and for three requests; a second call
-    (its split counters back at zero) repeats them."""
+def test_attention_fused_matches_the_oracle_and_writes_the_same_pools(env, B, positions):
+    """imq_attention_fused against imq_qk_norm_rope + imq_attention_decode: both KV pools
+    bit for bit, and the attention output within the attention bar of the oracle's
+    attention over the rotated q and the pools, with positions on both sides of the 64-key
+    chunk (split) boundaries, at the last row of the pools, and for three requests; a
+    second call (its split counters back at zero) repeats its bits."""
     torch, n, do, orc = env
-    announce("attention fused vs three launches", B, positions)
+    announce("attention fused vs oracle", B, positions)
     slots = list(RNG.permutation(B + 2)[:B].astype(int))
+    cap = 700
     a, b, fused, counters = _fused_pair(torch, n, B, positions, slots, B + 2, seed=B * 1000 + positions[0])
-    for x, y in zip(a, b):
-        assert np.array_equal(bf16_bits(x), bf16_bits(y))
+    got = _fused_against_oracle(a, b, positions, slots, B + 2, cap)
+    q_rot = _vals(fused_q_rot(torch, n, fused))
+    kp, vp = _vals(a[1]), _vals(a[2])
+    for r in range(B):
+        L = positions[r] + 1
+        ref = do.attention(q_rot[r].reshape(32, 128), kp[slots[r], :, :L], vp[slots[r], :, :L], 128 ** -0.5)
+        err = np.abs(got[r].reshape(32, 128) - ref)
+        bound = _ulp(ref) + 1e-5 * np.abs(vp[slots[r], :, :L]).max()
+        assert (err <= bound).all(), (r, (err - bound).max())
     assert not counters.any()
     first = bf16_bits(b[0]).copy()
     n.attention_fused(*fused)
@@ -198,19 +218,31 @@ def test_attention_fused_equals_the_three_launch_form(env, B, positions):
     assert np.array_equal(bf16_bits(b[0]), first)
 
 
+def fused_q_rot(torch, n, fused):
+    """The rotated q of the fused call's inputs, by imq_qk_norm_rope on fresh pools."""
+    q, k, v, qn, kn, pos, sl, kp, vp, out, max_len, theta, eps, ws, counters = fused
+    q_rot = torch.empty_like(q)
+    n.qk_norm_rope(q, k, v, qn, kn, pos, sl, q_rot, kp.clone(), vp.clone(), theta, eps)
+    torch.cuda.synchronize()
+    return q_rot
+
+
 def test_attention_fused_bad_requests(env):
     """A request with a slot outside the pools or a position at the capacity gets a zero
-    output and writes nothing, in both forms, and the valid request beside them keeps the
-    three-launch form's bits."""
+    output and writes nothing, in both forms, and the valid request beside them meets the
+    oracle's attention bar."""
     torch, n, do, orc = env
     announce("attention fused bad requests")
     cap = 96
-    a, b, _, _ = _fused_pair(torch, n, 3, [40, 10, cap], [1, 7, 0], 3, cap=cap, max_len=cap, seed=5)
-    for x, y in zip(a, b):
-        assert np.array_equal(bf16_bits(x), bf16_bits(y))
-    out = _vals(b[0])
+    a, b, fused, _ = _fused_pair(torch, n, 3, [40, 10, cap], [1, 7, 0], 3, cap=cap, max_len=cap, seed=5)
+    out = _fused_against_oracle(a, b, [40, 10, cap], [1, 7, 0], 3, cap)
     assert np.isfinite(out[0]).all() and out[0].any()
     assert not out[1].any() and not out[2].any()
+    q_rot = _vals(fused_q_rot(torch, n, fused))
+    kp, vp = _vals(a[1]), _vals(a[2])
+    ref = do.attention(q_rot[0].reshape(32, 128), kp[1, :, :41], vp[1, :, :41], 128 ** -0.5)
+    err = np.abs(out[0].reshape(32, 128) - ref)
+    assert (err <= _ulp(ref) + 1e-5 * np.abs(vp[1, :, :41]).max()).all(), err.max()
 
 
 def _attention_case(torch, n, do, B, hq, hkv, lengths, cap=600, slots_n=None, max_len=None):
