@@ -18,6 +18,19 @@ forward`; ironmule/dense_plan.py:337-371, `DensePlan.forward` and `_rope`):
         h = h + (silu(x @ Wg.T) * (x @ Wu.T)) @ Wd.T          (bf16 at each output)
     logits = rms_norm(h, norm) @ Whead.T                      (fp32)
 
+`gemma3_decode_step` restates the composition of the reference's paired step for its admitted
+architecture, Gemma 3 (ironmule/paired_research.py:177-215, over mlx-lm 0.31.3's
+`models/gemma3_text`, a dependency not in the reference tree): the embedding times
+bf16(sqrt(hidden)); per layer x = rms_norm(h) with weight 1 + w, q/k/v, q/k norm (1 + w),
+rotary with base 10^4 on sliding-window layers and 10^6 on global ones (every `pattern`-th
+layer is global), attention with scale query_pre_attn_scalar^-0.5 over the whole context
+(global) or the last `window` positions (sliding), h += rms_norm(o_proj(attn)) (1 + w; a
+plain add in bf16, the reference's clip_residual for bf16), the MLP gelu_tanh(gate) * up
+between a pre and a post RMSNorm, h += its output; a final RMSNorm (1 + w) and the tied head.
+It is pinned against transformers' Gemma3ForCausalLM (tests/test_decode_oracle_hf.py).
+Parity unpinned there: MLX's bf16 op-by-op rounding inside gelu_approx and rms_norm (this
+restatement rounds once per operation's output, as the GPU module form does).
+
 The "-> bf16" marks are where this build's GPU step rounds to bf16 (the projections'
 inputs and outputs are bf16, as in the reference's GPU plans); `round_bf16=False` drops
 them, giving the all-fp32 composition of the CPU plan.  Each helper names the reference
@@ -145,3 +158,96 @@ def decode_step(model: Model, keys: list, values: list, tokens, slots, positions
         h = h + r(act @ lay.wd.T)
     x = r(rms_norm(h, model.norm, model.eps))
     return x @ model.embed.T
+
+
+# ------------------------------------------------------------------ Gemma 3
+
+def gemma_norm(x: np.ndarray, weight: np.ndarray, eps: float, r=lambda a: np.asarray(a, np.float64)) -> np.ndarray:
+    """Gemma's RMSNorm: the weight is 1 + w (rounded by `r`, bf16 in the reference's
+    arithmetic), the rest as rms_norm."""
+    return rms_norm(x, r(1.0 + np.asarray(weight, np.float64)), eps)
+
+
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    """The tanh approximation of GELU (mlx's gelu_approx, transformers' gelu_pytorch_tanh)."""
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+@dataclass
+class Gemma3Layer:
+    """One Gemma 3 layer's dequantised weights (float64) and its six norm weights (w of
+    the 1 + w form)."""
+    wq: np.ndarray
+    wk: np.ndarray
+    wv: np.ndarray
+    wo: np.ndarray
+    wg: np.ndarray
+    wu: np.ndarray
+    wd: np.ndarray
+    input_norm: np.ndarray
+    post_attn_norm: np.ndarray
+    pre_ff_norm: np.ndarray
+    post_ff_norm: np.ndarray
+    q_norm: np.ndarray
+    k_norm: np.ndarray
+
+
+@dataclass
+class Gemma3Model:
+    layers: object       # an iterable of Gemma3Layer
+    embed: np.ndarray    # (vocab, hidden) dequantised, also the tied head
+    norm: np.ndarray
+    heads: int
+    kv_heads: int
+    head_dim: int
+    eps: float
+    theta_global: float
+    theta_local: float
+    window: int          # a sliding layer attends to positions pos - window + 1 .. pos
+    pattern: int         # layer i is global when i % pattern == pattern - 1
+    query_scalar: float  # attention scale query_scalar ** -0.5
+
+
+def gemma3_decode_step(model: Gemma3Model, keys: list, values: list, tokens, slots, positions,
+                       round_bf16: bool = True):
+    """One decode step of B requests through a Gemma 3 decoder; keys/values[layer] are
+    (slots, Hkv, C, D) float64 pools, updated in place at (slot, :, pos).  With round_bf16
+    every module output is rounded to bf16 (the residual stream included, as in the
+    reference's bf16 model); without, the all-float64 composition.  Returns float64 logits
+    (B, vocab)."""
+    r = bf16_round if round_bf16 else (lambda a: np.asarray(a, np.float64))
+    d = model.head_dim
+    tokens = np.asarray(tokens)
+    slots = np.asarray(slots)
+    positions = np.asarray(positions)
+    b = tokens.shape[0]
+    hidden = model.embed.shape[1]
+    h = r(r(model.embed[tokens]) * r(np.sqrt(float(hidden))))
+    scale = model.query_scalar ** -0.5
+    eps = model.eps
+    for i, lay in enumerate(model.layers):
+        is_global = i % model.pattern == model.pattern - 1
+        theta = model.theta_global if is_global else model.theta_local
+        x = r(gemma_norm(h, lay.input_norm, eps, r))
+        q = r(x @ lay.wq.T).reshape(b, model.heads, d)
+        k = r(x @ lay.wk.T).reshape(b, model.kv_heads, d)
+        v = r(x @ lay.wv.T).reshape(b, model.kv_heads, d)
+        q = r(rope(r(gemma_norm(q, lay.q_norm, eps, r)), positions, theta))
+        k = r(rope(r(gemma_norm(k, lay.k_norm, eps, r)), positions, theta))
+        outs = []
+        for row in range(b):
+            pos = int(positions[row])
+            keys[i][slots[row], :, pos] = k[row]
+            values[i][slots[row], :, pos] = v[row]
+            lo = 0 if is_global else max(0, pos - model.window + 1)
+            outs.append(r(attention(q[row], keys[i][slots[row], :, lo:pos + 1],
+                                    values[i][slots[row], :, lo:pos + 1], scale)))
+        o = np.stack(outs).reshape(b, model.heads * d)
+        h = r(h + r(gemma_norm(r(o @ lay.wo.T), lay.post_attn_norm, eps, r)))
+        x = r(gemma_norm(h, lay.pre_ff_norm, eps, r))
+        act = r(r(gelu_tanh(r(x @ lay.wg.T))) * r(x @ lay.wu.T))
+        h = r(h + r(gemma_norm(r(act @ lay.wd.T), lay.post_ff_norm, eps, r)))
+    x = r(gemma_norm(h, model.norm, eps, r))
+    return x @ model.embed.T
+

@@ -65,3 +65,37 @@ def logit_error(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+def oracle_gemma3(do, orc, weights):
+    """The decode oracle's Gemma3Model for a `gemma3.Gemma3Weights` on the GPU: every
+    projection and the tied embedding dequantised to float64 by the oracle (the layers one
+    at a time as the oracle walks them), norm weights widened from bf16."""
+    import numpy as np
+
+    def vals(t):
+        return t.float().cpu().numpy().astype(np.float64)
+
+    def deq(q):
+        w, s, b = (t.cpu() for t in q)
+        return orc.dequant_f32(w.numpy().view(np.uint32), s.view(torch.int16).numpy().view(np.uint16),
+                               b.view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+
+    def layer(L):
+        return do.Gemma3Layer(wq=deq(L["q"]), wk=deq(L["k"]), wv=deq(L["v"]), wo=deq(L["o"]),
+                              wg=deq(L["gate"]), wu=deq(L["up"]), wd=deq(L["down"]),
+                              input_norm=vals(L["input_norm"]), post_attn_norm=vals(L["post_attn_norm"]),
+                              pre_ff_norm=vals(L["pre_ff_norm"]), post_ff_norm=vals(L["post_ff_norm"]),
+                              q_norm=vals(L["q_norm"]), k_norm=vals(L["k_norm"]))
+
+    class _Layers:
+        def __iter__(self):
+            for L in weights.layers:
+                yield layer(L)
+
+    c = weights.config
+    return do.Gemma3Model(layers=_Layers(), embed=deq(weights.embed), norm=vals(weights.norm),
+                          heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim, eps=c.eps,
+                          theta_global=c.theta_global, theta_local=c.theta_local, window=c.window,
+                          pattern=c.pattern, query_scalar=c.query_scalar)
+
