@@ -465,12 +465,18 @@ constexpr int kUnit = 16;  // keys a wavefront takes at a time (the chunk's four
 // MFMA operand reads (16 lanes: 16 dimensions of one key quad) touch distinct banks.
 constexpr int kVtStride = 10;
 
-struct AttnLds {
+template <int W>
+struct AttnLdsT {
   union {
-    uint32_t vt[kAttnWaves][kD][kVtStride];  // per wavefront: V^T of its 16 keys, bf16 pairs of keys
     struct {
-      float acc[kAttnWaves][8][kD];  // per wavefront and query head: its chunks' weighted sum
-      float ml[kAttnWaves][8][2];    // and their (max, sum of exponentials)
+      uint32_t vt[W][kD][kVtStride];  // per wavefront: V^T of its 16 keys, bf16 pairs of keys
+      // per wavefront (the wide launch only): its 16 keys, 16-byte piece p of key r at
+      // r * 16 + (p ^ r)
+      uint4 ks[W > kAttnWaves ? W : 1][16 * 16];
+    } tile;
+    struct {
+      float acc[W][8][kD];  // per wavefront and query head: its chunks' weighted sum
+      float ml[W][8][2];    // and their (max, sum of exponentials)
     } merge;
   } u;
   uint32_t qs[8][kD / 2];  // rotated q of the task's heads, bf16 pairs
@@ -478,6 +484,7 @@ struct AttnLds {
   uint32_t vnew[kD / 2];
   int last;
 };
+using AttnLds = AttnLdsT<kAttnWaves>;
 
 // a if m is all ones, b if m is zero (a value select the compiler keeps in registers)
 __device__ __forceinline__ uint4 select4(uint32_t m, uint4 a, uint4 b) {
@@ -489,9 +496,10 @@ __device__ __forceinline__ uint16_t ld16_sc1(const uint16_t* base, uint32_t byte
   return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(base, bytes), off, 0, kSc1);
 }
 
-template <bool kStaged, typename SRef>
+template <bool kStaged, typename SRef, int W = kAttnWaves>
 __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs& a, uint4* smem) {
-  AttnLds& L = *reinterpret_cast<AttnLds*>(smem);
+  AttnLdsT<W>& L = *reinterpret_cast<AttnLdsT<W>*>(smem);
+  constexpr int kRounds = (8 + W - 1) / W;  // query heads (at most 8) per wavefront
   const int splits = S.splits, Hkv = S.Hkv, Hq = S.Hq, G = Hq / Hkv;
   const int s = task % splits, kvh = (task / splits) % Hkv, b = task / (splits * Hkv);
   const int tid = task_tid(), wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -510,32 +518,39 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   const int writer = write_ok ? min(pos / span, splits - 1) : -1;
   const size_t base = (((size_t)(slot_ok ? slot : 0) * Hkv + kvh) * S.capacity) * kD;
 
-  // This wavefront's keys: units of 16, units wave, wave + kAttnWaves, ... of the split's
-  // keys [first, last) (so the workgroup's four wavefronts share each 64-key chunk).  K goes
-  // from memory straight into registers in the A-operand layout of v_mfma_f32_16x16x32_bf16
-  // (lane (key h16 = lane % 16, quarter q4 = lane / 16): 16 bytes, dimensions 32 j + 8 q4
-  // .. + 8 of k-step j); V as 16-byte pieces (lane (key quad lane % 4, dimension group
-  // lane / 4)) that the wavefront transposes through its LDS tile.  Rows at or past `last`
-  // read row last - 1 (their scores are masked), a unit at or past `last` reads past the
-  // buffer (zeros, no traffic).
+  // This wavefront's keys: units of 16, units wave, wave + W, ... of the split's keys
+  // [first, last).  K ends up in the A-operand layout of v_mfma_f32_16x16x32_bf16 (lane
+  // (key h16 = lane % 16, quarter q4 = lane / 16): dimensions 32 j + 8 q4 .. + 8 of k-step
+  // j), V in the wavefront's transposed LDS tile, read as 16-byte pieces of whole 256-byte
+  // rows (lane (key quad vq = lane % 4, dimension group vg = lane / 4); load kk takes keys
+  // 4 vq + kk).  The wide launch reads K the same way and re-lays it through the
+  // wavefront's swizzled LDS tile: loading it straight in the operand layout reads half a
+  // cache line per row and load, which measured slower when the CU's load path is full
+  // (batch 32), while the tile's LDS round trip measured slower at batch 1.  Both are
+  // streamed with the non-temporal policy: every key is read once per launch.  Rows at or
+  // past `last` read row last - 1 (their scores are masked), a unit at or past `last`
+  // reads past the buffer (zeros, no traffic).
+  constexpr bool kRowK = W > kAttnWaves;
   const uint32_t pool_bytes = (uint32_t)(((size_t)(slot_ok ? slot : 0) * Hkv + kvh + 1) * S.capacity * kD * 2);
   const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(S.k_pool, pool_bytes);
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(S.v_pool, pool_bytes);
   const int h16 = lane & 15, q4 = lane >> 4;  // MFMA coordinates: row / column, k quarter
-  const int vq = lane & 3, vg = lane >> 2;    // V pieces: key quad, dimension group
+  const int vq = lane & 3, vg = lane >> 2;    // K and V pieces: key quad, dimension group
   auto row_bytes = [&](int key) __attribute__((always_inline)) -> uint32_t {
     return (uint32_t)((base + (size_t)(key < last ? key : last - 1) * kD) * 2);
   };
-  uint4 kr[4], vr[4];  // K [k-step]; V [key of the quad]
+  uint4 kr[4], vr[4];  // K [key of the quad] (kRowK) or [k-step]; V [key of the quad]
   auto load_k = [&](int start) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      kr[j] = load_b128(krs, start < last ? row_bytes(start + h16) + 64u * j + 16u * q4 : kPastBuffer);
+    for (int kk = 0; kk < 4; ++kk)
+      kr[kk] = load_b128_nt(krs, start >= last ? kPastBuffer
+                                 : kRowK ? row_bytes(start + 4 * vq + kk) + 16u * vg
+                                         : row_bytes(start + h16) + 64u * kk + 16u * q4);
   };
   auto load_v = [&](int start) __attribute__((always_inline)) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      vr[kk] = load_b128(vrs, start < last ? row_bytes(start + 4 * vq + kk) + 16u * vg : kPastBuffer);
+      vr[kk] = load_b128_nt(vrs, start < last ? row_bytes(start + 4 * vq + kk) + 16u * vg : kPastBuffer);
   };
   const int start0 = first + kUnit * wave;
 
@@ -557,7 +572,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     return kStaged ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p, bytes), off, 0, 0)
                    : (uint32_t)ld16_sc1(p, bytes, off);
   };
-  uint32_t qx[2][2], kx[2] = {0u, 0u}, vx[2] = {0u, 0u};
+  uint32_t qx[kRounds][2], kx[2] = {0u, 0u}, vx[2] = {0u, 0u};
   if (kStaged && S.qkv != nullptr) {
     // the planes of element `elem` of problem `pi` (width nw) for request b, added in plane
     // order from zero and rounded to bf16: every plane's load issued before the first add
@@ -578,8 +593,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     };
     const int nq = Hq * kD, nkv = Hkv * kD;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int g = wave + 4 * r;
+    for (int r = 0; r < kRounds; ++r) {
+      const int g = wave + W * r;
       const int e0 = (kvh * G + (g < G ? g : 0)) * kD;
       qx[r][0] = g < G ? planes(0, nq, e0 + lane) : 0u;
       qx[r][1] = g < G ? planes(0, nq, e0 + lane + 64) : 0u;
@@ -592,8 +607,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     }
   } else {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int g = wave + 4 * r;
+    for (int r = 0; r < kRounds; ++r) {
+      const int g = wave + W * r;
       const uint32_t off = (uint32_t)((b * Hq + kvh * G + (g < G ? g : 0)) * kD) * 2u;
       qx[r][0] = g < G ? ld16(S.q, qbytes, off + 2u * lane) : 0u;
       qx[r][1] = g < G ? ld16(S.q, qbytes, off + 2u * (lane + 64)) : 0u;
@@ -626,8 +641,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     dst[lane + 64] = to_bf(r1);
   };
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int g = wave + 4 * r;
+  for (int r = 0; r < kRounds; ++r) {
+    const int g = wave + W * r;
     if (g < G) rotate(qx[r][0], qx[r][1], qn0, qn1, reinterpret_cast<uint16_t*>(L.qs[g]));
   }
   if (wave == 0) {
@@ -652,8 +667,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   if (first >= last) {
     if (used == 0 && s == 0) {  // nothing to attend to: zeros
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int g = wave + 4 * r;
+      for (int r = 0; r < kRounds; ++r) {
+        const int g = wave + W * r;
         if (g < G)
           store_b32_sc1(buffer_rsrc(out, out_bytes),
                         (uint32_t)((b * Hq + kvh * G + g) * kD + 2 * lane) * 2u, 0u);
@@ -662,8 +677,9 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     return true;
   }
 
-  float M[2] = {-INFINITY, -INFINITY}, Ls[2] = {0.0f, 0.0f};
-  float a0[2] = {0.0f, 0.0f}, a1[2] = {0.0f, 0.0f};
+  float M[kRounds], Ls[kRounds], a0[kRounds], a1[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) M[r] = -INFINITY, Ls[r] = a0[r] = a1[r] = 0.0f;
   {
     // q^T as the B operand: lane (head h16, quarter q4) holds dimensions 32 j + 8 q4 .. + 8
     // of head h16 for k-step j (zeros for the columns past the task's G heads)
@@ -674,27 +690,43 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
                                                    : make_uint4(0u, 0u, 0u, 0u));
     const uint4* kn4 = reinterpret_cast<const uint4*>(L.knew);
     const uint4* vn4 = reinterpret_cast<const uint4*>(L.vnew);
-    uint32_t(*vt)[kVtStride] = L.u.vt[wave];
+    uint32_t(*vt)[kVtStride] = L.u.tile.vt[wave];
+    uint4* ks = L.u.tile.ks[kRowK ? wave : 0];
     // lane (h16, q4) carries head h16's running max and sum (the same in its four quarters)
     // and acc[dblk][i] = its weighted sum for dimension 16 dblk + 4 q4 + i
     float Mw = -INFINITY, Lw = 0.0f;
     f32x4_t acc[8];
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int start = start0; start < last; start += kAttnWaves * kUnit) {
-      const int next = start + kAttnWaves * kUnit;
+    for (int start = start0; start < last; start += W * kUnit) {
+      const int next = start + W * kUnit;
       // the unit that holds the new key: its row takes the rotated key (and below, the
       // value) from LDS
       const bool has_new = newrow >= start && newrow < start + kUnit;  // uniform
+      // K (through the tile: key r = 4 vq + kk, piece vg in; key h16, piece 4 j + q4 out;
+      // the 16 lanes of each quarter wavefront touch 16 distinct 16-byte bank groups)
+      uint4 ka[4];
+      if constexpr (kRowK) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int r = 4 * vq + kk;
+          ks[r * 16 + (vg ^ r)] = kr[kk];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ka[j] = ks[h16 * 16 + ((4 * j + q4) ^ h16)];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ka[j] = kr[j];
+      }
       if (has_new) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) kr[j] = select4(start + h16 == newrow ? ~0u : 0u, kn4[4 * j + q4], kr[j]);
+        for (int j = 0; j < 4; ++j) ka[j] = select4(start + h16 == newrow ? ~0u : 0u, kn4[4 * j + q4], ka[j]);
       }
       // scores: S^T (16 keys x heads) = K (keys x 128) q^T
       f32x4_t sc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[j]), qb[j], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[j]), qb[j], sc, 0, 0, 0);
       load_k(next);
       // online softmax: lane (h16, q4) holds head h16's scores of keys start + 4 q4 + i
       float mloc = -INFINITY;
@@ -775,15 +807,15 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int g = wave + 4 * r;
+    for (int r = 0; r < kRounds; ++r) {
+      const int g = wave + W * r;
       if (g < G) {
         float mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, L.u.merge.ml[w][g][0]);
+        for (int w = 0; w < W; ++w) mx = fmaxf(mx, L.u.merge.ml[w][g][0]);
         float ls = 0.0f, c0 = 0.0f, c1 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
           const float e = expf(L.u.merge.ml[w][g][0] - mx);  // a wavefront without keys: 0
           ls = fmaf(L.u.merge.ml[w][g][1], e, ls);
           const float2 x = *reinterpret_cast<const float2*>(&L.u.merge.acc[w][g][2 * lane]);
@@ -803,8 +835,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
     // L = fma(l, 1, 0) (exp(0) = 1), so it is written here with the same bits and no
     // partial round trip
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int g = wave + 4 * r;
+    for (int r = 0; r < kRounds; ++r) {
+      const int g = wave + W * r;
       if (g < G) {
         const float lx = Ls[r] + 0.0f;
         const uint32_t o = (uint32_t)to_bf((a0[r] + 0.0f) / lx) | ((uint32_t)to_bf((a1[r] + 0.0f) / lx) << 16);
@@ -819,8 +851,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(S.part, part_bytes);
   const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(S.ml, ml_bytes);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int g = wave + 4 * r;
+  for (int r = 0; r < kRounds; ++r) {
+    const int g = wave + W * r;
     if (g < G) {
       const uint32_t po = (uint32_t)((b * Hq + kvh * G + g) * splits + s);
       store_b32_sc1(prs, (po * kD + 2 * lane) * 4u, __float_as_uint(a0[r]));
@@ -841,8 +873,8 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   // every split has arrived: the counter is ready for the next launch
   if (tid == 0) st_sc1(S.combine + b * Hkv + kvh, 0u);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int g = wave + 4 * r;
+  for (int r = 0; r < kRounds; ++r) {
+    const int g = wave + W * r;
     if (g < G) {
       const int hh = kvh * G + g;
       const uint32_t p0 = (uint32_t)((b * Hq + hh) * splits);
@@ -973,9 +1005,10 @@ __global__ __launch_bounds__(kThreads) void qmv_stage_kernel(const Stage S, Step
   qmv_task<NCH, XR, XSRC, EPI, true, const Stage&>(S, blockIdx.x, a, smem);
 }
 
-__global__ __launch_bounds__(kThreads) void attention_stage_kernel(const Stage S, StepArgs a) {
+template <int W>
+__global__ __launch_bounds__(64 * W) void attention_stage_kernel(const Stage S, StepArgs a) {
   extern __shared__ uint4 smem[];
-  attention_task<true, const Stage&>(S, blockIdx.x, a, smem);
+  attention_task<true, const Stage&, W>(S, blockIdx.x, a, smem);
 }
 
 #undef IMQ_QMV_SHAPES_X2
@@ -1160,6 +1193,39 @@ void attention_split(int B, int Hkv, int span, int* splits, int* cps) {
   attention_splits(B, Hkv, span, splits, cps);
 }
 
+#ifndef IMQ_ATTN_WIDE_WAVES
+#define IMQ_ATTN_WIDE_WAVES 12
+#endif
+#ifndef IMQ_ATTN_WIDE_PAIRS
+#define IMQ_ATTN_WIDE_PAIRS 128
+#endif
+#ifndef IMQ_ATTN_WIDE_WORKGROUPS
+#define IMQ_ATTN_WIDE_WORKGROUPS 256
+#endif
+constexpr int kWideWaves = IMQ_ATTN_WIDE_WAVES;
+
+// The wide plan: with enough (request, KV head) pairs to fill the CUs by themselves, a
+// workgroup of kWideWaves wavefronts takes a split of at least one unit per wavefront, and
+// the splits target one workgroup per CU.  Never more splits than attention_split's plan,
+// so its workspace size holds.
+bool attention_wide_split(int B, int Hkv, int span, int* splits, int* cps) {
+  const int pairs = B * Hkv;
+  if (pairs < IMQ_ATTN_WIDE_PAIRS) return false;
+  const int chunks = (span + kChunk - 1) / kChunk;
+  const int min_c = (kWideWaves * kUnit + kChunk - 1) / kChunk;
+  int sp = (IMQ_ATTN_WIDE_WORKGROUPS + pairs - 1) / pairs;
+  sp = sp < chunks ? sp : chunks;
+  sp = sp > 1 ? sp : 1;
+  int c = (chunks + sp - 1) / sp;
+  c = c > min_c ? c : min_c;
+  c = c < chunks ? c : chunks;
+  *cps = c;
+  *splits = (chunks + c - 1) / c;
+  int base_splits, base_cps;
+  attention_split(B, Hkv, span, &base_splits, &base_cps);
+  return *splits <= base_splits;
+}
+
 int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* planes,
                         int64_t pstride, int32_t nplanes,
                             const uint16_t* q_norm, const uint16_t* k_norm,
@@ -1190,7 +1256,8 @@ int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
   if (!current_device(&code)) return code;
   const int span = std::min(max_len, capacity);
   int splits, cps;
-  attention_split(B, Hkv, span, &splits, &cps);
+  const bool wide = attention_wide_split(B, Hkv, span, &splits, &cps);
+  if (!wide) attention_split(B, Hkv, span, &splits, &cps);
   Stage A;
   memset(&A, 0, sizeof(A));
   A.kind = kKindAttention;
@@ -1227,9 +1294,20 @@ int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
   memset(&a, 0, sizeof(a));
   a.ntasks = A.count;
   a.staged = 1;
-  const size_t lds = (sizeof(AttnLds) + 15) & ~(size_t)15;
-  hipLaunchKernelGGL(attention_stage_kernel, dim3(A.count), dim3(kThreads), lds,
-                     static_cast<hipStream_t>(stream), A, a);
+  if (wide) {
+    const size_t lds = (sizeof(AttnLdsT<kWideWaves>) + 15) & ~(size_t)15;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(attention_stage_kernel<kWideWaves>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess)
+      return fail(IMQ_ELAUNCH, std::string("fused attention LDS size: ") + hipGetErrorString(attr));
+    hipLaunchKernelGGL(attention_stage_kernel<kWideWaves>, dim3(A.count), dim3(64 * kWideWaves), lds,
+                       static_cast<hipStream_t>(stream), A, a);
+  } else {
+    const size_t lds = (sizeof(AttnLds) + 15) & ~(size_t)15;
+    hipLaunchKernelGGL(attention_stage_kernel<kAttnWaves>, dim3(A.count), dim3(kThreads), lds,
+                       static_cast<hipStream_t>(stream), A, a);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused attention launch: ") + hipGetErrorString(e));
   return ok();
@@ -1492,7 +1570,7 @@ int32_t imq_program_launch_staged(imq_program* p, void* stream) {
     const dim3 grid(S.count), block(kThreads);
     const size_t lds = p->stage_lds[i];
     if (S.kind == kKindAttention) {
-      hipLaunchKernelGGL(attention_stage_kernel, grid, block, lds, st, S, a);
+      hipLaunchKernelGGL(attention_stage_kernel<kAttnWaves>, grid, block, lds, st, S, a);
       continue;
     }
 #define IMQ_STAGE_CASE(NCH, XR, XSRC, EPI, SHAPE)                                              \

@@ -189,14 +189,24 @@ def _fused_against_oracle(a, b, positions, slots, slots_n, cap, hq=32, hkv=8):
     return _vals(out_b)
 
 
+# 16 and 32 requests over 8 KV heads take the wide plan (16 wavefronts per workgroup; two
+# splits per request at 16, one at 32): positions at the 16-key unit, 64-key chunk and
+# 256-key wavefront-round boundaries and at the last row of the pools
+WIDE_16 = [699, 0, 255, 256, 64, 383, 384, 511, 512, 17, 640, 641, 320, 321, 5, 698]
+WIDE_32 = [0, 1, 15, 16, 63, 64, 65, 127, 128, 191, 192, 255, 256, 257, 300, 383, 384, 447,
+           448, 511, 512, 513, 575, 576, 600, 639, 640, 650, 690, 698, 699, 100]
+
+
 @pytest.mark.parametrize("B,positions", [(1, [63]), (1, [64]), (1, [511]), (1, [699]),
-                                         (3, [0, 127, 128]), (3, [64, 650, 5])])
+                                         (3, [0, 127, 128]), (3, [64, 650, 5]),
+                                         (16, WIDE_16), (32, WIDE_32)])
 def test_attention_fused_matches_the_oracle_and_writes_the_same_pools(env, B, positions):
     """imq_attention_fused against imq_qk_norm_rope + imq_attention_decode: both KV pools
     bit for bit, and the attention output within the attention bar of the oracle's
     attention over the rotated q and the pools, with positions on both sides of the 64-key
-    chunk (split) boundaries, at the last row of the pools, and for three requests; a
-    second call (its split counters back at zero) repeats its bits."""
+    chunk (split) boundaries, at the last row of the pools, for three requests, and for 16
+    and 32 requests (the wide plan); a second call (its split counters back at zero)
+    repeats its bits."""
     torch, n, do, orc = env
     announce("attention fused vs oracle", B, positions)
     slots = list(RNG.permutation(B + 2)[:B].astype(int))
