@@ -349,9 +349,11 @@ def test_decode_step_matches_oracle(env, batch):
     cfg = _tiny()
     weights = random_weights(cfg, "cuda", seed=5)
     state = DecodeState(cfg, batch=batch, slots=max(4, batch), capacity=80, max_len=80, device="cuda")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1000 + batch)
     for kp, vp in zip(state.k_pool, state.v_pool):  # a synthetic context in every slot
-        kp.copy_(torch.randn(kp.shape, device="cuda").to(torch.bfloat16))
-        vp.copy_(torch.randn(vp.shape, device="cuda").to(torch.bfloat16))
+        kp.copy_(torch.randn(kp.shape, device="cuda", generator=gen).to(torch.bfloat16))
+        vp.copy_(torch.randn(vp.shape, device="cuda", generator=gen).to(torch.bfloat16))
     keys = [_vals(kp) for kp in state.k_pool]
     values = [_vals(vp) for vp in state.v_pool]
     model = _oracle_model(torch, do, orc, weights)
@@ -366,8 +368,12 @@ def test_decode_step_matches_oracle(env, batch):
         got = logits.cpu().numpy().astype(np.float64)
         rel = np.abs(got - ref).max() / np.abs(ref).max()
         print(f"[observed] small decoder batch {batch} step {step}: max|dlogit|/max|logit| = {rel:.3e}", flush=True)
-        # observed 8.6e-8 (batch 3, RMSNorm launches), 2.2e-4 (batch 6, folded RMSNorms)
-        assert rel <= (2e-7 if batch < FUSED_NORM_ROWS else 5e-4), (step, rel)
+        # observed 8.1e-8 (batch 3, RMSNorm launches) and 2.2e-4 (batch 6, folded RMSNorms);
+        # one bf16 rounding of an intermediate (q, the attention output, SiLU * up) that
+        # lands on the other side of a tie moves the logits by about 3e-5 of their maximum
+        # (observed 2.9e-5 at batch 3 on other key and value draws), which the batch-3 bar
+        # admits
+        assert rel <= (1e-4 if batch < FUSED_NORM_ROWS else 5e-4), (step, rel)
         for i in range(cfg.layers):
             for r in range(batch):
                 kg = _vals(state.k_pool[i])[slots[r], :, positions[r]]

@@ -134,7 +134,7 @@ def test_decode_program_matches_decode_step_tiny(env, staged):
 
 def test_decode_program_tiny_against_the_oracle(env):
     """The persistent logits against the float64 decode oracle with the same rounding
-    points (the bar of test_decode_gpu.py's step test)."""
+    points (the bar of test_decode_gpu.py's step test at batch 3)."""
     torch, n, orc = env
     from ironmule_amd.decode import DecodeState, PersistentDecode, random_weights
     from oracle import decode_oracle as do
@@ -143,9 +143,11 @@ def test_decode_program_tiny_against_the_oracle(env):
     cfg = _tiny()
     weights = random_weights(cfg, "cuda", seed=6)
     state = DecodeState(cfg, batch=1, slots=2, capacity=70, max_len=70, device="cuda")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1006)
     for kp, vp in zip(state.k_pool, state.v_pool):
-        kp.copy_(torch.randn(kp.shape, device="cuda").to(torch.bfloat16))
-        vp.copy_(torch.randn(vp.shape, device="cuda").to(torch.bfloat16))
+        kp.copy_(torch.randn(kp.shape, device="cuda", generator=gen).to(torch.bfloat16))
+        vp.copy_(torch.randn(vp.shape, device="cuda", generator=gen).to(torch.bfloat16))
     keys = [_vals(kp) for kp in state.k_pool]
     values = [_vals(vp) for vp in state.v_pool]
     model = _oracle_model(torch, do, orc, weights)
@@ -158,7 +160,9 @@ def test_decode_program_tiny_against_the_oracle(env):
         ref = do.decode_step(model, keys, values, [tok], [slot], [pos], round_bf16=True)
         rel = np.abs(got - ref).max() / np.abs(ref).max()
         print(f"[observed] persistent decode step {step}: max|dlogit|/max|logit| = {rel:.3e}", flush=True)
-        assert rel <= 2e-7, (step, rel)  # observed 6.0e-8
+        # observed 6.0e-8; one bf16 rounding of an intermediate on the other side of a tie
+        # moves the logits by about 3e-5 of their maximum (the step test's bar)
+        assert rel <= 1e-4, (step, rel)
         tok, pos = int(np.argmax(got[0])), pos + 1
 
 
