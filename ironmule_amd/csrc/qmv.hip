@@ -1000,25 +1000,44 @@ __global__ __launch_bounds__(kThreads) void qmv_mma_staged_kernel(LaunchArgs a, 
     uint4 w[kWP];
     u32x2_t sb;
   };
+  // Each piece's offset at stage 0 is computed once; stage st adds its bytes as the loads'
+  // scalar offset, and a piece whose group lies past its K-range gets the past-the-buffer
+  // bit (the groups of a stage past the range are the same for every piece of a K-range
+  // with the same group slot, so one compare per slot and stage).
+  uint32_t xoff[kXP], woff[kWP];
+#pragma unroll
+  for (int i = 0; i < kXP; ++i) {
+    const int k = i / kXPK, m = (tid >> 5) + 8 * (i % kXPK);
+    xoff[i] = (uint32_t)(m < M ? m : M - 1) * ldx2 + 16u * (xp & 7) + 128u * (uint32_t)(klo[k] + (xp >> 3));
+  }
+#pragma unroll
+  for (int i = 0; i < kWP; ++i) {
+    const int slot = (tid >> 3) + 32 * i, k = slot / kRows;
+    woff[i] = (uint32_t)slot_row(slot % kRows) * (uint32_t)W * 4u + 16u * (wp & 1) +
+              32u * (uint32_t)(klo[k] + (wp >> 1));
+  }
   uint4 xreg[kXP];
   auto fetch_x = [&](int st) {
+    uint32_t past[kWK];
+#pragma unroll
+    for (int k = 0; k < kWK; ++k) past[k] = (xp >> 3) >= khi[k] - klo[k] - 4 * st ? kPastBuffer : 0u;
 #pragma unroll
     for (int i = 0; i < kXP; ++i) {
-      const int k = i / kXPK, m = (tid >> 5) + 8 * (i % kXPK);
-      const int g = klo[k] + (xp >> 3) + 4 * st;
-      const uint32_t off = (uint32_t)(m < M ? m : M - 1) * ldx2 + 16u * (xp & 7) + 128u * (uint32_t)g;
-      xreg[i] = load_b128(xrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, xoff[i] | past[i / kXPK], 512 * st, 0);
+      xreg[i] = make_uint4(v.x, v.y, v.z, v.w);
     }
   };
   auto fetch_w = [&](WRegs& R, int st) {
+    uint32_t past[kWK];
+#pragma unroll
+    for (int k = 0; k < kWK; ++k) past[k] = (wp >> 1) >= khi[k] - klo[k] - 4 * st ? kPastBuffer : 0u;
 #pragma unroll
     for (int i = 0; i < kWP; ++i) {
-      const int slot = (tid >> 3) + 32 * i, k = slot / kRows;
-      const int n = slot_row(slot % kRows);
-      const int g = klo[k] + (wp >> 1) + 4 * st;
-      const uint32_t off = (uint32_t)n * (uint32_t)W * 4u + 16u * (wp & 1) + 32u * (uint32_t)g;
+      const int k = ((tid >> 3) + 32 * i) / kRows;
       // slot % kRows < 32 exactly for even i: the weight is uniform per instruction
-      R.w[i] = load_b128_nt(PAIR && (i & 1) ? wrsrc_u : wrsrc, off | ((uint32_t)(g >= khi[k]) << 31));
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(PAIR && (i & 1) ? wrsrc_u : wrsrc,
+                                                              woff[i] | past[k], 128 * st, kNt);
+      R.w[i] = make_uint4(v.x, v.y, v.z, v.w);
     }
     const int g = klo[sb_k] + 4 * st;
     const uint32_t off = (sb_src + 2u * (uint32_t)g) | ((uint32_t)(g >= khi[sb_k]) << 31);
