@@ -353,7 +353,8 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
         stream = torch.cuda.Stream(device=device)
         # launches per step: the embedding, the layers, the final norm and the head; from
         # FUSED_NORM_ROWS requests the RMSNorms run inside the projections (five launches per
-        # layer and one more for the first layer's input norm), below it nine per layer
+        # layer and one more for the first layer's input norm), below it eight per layer
+        # (seven from 5 requests, where gate/up and SiLU * up are one launch)
         per_layer = 5 if b >= FUSED_NORM_ROWS else (7 if b >= 5 else 8)
         extra = 4 if b >= FUSED_NORM_ROWS else 3
         paths = {"per_kernel": (lambda: decode_step(weights, state, stream=stream),

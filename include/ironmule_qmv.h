@@ -188,7 +188,8 @@ IMQ_API size_t imq_qmv_gate_up_silu_norm_workspace(int32_t M, int32_t N, int32_t
  * imq_qmv_gate_up_silu on x' rows with the input RMSNorm folded in (`in` non-NULL):
  *   act[m][n] = bf16(silu(g) * u),  g = bf16(inv_m * sum_k x'[m][k] W_gate[n][k]),
  *                                   u = bf16(inv_m * sum_k x'[m][k] W_up[n][k]).
- * Same shapes and limits as imq_qmv_gate_up_silu.  With a workspace of
+ * Same shapes and limits as imq_qmv_gate_up_silu, except that any M from 1 to 32 is taken
+ * (the decode step folds its norms from 3 rows).  With a workspace of
  * imq_qmv_gate_up_silu_norm_workspace bytes (zero-filled before its first use and left
  * ready by every call; calls sharing one must not overlap) the last round's tiles are cut
  * into K-parts whose sums are added in part order; with none (NULL, 0 bytes) every tile is

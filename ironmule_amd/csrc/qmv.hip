@@ -3412,8 +3412,11 @@ int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint1
   if ((code = check_weights(w_up, s_up, b_up)) != IMQ_OK) return code;
   if ((code = check_rows(x, ldx, act, ld_act, M, N, K, IMQ_BF16)) != IMQ_OK) return code;
   if (in && (code = check_norm_in(in)) != IMQ_OK) return code;
-  if (M < 5 || K % 256 != 0)
-    return fail(IMQ_EUNSUPPORTED, "the fused gate/up launch takes 5 to 32 rows and K a multiple of 256");
+  // without the folded norm the launch keeps the bits of the grouped launch and silu_mul,
+  // whose plans take the few-row VALU kernel below 5 rows
+  if (M < (in ? 1 : 5) || K % 256 != 0)
+    return fail(IMQ_EUNSUPPORTED, in ? "the fused gate/up launch with the input norm takes K a multiple of 256"
+                                     : "the fused gate/up launch takes 5 to 32 rows and K a multiple of 256");
   if ((int64_t)N * (K / 2) >= ((int64_t)1 << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= ((int64_t)1 << 31))
     return fail(IMQ_EUNSUPPORTED, "a weight or activation of 2 GiB or more exceeds the kernel's offsets");
   const DeviceInfo* dev = current_device(&code);
@@ -3540,7 +3543,7 @@ int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate,
 }
 
 size_t imq_qmv_gate_up_silu_norm_workspace(int32_t M, int32_t N, int32_t K) {
-  if (M < 5 || M > IMQ_MAX_ROWS || N < 1 || K < 256 || K % 256) return 0;
+  if (M < 1 || M > IMQ_MAX_ROWS || N < 1 || K < 256 || K % 256) return 0;
   int32_t code;
   const DeviceInfo* dev = current_device(&code);
   if (!dev) return 0;

@@ -33,6 +33,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -1196,18 +1197,21 @@ void attention_split(int B, int Hkv, int span, int* splits, int* cps) {
 #ifndef IMQ_ATTN_WIDE_WAVES
 #define IMQ_ATTN_WIDE_WAVES 12
 #endif
+// From 64 (request, KV head) pairs (8 requests over 8 KV heads): at 8 requests the fused
+// launch took 12.0 us against 13.5 with 4 wavefronts per workgroup, at 4 requests 11.7
+// against 10.6.
 #ifndef IMQ_ATTN_WIDE_PAIRS
-#define IMQ_ATTN_WIDE_PAIRS 128
+#define IMQ_ATTN_WIDE_PAIRS 64
 #endif
 #ifndef IMQ_ATTN_WIDE_WORKGROUPS
 #define IMQ_ATTN_WIDE_WORKGROUPS 256
 #endif
 constexpr int kWideWaves = IMQ_ATTN_WIDE_WAVES;
 
-// The wide plan: with enough (request, KV head) pairs to fill the CUs by themselves, a
-// workgroup of kWideWaves wavefronts takes a split of at least one unit per wavefront, and
-// the splits target one workgroup per CU.  Never more splits than attention_split's plan,
-// so its workspace size holds.
+// The wide plan, from IMQ_ATTN_WIDE_PAIRS (request, KV head) pairs: a workgroup of
+// kWideWaves wavefronts takes a split of at least one unit per wavefront, and the splits
+// target one workgroup per CU.  Never more splits than attention_split's plan, so its
+// workspace size holds.
 bool attention_wide_split(int B, int Hkv, int span, int* splits, int* cps) {
   const int pairs = B * Hkv;
   if (pairs < IMQ_ATTN_WIDE_PAIRS) return false;
@@ -1254,6 +1258,9 @@ int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     return fail(IMQ_EUNSUPPORTED, "a KV pool of 2 GiB or more exceeds the attention's offsets");
   int32_t code;
   if (!current_device(&code)) return code;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= imq_rt::kMaxDevices)
+    return fail(IMQ_EUNAVAILABLE, "no current HIP device");
   const int span = std::min(max_len, capacity);
   int splits, cps;
   const bool wide = attention_wide_split(B, Hkv, span, &splits, &cps);
@@ -1296,11 +1303,16 @@ int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
   a.staged = 1;
   if (wide) {
     const size_t lds = (sizeof(AttnLdsT<kWideWaves>) + 15) & ~(size_t)15;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(attention_stage_kernel<kWideWaves>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (attr != hipSuccess)
-      return fail(IMQ_ELAUNCH, std::string("fused attention LDS size: ") + hipGetErrorString(attr));
+    // the launch's LDS is above the default dynamic limit: raised once per device
+    static std::atomic<bool> raised[imq_rt::kMaxDevices];
+    if (!raised[device].load(std::memory_order_acquire)) {
+      const hipError_t attr = hipFuncSetAttribute(
+          reinterpret_cast<const void*>(attention_stage_kernel<kWideWaves>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (attr != hipSuccess)
+        return fail(IMQ_ELAUNCH, std::string("fused attention LDS size: ") + hipGetErrorString(attr));
+      raised[device].store(true, std::memory_order_release);
+    }
     hipLaunchKernelGGL(attention_stage_kernel<kWideWaves>, dim3(A.count), dim3(64 * kWideWaves), lds,
                        static_cast<hipStream_t>(stream), A, a);
   } else {

@@ -126,8 +126,11 @@ def test_input_norm_matches_oracle(native, oracle, shapes, m, tiles):
         assert v.ok, v.detail
 
 
-@pytest.mark.parametrize("n,k,m", [(9728, 2560, 32), (9728, 2560, 5), (1000, 512, 9), (16416, 1024, 8)])
+@pytest.mark.parametrize("n,k,m", [(9728, 2560, 32), (9728, 2560, 5), (1000, 512, 9), (16416, 1024, 8),
+                                   (9728, 2560, 3), (1000, 512, 1)])
 def test_gate_up_norm_halves(native, oracle, n, k, m):
+    """With the input norm folded in the launch takes any M from 1 (the decode step folds
+    its norms from 3 requests); without it, from 5."""
     pg = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 2200 + m)
     pu = oracle.synthetic(n, k, m, seed=oracle.SEED_BASE + 2201 + m)
     pu = oracle.Problem(pu.w, pu.s, pu.b, pg.x, 0)
@@ -141,7 +144,14 @@ def test_gate_up_norm_halves(native, oracle, n, k, m):
                                      st, 0.0, split_tail=False)
     again = native.gate_up_silu_norm(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"),
                                      st, 0.0)
-    plain = native.gate_up_silu(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"))
+    if m >= 5:
+        plain = native.gate_up_silu(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"))
+    else:
+        with pytest.raises(native.NativeError):
+            native.gate_up_silu(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"))
+        plain = native.gate_up_silu_norm(gate, up, x, torch.empty((m, n), dtype=torch.bfloat16, device="cuda"),
+                                         _stats(native, m, 2560, 40, np.full((m, 40), 64.0, np.float32)),
+                                         0.0)  # inv = 1: no scaling
     torch.cuda.synchronize()
     assert torch.equal(out, again)  # the K-parts add in a fixed order
     # the tiles of whole rounds over the CUs are whole tiles either way: the same bits
@@ -149,7 +159,7 @@ def test_gate_up_norm_halves(native, oracle, n, k, m):
     tiles = -(-n // 32)
     cut = 32 * (tiles - tiles % cus) if tiles > cus else n
     assert torch.equal(out[:, :cut], whole[:, :cut])
-    if (n, k) == (9728, 2560):  # grouped launch on the staged kernel: the same row sums
+    if (n, k) == (9728, 2560) and m >= 5:  # grouped launch on the staged kernel: the same row sums
         g, u = native.qmv_grouped([gate, up], [x, x])
         ref = native.silu_mul((g.float() * 0.5).to(torch.bfloat16), (u.float() * 0.5).to(torch.bfloat16),
                               torch.empty_like(g))
