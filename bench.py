@@ -165,6 +165,74 @@ def _layer_stages(layers, xs, ys, index, chained=False):
     return stages
 
 
+STAGE_NAMES = ("q/k/v", "o", "gate/up", "down")
+
+
+def chain_trace(torch, native, device, layers_n=LAYERS, repeats=3):
+    """Where a chained streaming launch (the layer breakdown's `stream_chained`: the
+    decode-order stages of `layers_n` Qwen3-4B layers at batch 1, each waiting for the one
+    before it) spends its time, from the kernel's per-(stage, wavefront) stamps
+    (imq_stream_trace, a 100 MHz clock): for each stage kind, medians over the layers after
+    the first of
+      signal   a wavefront's last tile of the previous stage -> this stage's start (its
+               workgroup's barrier, the stores' acknowledgement and the counter add);
+      wait     start -> input ready (every workgroup of the previous stage counted);
+      x        input ready -> x staged in LDS (sc1 loads of the previous stage's output);
+      compute  x staged -> last tile done (the stage's tiles, dealt in turn);
+      tail     the stage's slowest wavefront done - its median wavefront done;
+      period   median input ready of this stage -> of the next stage."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(SEED + 1)
+    index = {name: i for i, (name, _, _) in enumerate(LAYER)}
+    layers = [[make_weight(torch, n, k, gen, device) for (_, n, k) in LAYER]
+              for _ in range(layers_n)]
+    xs = {k: make_x(torch, 1, k, gen, device) for k in {k for (_, _, k) in LAYER}}
+    xrow = {k: v.reshape(-1) for k, v in xs.items()}
+    stream = torch.cuda.Stream(device=device)
+    prog = native.stream_program(_layer_stages(layers, xrow, None, index, chained=True))
+    info = prog.info()
+    waves = info["workgroups"] * 12
+    nst = info["stages"]
+    buf = torch.zeros(nst * waves * 4, dtype=torch.int64, device=device)
+    for _ in range(20):
+        prog.launch(stream)
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(repeats):
+        buf.zero_()
+        prog.trace(buf)
+        prog.launch(stream)
+        torch.cuda.synchronize()
+        prog.trace(None)
+        if prog.failed():
+            raise SystemExit("the chained launch stopped on a bounded wait")
+        runs.append(buf.view(nst, waves, 4).cpu().numpy().astype("float64") * 0.01)  # us
+    import numpy as np
+    kinds = {name: {"signal": [], "wait": [], "x": [], "compute": [], "tail": [], "period": []}
+             for name in STAGE_NAMES}
+    launch_us = []
+    for t in runs:
+        launch_us.append(float(t[:, :, 3].max() - t[0, :, 0].min()))
+        for s in range(4, nst - 1):  # the layers after the first, up to the last stage
+            d = kinds[STAGE_NAMES[s % 4]]
+            d["signal"].append(float(np.median(t[s, :, 0] - t[s - 1, :, 3])))
+            d["wait"].append(float(np.median(t[s, :, 1] - t[s, :, 0])))
+            d["x"].append(float(np.median(t[s, :, 2] - t[s, :, 1])))
+            d["compute"].append(float(np.median(t[s, :, 3] - t[s, :, 2])))
+            d["tail"].append(float(t[s, :, 3].max() - np.median(t[s, :, 3])))
+            d["period"].append(float(np.median(t[s + 1, :, 1]) - np.median(t[s, :, 1])))
+    summary = {name: {k: round(float(np.median(v)), 2) for k, v in d.items()}
+               for name, d in kinds.items()}
+    per_layer = sum(v["period"] for v in summary.values())
+    prog.close()
+    del layers
+    torch.cuda.empty_cache()
+    return {"metric": "chained streaming launch, per-stage time (us, medians)",
+            "layers": layers_n, "workgroups": info["workgroups"], "stages": nst,
+            "launch_us": round(float(np.median(launch_us)), 1),
+            "per_layer_us": round(per_layer, 2), "by_stage": summary}
+
+
 def bench_layer(torch, native, steps, warmup, device, breakdown=True):
     """The headline: K steps of one layer's seven projections, rotating over 36 distinct
     layers, streamed by the streaming engine: one launch runs 36 layers' projections as
@@ -657,6 +725,9 @@ def main() -> None:
                     help="first run 1 GiB device copies (the yardstick for --pmc byte counters)")
     ap.add_argument("--profile-summary", nargs="+", default=None, metavar="DIR",
                     help="print a text summary of rocprofv3 CSV output under DIR... and exit")
+    ap.add_argument("--chain-trace", action="store_true",
+                    help="time the stages of the chained streaming launch from its per-stage "
+                         "stamps (imq_stream_trace) and exit")
     ap.add_argument("--only", default=None, metavar="N,K,M[,f32]",
                     help="time one qmv shape over rotating weights (>= 1 GiB) and exit; "
                          "a short program for profilers")
@@ -680,6 +751,9 @@ def main() -> None:
         raise SystemExit(f"unsupported device {arch!r}")
     if args.copy_calibration:
         copy_calibration(torch, device)
+    if args.chain_trace:
+        print(json.dumps(chain_trace(torch, _native, device)), flush=True)
+        return
     if args.decode_only:
         batches = tuple(int(b) for b in args.decode_batches.split(","))
         print(json.dumps({"metric": "decode tokens/s (profiling run)",

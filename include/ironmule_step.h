@@ -153,6 +153,14 @@ IMQ_API int32_t imq_stream_launch(imq_stream* program, void* stream);
  * wait (then clears the flag). */
 IMQ_API int32_t imq_stream_status(imq_stream* program, int32_t* failed);
 
+/* A diagnostic with no counterpart in the reference: later launches of a chained program
+ * record, per (stage s, wavefront v) at buffer[(s * V + v) * 4 ..], four s_memrealtime
+ * stamps (a 100 MHz clock): the stage's start (after the workgroup signalled the previous
+ * stage), its input ready (the wait for the previous stage done), its x staged in LDS and
+ * its last tile done.  V = workgroups * 12 (imq_stream_info); `words` >= stages * V * 4.  A
+ * NULL buffer stops the recording.  IMQ_EUNSUPPORTED for a program without waits. */
+IMQ_API int32_t imq_stream_trace(imq_stream* program, uint64_t* buffer, int64_t words);
+
 /* Tiles, stages, workgroups, LDS bytes per workgroup, and 1 if the stages are chained. */
 IMQ_API int32_t imq_stream_info(const imq_stream* program, int32_t* tiles, int32_t* stages,
                                 int32_t* workgroups, int32_t* lds_bytes, int32_t* chained);

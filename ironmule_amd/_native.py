@@ -162,6 +162,7 @@ _SIGNATURES = {
     "imq_stream_create": ([ctypes.POINTER(QmvStage), _I32, _I32, ctypes.POINTER(_P)], _I32),
     "imq_stream_launch": ([_P, _P], _I32),
     "imq_stream_status": ([_P, ctypes.POINTER(_I32)], _I32),
+    "imq_stream_trace": ([_P, _P, _I64], _I32),
     "imq_stream_info": ([_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32), ctypes.POINTER(_I32),
                          ctypes.POINTER(_I32), ctypes.POINTER(_I32)], _I32),
     "imq_stream_destroy": ([_P], None),
@@ -902,6 +903,7 @@ class StreamProgram:
     def __init__(self, handle: ctypes.c_void_p, keep: list) -> None:
         self._handle = handle
         self._keep = keep
+        self._trace = None
 
     @property
     def handle(self) -> ctypes.c_void_p:
@@ -927,6 +929,20 @@ class StreamProgram:
                        (v.value for v in vals)))
         out["chained"] = bool(out["chained"])
         return out
+
+    def trace(self, buffer: torch.Tensor | None) -> None:
+        """Chained programs: later launches record four stamps per (stage, wavefront) into
+        `buffer` (int64, stages * workgroups * 12 * 4 elements; imq_stream_trace), or stop
+        recording (None).  The program keeps a reference to the buffer."""
+        if buffer is None:
+            _check(lib().imq_stream_trace(self.handle, None, 0))
+            self._trace = None
+            return
+        _require(buffer, torch.int64, "trace buffer")
+        if not buffer.is_contiguous():
+            raise ValueError("the trace buffer must be contiguous")
+        _check(lib().imq_stream_trace(self.handle, _ptr(buffer), buffer.numel()))
+        self._trace = buffer
 
     def close(self) -> None:
         if self._handle is not None and _lib is not None:

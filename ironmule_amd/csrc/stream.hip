@@ -10,8 +10,8 @@
 // grid runs runs v, v + V, ...: the device streams one compact window of the weights, and
 // a wavefront resolves a problem's descriptors once per run, jumping to a run's problem
 // through a per-program run table.  For chained stages wavefront v runs tiles v, v + V,
-// ... of each stage (counted from the stage's first tile), so that every stage is spread
-// over the whole device.
+// ... of each stage (counted from the stage's first tile), v numbering the wavefronts
+// across the workgroups first, so that every stage is spread over the whole device.
 //
 // Pipelining.  A wavefront keeps two tiles in registers: while it computes one, the
 // loads of the next are in flight.  Loads are raw buffer loads issued unconditionally
@@ -130,6 +130,8 @@ struct SArgs {
   uint32_t* claim;          // independent stages: kShards claim counters, kLine words apart
   int32_t nstages, total, waves, sb_off;  // sb_off: LDS byte offset of the scale/bias areas
   int32_t nslots, pad;
+  // chained stages: per (stage, wavefront) four s_memrealtime stamps, or nullptr
+  uint64_t* trace;
   imq_runs::ShardPlan runs;  // independent stages: dealt and claimed runs, claim shards
   XSlot slot[kMaxSlots];
 };
@@ -548,13 +550,23 @@ __global__ __launch_bounds__(kThreads) void stream_chain_kernel(const SStage* __
   __shared__ int flag;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int v = blockIdx.x * kWaves + wave;
+  // wavefronts numbered across the workgroups first (wavefront w of workgroup b is w * grid
+  // + b), so that a stage of fewer tiles than wavefronts is spread over every CU rather
+  // than over the first workgroups' CUs
+  const int v = wave * (int)gridDim.x + (int)blockIdx.x;
   const int V = a.waves;
   uint32_t* sbw = reinterpret_cast<uint32_t*>(smem + a.sb_off) + kSbWords * wave;
   const uint32_t magic = in_vgpr(kMagic);
   const uint32_t groups = gridDim.x;
   Tile A, B;
 
+  // the optional trace: per (stage, wavefront) the stage's start (after signalling the
+  // previous one), its input ready, its x staged and its last tile done
+  uint64_t* const trace = uniform_ptr(a.trace);
+  uint64_t stamp[4];
+  auto mark = [&](int i) {
+    if (trace) stamp[i] = __builtin_amdgcn_s_memrealtime();
+  };
   for (int s = 0; s < a.nstages; ++s) {
     StageRef S = stage_at(st, s);
     if (s > 0 && stage_at(st, s - 1).signal) {  // this workgroup is done with stage s-1
@@ -564,6 +576,7 @@ __global__ __launch_bounds__(kThreads) void stream_chain_kernel(const SStage* __
         __hip_atomic_fetch_add(counter(a, s - 1, blockIdx.x % kSubs), 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
+    mark(0);
     const int first = S.first, end = S.first + S.tiles;
     // this wavefront's first tile of the stage: the smallest g >= first with g - first = v mod V
     int g = first + v;
@@ -574,8 +587,10 @@ __global__ __launch_bounds__(kThreads) void stream_chain_kernel(const SStage* __
     if (g + V < end) seek(st, ls, lp, lc, g + V);
     load_site(lc, g + V, g + V < end, lane, B);
     if (S.wait >= 0 && !wait_for(a, S.wait, groups, &flag)) return;
+    mark(1);
     stage_x(S.x, S.K, S.x_live != 0, smem + S.xoff, tid);
     lds_barrier();
+    mark(2);
     while (g < end) {
       seek(st, cs, cp, cc, g);
       compute_site(cc, g, lane, A, smem, sbw, magic);
@@ -588,6 +603,14 @@ __global__ __launch_bounds__(kThreads) void stream_chain_kernel(const SStage* __
       if (g + 2 * V < end) seek(st, ls, lp, lc, g + 2 * V);
       load_site(lc, g + 2 * V, g + 2 * V < end, lane, B);
       g += V;
+    }
+    if (trace) {
+      mark(3);
+      if (lane == 0) {
+        uint64_t* row = trace + ((size_t)s * V + v) * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) row[i] = stamp[i];
+      }
     }
   }
 }
@@ -849,6 +872,15 @@ int32_t imq_stream_status(imq_stream* p, int32_t* failed) {
   *failed = v != 0;
   if (v && hipMemset(p->d_words + p->counter_words, 0, 4) != hipSuccess)
     return fail(IMQ_ELAUNCH, "clearing the stream status failed");
+  return ok();
+}
+
+int32_t imq_stream_trace(imq_stream* p, uint64_t* buffer, int64_t words) {
+  if (!p) return fail(IMQ_EINVAL, "null program");
+  if (!p->chained) return fail(IMQ_EUNSUPPORTED, "only chained programs record a stage trace");
+  if (buffer && (!aligned(buffer, 8) || words < (int64_t)p->args.nstages * p->args.waves * 4))
+    return fail(IMQ_EINVAL, "the trace needs stages * workgroups * wavefronts * 4 8-byte-aligned words");
+  p->args.trace = buffer;
   return ok();
 }
 

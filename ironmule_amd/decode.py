@@ -187,8 +187,8 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
         n.add_rmsnorm(s.h, layer["input_norm"], s.x, c.eps, delta=delta, stream=stream)
         n.qmv_grouped([layer["q"], layer["k"], layer["v"]], [s.x, s.x, s.x],
                       outs=[s.q, s.k, s.v], stream=stream)
-        # one launch (the decode programs' attention stage, the same bits as qk_norm_rope
-        # followed by attention_decode)
+        # one launch (the decode programs' attention stage; the KV pools of qk_norm_rope
+        # followed by attention_decode, the output to the attention's oracle bar)
         n.attention_fused(s.q, s.k, s.v, layer["q_norm"], layer["k_norm"], s.positions,
                           s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len, c.theta,
                           c.eps, s.workspace, s.attn_counters, stream=stream)
