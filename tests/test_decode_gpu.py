@@ -257,6 +257,29 @@ def test_attention_fused_bad_requests(env):
     assert (err <= _ulp(ref) + 1e-5 * np.abs(vp[1, :, :41]).max()).all(), err.max()
 
 
+def test_attention_fused_bad_requests_wide_plan(env):
+    """The same at 8 requests (the 12-wavefront plan, splits of 192 keys): a slot outside
+    the pools and a position at the capacity give zeros and write nothing, a request at
+    position 0 attends to its new key alone, and the valid requests meet the oracle's
+    bar."""
+    torch, n, do, orc = env
+    announce("attention fused bad requests, wide plan")
+    cap = 700
+    positions = [40, 10, cap, 0, 699, 191, 384, 5]
+    slots = [1, 9, 0, 2, 3, 4, 5, 6]  # 9: past the 8 slots
+    a, b, fused, counters = _fused_pair(torch, n, 8, positions, slots, 8, seed=8)
+    out = _fused_against_oracle(a, b, positions, slots, 8, cap)
+    assert not out[1].any() and not out[2].any()
+    q_rot = _vals(fused_q_rot(torch, n, fused))
+    kp, vp = _vals(a[1]), _vals(a[2])
+    for r in (0, 3, 4, 5, 6, 7):
+        L = positions[r] + 1
+        ref = do.attention(q_rot[r].reshape(32, 128), kp[slots[r], :, :L], vp[slots[r], :, :L], 128 ** -0.5)
+        err = np.abs(out[r].reshape(32, 128) - ref)
+        assert (err <= _ulp(ref) + 1e-5 * np.abs(vp[slots[r], :, :L]).max()).all(), (r, err.max())
+    assert not counters.any()
+
+
 def _attention_case(torch, n, do, B, hq, hkv, lengths, cap=600, slots_n=None, max_len=None):
     slots_n = slots_n or B + 1
     kp, kpv = _bf16(torch, RNG.standard_normal((slots_n, hkv, cap, 128)))

@@ -12,6 +12,7 @@ replays, and the refusals.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 
 from tests.conftest import gpu_available
@@ -200,6 +201,52 @@ def test_chained_layers_replay_in_a_graph(env):
         assert not prog.failed(), rep
         _check_stages(torch, n, stages, rep)
     prog.close()
+
+
+def test_chained_stage_trace(env):
+    """imq_stream_trace: a traced launch of a chained program gives the same outputs as an
+    untraced one and, per (stage, wavefront), four stamps in order (start <= input ready <=
+    x staged <= done), every stage starting after the previous stage's first wavefront was
+    done; a buffer too small is refused, an independent program has no trace, and a NULL
+    buffer stops the recording."""
+    torch, n, orc = env
+    from ironmule_amd._native import NativeError
+    announce("stream chained trace")
+    x = _row(torch, 2560, 11)
+    wq = [_weight(orc, nn, 2560, 2400 + j) for j, nn in enumerate((4096, 1024))]
+    yq = [torch.empty(nn, dtype=torch.bfloat16, device="cuda") for nn in (4096, 1024)]
+    wo = [_weight(orc, 2560, 4096, 2410)]
+    yo = [torch.empty(2560, dtype=torch.bfloat16, device="cuda")]
+    wd = [_weight(orc, 64, 2560, 2420)]
+    yd = [torch.empty(64, dtype=torch.bfloat16, device="cuda")]
+    stages = [(wq, x, yq, False), (wo, yq[0], yo, True), (wd, yo[0], yd, True)]
+    prog = n.stream_program(stages, workgroups=5)
+    info = prog.info()
+    waves = info["workgroups"] * 12
+    with pytest.raises(NativeError):
+        prog.trace(torch.zeros(3 * waves * 4 - 1, dtype=torch.int64, device="cuda"))
+    buf = torch.zeros(3 * waves * 4, dtype=torch.int64, device="cuda")
+    prog.trace(buf)
+    prog.launch()
+    torch.cuda.synchronize()
+    assert not prog.failed()
+    _check_stages(torch, n, stages, 0)
+    t = buf.view(3, waves, 4).cpu().numpy()
+    assert (t > 0).all()
+    assert (np.diff(t, axis=2) >= 0).all()
+    for s in (1, 2):
+        assert t[s, :, 1].min() >= t[s - 1, :, 3].min()
+    prog.trace(None)
+    buf.zero_()
+    prog.launch()
+    torch.cuda.synchronize()
+    assert not buf.any()
+    _check_stages(torch, n, stages, 1)
+    prog.close()
+    ind = n.stream_program([([_weight(orc, 64, 2560, 2430)], x, [yd[0]], False)])
+    with pytest.raises(NativeError, match="chained"):
+        ind.trace(torch.zeros(1024, dtype=torch.int64, device="cuda"))
+    ind.close()
 
 
 def test_refusals(env):
