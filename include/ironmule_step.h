@@ -21,9 +21,10 @@
  *   * Every wait inside the kernel is bounded: if a stage does not complete in time (it
  *     cannot, unless the co-residency assumption is broken) the kernel stops and
  *     imq_program_status() reports it.
- *   * Results are bit-identical to the per-kernel path (imq_qmv / imq_qmv_grouped and the
- *     ironmule_decode.h kernels) on the same inputs: every stage uses the same arithmetic
- *     in the same order.
+ *   * A qmv program's results are bit-identical to the per-kernel path (imq_qmv /
+ *     imq_qmv_grouped) on the same inputs: every stage uses the same arithmetic in the
+ *     same order.  A decode program folds its RMSNorms into the projections (below); its
+ *     persistent and staged launches give each other's bits.
  *   * Return codes are the IMQ_* values of ironmule_qmv.h, with imq_last_error().
  */
 #ifndef IRONMULE_STEP_H
@@ -65,7 +66,12 @@ typedef struct {
  *              h += bf16(o Wo^T) ; x = rms_norm(h) ;
  *              h += bf16(bf16(silu(bf16(x Wg^T)) * bf16(x Wu^T)) Wd^T)
  *   logits = rms_norm(h) E^T (fp32)
- * with the same rounding points as the per-kernel path (ironmule_decode.h).  A request
+ * with the per-kernel path's rounding points (ironmule_decode.h) except that every
+ * RMSNorm but the first layer's input norm is folded into the projections around it: the
+ * o and down stages also write x' = bf16(h * w_next) and one sum of squares of the new h
+ * per tile, and the next stage computes inv * (x' W^T) with inv = 1 / rms(h) from those
+ * sums, rounding x before the scaling instead of after it (imq_qmv_norm's arithmetic at one
+ * row; logits within about 5e-4 of the unfolded step's, relative to their maximum).  A request
  * whose slot is outside [0, num_slots) or whose position is outside [0, capacity) gets
  * no KV write and zeros from attention.
  * Replaces DensePlan.forward's decode step (ironmule/dense_plan.py:337-363;

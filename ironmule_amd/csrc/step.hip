@@ -63,8 +63,14 @@ constexpr int kMaxHidden = 4096;  // the fused RMSNorm stages one row of h whole
 constexpr int kNormVpt = kMaxHidden / kThreads;
 
 enum : int32_t { kKindQmv = 0, kKindAttention = 1 };
-enum : int32_t { kXVector = 0, kXNorm = 1 };
-enum : int32_t { kEpiBf16 = 0, kEpiF32 = 1, kEpiResidual = 2, kEpiSiluPair = 3 };
+// x sources: a bf16 row; the RMSNorm of the fp32 row of h computed in the task; or x' =
+// bf16(h * w) with the rows' outputs scaled by 1/rms(h) from the producer's partial sums of
+// squares (the RMSNorm folded into the projections around it)
+enum : int32_t { kXVector = 0, kXNorm = 1, kXScaled = 2 };
+// epilogues: bf16 or fp32 y; h += bf16(y); SiLU(gate) * up; h += bf16(y) with the next
+// RMSNorm's x' = bf16(h * w_next) and the tile's sum of squares of h
+enum : int32_t { kEpiBf16 = 0, kEpiF32 = 1, kEpiResidual = 2, kEpiSiluPair = 3, kEpiResidualNorm = 4 };
+constexpr int kMaxNormParts = 4096;  // partial sums of squares a kXScaled stage reads
 // (chunks per lane, x pieces per thread) of the qmv tile instantiations
 enum : int32_t { kShape22 = 0, kShape52 = 1, kShape82 = 2, kShape55 = 3 };
 
@@ -81,12 +87,16 @@ struct QProb {
 struct Stage {
   int32_t kind, first, count, wait;  // wait: stage index, or -1
   int32_t wait_count, shape, xsrc, epi;
-  int32_t nprob, pad0, pad1, pad2a;
+  int32_t nprob, nssq, pad1, pad2a;  // nssq: kXScaled's partial sums of squares
   float eps, log2_theta, scale, pad2;
-  const uint16_t* x;       // bf16 activation row (kXVector)
-  float* h;                // residual stream (kXNorm source, kEpiResidual target)
+  const uint16_t* x;       // bf16 activation row (kXVector, kXScaled)
+  float* h;                // residual stream (kXNorm source, kEpiResidual(Norm) target)
   const uint16_t* norm_w;  // kXNorm weight
   uint16_t* act;           // kEpiSiluPair output
+  const float* ssq_in;         // kXScaled: the producer's per-tile sums of squares of h
+  float* ssq_out;              // kEpiResidualNorm: this stage's per-tile sums of squares
+  uint16_t* xn_out;            // kEpiResidualNorm: x' = bf16(h * norm_next)
+  const uint16_t* norm_next;   // kEpiResidualNorm: the next RMSNorm's weight
   QProb p[kMaxStageProblems];
   // attention
   const uint16_t* q;
@@ -207,7 +217,8 @@ struct QLds {
   static constexpr size_t kSx = kX + (size_t)4 * kChunks * 16;
   static constexpr size_t kSb = kSx + (size_t)kChunks * 4;
   static constexpr size_t kPair = kSb + (size_t)kSbr * kThreads * 8;  // 8 floats
-  static constexpr size_t kBytes = kPair + 8 * 4;
+  static constexpr size_t kRed = kPair + 8 * 4;  // the wavefronts' sums of squares (4 floats)
+  static constexpr size_t kBytes = kRed + 4 * 4;
 };
 
 // The fused RMSNorm holds the fp32 row of h at the start of LDS (it is consumed before
@@ -324,19 +335,32 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
   uint32_t* sbl = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(smem) + L::kSb);
   const uint32_t magic = in_vgpr(kMagic);
 
-  // the activation inputs: x, or the row of h and the norm weight; a residual stage also
-  // reads its rows of h (final once the input stage is done)
+  // the activation inputs: x, or the row of h and the norm weight (or x' and the partial
+  // sums of squares); a residual stage also reads its rows of h (final once the input
+  // stage is done) and, folding the next RMSNorm, that norm's weights of its rows
   const bool owner = j == 0 && row < N;
+  constexpr bool kScaled = XSRC == kXScaled;
+  constexpr bool kResNorm = EPI == kEpiResidualNorm;
   constexpr int HX = XSRC == kXNorm ? XR : 1;
-  uint4 xs[XR], h0[HX], h1[HX], wn[HX];
+  constexpr int NQ = kScaled ? kMaxNormParts / (4 * kThreads) : 1;
+  uint4 xs[XR], h0[HX], h1[HX], wn[HX], nq[NQ];
   float hres = 0.0f;
+  uint32_t wnext = 0u;
   auto load_inputs = [&]() {
     if constexpr (XSRC == kXNorm)
       load_h<XR, !kStaged>(S.h, K, tid, h0, h1);
     else
       load_x<XR, !kStaged>(S.x, K, tid, xs);
-    if constexpr (EPI == kEpiResidual) {
+    if constexpr (kScaled) {
+      const __amdgpu_buffer_rsrc_t qr = buffer_rsrc(S.ssq_in, (uint32_t)S.nssq * 4u);
+#pragma unroll
+      for (int t = 0; t < NQ; ++t) nq[t] = load_act<!kStaged>(qr, 16u * (tid + kThreads * t));
+    }
+    if constexpr (EPI == kEpiResidual || kResNorm) {
       if (owner) hres = kStaged ? S.h[row] : ldf_sc1(S.h + row);
+    }
+    if constexpr (kResNorm) {
+      if (owner) wnext = S.norm_next[row];
     }
   };
   auto load_norm_weight = [&]() {
@@ -395,6 +419,18 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
     part += dpp<0x4E>(part);  // lane ^ 2
     if ((i & 3) == 0) sx[i >> 2] = part;
   }
+  // 1/rms(h) from the partial sums: each thread adds its pieces in order, the wavefronts
+  // their lanes (wave_sum), the four wavefront sums meet after the barrier below
+  float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kRed);
+  if constexpr (kScaled) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NQ; ++t)
+      ss += (__uint_as_float(nq[t].x) + __uint_as_float(nq[t].y)) +
+            (__uint_as_float(nq[t].z) + __uint_as_float(nq[t].w));
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[wave] = ss;
+  }
   const int sbase = kPair && tid >= 128 ? 4 * G : 0;  // dword offset of the up rows' span
 #pragma unroll
   for (int q = 0; q < SBR; ++q) {
@@ -426,6 +462,7 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
   float v = row16_sum(acc);
   if (sh >= 5) v = add_xor16(v);
   if (sh >= 6) v = add_xor32(v);
+  if constexpr (kScaled) v *= 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)K + S.eps);
 
   if (EPI == kEpiBf16) {
     if (owner) store_b16_sc1(buffer_rsrc(S.p[qi].y, (uint32_t)N * 2u), 2u * row, to_bf(v));
@@ -433,6 +470,20 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
     if (owner) static_cast<float*>(S.p[qi].y)[row] = v;
   } else if (EPI == kEpiResidual) {
     if (owner) stf_sc1(S.h + row, hres + bf(to_bf(v)));
+  } else if (EPI == kEpiResidualNorm) {
+    // h += bf16(y), x' = bf16(h * w_next), and the tile's sum of squares of the new h: the
+    // owners' squares summed per wavefront (wave_sum), then the four wavefronts in order
+    float sq = 0.0f;
+    if (owner) {
+      const float hn = hres + bf(to_bf(v));
+      stf_sc1(S.h + row, hn);
+      store_b16_sc1(buffer_rsrc(S.xn_out, (uint32_t)N * 2u), 2u * row, to_bf(hn * bf(wnext)));
+      sq = hn * hn;
+    }
+    sq = wave_sum(sq);
+    if ((tid & 63) == 0) red[wave] = sq;
+    lds_barrier();
+    if (tid == 0) stf_sc1(S.ssq_out + tile, (red[0] + red[1]) + (red[2] + red[3]));
   } else {  // SiLU * up: the up rows hand their values to the gate rows
     float* pairx = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kPair);
     if (j == 0 && rl >= 8) pairx[rl - 8] = v;
@@ -954,7 +1005,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
 
 // One qmv instantiation per (x source, epilogue, tile shape) that a program can hold.
 #define IMQ_QMV_CASE(NCH, XR, XSRC, EPI, SHAPE)                   \
-  case (XSRC) * 16 + (EPI) * 4 + (SHAPE):                          \
+  case (XSRC) * 32 + (EPI) * 4 + (SHAPE):                          \
     good = qmv_task<NCH, XR, XSRC, EPI, false, StageRef>(S, task, a, smem); \
     break;
 #define IMQ_QMV_SHAPES_X2(XSRC, EPI)         \
@@ -967,14 +1018,19 @@ __device__ __forceinline__ bool run_task(StageRef S, int task, const StepArgs& a
   if (S.kind == kKindAttention) {
     good = attention_task<false, StageRef>(S, task, a, smem);
   } else {
-    switch (S.xsrc * 16 + S.epi * 4 + S.shape) {
+    switch (S.xsrc * 32 + S.epi * 4 + S.shape) {
       IMQ_QMV_SHAPES_X2(kXVector, kEpiBf16)
       IMQ_QMV_CASE(5, 5, kXVector, kEpiBf16, kShape55)
       IMQ_QMV_SHAPES_X2(kXVector, kEpiResidual)
       IMQ_QMV_CASE(5, 5, kXVector, kEpiResidual, kShape55)
+      IMQ_QMV_SHAPES_X2(kXVector, kEpiResidualNorm)
+      IMQ_QMV_CASE(5, 5, kXVector, kEpiResidualNorm, kShape55)
       IMQ_QMV_SHAPES_X2(kXNorm, kEpiBf16)
       IMQ_QMV_SHAPES_X2(kXNorm, kEpiSiluPair)
       IMQ_QMV_SHAPES_X2(kXNorm, kEpiF32)
+      IMQ_QMV_SHAPES_X2(kXScaled, kEpiBf16)
+      IMQ_QMV_SHAPES_X2(kXScaled, kEpiSiluPair)
+      IMQ_QMV_SHAPES_X2(kXScaled, kEpiF32)
       default: break;  // the host plans only the cases above
     }
   }
@@ -1439,17 +1495,32 @@ int32_t imq_decode_program_create(const imq_step_desc* d, imq_program** out) {
   if ((int64_t)d->num_slots * Hkv * d->capacity * kD * 2 >= ((int64_t)1 << 31))
     return fail(IMQ_EUNSUPPORTED, "a KV pool of 2 GiB or more exceeds the attention's offsets");
 
+  // the RMSNorms folded into the projections around them (every one but the first layer's
+  // input norm): the o and down stages write x' = bf16(h * w_next) and one sum of squares
+  // of the new h per tile, which the next stage reads
+  const TileShape ts_o = tile_shape(qd), ts_d = tile_shape(I);
+  if (ts_o.shape < 0 || ts_d.shape < 0)
+    return fail(IMQ_EUNSUPPORTED, "o or down outside the persistent qmv tiles");
+  const int tiles_o = (D + (kThreads >> ts_o.sh) - 1) / (kThreads >> ts_o.sh);
+  const int tiles_d = (D + (kThreads >> ts_d.sh) - 1) / (kThreads >> ts_d.sh);
+  if (tiles_o > kMaxNormParts || tiles_d > kMaxNormParts)
+    return fail(IMQ_EUNSUPPORTED, "more tiles of o or down than the folded norm reads");
+
   imq_program* prog = new imq_program();
   (void)hipGetDevice(&prog->device);
   const int span = std::min(d->max_len, d->capacity);
   int splits, cps;
   attention_split(B, Hkv, span, &splits, &cps);
-  // activations: q, k, v, attention output, SiLU*up (bf16), then the partials (fp32)
+  // activations: q, k, v, attention output, SiLU*up, x' (bf16), then the partials and the
+  // sums of squares (fp32)
   const size_t off_q = 0, off_k = off_q + (size_t)B * qd * 2, off_v = off_k + (size_t)B * kvd * 2;
   const size_t off_attn = off_v + (size_t)B * kvd * 2, off_act = off_attn + (size_t)B * qd * 2;
-  const size_t off_part = (off_act + (size_t)B * I * 2 + 255) & ~(size_t)255;
+  const size_t off_xn = off_act + (size_t)B * I * 2;
+  const size_t off_part = (off_xn + (size_t)B * D * 2 + 255) & ~(size_t)255;
   const size_t off_ml = off_part + (size_t)B * Hq * splits * kD * 4;
-  const size_t scratch = off_ml + (size_t)B * Hq * splits * 8;
+  const size_t off_sso = (off_ml + (size_t)B * Hq * splits * 8 + 255) & ~(size_t)255;
+  const size_t off_ssd = off_sso + (size_t)tiles_o * 4;
+  const size_t scratch = off_ssd + (size_t)tiles_d * 4;
   if (hipMalloc(&prog->d_scratch, scratch) != hipSuccess) {
     free_program(prog);
     return fail(IMQ_ELAUNCH, "hipMalloc of the program activations failed");
@@ -1460,8 +1531,24 @@ int32_t imq_decode_program_create(const imq_step_desc* d, imq_program** out) {
   uint16_t* v = reinterpret_cast<uint16_t*>(sc + off_v);
   uint16_t* attn = reinterpret_cast<uint16_t*>(sc + off_attn);
   uint16_t* act = reinterpret_cast<uint16_t*>(sc + off_act);
+  uint16_t* xn = reinterpret_cast<uint16_t*>(sc + off_xn);
   float* part = reinterpret_cast<float*>(sc + off_part);
   float* ml = reinterpret_cast<float*>(sc + off_ml);
+  float* ssq_o = reinterpret_cast<float*>(sc + off_sso);
+  float* ssq_d = reinterpret_cast<float*>(sc + off_ssd);
+  // the last stage added takes x' and 1/rms from `ssq` (`parts` sums of squares) ...
+  auto scaled = [&](const float* ssq, int parts) {
+    Stage& S = prog->stages.back();
+    S.ssq_in = ssq;
+    S.nssq = parts;
+  };
+  // ... or writes them for the next stage
+  auto residual_norm = [&](const uint16_t* w_next, float* ssq) {
+    Stage& S = prog->stages.back();
+    S.norm_next = w_next;
+    S.xn_out = xn;
+    S.ssq_out = ssq;
+  };
   auto qp = [](const imq_qweight& w, void* y, int N, int K) {
     QProb p;
     memset(&p, 0, sizeof(p));
@@ -1476,9 +1563,13 @@ int32_t imq_decode_program_create(const imq_step_desc* d, imq_program** out) {
   int prev = -1;
   for (int i = 0; i < d->layers && code == IMQ_OK; ++i) {
     const imq_step_layer& Ly = d->layer[i];
+    // the first layer's input norm runs in its q/k/v stage; later ones were folded into the
+    // previous layer's down stage
     code = add_qmv_stage(prog, {qp(Ly.q, q, qd, D), qp(Ly.k, k, kvd, D), qp(Ly.v, v, kvd, D)},
-                         kXNorm, kEpiBf16, prev, nullptr, d->h, Ly.input_norm, d->eps, nullptr);
+                         i == 0 ? kXNorm : kXScaled, kEpiBf16, prev, i == 0 ? nullptr : xn, d->h,
+                         Ly.input_norm, d->eps, nullptr);
     if (code) break;
+    if (i > 0) scaled(ssq_d, tiles_d);
     const int s_qkv = (int)prog->stages.size() - 1;
     Stage A;
     memset(&A, 0, sizeof(A));
@@ -1512,21 +1603,27 @@ int32_t imq_decode_program_create(const imq_step_desc* d, imq_program** out) {
     prog->ntasks += A.count;
     prog->stages.push_back(A);
     const int s_attn = (int)prog->stages.size() - 1;
-    code = add_qmv_stage(prog, {qp(Ly.o, nullptr, D, qd)}, kXVector, kEpiResidual, s_attn, attn,
-                         d->h, nullptr, d->eps, nullptr);
+    code = add_qmv_stage(prog, {qp(Ly.o, nullptr, D, qd)}, kXVector, kEpiResidualNorm, s_attn,
+                         attn, d->h, nullptr, d->eps, nullptr);
     if (code) break;
+    residual_norm(Ly.post_norm, ssq_o);
     const int s_o = (int)prog->stages.size() - 1;
-    code = add_qmv_stage(prog, {qp(Ly.gate, nullptr, I, D), qp(Ly.up, nullptr, I, D)}, kXNorm,
-                         kEpiSiluPair, s_o, nullptr, d->h, Ly.post_norm, d->eps, act);
+    code = add_qmv_stage(prog, {qp(Ly.gate, nullptr, I, D), qp(Ly.up, nullptr, I, D)}, kXScaled,
+                         kEpiSiluPair, s_o, xn, d->h, nullptr, d->eps, act);
     if (code) break;
+    scaled(ssq_o, tiles_o);
     const int s_gu = (int)prog->stages.size() - 1;
-    code = add_qmv_stage(prog, {qp(Ly.down, nullptr, D, I)}, kXVector, kEpiResidual, s_gu, act,
+    code = add_qmv_stage(prog, {qp(Ly.down, nullptr, D, I)}, kXVector, kEpiResidualNorm, s_gu, act,
                          d->h, nullptr, d->eps, nullptr);
+    if (code) break;
+    residual_norm(i + 1 < d->layers ? d->layer[i + 1].input_norm : d->final_norm, ssq_d);
     prev = (int)prog->stages.size() - 1;
   }
-  if (code == IMQ_OK)
-    code = add_qmv_stage(prog, {qp(d->head, d->logits, d->vocab, D)}, kXNorm, kEpiF32, prev,
-                         nullptr, d->h, d->final_norm, d->eps, nullptr);
+  if (code == IMQ_OK) {
+    code = add_qmv_stage(prog, {qp(d->head, d->logits, d->vocab, D)}, kXScaled, kEpiF32, prev, xn,
+                         d->h, nullptr, d->eps, nullptr);
+    if (code == IMQ_OK) scaled(ssq_d, tiles_d);
+  }
   if (code == IMQ_OK) code = finish_program(prog);
   if (code != IMQ_OK) {
     free_program(prog);
@@ -1586,21 +1683,26 @@ int32_t imq_program_launch_staged(imq_program* p, void* stream) {
       continue;
     }
 #define IMQ_STAGE_CASE(NCH, XR, XSRC, EPI, SHAPE)                                              \
-  case (XSRC) * 16 + (EPI) * 4 + (SHAPE):                                                   \
+  case (XSRC) * 32 + (EPI) * 4 + (SHAPE):                                                   \
     hipLaunchKernelGGL((qmv_stage_kernel<NCH, XR, XSRC, EPI>), grid, block, lds, st, S, a);   \
     break;
 #define IMQ_STAGE_SHAPES_X2(XSRC, EPI)      \
   IMQ_STAGE_CASE(2, 2, XSRC, EPI, kShape22) \
   IMQ_STAGE_CASE(5, 2, XSRC, EPI, kShape52) \
   IMQ_STAGE_CASE(8, 2, XSRC, EPI, kShape82)
-    switch (S.xsrc * 16 + S.epi * 4 + S.shape) {
+    switch (S.xsrc * 32 + S.epi * 4 + S.shape) {
       IMQ_STAGE_SHAPES_X2(kXVector, kEpiBf16)
       IMQ_STAGE_CASE(5, 5, kXVector, kEpiBf16, kShape55)
       IMQ_STAGE_SHAPES_X2(kXVector, kEpiResidual)
       IMQ_STAGE_CASE(5, 5, kXVector, kEpiResidual, kShape55)
+      IMQ_STAGE_SHAPES_X2(kXVector, kEpiResidualNorm)
+      IMQ_STAGE_CASE(5, 5, kXVector, kEpiResidualNorm, kShape55)
       IMQ_STAGE_SHAPES_X2(kXNorm, kEpiBf16)
       IMQ_STAGE_SHAPES_X2(kXNorm, kEpiSiluPair)
       IMQ_STAGE_SHAPES_X2(kXNorm, kEpiF32)
+      IMQ_STAGE_SHAPES_X2(kXScaled, kEpiBf16)
+      IMQ_STAGE_SHAPES_X2(kXScaled, kEpiSiluPair)
+      IMQ_STAGE_SHAPES_X2(kXScaled, kEpiF32)
       default:
         return fail(IMQ_EUNSUPPORTED, "stage variant without a kernel");
     }

@@ -25,9 +25,10 @@ All buffers are allocated once per (model, batch size) in `DecodeState`; a step 
 launches kernels, so it can be captured in a HIP graph and replayed.  Every launch goes
 through the C ABI; there is no host fallback.
 
-`PersistentDecode` runs the same step at batch 1 as one persistent-kernel program
+`PersistentDecode` runs the step at batch 1 as a program of fused stages
 (include/ironmule_step.h): the embedding launch, then one launch for all layers and the
-head, with bit-identical results.
+head (or one launch per stage), with every RMSNorm but the first layer's input norm folded
+into the projections around it.
 
 `prefill` runs a whole prompt through the same model at once, the library path a prompt
 takes (ironmule/cuda_native.py:171-179): every projection of more than 32 rows is
@@ -256,7 +257,11 @@ class PersistentDecode:
     `staged` each stage is its own launch (5 per layer: q/k/v with the RMSNorm, attention
     with q/k norm + rotary + KV write + the split merge, o with the residual add, gate/up
     with the RMSNorm and SiLU * up, down with the residual add); otherwise one persistent
-    launch runs them all.  Same inputs, same bits as `decode_step`."""
+    launch runs them all.  The two forms give the same bits; every RMSNorm but the first
+    layer's input norm is folded into the projections around it (the o and down stages
+    write x' = bf16(h * w_next) and per-tile sums of squares, the next stage scales its
+    outputs by 1/rms), so against `decode_step` at batch 1 (RMSNorm launches) the logits
+    agree to the folding's rounding level."""
 
     def __init__(self, weights: DecoderWeights, state: DecodeState, staged: bool = False) -> None:
         if state.batch != 1:

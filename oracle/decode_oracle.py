@@ -41,6 +41,16 @@ returns its value), and tests/test_decode_oracle_hf.py pins the composition itse
 round_bf16=False, step-by-step decoding matches transformers' Qwen3ForCausalLM (same
 weights, one causal forward) at the fp32 rounding level, while compositions with the rotary
 or the q/k-norm skipped, or the MLP fed from the residual stream, do not.
+
+`fold_norms` restates the rounding points of this build's GPU steps that fold an RMSNorm
+into the projections it feeds: x' = bf16(h * w) is the projections' input and each output
+row is scaled by 1 / rms(h) before its own rounding, so rms_norm(h) W^T is computed as
+inv * ((h * w) W^T) with the bf16 rounding of the input placed before the scaling instead
+of after it.  `fold_first` and `fold_final` say whether the first layer's input norm and the
+final norm are folded too (the batched step folds every layer's norms but not the final
+one; the batch-1 program folds every norm but the first layer's input norm).  Without
+rounding the two placements are the same composition (tests/test_decode_oracle.py pins
+that fold_norms=True with round_bf16=False equals the unfolded step).
 """
 
 from __future__ import annotations
@@ -128,10 +138,22 @@ class Model:
 
 
 def decode_step(model: Model, keys: list, values: list, tokens, slots, positions,
-                round_bf16: bool = True):
+                round_bf16: bool = True, fold_norms: bool = False, fold_first: bool = True,
+                fold_final: bool = False):
     """One decode step of B requests; keys/values[layer] are (slots, Hkv, C, D) float64
-    pools, updated in place at (slot, :, pos).  Returns float64 logits (B, vocab)."""
+    pools, updated in place at (slot, :, pos).  Returns float64 logits (B, vocab).
+    fold_norms (with fold_first, fold_final): the folded-norm rounding points (module
+    docstring)."""
     r = bf16_round if round_bf16 else (lambda a: np.asarray(a, np.float64))
+
+    def normed(h, weight, folded):
+        """The projections' input and the scale of their outputs for rms_norm(h, weight)."""
+        if not (fold_norms and folded):
+            return r(rms_norm(h, weight, model.eps)), 1.0
+        hh = np.asarray(h, np.float64)
+        inv = 1.0 / np.sqrt(np.mean(hh * hh, axis=-1, keepdims=True) + model.eps)
+        return r(hh * np.asarray(weight, np.float64)), inv
+
     d = HEAD_DIM
     tokens = np.asarray(tokens)
     slots = np.asarray(slots)
@@ -140,10 +162,10 @@ def decode_step(model: Model, keys: list, values: list, tokens, slots, positions
     h = model.embed[tokens].astype(np.float64)
     scale = d ** -0.5
     for i, lay in enumerate(model.layers):
-        x = r(rms_norm(h, lay.input_norm, model.eps))
-        q = r(x @ lay.wq.T).reshape(b, model.heads, d)
-        k = r(x @ lay.wk.T).reshape(b, model.kv_heads, d)
-        v = r(x @ lay.wv.T).reshape(b, model.kv_heads, d)
+        x, s = normed(h, lay.input_norm, i > 0 or fold_first)
+        q = r(s * (x @ lay.wq.T)).reshape(b, model.heads, d)
+        k = r(s * (x @ lay.wk.T)).reshape(b, model.kv_heads, d)
+        v = r(s * (x @ lay.wv.T)).reshape(b, model.kv_heads, d)
         q = r(rope(r(rms_norm(q, lay.q_norm, model.eps)), positions, model.theta))
         k = r(rope(r(rms_norm(k, lay.k_norm, model.eps)), positions, model.theta))
         for row in range(b):
@@ -153,11 +175,11 @@ def decode_step(model: Model, keys: list, values: list, tokens, slots, positions
                                   values[i][slots[row], :, :positions[row] + 1], scale))
                       for row in range(b)]).reshape(b, model.heads * d)
         h = h + r(o @ lay.wo.T)
-        x = r(rms_norm(h, lay.post_norm, model.eps))
-        act = r(silu_mul(r(x @ lay.wg.T), r(x @ lay.wu.T)))
+        x, s = normed(h, lay.post_norm, True)
+        act = r(silu_mul(r(s * (x @ lay.wg.T)), r(s * (x @ lay.wu.T))))
         h = h + r(act @ lay.wd.T)
-    x = r(rms_norm(h, model.norm, model.eps))
-    return x @ model.embed.T
+    x, s = normed(h, model.norm, fold_final)
+    return s * (x @ model.embed.T)
 
 
 # ------------------------------------------------------------------ Gemma 3

@@ -149,3 +149,32 @@ def test_decode_step_rounding_points_are_small_perturbations():
     b = do.decode_step(model, k2, v2, [7], [1], [9], False)
     rel = np.abs(a - b).max() / np.abs(b).max()
     assert 1e-5 < rel < 5e-2, rel
+
+
+@pytest.mark.parametrize("fold_first,fold_final", [(True, False), (False, True), (True, True)])
+def test_folded_norms_are_the_same_composition_without_rounding(fold_first, fold_final):
+    """Without rounding, inv * ((h * w) W^T) is rms_norm(h) W^T: the folded-norm step equals
+    the unfolded one to float64 precision, whichever norms are folded."""
+    model = _tiny_model()
+    keys, values = _pools(model)
+    k2, v2 = [a.copy() for a in keys], [a.copy() for a in values]
+    a = do.decode_step(model, keys, values, [7, 120], [1, 2], [9, 3], False)
+    b = do.decode_step(model, k2, v2, [7, 120], [1, 2], [9, 3], False, fold_norms=True,
+                       fold_first=fold_first, fold_final=fold_final)
+    np.testing.assert_allclose(b, a, rtol=1e-11, atol=1e-13 * np.abs(a).max())
+    for i in range(len(model.layers)):
+        np.testing.assert_allclose(k2[i], keys[i], rtol=1e-11, atol=1e-13)
+
+
+def test_folded_norms_move_only_rounding_points():
+    """With rounding the folded step differs from the unfolded one by bf16-level amounts
+    (the inputs are rounded before the 1/rms scaling instead of after it); the previous test
+    shows that without rounding they are one composition, so a fold that dropped the scale
+    or applied it twice would fail there."""
+    model = _tiny_model()
+    keys, values = _pools(model)
+    k2, v2 = [a.copy() for a in keys], [a.copy() for a in values]
+    a = do.decode_step(model, keys, values, [7], [1], [9], True)
+    b = do.decode_step(model, k2, v2, [7], [1], [9], True, fold_norms=True)
+    rel = np.abs(a - b).max() / np.abs(a).max()
+    assert 0 < rel < 5e-2, rel

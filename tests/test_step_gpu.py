@@ -1,10 +1,13 @@
 """GPU parity of the persistent engine (include/ironmule_step.h), through the C ABI.
 
-The bar is bit-identity with the per-kernel path on the same inputs: every output of a
-qmv program equals imq_qmv / imq_qmv_grouped's, and the persistent decode step's logits,
-residual stream and KV pools equal `decode_step`'s, over several consecutive steps (the
-per-kernel step is itself checked against the decode oracle in test_decode_gpu.py, and
-the tiny decoder's persistent logits are checked against the oracle here as well).
+Every output of a qmv program equals imq_qmv / imq_qmv_grouped's on the same inputs, bit
+for bit.  The decode program folds every RMSNorm but the first layer's input norm into the
+projections around it (the o and down stages write x' = bf16(h * w_next) and per-tile sums
+of squares; the next stage scales its outputs by 1/rms), so its two forms (one persistent
+launch, one launch per stage) give each other's bits, its logits are checked against the
+decode oracle with those rounding points, and against the per-kernel `decode_step` (RMSNorm
+launches at batch 1) it agrees to the folding's rounding level, with the first layer's KV
+written identically.
 """
 
 from __future__ import annotations
@@ -99,42 +102,63 @@ def _twin_states(torch, cfg, capacity, seed):
     return a, b
 
 
-def _compare_steps(torch, weights, cfg, capacity, requests, seed, staged=False):
-    """Runs decode_step on one state and the program's step on a twin for each request
-    (token, slot, position) in turn; logits, h and every KV pool must agree bit for bit."""
+# max|dlogit| / max|logit| of the program against the per-kernel step with RMSNorm launches:
+# the folded norms round x before the 1/rms scaling instead of after it (observed 2.3e-4 to
+# 4.8e-4 on the tiny and the Qwen3-4B-shaped decoders)
+FOLD_BAR = 1e-3
+
+
+def _compare_steps(torch, weights, cfg, capacity, requests, seed, forms=True):
+    """For each request (token, slot, position) in turn: the staged program (one launch per
+    stage) and, with `forms`, the persistent one on a twin state give each other's logits,
+    h and KV pools bit for bit; against decode_step on a third twin the logits agree within
+    FOLD_BAR with the same argmax, and the first layer's KV pools bit for bit."""
     from ironmule_amd.decode import PersistentDecode, decode_step
     ref, per = _twin_states(torch, cfg, capacity, seed)
-    engine = PersistentDecode(weights, per, staged=staged)
+    engine = PersistentDecode(weights, per, staged=True)
+    other = None
+    if forms:
+        _, per2 = _twin_states(torch, cfg, capacity, seed)
+        other = PersistentDecode(weights, per2, staged=False)
     for step, (tok, slot, pos) in enumerate(requests):
-        ref.set_requests([tok], [slot], [pos])
-        per.set_requests([tok], [slot], [pos])
+        for st in (ref, per) + ((per2,) if forms else ()):
+            st.set_requests([tok], [slot], [pos])
         want = decode_step(weights, ref)
         got = engine.step()
+        got2 = other.step() if forms else None
         torch.cuda.synchronize()
         assert not engine.failed(), step
-        assert torch.equal(got, want), (step, (got - want).abs().max().item())
-        assert torch.equal(per.h, ref.h), step
-        for i in range(cfg.layers):
-            assert torch.equal(per.k_pool[i], ref.k_pool[i]), (step, i)
-            assert torch.equal(per.v_pool[i], ref.v_pool[i]), (step, i)
+        if forms:
+            assert not other.failed(), step
+            assert torch.equal(got, got2), step
+            assert torch.equal(per.h, per2.h), step
+            for i in range(cfg.layers):
+                assert torch.equal(per.k_pool[i], per2.k_pool[i]), (step, i)
+                assert torch.equal(per.v_pool[i], per2.v_pool[i]), (step, i)
+        rel = float((got - want).abs().max() / want.abs().max())
+        print(f"[observed] program against decode_step, step {step}: max|dlogit|/max|logit| = {rel:.3e}",
+              flush=True)
+        assert rel <= FOLD_BAR, (step, rel)
+        assert int(got.argmax()) == int(want.argmax()), step
+        assert torch.equal(per.k_pool[0], ref.k_pool[0]), step
+        assert torch.equal(per.v_pool[0], ref.v_pool[0]), step
     return engine, per
 
 
-@pytest.mark.parametrize("staged", [False, True])
-def test_decode_program_matches_decode_step_tiny(env, staged):
+def test_decode_program_forms_and_decode_step_tiny(env):
     torch, n, orc = env
     from ironmule_amd.decode import random_weights
-    announce("program decode, tiny decoder, staged", staged)
+    announce("program decode, tiny decoder")
     cfg = _tiny()
     weights = random_weights(cfg, "cuda", seed=5)
     # first token of a slot, a chunk boundary, the last position, then a continuing request
     _compare_steps(torch, weights, cfg, 80, [(5, 1, 0), (17, 0, 63), (300, 2, 64), (511, 2, 79),
-                                             (42, 1, 1)], seed=11, staged=staged)
+                                             (42, 1, 1)], seed=11)
 
 
 def test_decode_program_tiny_against_the_oracle(env):
     """The persistent logits against the float64 decode oracle with the same rounding
-    points (the bar of test_decode_gpu.py's step test at batch 3)."""
+    points (every RMSNorm but the first layer's input norm folded)."""
     torch, n, orc = env
     from ironmule_amd.decode import DecodeState, PersistentDecode, random_weights
     from oracle import decode_oracle as do
@@ -157,35 +181,33 @@ def test_decode_program_tiny_against_the_oracle(env):
         state.set_requests([tok], [slot], [pos])
         got = engine.step().cpu().numpy().astype(np.float64)
         assert not engine.failed()
-        ref = do.decode_step(model, keys, values, [tok], [slot], [pos], round_bf16=True)
+        ref = do.decode_step(model, keys, values, [tok], [slot], [pos], round_bf16=True,
+                             fold_norms=True, fold_first=False, fold_final=True)
         rel = np.abs(got - ref).max() / np.abs(ref).max()
         print(f"[observed] persistent decode step {step}: max|dlogit|/max|logit| = {rel:.3e}", flush=True)
-        # observed 6.0e-8; one bf16 rounding of an intermediate on the other side of a tie
-        # moves the logits by about 3e-5 of their maximum (the step test's bar)
-        assert rel <= 1e-4, (step, rel)
+        assert rel <= 5e-7, (step, rel)  # observed 1.0e-7
         tok, pos = int(np.argmax(got[0])), pos + 1
 
 
-@pytest.mark.parametrize("staged", [False, True])
-def test_decode_program_matches_decode_step_qwen3_4b_shapes(env, staged):
+def test_decode_program_forms_and_decode_step_qwen3_4b_shapes(env):
     """Two Qwen3-4B-shaped layers with the full 151,936-token head and a 512-token
     context, at the first and a later position."""
     torch, n, orc = env
     from ironmule_amd.decode import DecoderConfig, random_weights
-    announce("program decode, qwen3-4b shapes, 2 layers, staged", staged)
+    announce("program decode, qwen3-4b shapes, 2 layers")
     cfg = DecoderConfig(layers=2)
     weights = random_weights(cfg, "cuda", seed=9)
     engine, state = _compare_steps(torch, weights, cfg, 520,
-                                   [(11, 0, 512), (151935, 0, 513), (7, 2, 0)], seed=3,
-                                   staged=staged)
+                                   [(11, 0, 512), (151935, 0, 513), (7, 2, 0)], seed=3)
     info = engine.program.info()
     assert info["stages"] == 2 * 5 + 1 and info["workgroups"] >= 256
 
 
 def test_decode_program_matches_decode_step_full_36_layers(env):
     """The full synthetic Qwen3-4B step (36 layers, the 151,936-token head, a 512-token
-    context): the staged batch-1 program behind the bench's batch-1 figure gives the
-    per-kernel step's bits over two consecutive steps."""
+    context): the staged batch-1 program behind the bench's batch-1 figure agrees with the
+    per-kernel step over two consecutive steps (its oracle check at this size is in
+    test_decode_full_gpu.py)."""
     torch, n, orc = env
     from ironmule_amd.decode import DecoderConfig, random_weights
     announce("program decode, qwen3-4b, 36 layers, staged")
@@ -193,7 +215,7 @@ def test_decode_program_matches_decode_step_full_36_layers(env):
     assert cfg.layers == 36
     weights = random_weights(cfg, "cuda", seed=21)
     engine, state = _compare_steps(torch, weights, cfg, 520, [(11, 0, 512), (4097, 0, 513)],
-                                   seed=5, staged=True)
+                                   seed=5, forms=False)
     assert engine.program.info()["stages"] == 36 * 5 + 1
     del engine, state, weights
     torch.cuda.empty_cache()
