@@ -100,8 +100,9 @@ IMQ_API int32_t imq_attention_decode(const uint16_t* q, const uint16_t* k_pool,
  * row positions[b] of slot slots[b]; then out[b][h] = softmax(q . K / sqrt(128)) V over
  * rows 0 .. positions[b] of the slot (clamped to max_len and capacity), split over 64-key
  * chunks with the split plan of imq_attention_decode and merged in split order by the
- * last split of each (request, KV head); from 128 (request, KV head) pairs one workgroup
- * of 12 wavefronts per pair, without splits.  The KV pools get the same bits as
+ * last split of each (request, KV head); from 64 (request, KV head) pairs a workgroup of
+ * 12 wavefronts per task, split so that about 256 tasks run (never more splits than that
+ * plan; none from 256 pairs).  The KV pools get the same bits as
  * imq_qk_norm_rope followed by imq_attention_decode with lengths = positions + 1 for every
  * valid request, and the output agrees with theirs to the attention's oracle bar (the
  * scores and P.V run on MFMA, in another summation order); a request with
