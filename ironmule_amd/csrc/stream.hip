@@ -399,14 +399,16 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, int K, bool live, cha
 // that stream faster take more of them and all finish together (measured on MI355X: with
 // every run dealt, the last wavefronts of a 20-layer launch ended 35 us after the median
 // one; claiming the last 25% in runs of 8 tiles took that launch from 5.83 to 6.13 TB/s,
-// while runs of 4 or 16 tiles and a 12% share gained less).  The claimed runs are split
+// while runs of 4 or 16 tiles and a 12% share gained less; each shard's last 30% in single
+// tiles then ended a 20-layer launch about 2 us earlier than runs of 2).  The claimed runs are split
 // between `shards` counters, each on its own line (one counter serialises its atomic adds:
 // 16K claims on one counter cost a 20-layer launch 100 us).  The plan, the claim count
 // that returns a shard's counter to zero and the two cursors' steps are in stream_runs.h,
-// which a host simulation of this protocol compiles as well.  kDepth tiles are in flight:
-// the loads of a wavefront's tile k + kDepth are issued as soon as its tile k has been
-// computed; the load cursor claims the runs and the compute cursor, kDepth tiles behind,
-// takes them from a two-entry queue.
+// which a host simulation of this protocol compiles as well.  kDepth tiles are in flight
+// (one at the start, until the first is computed): the loads of a wavefront's tile
+// k + kDepth are issued as soon as its tile k has been computed; the load cursor claims the
+// runs and the compute cursor, at most kDepth tiles behind, takes them from a two-entry
+// queue.
 constexpr int kRunTarget = 16;
 #ifndef IMQ_STREAM_DYN_RUN
 #define IMQ_STREAM_DYN_RUN 8
@@ -415,7 +417,7 @@ constexpr int kRunTarget = 16;
 #define IMQ_STREAM_DYN_PERCENT 25
 #endif
 #ifndef IMQ_STREAM_TAIL_RUN
-#define IMQ_STREAM_TAIL_RUN 2
+#define IMQ_STREAM_TAIL_RUN 1
 #endif
 #ifndef IMQ_STREAM_TAIL_PERCENT
 #define IMQ_STREAM_TAIL_PERCENT 30
@@ -482,13 +484,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
 #pragma unroll
   for (int k = 0; k < kPreSlots; ++k)
     load_x(a.slot[k].x, k < a.nslots ? a.slot[k].K : 0, false, tid, xs[k]);
-#pragma unroll
-  for (int d = 0; d < kDepth; ++d) issue(T[d]);
+  // The pipeline starts one tile deep: the first tile's loads go out behind x, the
+  // wavefront computes that tile as soon as x is staged and it has landed, and only then
+  // issues the next two.  (With both tiles issued up front, issuing them held every
+  // wavefront until its CU's load queue drained, about 5 us, so no tile was computed before
+  // the whole first wave of weights had arrived and HBM then waited for new requests.)
+  static_assert(kDepth == 2, "the start peels one tile of a two-tile pipeline");
+  issue(T[1]);
 #pragma unroll
   for (int k = 0; k < kPreSlots; ++k)
     if (k < a.nslots) store_x(xs[k], a.slot[k].K, smem + a.slot[k].off, tid);
   for (int k = kPreSlots; k < a.nslots; ++k) stage_x(a.slot[k].x, a.slot[k].K, false, smem + a.slot[k].off, tid);
   lds_barrier();
+  {
+    const int gf = tile(cpos);
+    if (gf >= total) return;  // uniform: no tiles (its one load read past its buffer)
+    move(cs, cp, cc, gf, cpos.r);
+    compute_site(cc, gf, lane, T[1], smem, sbw, magic, true);
+    step_compute(cpos);
+    issue(T[0]);
+    issue(T[1]);
+  }
 
   // Every pass runs all kDepth tiles with no exit in between, so that every path into the
   // loop head has issued the tiles' loads in the same order and each tile's compute waits

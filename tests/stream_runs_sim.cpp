@@ -1,8 +1,9 @@
 // Host simulation of the streaming engine's run plan and claim protocol
 // (ironmule_amd/csrc/stream_runs.h, the same header the kernel compiles).
 //
-// Each simulated wavefront executes the kernel's sequence of events: kDepth issues, then
-// passes of (compute, issue) x kDepth until a pass starts past the last tile.  A random
+// Each simulated wavefront executes the kernel's sequence of events: one issue; unless
+// that first tile lies past the last one, its compute and two issues; then passes of
+// (compute, issue) x kDepth until a pass starts past the last tile.  A random
 // scheduler interleaves the wavefronts one event at a time, sometimes letting one run a
 // long burst, so that claims arrive in many orders.  The claim counters persist across
 // launches, as the device's do.  After every launch it checks that every tile was
@@ -56,7 +57,7 @@ struct Params {
   int total, grid, waves_per_group, dyn_run, pct, tail_run, tail_pct;
 };
 
-enum State { kInit, kPassStart, kCompute, kIssue, kDone };
+enum State { kInit, kFirst, kFirstIssue, kPassStart, kCompute, kIssue, kDone };
 
 struct Wave {
   Pos lpos, cpos;
@@ -79,6 +80,24 @@ bool launch(const ShardPlan& sp, const Plan& P, const Params& pr, std::vector<ui
   }
   std::vector<int> computed((size_t)P.total, 0);
   int max_queue = 0;
+  // the compute of the tile at the front of the wavefront's loads (its compute cursor's)
+  auto compute = [&](Wave& w) -> bool {
+    const int gd = tile_of(P, sp.shard[w.shard], w.cpos);
+    const int got = w.loaded.front();
+    w.loaded.pop_front();
+    if (gd < P.total) {
+      if (got != gd) {
+        snprintf(why, why_len, "wavefront computes tile %d from the loads of tile %d", gd, got);
+        return false;
+      }
+      ++computed[(size_t)gd];
+    } else if (got >= 0) {
+      snprintf(why, why_len, "loaded tile %d is dropped", got);
+      return false;
+    }
+    step_compute(P, sp.shard[w.shard], w.cpos, w.cq);
+    return true;
+  };
   auto issue = [&](Wave& w) {
     const ShardRuns& sh = sp.shard[w.shard];
     const int g = tile_of(P, sh, w.lpos);
@@ -109,7 +128,20 @@ bool launch(const ShardPlan& sp, const Plan& P, const Params& pr, std::vector<ui
     }
     Wave& w = waves[(size_t)live[(size_t)idx]];
     switch (w.state) {
-      case kInit:
+      case kInit:  // the first tile's loads, then x is staged
+        issue(w);
+        w.state = kFirst;
+        break;
+      case kFirst:  // the first tile, computed before the next two are issued
+        if (tile_of(P, sp.shard[w.shard], w.cpos) >= P.total) {
+          w.state = kDone;
+          break;
+        }
+        if (!compute(w)) return false;
+        w.inits = 0;
+        w.state = kFirstIssue;
+        break;
+      case kFirstIssue:
         issue(w);
         if (++w.inits == kDepth) w.state = kPassStart;
         break;
@@ -122,24 +154,10 @@ bool launch(const ShardPlan& sp, const Plan& P, const Params& pr, std::vector<ui
           w.state = kCompute;
         }
         break;
-      case kCompute: {
-        const int gd = tile_of(P, sp.shard[w.shard], w.cpos);
-        const int got = w.loaded.front();
-        w.loaded.pop_front();
-        if (gd < P.total) {
-          if (got != gd) {
-            snprintf(why, why_len, "wavefront computes tile %d from the loads of tile %d", gd, got);
-            return false;
-          }
-          ++computed[(size_t)gd];
-        } else if (got >= 0) {
-          snprintf(why, why_len, "loaded tile %d is dropped", got);
-          return false;
-        }
-        step_compute(P, sp.shard[w.shard], w.cpos, w.cq);
+      case kCompute:
+        if (!compute(w)) return false;
         w.state = kIssue;
         break;
-      }
       case kIssue:
         issue(w);
         w.state = ++w.d < kDepth ? kCompute : kPassStart;
@@ -223,7 +241,7 @@ int main(int argc, char** argv) {
   Rng rng{(uint64_t)strtoull(argv[a], nullptr, 10) * 2654435761ull + 1};
   const int cases = atoi(argv[a + 1]), launches = atoi(argv[a + 2]);
   // fixed cases first: one workgroup of 4 wavefronts over 1250 tiles (a 5000-row,
-  // K = 2560 stage: the last claimed run is 2 tiles), the 20- and 36-layer programs of
+  // K = 2560 stage whose last claimed runs are short), the 20- and 36-layer programs of
   // the streaming engine's grid (256 workgroups of 12 wavefronts), then random cases
   struct Fixed {
     int total, grid, waves;
@@ -235,7 +253,7 @@ int main(int argc, char** argv) {
   for (int c = 0; c < nfixed + cases; ++c) {
     Params pr;
     if (c < nfixed) {
-      pr = Params{fixed[c].total, fixed[c].grid, fixed[c].waves, 8, 25, 2, 30};
+      pr = Params{fixed[c].total, fixed[c].grid, fixed[c].waves, 8, 25, 1, 30};
     } else {
       pr.waves_per_group = rng.below(2) == 0 ? 4 : 12;
       pr.grid = 1 + rng.below(rng.below(4) == 0 ? 300 : 40);
