@@ -179,6 +179,20 @@ IMQ_API int32_t imq_qmv_norm_planes(const imq_problem* problems, int32_t count, 
                                     int32_t group_size, int32_t bits, const imq_norm_in* in,
                                     float* planes, int64_t pstride, int32_t* splits, void* stream);
 
+/*
+ * imq_qmv_norm's residual epilogue (`out`) as a launch of its own, for one projection of N
+ * columns computed as K-range planes by imq_qmv_norm_planes: y[m][n] = the nplanes planes
+ * at planes[(s * M + m) * N + n] added in plane order from zero, then h += bf16(y),
+ * x' = bf16(h * weight) and the per-tile sums of squares of the new h, with the bits of
+ * imq_qmv_norm with that `out` over the same problem.  1 <= nplanes <= 16, 1 <= M <= 32; the
+ * planes must not overlap h, x' or ssq.  The projection's launch then ends after its K-ranges
+ * (no split counter or reload), and the epilogue runs on every CU instead of one workgroup
+ * per 64-column tile.  Replaces the residual adds of the reference's decode step and the
+ * RMSNorm after each, ironmule/dense_plan.py:348, 357-360.
+ */
+IMQ_API int32_t imq_residual_planes(const float* planes, int32_t nplanes, int32_t M, int32_t N,
+                                    const imq_residual_out* out, void* stream);
+
 /* Bytes of workspace imq_qmv_gate_up_silu_norm uses at these shapes (0: none): when the
  * launch's 32-row tiles make more than one round over the CUs, the tiles of the last,
  * partial round are cut into K-parts that occupy the CUs the whole tiles leave free. */

@@ -126,6 +126,7 @@ _SIGNATURES = {
     "imq_qmv_norm_splits": ([ctypes.POINTER(Problem), _I32, _I32], _I32),
     "imq_qmv_norm_planes": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, ctypes.POINTER(NormIn),
                              _P, _I64, ctypes.POINTER(_I32), _P], _I32),
+    "imq_residual_planes": ([_P, _I32, _I32, _I32, ctypes.POINTER(ResidualOut), _P], _I32),
     "imq_qmv_gate_up_silu_norm_workspace": ([_I32, _I32, _I32], ctypes.c_size_t),
     "imq_qmv_gate_up_silu_norm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32,
                                    _I32, _I32, ctypes.POINTER(NormIn), _P, ctypes.c_size_t, _P],
@@ -705,6 +706,88 @@ def rmsnorm_prescale(h: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, s
                                       _stream(stream)))
     stats.tiles = 1
     return out
+
+
+RESIDUAL_MAX_PLANES = 16  # planes imq_residual_planes adds
+
+
+class ResidualPlanes:
+    """fp32 K-range planes of one projection of `cols` columns for `rows` requests
+    (imq_qmv_norm_planes over one weight), added into the residual stream by
+    residual_planes: plane s, row m, column n at element (s * rows + m) * cols + n."""
+
+    def __init__(self, rows: int, cols: int, device, max_planes: int = RESIDUAL_MAX_PLANES) -> None:
+        if not 1 <= max_planes <= RESIDUAL_MAX_PLANES:
+            raise ValueError(f"1 to {RESIDUAL_MAX_PLANES} planes")
+        self.rows, self.cols, self.max_planes = rows, cols, max_planes
+        self.data = torch.empty(max_planes * rows * cols, dtype=torch.float32, device=device)
+        self.planes = 0
+
+    def view(self) -> torch.Tensor:
+        """(planes, rows, cols) of the last projection, for tests."""
+        return self.data[:self.planes * self.rows * self.cols].view(self.planes, self.rows, self.cols)
+
+
+def _one_problem(weight, x: torch.Tensor) -> tuple[ctypes.Array, int, int]:
+    w, s, b = weight
+    _require(x, torch.bfloat16, "x")
+    if x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous (M, K) tensor")
+    n, k = check_weights(w, s, b)
+    if int(x.shape[1]) != k:
+        raise ValueError(f"the weight takes K = {k}, x has {int(x.shape[1])}")
+    probs = (Problem * 1)()
+    probs[0] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), k, None, n, n, k)
+    return probs, n, k
+
+
+def residual_split_planes(weight, x: torch.Tensor) -> int:
+    """The K-ranges (planes) imq_qmv_norm_planes cuts this one-weight projection into at
+    x's row count; 0 if it would refuse it."""
+    probs, _, _ = _one_problem(weight, x)
+    return int(lib().imq_qmv_norm_splits(probs, 1, int(x.shape[0])))
+
+
+def qmv_residual_planes(weight, x: torch.Tensor, out: ResidualPlanes, stream=None) -> int:
+    """One projection of x (M, K) as fp32 K-range planes (imq_qmv_norm_planes, no input
+    norm), left for residual_planes to add; returns the plane count."""
+    probs, n, _ = _one_problem(weight, x)
+    m = int(x.shape[0])
+    if m != out.rows or n != out.cols:
+        raise ValueError(f"the planes hold ({out.rows}, {out.cols}), the projection is ({m}, {n})")
+    if int(lib().imq_qmv_norm_splits(probs, 1, m)) > out.max_planes:
+        raise ValueError("the plan splits into more planes than the buffer holds")
+    splits = _I32(0)
+    _check(lib().imq_qmv_norm_planes(probs, 1, m, GROUP_SIZE, BITS, None, _ptr(out.data),
+                                     out.max_planes * m * n, ctypes.byref(splits), _stream(stream)))
+    out.planes = int(splits.value)
+    return out.planes
+
+
+def residual_planes(planes: ResidualPlanes, residual: torch.Tensor, next_norm: torch.Tensor | None = None,
+                    x_out: torch.Tensor | None = None, stats_out: NormStats | None = None,
+                    stream=None) -> None:
+    """qmv_norm's residual epilogue as a launch of its own (imq_residual_planes): y = the
+    planes added in order, residual += bf16(y), x_out = bf16(residual * next_norm) and the
+    per-tile sums of squares into stats_out; the bits of qmv_norm(..., residual=...)."""
+    m, n = planes.rows, planes.cols
+    if not 1 <= planes.planes <= planes.max_planes:
+        raise ValueError("no planes to add")
+    _require(residual, torch.float32, "residual")
+    if tuple(residual.shape) != (m, n) or not residual.is_contiguous():
+        raise ValueError(f"residual must be a contiguous ({m}, {n}) fp32 tensor")
+    if next_norm is not None:
+        _require(next_norm, torch.bfloat16, "next_norm")
+        if x_out is None or tuple(x_out.shape) != (m, n) or x_out.dtype != torch.bfloat16:
+            raise ValueError(f"x_out must be a ({m}, {n}) bf16 tensor")
+    rout = ResidualOut(residual.data_ptr(), n, next_norm.data_ptr() if next_norm is not None else None,
+                       x_out.data_ptr() if next_norm is not None else None, n,
+                       stats_out.ssq.data_ptr() if stats_out is not None else None,
+                       stats_out.ld if stats_out is not None else 0)
+    _check(lib().imq_residual_planes(_ptr(planes.data), planes.planes, m, n, ctypes.byref(rout),
+                                     _stream(stream)))
+    if stats_out is not None:
+        stats_out.tiles = -(-n // 64)
 
 
 def qmv_norm(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]], x: torch.Tensor,

@@ -1966,6 +1966,52 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
 }
 
+// ------------------------- the residual epilogue over K-range planes, a launch of its own
+//
+// qmv_dma_kernel's residual epilogue for a projection computed as K-range output planes
+// (imq_qmv_norm_planes): y[m][n] = the planes added in plane order from zero, then
+// h += bf16(y), x' = bf16(h * w) and each row's sum of squares of the new h over every
+// 64-column tile.  The expressions and reduction orders are those of the last K-range of
+// a split qmv_dma_kernel tile, so the two forms give the same bits.  A wavefront per
+// (row, 64-column tile), lane l on column 64 tile + l: the epilogue that one workgroup per
+// tile ran after the split counter's round trips is spread over every CU (at batch 32 the
+// o projection's launch ran 6.4 us longer per layer with it than as planes alone).
+constexpr int kResPlanes = 16;   // planes one launch adds
+constexpr int kResRowsPerGroup = 4;
+__global__ __launch_bounds__(64 * kResRowsPerGroup) void residual_planes_kernel(const float* __restrict__ planes,
+                                                                               int nplanes, int M, int N,
+                                                                               ResidualOut r) {
+  const int tile = blockIdx.x, lane = threadIdx.x & 63;
+  const int m = blockIdx.y * kResRowsPerGroup + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (m >= M) return;  // uniform per wavefront
+  const int n = tile * 64 + lane;
+  const bool in = n < N;
+  const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(planes, (uint32_t)((int64_t)nplanes * M * N * 4));
+  float v[kResPlanes];
+#pragma unroll
+  for (int q = 0; q < kResPlanes; ++q)
+    v[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        prs, in && q < nplanes ? (uint32_t)(((q * M + m) * N + n) * 4) : kPastBuffer, 0, 0));
+  const float hv = in ? r.h[(size_t)m * r.ldh + n] : 0.0f;
+  const float wn = r.w && in ? bf16_bits_to_f32(r.w[n]) : 0.0f;
+  float tot = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kResPlanes; ++q)
+    if (q < nplanes) tot += v[q];
+  const float hn = hv + bf16_bits_to_f32(f32_to_bf16_bits(tot));
+  float sq = 0.0f;
+  if (in) {
+    r.h[(size_t)m * r.ldh + n] = hn;
+    if (r.w) r.x[(size_t)m * r.ldx + n] = f32_to_bf16_bits(hn * wn);
+    sq = hn * hn;
+  }
+  if (r.ssq) {
+    sq = row16_sum(sq);
+    const float ss = (lane_value(sq, 0) + lane_value(sq, 16)) + (lane_value(sq, 32) + lane_value(sq, 48));
+    if (lane == 0) r.ssq[m * r.ld + tile] = ss;
+  }
+}
+
 // -------------------------------------------- MFMA kernel over 256-row bands (M >= 5)
 //
 // The direct-to-LDS kernel's 64-row workgroup reads, at 32 activation rows, twice as many
@@ -3523,6 +3569,35 @@ int32_t imq_qmv_norm(const imq_problem* problems, int32_t count, int32_t M, int3
                                 std::to_string(pl.bytes) + ")");
   const hipError_t e = launch_dma(a, pl, workspace, static_cast<hipStream_t>(stream), &nin, &res);
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused-norm qmv launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+int32_t imq_residual_planes(const float* planes, int32_t nplanes, int32_t M, int32_t N,
+                            const imq_residual_out* out, void* stream) {
+  if (!planes || !aligned(planes, 4)) return fail(IMQ_EINVAL, "planes must be non-null and 4-byte aligned");
+  if (!out) return fail(IMQ_EINVAL, "out must be non-null");
+  if (nplanes < 1 || nplanes > kResPlanes) return fail(IMQ_EINVAL, "nplanes must be 1..16");
+  if (M < 1 || M > IMQ_MAX_ROWS) return fail(IMQ_EINVAL, "M must be 1..32");
+  if (N < 1) return fail(IMQ_EINVAL, "N must be >= 1");
+  if ((int64_t)nplanes * M * N * 4 >= ((int64_t)1 << 31)) return fail(IMQ_EUNSUPPORTED, "planes of 2 GiB or more");
+  if (!out->h || !aligned(out->h, 4)) return fail(IMQ_EINVAL, "residual h must be non-null and 4-byte aligned");
+  if (M > 1 && out->ldh < N) return fail(IMQ_EINVAL, "residual ldh must be >= N");
+  const int tiles = (N + 63) / 64;
+  if (out->weight) {
+    if (!aligned(out->weight, 2) || !out->x || !aligned(out->x, 2))
+      return fail(IMQ_EINVAL, "norm weight and x' must be non-null and 2-byte aligned");
+    if (M > 1 && out->ldx < N) return fail(IMQ_EINVAL, "x' ldx must be >= N");
+  }
+  if (out->ssq && (!aligned(out->ssq, 4) || out->ld < tiles || out->ld % 4))
+    return fail(IMQ_EINVAL, "residual ssq must be 4-byte aligned with ld >= ceil(N / 64), a multiple of 4");
+  int32_t code;
+  if (!current_device(&code)) return code;
+  const ResidualOut r{out->h, M > 1 ? out->ldh : N, out->weight, out->x, M > 1 ? out->ldx : N, out->ssq,
+                      out->ld, 0};
+  hipLaunchKernelGGL(residual_planes_kernel, dim3(tiles, (M + kResRowsPerGroup - 1) / kResRowsPerGroup),
+                     dim3(64 * kResRowsPerGroup), 0, static_cast<hipStream_t>(stream), planes, nplanes, M, N, r);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("residual planes launch failed: ") + hipGetErrorString(e));
   return ok();
 }
 

@@ -150,6 +150,9 @@ class DecodeState:
         self.stats_in = _native.NormStats(batch, c.hidden, device)
         self.stats_post = _native.NormStats(batch, c.hidden, device)
         self.qkv_planes = _native.QkvPlanes(batch, c.heads, c.kv_heads, device)
+        # the o and down projections' K-range planes (both hidden wide), added into h by
+        # their own epilogue launch
+        self.res_planes = _native.ResidualPlanes(batch, c.hidden, device)
         self.workspace = torch.empty(_native.attention_workspace(batch, c.heads, self.max_len),
                                      dtype=torch.float32, device=device)
         self.attn_counters = torch.zeros(batch * c.kv_heads, dtype=torch.int32, device=device)
@@ -208,6 +211,19 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
     return s.logits
 
 
+def _residual_projection(weight, x, state: DecodeState, next_norm, x_out, stats_out, stream) -> None:
+    """h += bf16(x @ W.T), x_out = bf16(h * next_norm) and its per-tile sums of squares: as
+    K-range planes and an epilogue launch when the projection splits, else in one launch."""
+    n, s = _native, state
+    if 2 <= n.residual_split_planes(weight, x) <= s.res_planes.max_planes:
+        n.qmv_residual_planes(weight, x, s.res_planes, stream=stream)
+        n.residual_planes(s.res_planes, s.h, next_norm=next_norm, x_out=x_out, stats_out=stats_out,
+                          stream=stream)
+    else:
+        n.qmv_norm([weight], x, residual=s.h, next_norm=next_norm, x_out=x_out, stats_out=stats_out,
+                   stream=stream)
+
+
 def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream=None) -> torch.Tensor:
     """decode_step with every RMSNorm but the last folded into the launches around it, five
     launches per layer:
@@ -218,15 +234,20 @@ def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream
                                                    the K-ranges' partials as output planes)
             attention                              imq_attention_fused_planes (adds the
                                                    planes as it reads q, k and v)
-            h += o @ Wo.T; x' = bf16(h * w_post)   imq_qmv_norm (residual epilogue: h, x'
-                                                   and the per-tile sums of squares)
+            h += o @ Wo.T; x' = bf16(h * w_post)   imq_qmv_norm_planes + imq_residual_planes
+                                                   (the K-ranges as planes, then the residual
+                                                   epilogue: h, x' and the per-tile sums of
+                                                   squares)
             act = silu(inv * g) * (inv * u)        imq_qmv_gate_up_silu_norm
-            h += act @ Wd.T; x' = bf16(h * w_in')  imq_qmv_norm (residual epilogue; the last
-                                                   layer updates h only)
+            h += act @ Wd.T; x' = bf16(h * w_in')  as for o (the last layer updates h only)
         logits = rms_norm(h) @ E.T                 imq_add_rmsnorm, imq_qmv
 
     inv is each row's 1 / rms(h), so inv * (x' W^T) is rms_norm(h) W^T up to the place of one
-    bf16 rounding (x' is rounded before the scaling instead of after it)."""
+    bf16 rounding (x' is rounded before the scaling instead of after it).  The o and down
+    projections and their epilogue are two launches when the projection splits K into 2 to
+    16 ranges (the split launch's counter and reload round trips, and an epilogue run by one
+    workgroup per 64 columns, cost more than a launch), else one (imq_qmv_norm with the
+    epilogue); both forms give the same bits."""
     c, s = weights.config, state
     n = _native
     n.embed(*weights.embed, s.tokens, s.h, stream=stream)
@@ -237,15 +258,12 @@ def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream
         n.attention_fused_planes(s.qkv_planes, layer["q_norm"], layer["k_norm"], s.positions,
                                  s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len,
                                  c.theta, c.eps, s.workspace, s.attn_counters, stream=stream)
-        n.qmv_norm([layer["o"]], s.attn, residual=s.h, next_norm=layer["post_norm"], x_out=s.x,
-                   stats_out=s.stats_post, stream=stream)
+        _residual_projection(layer["o"], s.attn, s, layer["post_norm"], s.x, s.stats_post, stream)
         n.gate_up_silu_norm(layer["gate"], layer["up"], s.x, s.act, s.stats_post, c.eps,
                             stream=stream)
         last = i + 1 == len(weights.layers)
-        n.qmv_norm([layer["down"]], s.act, residual=s.h,
-                   next_norm=None if last else weights.layers[i + 1]["input_norm"],
-                   x_out=None if last else s.x, stats_out=None if last else s.stats_in,
-                   stream=stream)
+        _residual_projection(layer["down"], s.act, s, None if last else weights.layers[i + 1]["input_norm"],
+                             None if last else s.x, None if last else s.stats_in, stream)
     n.add_rmsnorm(s.h, weights.norm, s.x, c.eps, stream=stream)
     n.qmv(*weights.embed, s.x, out=s.logits, stream=stream)
     return s.logits

@@ -76,6 +76,28 @@ def test_multi_refuses_too_many_vectors(lib):
                              0, None) == _native.IMQ_EUNSUPPORTED
 
 
+def _residual_planes(lib, **over):
+    args = dict(planes=1 << 20, nplanes=4, M=32, N=2560, h=1 << 22, ldh=2560, weight=1 << 24,
+                x=1 << 25, ldx=2560, ssq=1 << 26, ld=40)
+    args.update(over)
+    P = ctypes.c_void_p
+    out = _native.ResidualOut(args["h"], args["ldh"], args["weight"], args["x"], args["ldx"],
+                              args["ssq"], args["ld"])
+    return lib.imq_residual_planes(P(args["planes"]), args["nplanes"], args["M"], args["N"],
+                                   ctypes.byref(out), None)
+
+
+@pytest.mark.parametrize("over", [
+    {"planes": 0}, {"planes": (1 << 20) + 2}, {"nplanes": 0}, {"nplanes": 17}, {"M": 0}, {"M": 33},
+    {"N": 0}, {"h": 0}, {"ldh": 100}, {"x": 0}, {"ldx": 100}, {"ld": 38}, {"ld": 42},
+    {"nplanes": 16, "M": 32, "N": 1 << 20},
+])
+def test_residual_planes_refusals(lib, over):
+    """imq_residual_planes refuses malformed calls before it looks for a device."""
+    code = _residual_planes(lib, **over)
+    assert code in (_native.IMQ_EINVAL, _native.IMQ_EUNSUPPORTED), (over, code)
+
+
 def test_python_side_validates_before_the_abi():
     import torch
     w = torch.zeros((8, 8), dtype=torch.int32)

@@ -209,6 +209,48 @@ def test_residual_epilogue(native, oracle, n, k, m):
     assert torch.allclose(st.ssq[:, :tiles].double(), ss, rtol=2e-6, atol=0)
 
 
+@pytest.mark.parametrize("n,k,m", [(2560, 4096, 32), (2560, 9728, 32), (2560, 4096, 5),
+                                   (2560, 9728, 3), (1000, 4096, 8), (2560, 4096, 1)])
+def test_residual_planes_same_bits(native, oracle, n, k, m):
+    """The projection as K-range planes (imq_qmv_norm_planes) and the residual epilogue as a
+    launch of its own (imq_residual_planes) give the bits of imq_qmv_norm's residual epilogue:
+    h, x' and the per-tile sums of squares, with and without the next norm (a ragged last
+    tile at N = 1000)."""
+    probs, weights, x = _weights(oracle, [(n, k)], m, oracle.SEED_BASE + 2350 + m)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2350 + m)
+    h = torch.randn((m, n), device="cuda", generator=g) * 4
+    w = (torch.rand(n, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+    count = native.residual_split_planes(weights[0], x)
+    announce("residual planes", n, k, m, count)
+    assert 1 <= count <= native.RESIDUAL_MAX_PLANES
+    fused_h, fused_x = h.clone(), torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    fused_st = native.NormStats(m, n, "cuda")
+    native.qmv_norm(weights, x, residual=fused_h, next_norm=w, x_out=fused_x, stats_out=fused_st)
+    planes = native.ResidualPlanes(m, n, "cuda")
+    assert native.qmv_residual_planes(weights[0], x, planes) == count
+    two_h, two_x = h.clone(), torch.full((m, n), 7, dtype=torch.bfloat16, device="cuda")
+    two_st = native.NormStats(m, n, "cuda")
+    native.residual_planes(planes, two_h, next_norm=w, x_out=two_x, stats_out=two_st)
+    only_h = h.clone()
+    native.residual_planes(planes, only_h)  # h only
+    torch.cuda.synchronize()
+    assert torch.equal(two_h, fused_h)
+    assert torch.equal(only_h, fused_h)
+    assert torch.equal(two_x, fused_x)
+    tiles = -(-n // 64)
+    assert two_st.tiles == fused_st.tiles == tiles
+    assert torch.equal(two_st.ssq[:, :tiles], fused_st.ssq[:, :tiles])
+    # and the planes hold the projection: their sum in plane order, rounded, is within the
+    # oracle's bar
+    tot = torch.zeros((m, n), device="cuda")
+    for sp in range(count):
+        tot = tot + planes.view()[sp]
+    v, lit = oracle.check_bf16_both(bf16_bits(tot.to(torch.bfloat16)), probs[0].w, probs[0].s, probs[0].b,
+                                    probs[0].x)
+    assert v.ok and lit.ok, (v.detail, lit.detail)
+
+
 def test_residual_epilogue_forced_plan_matches_oracle(native, oracle):
     n, k, m = 256, 512, 8  # the usual plan would not take the direct-to-LDS kernel here
     probs, weights, x = _weights(oracle, [(n, k)], m, oracle.SEED_BASE + 2400)
