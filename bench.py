@@ -615,7 +615,8 @@ def _short(name: str) -> str:
                    "qmv_mma_staged_kernel", "qmv_mma_kernel", "qmv_dma_kernel", "qmv_band_kernel", "xprep_kernel",
                    "qmv_xs_kernel", "qmv_mr_kernel", "clear_words_kernel",
                    "dequant_kernel", "embed_kernel", "add_rmsnorm_kernel", "qk_norm_rope_kernel",
-                   "attention_partial_kernel", "attention_combine_kernel", "silu_mul_kernel"):
+                   "attention_partial_kernel", "attention_combine_kernel", "silu_mul_kernel",
+                   "residual_planes_kernel"):
         if marker in name:
             return name[name.index(marker):].split("(")[0]
     if "direct_copy_kernel" in name:
