@@ -398,6 +398,22 @@ def bench_prefill(torch, weights, device, gen, count: int = CONTEXT, repeats: in
                     "head at the last position only"}
 
 
+def _epilogue_launches(weights, batch: int) -> int:
+    """Residual-epilogue launches per layer of the fused-norm step at `batch` rows: one after
+    each of o and down where it splits K (decode._residual_projection)."""
+    import torch
+
+    from ironmule_amd import _native
+    layer = weights.layers[0]
+    count = 0
+    c = weights.config
+    for name, k in (("o", c.heads * c.head_dim), ("down", c.intermediate)):
+        x = torch.empty((batch, k), dtype=torch.bfloat16, device=layer[name][0].device)
+        if 2 <= _native.residual_split_planes(layer[name], x) <= _native.RESIDUAL_MAX_PLANES:
+            count += 1
+    return count
+
+
 def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, device="cuda:0",
                  seed: int = SEED + 4, prefill_tokens: bool = True):
     """Full synthetic Qwen3-4B decode step (36 layers of 4-bit projections + the 151,936-
@@ -421,9 +437,10 @@ def bench_decode(torch, batches=(1, 32), steps: int = 30, warmup: int = 5, devic
         stream = torch.cuda.Stream(device=device)
         # launches per step: the embedding, the layers, the final norm and the head; from
         # FUSED_NORM_ROWS requests the RMSNorms run inside the projections (five launches per
-        # layer and one more for the first layer's input norm), below it eight per layer
+        # layer, the residual epilogues of o and down as two more where those projections
+        # split K, and one more for the first layer's input norm), below it eight per layer
         # (seven from 5 requests, where gate/up and SiLU * up are one launch)
-        per_layer = 5 if b >= FUSED_NORM_ROWS else (7 if b >= 5 else 8)
+        per_layer = (5 + _epilogue_launches(weights, b)) if b >= FUSED_NORM_ROWS else (7 if b >= 5 else 8)
         extra = 4 if b >= FUSED_NORM_ROWS else 3
         paths = {"per_kernel": (lambda: decode_step(weights, state, stream=stream),
                                 extra + cfg.layers * per_layer)}

@@ -19,7 +19,8 @@ continuous-batched requests, each with its own KV slot and position:
     logits = rms_norm(h) @ E.T                 imq_add_rmsnorm, imq_qmv (fp32, tied head)
 
 for 1 and 2 requests; from FUSED_NORM_ROWS (3) requests the same step runs with the RMSNorms
-folded into the projections (`_decode_step_fused_norms`, five launches per layer).
+folded into the projections (`_decode_step_fused_norms`: five projection or attention
+launches per layer, and an epilogue launch after each of o and down where they split K).
 
 All buffers are allocated once per (model, batch size) in `DecodeState`; a step only
 launches kernels, so it can be captured in a HIP graph and replayed.  Every launch goes
