@@ -1849,6 +1849,10 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
 #pragma unroll
     for (int e = 0; e < 16; ++e) red[((wave * 2 + t) * 16 + e) * 64 + lane] = acc[t][e];
   __syncthreads();
+  // with an input norm, lane m of every wavefront holds row m's 1/rms (norm_row_inv of the
+  // pair sums the barrier above published); an output of row m reads it from that lane
+  const float inv_lane = norm_in && lane < 32 ? norm_row_inv(d.nin, nsum, lane) : 1.0f;
+  auto row_inv = [&](int m) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_lane), m)); };
   // thread (wave, nl) adds rows m = wave, wave + W, ... of tile row nl; every LDS read before
   // the first store
   constexpr int MI = (32 + W - 1) / W;
@@ -1874,7 +1878,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
       const int m = wave + i * W;
       sq[i] = 0.0f;
       if (m >= M) continue;
-      const float y = norm_in ? v[i] * norm_row_inv(d.nin, nsum, m) : v[i];
+      const float y = norm_in ? v[i] * row_inv(m) : v[i];
       if (!res) {
         if (n < N) store_y(a, P, m, n, y);
         continue;
@@ -1924,7 +1928,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   for (int i = 0; i < MI; ++i) {
     const int m = wave + i * W;
     if (m < M && n < N) {
-      const float v = d.planes && norm_in ? sums[i] * norm_row_inv(d.nin, nsum, m) : sums[i];
+      const float v = d.planes && norm_in ? sums[i] * row_inv(m) : sums[i];
       store_b32_sc1(prs, (uint32_t)(((split * M + m) * N + n) * 4), __float_as_uint(v));
     }
   }
