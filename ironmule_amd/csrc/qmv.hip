@@ -1982,6 +1982,7 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
 // o projection's launch ran 6.4 us longer per layer with it than as planes alone).
 constexpr int kResPlanes = 16;   // planes one launch adds
 constexpr int kResRowsPerGroup = 4;
+template <int S>  // at most S planes: the loads past the call's planes are not issued
 __global__ __launch_bounds__(64 * kResRowsPerGroup) void residual_planes_kernel(const float* __restrict__ planes,
                                                                                int nplanes, int M, int N,
                                                                                ResidualOut r) {
@@ -1991,16 +1992,16 @@ __global__ __launch_bounds__(64 * kResRowsPerGroup) void residual_planes_kernel(
   const int n = tile * 64 + lane;
   const bool in = n < N;
   const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(planes, (uint32_t)((int64_t)nplanes * M * N * 4));
-  float v[kResPlanes];
+  float v[S];
 #pragma unroll
-  for (int q = 0; q < kResPlanes; ++q)
+  for (int q = 0; q < S; ++q)
     v[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         prs, in && q < nplanes ? (uint32_t)(((q * M + m) * N + n) * 4) : kPastBuffer, 0, 0));
   const float hv = in ? r.h[(size_t)m * r.ldh + n] : 0.0f;
   const float wn = r.w && in ? bf16_bits_to_f32(r.w[n]) : 0.0f;
   float tot = 0.0f;
 #pragma unroll
-  for (int q = 0; q < kResPlanes; ++q)
+  for (int q = 0; q < S; ++q)
     if (q < nplanes) tot += v[q];
   const float hn = hv + bf16_bits_to_f32(f32_to_bf16_bits(tot));
   float sq = 0.0f;
@@ -3598,8 +3599,14 @@ int32_t imq_residual_planes(const float* planes, int32_t nplanes, int32_t M, int
   if (!current_device(&code)) return code;
   const ResidualOut r{out->h, M > 1 ? out->ldh : N, out->weight, out->x, M > 1 ? out->ldx : N, out->ssq,
                       out->ld, 0};
-  hipLaunchKernelGGL(residual_planes_kernel, dim3(tiles, (M + kResRowsPerGroup - 1) / kResRowsPerGroup),
-                     dim3(64 * kResRowsPerGroup), 0, static_cast<hipStream_t>(stream), planes, nplanes, M, N, r);
+  const dim3 grid(tiles, (M + kResRowsPerGroup - 1) / kResRowsPerGroup), block(64 * kResRowsPerGroup);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (nplanes <= 4)
+    hipLaunchKernelGGL(residual_planes_kernel<4>, grid, block, 0, st, planes, nplanes, M, N, r);
+  else if (nplanes <= 8)
+    hipLaunchKernelGGL(residual_planes_kernel<8>, grid, block, 0, st, planes, nplanes, M, N, r);
+  else
+    hipLaunchKernelGGL(residual_planes_kernel<kResPlanes>, grid, block, 0, st, planes, nplanes, M, N, r);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("residual planes launch failed: ") + hipGetErrorString(e));
   return ok();
