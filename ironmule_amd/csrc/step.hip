@@ -548,14 +548,97 @@ __device__ __forceinline__ uint16_t ld16_sc1(const uint16_t* base, uint32_t byte
   return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(base, bytes), off, 0, kSc1);
 }
 
-template <bool kStaged, typename SRef, int W = kAttnWaves>
+// kPlanes (staged launches only): q, k and v arrive as the fp32 K-range planes of the q/k/v
+// launch (Stage::qkv) rather than as bf16 rows; one instantiation per form, so that each has
+// one sequence of loads and its waits count them exactly.
+template <bool kStaged, typename SRef, int W = kAttnWaves, bool kPlanes = false>
 __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs& a, uint4* smem) {
   AttnLdsT<W>& L = *reinterpret_cast<AttnLdsT<W>*>(smem);
   constexpr int kRounds = (8 + W - 1) / W;  // query heads (at most 8) per wavefront
   const int splits = S.splits, Hkv = S.Hkv, Hq = S.Hq, G = Hq / Hkv;
   const int s = task % splits, kvh = (task / splits) % Hkv, b = task / (splits * Hkv);
   const int tid = task_tid(), wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int pos = uni(S.positions[b]), slot = uni(S.slots[b]);
+  // Every load that needs only the task goes out first: the position and slot, then (staged)
+  // q, the new key and value (or their planes) and the norm weights.  The K/V loads need the
+  // position and follow as soon as it has landed; the q/k/v values are used only after them
+  // (loads return in issue order, so each wait covers exactly the loads before it).  With
+  // the q/k/v values first read after the position, the first K/V load left 4 us into the
+  // launch at batch 32.
+  const int pos_in = S.positions[b], slot_in = S.slots[b];
+  const float eps = S.eps;
+  const uint32_t qbytes = (uint32_t)(b + 1) * Hq * kD * 2u;
+  const uint32_t kvbytes = (uint32_t)(b + 1) * Hkv * kD * 2u;
+  const uint32_t kvoff = (uint32_t)((b * Hkv + kvh) * kD) * 2u;
+  auto ld16 = [&](const uint16_t* p, uint32_t bytes, uint32_t off) -> uint32_t {
+    return kStaged ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p, bytes), off, 0, 0)
+                   : (uint32_t)ld16_sc1(p, bytes, off);
+  };
+  // q of the task's heads (a wavefront per head: element e of head g at lane e % 64, slot
+  // e / 64) and, on wavefront 0, the new key and value: as bf16 values, or as the fp32
+  // planes of a q/k/v launch that left its K-ranges to the reader (added below in plane
+  // order from zero and rounded to bf16).  Loads a wavefront does not need read past their
+  // buffer (zeros, no traffic), so every wavefront issues the same loads.
+  constexpr bool use_planes = kStaged && kPlanes;
+  const int np = S.qkv_splits, prow = S.qkv_rows;
+  const int nq = Hq * kD, nkv = Hkv * kD;
+  const __amdgpu_buffer_rsrc_t qkv_rs = buffer_rsrc(S.qkv, use_planes ? (uint32_t)(3 * S.qkv_pstride * 4) : 0u);
+  // (bit 31 of an offset puts it past every buffer here, every buffer being under 2 GiB.  The
+  // flag is made opaque to the optimizer, which would otherwise branch on it, and a load into
+  // a register another path also loads then waits for every load before it.)
+  auto plane_loads = [&](int pi, int nw, int elem, bool need, float (&v)[kMaxQkvPlanes]) {
+    uint32_t skip = need ? 0u : kPastBuffer;
+    asm("" : "+s"(skip));
+#pragma unroll
+    for (int sp = 0; sp < kMaxQkvPlanes; ++sp) {
+      const uint32_t off = (uint32_t)(pi * S.qkv_pstride + (int64_t)(sp * prow + b) * nw + elem) * 4u;
+      v[sp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(qkv_rs, off | (sp < np ? skip : kPastBuffer), 0, 0));
+    }
+  };
+  auto plane_sum = [&](const float (&v)[kMaxQkvPlanes]) -> uint32_t {
+    float t = 0.0f;
+#pragma unroll
+    for (int sp = 0; sp < kMaxQkvPlanes; ++sp)
+      if (sp < np) t += v[sp];
+    return to_bf(t);
+  };
+  uint32_t qx[kRounds][2], kx[2] = {0u, 0u}, vx[2] = {0u, 0u};
+  float pq[kRounds][2][kMaxQkvPlanes], pk[2][kMaxQkvPlanes], pv[2][kMaxQkvPlanes];
+  auto fetch_qkv = [&]() __attribute__((always_inline)) {
+    if (use_planes) {
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        const int g = wave + W * r;
+        const int e0 = (kvh * G + (g < G ? g : 0)) * kD;
+        plane_loads(0, nq, e0 + lane, g < G, pq[r][0]);
+        plane_loads(0, nq, e0 + lane + 64, g < G, pq[r][1]);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        plane_loads(1, nkv, kvh * kD + lane + 64 * h, wave == 0, pk[h]);
+        plane_loads(2, nkv, kvh * kD + lane + 64 * h, wave == 0, pv[h]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        const int g = wave + W * r;
+        uint32_t skip = g < G ? 0u : kPastBuffer;
+        asm("" : "+s"(skip));
+        const uint32_t off = (uint32_t)((b * Hq + kvh * G + (g < G ? g : 0)) * kD) * 2u;
+        qx[r][0] = ld16(S.q, qbytes, (off + 2u * lane) | skip);
+        qx[r][1] = ld16(S.q, qbytes, (off + 2u * (lane + 64)) | skip);
+      }
+      uint32_t skip = wave == 0 ? 0u : kPastBuffer;
+      asm("" : "+s"(skip));
+      kx[0] = ld16(S.k, kvbytes, (kvoff + 2u * lane) | skip);
+      kx[1] = ld16(S.k, kvbytes, (kvoff + 2u * (lane + 64)) | skip);
+      vx[0] = ld16(S.v, kvbytes, (kvoff + 2u * lane) | skip);
+      vx[1] = ld16(S.v, kvbytes, (kvoff + 2u * (lane + 64)) | skip);
+    }
+  };
+  if (kStaged) fetch_qkv();
+  const float qn0 = bf(S.q_norm[lane]), qn1 = bf(S.q_norm[lane + 64]);
+  const float kn0 = bf(S.k_norm[lane]), kn1 = bf(S.k_norm[lane + 64]);
+  const int pos = uni(pos_in), slot = uni(slot_in);
   const bool slot_ok = slot >= 0 && slot < S.num_slots;
   const bool write_ok = slot_ok && pos >= 0 && pos < S.capacity;
   int len = pos + 1;
@@ -606,77 +689,45 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   };
   const int start0 = first + kUnit * wave;
 
-  // q of the task's heads (a wavefront per head), the new key and value and the norm
-  // weights.  A staged launch reads them first (its inputs are complete; loads return in
-  // issue order, so the rotation below waits only for these) and then puts its first chunk
-  // in flight; the persistent form puts the chunk in flight, waits for its input stage and
-  // reads them through sc1.
+  // The persistent form puts the chunk in flight, waits for its input stage and reads q,
+  // k and v through sc1; the staged form has them in flight already.
   if (!kStaged) {
     load_k(start0);
     load_v(start0);
     if (!wait_stage(a, S.wait, (uint32_t)S.wait_count)) return false;
-  }
-  const float eps = S.eps;
-  const uint32_t qbytes = (uint32_t)(b + 1) * Hq * kD * 2u;
-  const uint32_t kvbytes = (uint32_t)(b + 1) * Hkv * kD * 2u;
-  const uint32_t kvoff = (uint32_t)((b * Hkv + kvh) * kD) * 2u;
-  auto ld16 = [&](const uint16_t* p, uint32_t bytes, uint32_t off) -> uint32_t {
-    return kStaged ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p, bytes), off, 0, 0)
-                   : (uint32_t)ld16_sc1(p, bytes, off);
-  };
-  uint32_t qx[kRounds][2], kx[2] = {0u, 0u}, vx[2] = {0u, 0u};
-  if (kStaged && S.qkv != nullptr) {
-    // the planes of element `elem` of problem `pi` (width nw) for request b, added in plane
-    // order from zero and rounded to bf16: every plane's load issued before the first add
-    const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(S.qkv, (uint32_t)(3 * S.qkv_pstride * 4));
-    const int np = S.qkv_splits, rows = S.qkv_rows;
-    auto planes = [&](int pi, int nw, int elem) -> uint32_t {
-      float v[kMaxQkvPlanes];
-#pragma unroll
-      for (int sp = 0; sp < kMaxQkvPlanes; ++sp) {
-        const uint32_t off = (uint32_t)(pi * S.qkv_pstride + (int64_t)(sp * rows + b) * nw + elem) * 4u;
-        v[sp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, sp < np ? off : kPastBuffer, 0, 0));
-      }
-      float t = 0.0f;
-#pragma unroll
-      for (int sp = 0; sp < kMaxQkvPlanes; ++sp)
-        if (sp < np) t += v[sp];
-      return to_bf(t);
-    };
-    const int nq = Hq * kD, nkv = Hkv * kD;
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-      const int g = wave + W * r;
-      const int e0 = (kvh * G + (g < G ? g : 0)) * kD;
-      qx[r][0] = g < G ? planes(0, nq, e0 + lane) : 0u;
-      qx[r][1] = g < G ? planes(0, nq, e0 + lane + 64) : 0u;
-    }
-    if (wave == 0) {
-      kx[0] = planes(1, nkv, kvh * kD + lane);
-      kx[1] = planes(1, nkv, kvh * kD + lane + 64);
-      vx[0] = planes(2, nkv, kvh * kD + lane);
-      vx[1] = planes(2, nkv, kvh * kD + lane + 64);
-    }
+    fetch_qkv();
   } else {
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-      const int g = wave + W * r;
-      const uint32_t off = (uint32_t)((b * Hq + kvh * G + (g < G ? g : 0)) * kD) * 2u;
-      qx[r][0] = g < G ? ld16(S.q, qbytes, off + 2u * lane) : 0u;
-      qx[r][1] = g < G ? ld16(S.q, qbytes, off + 2u * (lane + 64)) : 0u;
-    }
-    if (wave == 0) {
-      kx[0] = ld16(S.k, kvbytes, kvoff + 2u * lane);
-      kx[1] = ld16(S.k, kvbytes, kvoff + 2u * (lane + 64));
-      vx[0] = ld16(S.v, kvbytes, kvoff + 2u * lane);
-      vx[1] = ld16(S.v, kvbytes, kvoff + 2u * (lane + 64));
-    }
-  }
-  const float qn0 = bf(S.q_norm[lane]), qn1 = bf(S.q_norm[lane + 64]);
-  const float kn0 = bf(S.k_norm[lane]), kn1 = bf(S.k_norm[lane + 64]);
-  if (kStaged) {
     load_k(start0);
     load_v(start0);
+    // q, k and v are first used here, behind the K/V loads: an empty asm that reads and
+    // writes each value (ordered after the loads by its memory clobber) keeps the compiler
+    // from adding the planes, and so waiting for them, before those loads are issued
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        asm volatile("" : "+v"(qx[r][h]) :: "memory");
+#pragma unroll
+        for (int sp = 0; sp < kMaxQkvPlanes; ++sp) asm volatile("" : "+v"(pq[r][h][sp]) :: "memory");
+      }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      asm volatile("" : "+v"(kx[h]), "+v"(vx[h]) :: "memory");
+#pragma unroll
+      for (int sp = 0; sp < kMaxQkvPlanes; ++sp) asm volatile("" : "+v"(pk[h][sp]), "+v"(pv[h][sp]) :: "memory");
+    }
+  }
+  if (use_planes) {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      qx[r][0] = plane_sum(pq[r][0]);
+      qx[r][1] = plane_sum(pq[r][1]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      kx[h] = plane_sum(pk[h]);
+      vx[h] = plane_sum(pv[h]);
+    }
   }
   const float inv_freq = exp2f(-(float)lane * (S.log2_theta / 64.0f));
   float sn, cs;
@@ -1062,10 +1113,10 @@ __global__ __launch_bounds__(kThreads) void qmv_stage_kernel(const Stage S, Step
   qmv_task<NCH, XR, XSRC, EPI, true, const Stage&>(S, blockIdx.x, a, smem);
 }
 
-template <int W>
+template <int W, bool kPlanes>
 __global__ __launch_bounds__(64 * W) void attention_stage_kernel(const Stage S, StepArgs a) {
   extern __shared__ uint4 smem[];
-  attention_task<true, const Stage&, W>(S, blockIdx.x, a, smem);
+  attention_task<true, const Stage&, W, kPlanes>(S, blockIdx.x, a, smem);
 }
 
 #undef IMQ_QMV_SHAPES_X2
@@ -1357,24 +1408,31 @@ int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
   memset(&a, 0, sizeof(a));
   a.ntasks = A.count;
   a.staged = 1;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
   if (wide) {
     const size_t lds = (sizeof(AttnLdsT<kWideWaves>) + 15) & ~(size_t)15;
-    // the launch's LDS is above the default dynamic limit: raised once per device
+    // the launch's LDS is above the default dynamic limit: raised once per device, for both
+    // forms of the kernel
     static std::atomic<bool> raised[imq_rt::kMaxDevices];
     if (!raised[device].load(std::memory_order_acquire)) {
-      const hipError_t attr = hipFuncSetAttribute(
-          reinterpret_cast<const void*>(attention_stage_kernel<kWideWaves>),
-          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (attr != hipSuccess)
-        return fail(IMQ_ELAUNCH, std::string("fused attention LDS size: ") + hipGetErrorString(attr));
+      for (const void* fn : {reinterpret_cast<const void*>(attention_stage_kernel<kWideWaves, true>),
+                             reinterpret_cast<const void*>(attention_stage_kernel<kWideWaves, false>)}) {
+        const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess)
+          return fail(IMQ_ELAUNCH, std::string("fused attention LDS size: ") + hipGetErrorString(attr));
+      }
       raised[device].store(true, std::memory_order_release);
     }
-    hipLaunchKernelGGL(attention_stage_kernel<kWideWaves>, dim3(A.count), dim3(64 * kWideWaves), lds,
-                       static_cast<hipStream_t>(stream), A, a);
+    if (planes)
+      hipLaunchKernelGGL((attention_stage_kernel<kWideWaves, true>), dim3(A.count), dim3(64 * kWideWaves), lds, st, A, a);
+    else
+      hipLaunchKernelGGL((attention_stage_kernel<kWideWaves, false>), dim3(A.count), dim3(64 * kWideWaves), lds, st, A, a);
   } else {
     const size_t lds = (sizeof(AttnLds) + 15) & ~(size_t)15;
-    hipLaunchKernelGGL(attention_stage_kernel<kAttnWaves>, dim3(A.count), dim3(kThreads), lds,
-                       static_cast<hipStream_t>(stream), A, a);
+    if (planes)
+      hipLaunchKernelGGL((attention_stage_kernel<kAttnWaves, true>), dim3(A.count), dim3(kThreads), lds, st, A, a);
+    else
+      hipLaunchKernelGGL((attention_stage_kernel<kAttnWaves, false>), dim3(A.count), dim3(kThreads), lds, st, A, a);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused attention launch: ") + hipGetErrorString(e));
@@ -1679,7 +1737,7 @@ int32_t imq_program_launch_staged(imq_program* p, void* stream) {
     const dim3 grid(S.count), block(kThreads);
     const size_t lds = p->stage_lds[i];
     if (S.kind == kKindAttention) {
-      hipLaunchKernelGGL(attention_stage_kernel<kAttnWaves>, grid, block, lds, st, S, a);
+      hipLaunchKernelGGL((attention_stage_kernel<kAttnWaves, false>), grid, block, lds, st, S, a);
       continue;
     }
 #define IMQ_STAGE_CASE(NCH, XR, XSRC, EPI, SHAPE)                                              \
