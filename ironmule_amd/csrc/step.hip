@@ -356,12 +356,17 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
 #pragma unroll
       for (int t = 0; t < NQ; ++t) nq[t] = load_act<!kStaged>(qr, 16u * (tid + kThreads * t));
     }
+    // (branch-free: a lane that owns no row reads past the buffers, zeros; under a branch
+    // the compiler widened the weight inside it and waited there for every earlier load,
+    // x's included, before issuing any of the tile's weights)
     if constexpr (EPI == kEpiResidual || kResNorm) {
-      if (owner) hres = kStaged ? S.h[row] : ldf_sc1(S.h + row);
+      const __amdgpu_buffer_rsrc_t hr = buffer_rsrc(S.h, (uint32_t)N * 4u);
+      const uint32_t off = owner ? 4u * (uint32_t)row : kPastBuffer;
+      hres = __uint_as_float(kStaged ? __builtin_amdgcn_raw_buffer_load_b32(hr, off, 0, 0) : load_b32_sc1(hr, off));
     }
-    if constexpr (kResNorm) {
-      if (owner) wnext = S.norm_next[row];
-    }
+    if constexpr (kResNorm)
+      wnext = __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(S.norm_next, (uint32_t)N * 2u),
+                                                   owner ? 2u * (uint32_t)row : kPastBuffer, 0, 0);
   };
   auto load_norm_weight = [&]() {
     if constexpr (XSRC == kXNorm) {
@@ -401,6 +406,9 @@ __device__ __forceinline__ bool qmv_task(SRef S, int task, const StepArgs& a, ui
     const int kc = j + (i << sh);
     wv[i] = load_b128_nt(wrsrc, (i < nch && kc < C && row < N) ? wrow + 16u * kc : kPastBuffer);
   }
+  // every load is issued before the first wait: left to itself the scheduler moves the x
+  // staging below (and the wait for x it needs) ahead of the last weight chunks' loads
+  __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (!kStaged) {
     load_norm_weight();
