@@ -1970,6 +1970,215 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   if (tid == 0) st_sc1(cnt, 0u);  // ready for the next call
 }
 
+// ------------------- gate/up with SiLU * up over bands of rows (direct-to-LDS, M <= 32)
+//
+// The gate/up launch with the input RMSNorm folded in, laid out so that every CU streams
+// about the same share of the two weights, once, with no K-split partials to add across
+// workgroups.  The weights' rows are U = ceil(N / 8) units of 8; workgroup i of nwg owns
+// units [i U / nwg, (i + 1) U / nwg) (at most pr::kMaxUnits), i.e. R gate rows and the same
+// R up rows from row r0, over the whole K, with W = K / 256 wavefronts, wavefront w owning
+// groups [4 w, 4 w + 4).  The 2R rows are the workgroup's slots (slot s < R: gate row
+// r0 + s, else up row r0 + s - R), 32 to an MFMA block.
+//   * Weights go from memory to LDS by the buffer loads' LDS path, an instruction per 8
+//     slots x 128 bytes (a slot's four groups: whole lines), swizzled as in qmv_dma_kernel,
+//     in block order, block b into LDS array b: the compiler tells the arrays apart, so a
+//     wavefront's reads of block b wait for block b's loads only, and it computes block b
+//     as soon as they have landed.
+//   * Scales and biases: lane (j, kb) loads the 8 bytes of slot 32 b + j's four groups of
+//     each array straight into registers, from the gate or the up array by its own address
+//     (slots past the rows read a valid row: their columns are never stored).
+//   * x: lane (m, kb) holds the 64 bytes x[m][64 g + 32 kb ..+32] of each of its groups g,
+//     as in qmv_dma_kernel; all four groups are in flight before the first weight wait.
+// Per group and block: P = sum_k v x from four bf16 MFMAs (v = 1 + q/16), acc += 16 s P;
+// per pair of groups one v_mfma_f32_32x32x2_f32 adds (b - 16 s) sum x.  The wavefronts'
+// accumulators are added in wavefront order (K order) through LDS, then
+// act[m][n] = bf16(silu(g) * u) with g, u = bf16(the gate, up sums times row m's 1/rms)
+// (silu_mul_kernel's expression).  Rows m >= M read zeros and are never stored.  Requires
+// K % 256 == 0, K / 256 == W and x rows 16-byte aligned.
+namespace pr {
+constexpr int kMaxUnits = 5;                // 8-row units of a workgroup: R <= 40
+constexpr int kLoadOctets = 2 * kMaxUnits;  // 8-slot weight loads of a wavefront
+constexpr int kBlocks = 3;                  // 32-slot MFMA blocks: 2R <= 96
+constexpr int kChunk = 4 * 1024;            // a wavefront's block: 32 slots x 128 bytes
+}  // namespace pr
+
+template <int W>
+__global__ __launch_bounds__(64 * W) void qmv_pair_rows_kernel(LaunchArgs a, NormIn ni, int nwg, int units) {
+  static_assert(pr::kLoadOctets <= 4 * pr::kBlocks, "the loads fit the blocks");
+  static_assert(16 * 64 * 4 <= pr::kChunk, "a block's accumulators fit its chunk");
+  __shared__ __attribute__((aligned(16))) char lds0[W * pr::kChunk];
+  __shared__ __attribute__((aligned(16))) char lds1[W * pr::kChunk];
+  __shared__ __attribute__((aligned(16))) char lds2[W * pr::kChunk];
+  __shared__ float nsum[kNormMaxTiles / 4][32];  // input norm: pair sums [j][row]
+  const Problem& Pg = a.p[0];
+  const Problem& Pu = a.p[1];
+  const int N = Pg.N, K = Pg.K, M = a.M, G = K >> 6;
+  const int u0 = (int)(((int64_t)blockIdx.x * units) / nwg);
+  const int u1 = (int)(((int64_t)(blockIdx.x + 1) * units) / nwg);
+  const int R = 8 * (u1 - u0), r0 = 8 * u0;
+  const int nb = (2 * R + 31) >> 5;  // blocks with slots (uniform)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, kb = lane >> 5;
+  const int g0 = 4 * wave;
+
+  const uint32_t wbytes = (uint32_t)N * (uint32_t)(K >> 1);
+  const __amdgpu_buffer_rsrc_t wgr = buffer_rsrc(Pg.w, wbytes), wur = buffer_rsrc(Pu.w, wbytes);
+  const __amdgpu_buffer_rsrc_t xrs =
+      buffer_rsrc(Pg.x, (uint32_t)(((int64_t)(M - 1) * Pg.ldx + K) * 2));
+
+  // 0. the input norm's partial sums of squares, before every other load
+  constexpr int NQ = (kNormSlots + 64 * W - 1) / (64 * W);
+  const bool norm_in = ni.ssq != nullptr;  // uniform
+  uint4 nq[NQ];
+  if (norm_in) {
+    const __amdgpu_buffer_rsrc_t qrs = buffer_rsrc(ni.ssq, (uint32_t)(M * ni.ld * 4));
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      const int p = tid + 64 * W * r;
+      nq[r] = load_b128(qrs, p < kNormSlots ? norm_pair_offset(ni, M, p) : kPastBuffer);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 1. scales and biases of this lane's slot in each block, this wavefront's four groups
+  u32x2_t sv[pr::kBlocks], bv[pr::kBlocks];
+#pragma unroll
+  for (int b = 0; b < pr::kBlocks; ++b) {
+    const int s = 32 * b + j;
+    const bool up = s >= R;
+    int n = r0 + (up ? s - R : s);
+    n = s < 2 * R && n < N ? n : r0;
+    const size_t o = (size_t)n * G + g0;  // 8-byte aligned: G and g0 are multiples of 4
+    sv[b] = *reinterpret_cast<const u32x2_t*>((up ? Pu.s : Pg.s) + o);
+    bv[b] = *reinterpret_cast<const u32x2_t*>((up ? Pu.b : Pg.b) + o);
+  }
+  // 2. x: four groups of 64 bytes a lane
+  const uint32_t xrow = j < M ? (uint32_t)j * (uint32_t)Pg.ldx * 2u + 64u * (uint32_t)kb : kPastBuffer;
+  uint4 xq[4][4];
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xq[gi][t] = load_b128(xrs, xrow + 128u * (uint32_t)(g0 + gi) + 16u * (uint32_t)t);
+  // 3. weights: octet o = slots [8 o, 8 o + 8) x this wavefront's 128 bytes of each, to
+  //    byte (o % 4) * 1024 + 16 lane of the wavefront's chunk of block o / 4 (octets past
+  //    the slots or the rows read zeros, no traffic)
+  char* const chunk[pr::kBlocks] = {lds0 + wave * pr::kChunk, lds1 + wave * pr::kChunk, lds2 + wave * pr::kChunk};
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int o = 0; o < pr::kLoadOctets; ++o) {
+    const bool up = 8 * o >= R;  // uniform: R is a multiple of 8
+    const int r = 8 * o + (lane >> 3);
+    const int c = (lane & 7) ^ dm::swz(r);
+    const int n = r0 + (up ? r - R : r);
+    const uint32_t off = 8 * o < 2 * R && n < N
+                             ? (uint32_t)n * (uint32_t)(K >> 1) + 32u * (uint32_t)(g0 + (c >> 1)) + 16u * (uint32_t)(c & 1)
+                             : kPastBuffer;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(up ? wur : wgr,
+                                             (__attribute__((address_space(3))) void*)(chunk[o >> 2] + (o & 3) * 1024),
+                                             16, off, 0, 0, kNt);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // x in pair order (the MFMAs' A operands) and its row sums per group
+  const uint32_t one = in_vgpr(kNibOne);
+  bf16x8_t xa[4][4];
+  float gsum[4];
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) {
+    float half = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      xa[gi][t] = as_bf16x8(pair_order(xq[gi][t]));
+      half = dot2(xq[gi][t].x, one, half);
+      half = dot2(xq[gi][t].y, one, half);
+      half = dot2(xq[gi][t].z, one, half);
+      half = dot2(xq[gi][t].w, one, half);
+    }
+    gsum[gi] = add_xor32(half);
+  }
+
+  const f32x16_t zero = {};
+  f32x16_t acc[pr::kBlocks] = {zero, zero, zero};
+  auto block = [&](const int b) {
+    const int r = 32 * b + j;
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const int c = 2 * gi + kb;
+      const uint4 wv = *reinterpret_cast<const uint4*>(chunk[b] + ((r >> 3) & 3) * 1024 +
+                                                       16 * (8 * (r & 7) + (c ^ dm::swz(r))));
+      f32x16_t p = zero;
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[gi][0], unpack16(wv.x, one), p, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[gi][1], unpack16(wv.y, one), p, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[gi][2], unpack16(wv.z, one), p, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[gi][3], unpack16(wv.w, one), p, 0, 0, 0);
+      const uint32_t sw = sv[b][gi >> 1];
+      const float s16 = 16.0f * __uint_as_float((gi & 1) ? (sw & 0xffff0000u) : (sw << 16));
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[b][e] = fmaf(s16, p[e], acc[b][e]);
+      if (gi & 1) {
+        // the pair's offset term: A = the rows' sums (lanes kb = 0 / 1: the pair's first /
+        // second group), B = b - 16 s of the same groups per slot
+        const uint32_t sp = sv[b][gi >> 1], bp = bv[b][gi >> 1];
+        const uint32_t sk = kb ? (sp & 0xffff0000u) : (sp << 16);
+        const uint32_t bk = kb ? (bp & 0xffff0000u) : (bp << 16);
+        const float cg = fmaf(-16.0f, __uint_as_float(sk), __uint_as_float(bk));
+        const float xs = kb ? gsum[gi] : gsum[gi - 1];
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs, cg, acc[b], 0, 0, 0);
+      }
+    }
+  };
+  // block b once its octets 4 b .. 4 b + 3 have landed (the loads after them may not have)
+  static_assert(pr::kBlocks == 3 && pr::kLoadOctets == 10, "the waits count the octets");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(6));
+  __builtin_amdgcn_sched_barrier(0);
+  block(0);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(2));
+  __builtin_amdgcn_sched_barrier(0);
+  if (nb > 1) block(1);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(0));
+  __builtin_amdgcn_sched_barrier(0);
+  if (nb > 2) block(2);
+
+  // the wavefronts' accumulators through LDS: wavefront w's chunk of block b holds [e][lane]
+  // (its own weight reads are done: LDS accesses of a wavefront complete in order)
+#pragma unroll
+  for (int b = 0; b < pr::kBlocks; ++b)
+    if (b < nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) reinterpret_cast<float*>(chunk[b])[e * 64 + lane] = acc[b][e];
+  if (norm_in) {
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      const int p = tid + 64 * W * r;
+      if (p < kNormSlots) nsum[p >> 5][p & 31] = norm_pair_sum(ni, p, nq[r]);
+    }
+  }
+  __syncthreads();
+  // outputs (m, n = r0 + nl), nl fastest across the threads: the gate sum at slot nl, the up
+  // sum at slot R + nl, each added over the wavefronts in order
+  uint16_t* act = static_cast<uint16_t*>(Pg.y);
+  auto slot_sum = [&](int s, int m) {
+    const float* red = reinterpret_cast<const float*>((s >> 5) == 0 ? lds0 : (s >> 5) == 1 ? lds1 : lds2);
+    const int at = (4 * (m >> 3) + (m & 3)) * 64 + (s & 31) + 32 * ((m >> 2) & 1);
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) v += red[w * (pr::kChunk / 4) + at];
+    return v;
+  };
+  for (int idx = tid; idx < 32 * R; idx += 64 * W) {
+    const int m = idx / R, nl = idx - m * R, n = r0 + nl;
+    if (m >= M || n >= N) continue;
+    const float gs = slot_sum(nl, m), us = slot_sum(R + nl, m);
+    const float sc = norm_in ? norm_row_inv(ni, nsum, m) : 1.0f;
+    const float g0v = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? gs * sc : gs));
+    const float u0v = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? us * sc : us));
+    act[(size_t)m * Pg.ldy + n] = f32_to_bf16_bits(g0v / (1.0f + expf(-g0v)) * u0v);
+  }
+}
+
 // ------------------------- the residual epilogue over K-range planes, a launch of its own
 //
 // qmv_dma_kernel's residual epilogue for a projection computed as K-range output planes
@@ -3478,6 +3687,9 @@ int32_t build_norm(LaunchArgs& a, DmaPlan* pl, NormIn* nin, ResidualOut* res,
 
 // The gate/up launch's plan: whole tiles of 32 gate and 32 up rows, and with a workspace the
 // tiles past the last whole round over the CUs cut into K-parts (0 parts: none).
+#ifndef IMQ_PAIR_ROWS
+#define IMQ_PAIR_ROWS 1
+#endif
 struct PairPlan {
   int whole = 0, tail = 0, parts = 1;
   size_t bytes = 0;
@@ -3494,6 +3706,36 @@ PairPlan plan_pair(int N, int K, int cu_count) {
     pl.bytes = kCounterBytes + (size_t)r * pl.parts * 2048 * sizeof(float);
   }
   return pl;
+}
+
+// The gate/up launch over bands of rows (qmv_pair_rows_kernel, the folded-norm form): one
+// workgroup per CU, each with at most pr::kMaxUnits units of 8 gate and 8 up rows.  Not
+// applicable: K / 256 not an instantiated wavefront count, x rows not 16-byte aligned.
+struct PairRowsPlan {
+  int waves = 0, nwg = 0, units = 0;
+};
+bool plan_pair_rows(int M, int N, int K, int64_t ldx, const void* x, int cu_count, PairRowsPlan* pl) {
+  const int w = K / 256;
+  if (K % 256 != 0 || !(w == 4 || w == 8 || w == 10 || w == 12)) return false;
+  if (M < 1 || M > 32 || ldx % 8 != 0 || !imq_rt::aligned(x, 16)) return false;
+  const int units = (N + 7) / 8;
+  int nwg = units < cu_count ? units : cu_count;
+  if ((units + nwg - 1) / nwg > pr::kMaxUnits) nwg = (units + pr::kMaxUnits - 1) / pr::kMaxUnits;
+  pl->waves = w;
+  pl->nwg = nwg;
+  pl->units = units;
+  return true;
+}
+
+hipError_t launch_pair_rows(const LaunchArgs& a, const NormIn& ni, const PairRowsPlan& pl, hipStream_t stream) {
+  switch (pl.waves) {
+    case 4: hipLaunchKernelGGL((qmv_pair_rows_kernel<4>), dim3(pl.nwg), dim3(64 * 4), 0, stream, a, ni, pl.nwg, pl.units); break;
+    case 8: hipLaunchKernelGGL((qmv_pair_rows_kernel<8>), dim3(pl.nwg), dim3(64 * 8), 0, stream, a, ni, pl.nwg, pl.units); break;
+    case 10: hipLaunchKernelGGL((qmv_pair_rows_kernel<10>), dim3(pl.nwg), dim3(64 * 10), 0, stream, a, ni, pl.nwg, pl.units); break;
+    case 12: hipLaunchKernelGGL((qmv_pair_rows_kernel<12>), dim3(pl.nwg), dim3(64 * 12), 0, stream, a, ni, pl.nwg, pl.units); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint16_t* b_gate,
@@ -3522,6 +3764,12 @@ int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint1
   a.p[1] = Problem{w_up, s_up, b_up, x, nullptr, ldx, ld_act, N, K, 0, 0, 0, 0};
   a.count = 2;
   a.M = M;
+  PairRowsPlan rp;
+  if (in && IMQ_PAIR_ROWS && plan_pair_rows(M, N, K, ldx, x, dev->cu_count, &rp)) {
+    const hipError_t e = launch_pair_rows(a, to_norm_in(in), rp, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("gate/up launch failed: ") + hipGetErrorString(e));
+    return ok();
+  }
   PairPlan pl = plan_pair(N, K, dev->cu_count);
   if (pl.parts > 1 && (!workspace || workspace_bytes < pl.bytes)) pl = PairPlan{(N + 31) / 32, 0, 1, 0};
   if (pl.parts > 1 && !aligned(workspace, 16)) return fail(IMQ_EINVAL, "workspace must be 16-byte aligned");
@@ -3677,6 +3925,8 @@ size_t imq_qmv_gate_up_silu_norm_workspace(int32_t M, int32_t N, int32_t K) {
   int32_t code;
   const DeviceInfo* dev = current_device(&code);
   if (!dev) return 0;
+  PairRowsPlan rp;
+  if (IMQ_PAIR_ROWS && plan_pair_rows(M, N, K, K, nullptr, dev->cu_count, &rp)) return 0;
   return plan_pair(N, K, dev->cu_count).bytes;
 }
 
