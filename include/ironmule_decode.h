@@ -126,16 +126,19 @@ IMQ_API int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const 
  * (imq_qmv_norm_planes over the q, k and v weights, ironmule_qmv.h) instead of bf16 rows:
  * each q/k/v value is the sum of its `nplanes` planes (1..4) in plane order, rounded to bf16,
  * problem i (0 q, 1 k, 2 v), plane s, request b at planes[i * pstride + (s * B + b) * N_i]
- * with N_i = Hq * 128 or Hkv * 128.  Otherwise as imq_attention_fused.  Replaces the same
- * reference steps, with the q/k/v projections' final reduction folded in
+ * with N_i = Hq * 128 or Hkv * 128.  out: rows of Hq * 128 (ld_out = Hq * 128) or, for at most
+ * 32 requests, the 32-row tile layout (ld_out = IMQ_LD_TILED, ironmule_qmv.h) that the o
+ * projection reads in contiguous pieces.  Otherwise as imq_attention_fused.  Replaces the
+ * same reference steps, with the q/k/v projections' final reduction folded in
  * (ironmule/dense_plan.py:348-357). */
 IMQ_API int32_t imq_attention_fused_planes(const float* planes, int64_t pstride, int32_t nplanes,
                                            const uint16_t* q_norm, const uint16_t* k_norm,
                                            const int32_t* positions, const int32_t* slots,
                                            uint16_t* k_pool, uint16_t* v_pool, uint16_t* out,
-                                           int32_t B, int32_t Hq, int32_t Hkv, int32_t capacity,
-                                           int32_t num_slots, int32_t max_len, float theta, float eps,
-                                           float* workspace, uint32_t* counters, void* stream);
+                                           int64_t ld_out, int32_t B, int32_t Hq, int32_t Hkv,
+                                           int32_t capacity, int32_t num_slots, int32_t max_len,
+                                           float theta, float eps, float* workspace, uint32_t* counters,
+                                           void* stream);
 
 /* out = bf16(silu(gate) * up), silu(g) = g / (1 + exp(-g)), n elements.
  * Replaces swiglu(gate, up) (ironmule/dense_plan.py:360; nn.silu in dense_cpu.py:216). */

@@ -123,7 +123,7 @@ IMQ_API int32_t imq_qmv_gate_up_silu(const uint32_t* w_gate, const uint16_t* s_g
  */
 typedef struct imq_norm_in {
   const float* ssq;  /* row m's partial sums at ssq[m * ld + t], t < tiles; 16-byte aligned */
-  int32_t tiles;     /* 1..64 partials per row, added in a fixed order */
+  int32_t tiles;     /* 1..128 partials per row, added in a fixed order */
   int32_t ld;        /* a multiple of 4, >= tiles */
   int32_t dim;       /* h's row length, the mean's divisor */
   float eps;
@@ -192,6 +192,33 @@ IMQ_API int32_t imq_qmv_norm_planes(const imq_problem* problems, int32_t count, 
  */
 IMQ_API int32_t imq_residual_planes(const float* planes, int32_t nplanes, int32_t M, int32_t N,
                                     const imq_residual_out* out, void* stream);
+
+/*
+ * The 32-row tile layout of a bf16 activation of M <= 32 rows and K columns (K a multiple of
+ * 64), selected by the row stride IMQ_LD_TILED where an entry point accepts it: element
+ * (m, k) at element offset
+ *   ((((k / 64) * 4 + (k % 32) / 8) * 2 + (k % 64) / 32) * 32 + m) * 8 + k % 8,
+ * a buffer of 32 * K elements whatever M (rows m >= M are neither read nor written).  Each
+ * 64-column group is 4 KB in which the 16 bytes an MFMA lane (m, half) reads for one k-step
+ * lie next to those of the other 63 lanes, so the batched kernels read the activation as
+ * contiguous 1 KB pieces instead of 32 rows x 32 bytes.  No reference counterpart: the
+ * layout in which the decode step's launches hand activations to one another.
+ */
+#define IMQ_LD_TILED 0
+
+/*
+ * imq_qmv_norm's residual form for one projection (no input norm) over bands of 32 weight
+ * rows and the whole K, a workgroup per band: y = x W^T is never written and the K-ranges
+ * never leave the workgroup (no partials, planes or epilogue launch); then h += bf16(y),
+ * x' = bf16(h * weight) and, per band of 32 columns, each row's sum of squares of the new
+ * h: ssq[m * ld + t], t < ceil(N / 32) (`ld` a multiple of 4, at least that).  x as rows
+ * (ldx >= K, a multiple of 8) or in the tile layout (ldx == IMQ_LD_TILED); M 1..32,
+ * K a multiple of 256 and at most 9728.  Same bits on every call.  Replaces the o and down
+ * projections of the reference's decode step with the residual add after each and the
+ * RMSNorm after that, ironmule/dense_plan.py:357-361.
+ */
+IMQ_API int32_t imq_qmv_residual_bands(const imq_problem* problem, int32_t M, int32_t group_size,
+                                       int32_t bits, const imq_residual_out* out, void* stream);
 
 /* Bytes of workspace imq_qmv_gate_up_silu_norm uses at these shapes (0: none): when the
  * launch's 32-row tiles make more than one round over the CUs, the tiles of the last,

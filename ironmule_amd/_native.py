@@ -127,6 +127,7 @@ _SIGNATURES = {
     "imq_qmv_norm_planes": ([ctypes.POINTER(Problem), _I32, _I32, _I32, _I32, ctypes.POINTER(NormIn),
                              _P, _I64, ctypes.POINTER(_I32), _P], _I32),
     "imq_residual_planes": ([_P, _I32, _I32, _I32, ctypes.POINTER(ResidualOut), _P], _I32),
+    "imq_qmv_residual_bands": ([ctypes.POINTER(Problem), _I32, _I32, _I32, ctypes.POINTER(ResidualOut), _P], _I32),
     "imq_qmv_gate_up_silu_norm_workspace": ([_I32, _I32, _I32], ctypes.c_size_t),
     "imq_qmv_gate_up_silu_norm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32,
                                    _I32, _I32, ctypes.POINTER(NormIn), _P, ctypes.c_size_t, _P],
@@ -146,7 +147,7 @@ _SIGNATURES = {
                               ctypes.c_float, _P, _P], _I32),
     "imq_attention_fused": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                              _I32, _I32, ctypes.c_float, ctypes.c_float, _P, _P, _P], _I32),
-    "imq_attention_fused_planes": ([_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+    "imq_attention_fused_planes": ([_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32,
                                     _I32, _I32, _I32, ctypes.c_float, ctypes.c_float, _P, _P, _P],
                                    _I32),
     "imq_silu_mul": ([_P, _P, _P, _I64, _P], _I32),
@@ -572,22 +573,26 @@ class QkvPlanes:
 
 
 def qmv_norm_planes(weights, x: torch.Tensor, out: QkvPlanes, norm_in: NormStats | None = None,
-                    eps: float = 1e-6, stream=None) -> int:
+                    eps: float = 1e-6, stream=None, tiled: bool = False) -> int:
     """The q, k and v projections of x' rows (with the RMSNorm folded in when `norm_in` is
     given) as fp32 output planes, one per K-range of the plan, left for the reader to add
     (imq_qmv_norm_planes); returns the plane count."""
     if len(weights) != 3:
         raise ValueError("q, k and v: three weights")
     _require(x, torch.bfloat16, "x")
-    m = int(x.shape[0])
-    if x.dim() != 2 or not x.is_contiguous() or m != out.rows:
+    m = out.rows
+    if tiled:
+        if not x.is_contiguous() or x.dim() != 1:
+            raise ValueError("a tiled x is a contiguous tile-layout buffer (tile_rows)")
+    elif x.dim() != 2 or not x.is_contiguous() or m != int(x.shape[0]):
         raise ValueError("x must be a contiguous (rows, K) tensor of the planes' rows")
     probs = (Problem * 3)()
     for i, (w, s, b) in enumerate(weights):
         n, k = check_weights(w, s, b)
-        if int(x.shape[1]) != k or n != (out.hq if i == 0 else out.hkv) * 128:
+        if (x.numel() != MAX_ROWS * k if tiled else int(x.shape[1]) != k) or n != (out.hq if i == 0 else out.hkv) * 128:
             raise ValueError(f"weight {i} does not match x or the planes' head counts")
-        probs[i] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), k, None, n, n, k)
+        probs[i] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), LD_TILED if tiled else k,
+                           None, n, n, k)
     nin = norm_in.norm_in(eps) if norm_in is not None else None
     splits = _I32(0)
     if int(lib().imq_qmv_norm_splits(probs, 3, m)) > out.max_planes:
@@ -601,9 +606,10 @@ def qmv_norm_planes(weights, x: torch.Tensor, out: QkvPlanes, norm_in: NormStats
 
 def attention_fused_planes(qkv: QkvPlanes, q_norm, k_norm, positions, slots, k_pool, v_pool, out,
                            max_len: int, theta: float, eps: float, workspace: torch.Tensor,
-                           counters: torch.Tensor, stream=None) -> torch.Tensor:
+                           counters: torch.Tensor, stream=None, tiled: bool = False) -> torch.Tensor:
     """attention_fused reading q, k and v as the planes of qmv_norm_planes (each value the
-    sum of its planes in order, rounded to bf16)."""
+    sum of its planes in order, rounded to bf16).  With `tiled` out is a 32-row tile layout
+    buffer of 32 * Hq * 128 elements (tile_rows) instead of (B, Hq * 128) rows."""
     for name, t in (("q_norm", q_norm), ("k_norm", k_norm), ("k_pool", k_pool), ("v_pool", v_pool),
                     ("out", out)):
         _require(t, torch.bfloat16, name)
@@ -613,8 +619,9 @@ def attention_fused_planes(qkv: QkvPlanes, q_norm, k_norm, positions, slots, k_p
     _require(counters, torch.int32, "counters")
     num_slots, hkv, capacity, d = k_pool.shape
     b = int(positions.numel())
+    want = (MAX_ROWS if tiled else b) * qkv.hq * d
     if (d != 128 or v_pool.shape != k_pool.shape or hkv != qkv.hkv or b != qkv.rows
-            or out.numel() != b * qkv.hq * d or slots.numel() != b or qkv.planes < 1):
+            or out.numel() != want or slots.numel() != b or qkv.planes < 1):
         raise ValueError("inconsistent planes/pool/out shapes (head dim 128)")
     if workspace.numel() < attention_workspace(b, qkv.hq, max_len):
         raise ValueError("workspace too small")
@@ -622,7 +629,8 @@ def attention_fused_planes(qkv: QkvPlanes, q_norm, k_norm, positions, slots, k_p
         raise ValueError("counters too small")
     _check(lib().imq_attention_fused_planes(_ptr(qkv.data), qkv.pstride, qkv.planes, _ptr(q_norm),
                                             _ptr(k_norm), _ptr(positions), _ptr(slots), _ptr(k_pool),
-                                            _ptr(v_pool), _ptr(out), b, qkv.hq, hkv, capacity, num_slots,
+                                            _ptr(v_pool), _ptr(out), LD_TILED if tiled else qkv.hq * d, b,
+                                            qkv.hq, hkv, capacity, num_slots,
                                             int(max_len), float(theta), float(eps), _ptr(workspace),
                                             _ptr(counters), _stream(stream)))
     return out
@@ -670,6 +678,26 @@ def gate_up_silu(gate: tuple[torch.Tensor, torch.Tensor, torch.Tensor],
 
 # ------------------------------------------------------- RMSNorm folded into projections
 
+LD_TILED = 0  # IMQ_LD_TILED: an activation row stride that selects the 32-row tile layout
+
+
+def tile_rows(x: torch.Tensor) -> torch.Tensor:
+    """x (M <= 32, K) bf16 rows -> the 32-row tile layout (a (32 * K,) tensor, rows past M
+    zero): element (m, k) at ((((k/64) * 4 + (k%32)/8) * 2 + (k%64)/32) * 32 + m) * 8 + k%8."""
+    m, k = int(x.shape[0]), int(x.shape[1])
+    if m > MAX_ROWS or k % 64:
+        raise ValueError("at most 32 rows and K a multiple of 64")
+    full = torch.zeros((MAX_ROWS, k), dtype=x.dtype, device=x.device)
+    full[:m] = x
+    # [m][g][kb][t][e] -> [g][t][kb][m][e]
+    return full.view(MAX_ROWS, k // 64, 2, 4, 8).permute(1, 3, 2, 0, 4).contiguous().view(-1)
+
+
+def untile_rows(t: torch.Tensor, m: int, k: int) -> torch.Tensor:
+    """The first m rows of a 32-row tile layout buffer of K columns, as (m, K) rows."""
+    return t[:MAX_ROWS * k].view(k // 64, 4, 2, MAX_ROWS, 8).permute(3, 0, 2, 1, 4).reshape(MAX_ROWS, k)[:m]
+
+
 class NormStats:
     """Per-row partial sums of squares of a residual stream h: `ssq` (rows, ld) fp32 with
     `tiles` partials per row, the input of a projection that folds in the RMSNorm
@@ -678,7 +706,7 @@ class NormStats:
 
     def __init__(self, rows: int, dim: int, device) -> None:
         self.dim = dim
-        tiles = -(-dim // 64)
+        tiles = -(-dim // 32)  # room for the row-band projections' 32-column partials
         self.ld = -(-tiles // 4) * 4
         self.ssq = torch.zeros((rows, self.ld), dtype=torch.float32, device=device)
         self.tiles = 1
@@ -748,11 +776,22 @@ def residual_split_planes(weight, x: torch.Tensor) -> int:
     return int(lib().imq_qmv_norm_splits(probs, 1, int(x.shape[0])))
 
 
-def qmv_residual_planes(weight, x: torch.Tensor, out: ResidualPlanes, stream=None) -> int:
+def qmv_residual_planes(weight, x: torch.Tensor, out: ResidualPlanes, stream=None, tiled: bool = False) -> int:
     """One projection of x (M, K) as fp32 K-range planes (imq_qmv_norm_planes, no input
-    norm), left for residual_planes to add; returns the plane count."""
-    probs, n, _ = _one_problem(weight, x)
-    m = int(x.shape[0])
+    norm), left for residual_planes to add; returns the plane count.  With `tiled` x is a
+    32-row tile layout buffer (tile_rows) of out.rows rows."""
+    if tiled:
+        w, s, b = weight
+        n, k = check_weights(w, s, b)
+        _require(x, torch.bfloat16, "x")
+        if x.numel() != MAX_ROWS * k or not x.is_contiguous():
+            raise ValueError(f"a tiled x holds 32 * {k} elements")
+        probs = (Problem * 1)()
+        probs[0] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), LD_TILED, None, n, n, k)
+        m = out.rows
+    else:
+        probs, n, _ = _one_problem(weight, x)
+        m = int(x.shape[0])
     if m != out.rows or n != out.cols:
         raise ValueError(f"the planes hold ({out.rows}, {out.cols}), the projection is ({m}, {n})")
     if int(lib().imq_qmv_norm_splits(probs, 1, m)) > out.max_planes:
@@ -764,9 +803,18 @@ def qmv_residual_planes(weight, x: torch.Tensor, out: ResidualPlanes, stream=Non
     return out.planes
 
 
+def _check_x_out(next_norm, x_out, m: int, n: int, tiled: bool) -> None:
+    if next_norm is None:
+        return
+    _require(next_norm, torch.bfloat16, "next_norm")
+    want = (MAX_ROWS * n,) if tiled else (m, n)
+    if x_out is None or tuple(x_out.shape) != want or x_out.dtype != torch.bfloat16:
+        raise ValueError(f"x_out must be a {want} bf16 tensor")
+
+
 def residual_planes(planes: ResidualPlanes, residual: torch.Tensor, next_norm: torch.Tensor | None = None,
                     x_out: torch.Tensor | None = None, stats_out: NormStats | None = None,
-                    stream=None) -> None:
+                    stream=None, tiled_out: bool = False) -> None:
     """qmv_norm's residual epilogue as a launch of its own (imq_residual_planes): y = the
     planes added in order, residual += bf16(y), x_out = bf16(residual * next_norm) and the
     per-tile sums of squares into stats_out; the bits of qmv_norm(..., residual=...)."""
@@ -776,18 +824,49 @@ def residual_planes(planes: ResidualPlanes, residual: torch.Tensor, next_norm: t
     _require(residual, torch.float32, "residual")
     if tuple(residual.shape) != (m, n) or not residual.is_contiguous():
         raise ValueError(f"residual must be a contiguous ({m}, {n}) fp32 tensor")
-    if next_norm is not None:
-        _require(next_norm, torch.bfloat16, "next_norm")
-        if x_out is None or tuple(x_out.shape) != (m, n) or x_out.dtype != torch.bfloat16:
-            raise ValueError(f"x_out must be a ({m}, {n}) bf16 tensor")
+    _check_x_out(next_norm, x_out, m, n, tiled_out)
     rout = ResidualOut(residual.data_ptr(), n, next_norm.data_ptr() if next_norm is not None else None,
-                       x_out.data_ptr() if next_norm is not None else None, n,
+                       x_out.data_ptr() if next_norm is not None else None, LD_TILED if tiled_out else n,
                        stats_out.ssq.data_ptr() if stats_out is not None else None,
                        stats_out.ld if stats_out is not None else 0)
     _check(lib().imq_residual_planes(_ptr(planes.data), planes.planes, m, n, ctypes.byref(rout),
                                      _stream(stream)))
     if stats_out is not None:
         stats_out.tiles = -(-n // 64)
+
+
+def qmv_residual_bands(weight, x: torch.Tensor, rows: int, residual: torch.Tensor,
+                       next_norm: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
+                       stats_out: NormStats | None = None, tiled: bool = False, stream=None,
+                       tiled_out: bool = False) -> None:
+    """One projection of `rows` activation rows over bands of 32 weight rows and the whole K
+    (imq_qmv_residual_bands): residual += bf16(x W^T), x_out = bf16(residual * next_norm) and
+    per 32-column band the rows' sums of squares into stats_out.  x: (rows, K) rows, or with
+    `tiled` a tile-layout buffer of 32 * K elements (tile_rows)."""
+    w, s, b = weight
+    n, k = check_weights(w, s, b)
+    _require(x, torch.bfloat16, "x")
+    if not 1 <= rows <= MAX_ROWS:
+        raise ValueError("rows must be 1..32")
+    if tiled:
+        if x.numel() < MAX_ROWS * k or not x.is_contiguous():
+            raise ValueError(f"a tiled x holds 32 * {k} elements")
+    elif x.dim() != 2 or not x.is_contiguous() or tuple(x.shape) != (rows, k):
+        raise ValueError(f"x must be a contiguous ({rows}, {k}) tensor")
+    _require(residual, torch.float32, "residual")
+    if tuple(residual.shape) != (rows, n) or not residual.is_contiguous():
+        raise ValueError(f"residual must be a contiguous ({rows}, {n}) fp32 tensor")
+    _check_x_out(next_norm, x_out, rows, n, tiled_out)
+    probs = (Problem * 1)()
+    probs[0] = Problem(w.data_ptr(), s.data_ptr(), b.data_ptr(), x.data_ptr(), LD_TILED if tiled else k,
+                       None, n, n, k)
+    rout = ResidualOut(residual.data_ptr(), n, next_norm.data_ptr() if next_norm is not None else None,
+                       x_out.data_ptr() if next_norm is not None else None, LD_TILED if tiled_out else n,
+                       stats_out.ssq.data_ptr() if stats_out is not None else None,
+                       stats_out.ld if stats_out is not None else 0)
+    _check(lib().imq_qmv_residual_bands(probs, rows, GROUP_SIZE, BITS, ctypes.byref(rout), _stream(stream)))
+    if stats_out is not None:
+        stats_out.tiles = -(-n // 32)
 
 
 def qmv_norm(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]], x: torch.Tensor,
@@ -854,23 +933,28 @@ def qmv_norm(weights: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]], x: 
 
 
 def gate_up_silu_norm(gate, up, x: torch.Tensor, out: torch.Tensor, norm_in: NormStats,
-                      eps: float, stream=None, split_tail: bool = True) -> torch.Tensor:
+                      eps: float, stream=None, split_tail: bool = True, rows: int | None = None,
+                      tiled_x: bool = False, tiled_out: bool = False) -> torch.Tensor:
     """gate_up_silu on x' = bf16(h * w) with the RMSNorm folded in: the gate and up rows are
     scaled by 1/rms(h) from `norm_in` before the SwiGLU.  With `split_tail` the tiles of the
-    launch's last, partial round over the CUs run as K-parts (this stream's workspace)."""
+    launch's last, partial round over the CUs run as K-parts (this stream's workspace).
+    `tiled_x` / `tiled_out`: x / out are 32-row tile layout buffers (tile_rows) of `rows`
+    rows instead of (M, K) / (M, N) rows."""
     n, k = check_weights(*gate)
     if check_weights(*up) != (n, k):
         raise ValueError("gate and up must have the same shape")
     _require(x, torch.bfloat16, "x")
     _require(out, torch.bfloat16, "out")
-    if x.dim() != 2 or int(x.shape[1]) != k or tuple(out.shape) != (int(x.shape[0]), n):
-        raise ValueError(f"x must be (M, {k}) and out (M, {n})")
-    m = int(x.shape[0])
+    m = int(rows if rows is not None else x.shape[0])
+    if (x.numel() != MAX_ROWS * k if tiled_x else (x.dim() != 2 or tuple(x.shape) != (m, k))) or \
+            (out.numel() != MAX_ROWS * n if tiled_out else tuple(out.shape) != (m, n)):
+        raise ValueError(f"x must be (M, {k}) and out (M, {n}) rows, or tile-layout buffers")
     nin = norm_in.norm_in(eps)
     nbytes = int(lib().imq_qmv_gate_up_silu_norm_workspace(m, n, k)) if split_tail else 0
     ws = _workspace(nbytes, gate[0].device, stream) if nbytes else None
     _check(lib().imq_qmv_gate_up_silu_norm(_ptr(gate[0]), _ptr(gate[1]), _ptr(gate[2]), _ptr(up[0]),
-                                           _ptr(up[1]), _ptr(up[2]), _ptr(x), k, _ptr(out), n, m, n,
+                                           _ptr(up[1]), _ptr(up[2]), _ptr(x), LD_TILED if tiled_x else k,
+                                           _ptr(out), LD_TILED if tiled_out else n, m, n,
                                            k, GROUP_SIZE, BITS, ctypes.byref(nin),
                                            _ptr(ws) if ws is not None else None,
                                            ws.numel() * 4 if ws is not None else 0, _stream(stream)))

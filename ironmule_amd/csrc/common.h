@@ -129,6 +129,13 @@ __device__ __forceinline__ float chunk_dot(uint4 wv, uint4 x0, uint4 x1, uint4 x
   return d;
 }
 
+// The 32-row tile layout of an activation (row stride IMQ_LD_TILED: a row stride of 0): element (m, k) at element offset tile_elem(m, k).  Each 64-column group
+// is 4 KB, and the 16 bytes lane (m, kb) of an MFMA kernel reads for k-step t of group g lie
+// at byte (4 g + t) * 1024 + 16 (32 kb + m): a contiguous 1 KB per load instruction.
+__host__ __device__ constexpr uint32_t tile_elem(uint32_t m, uint32_t k) {
+  return ((((k >> 6) * 4 + ((k >> 3) & 3)) * 2 + ((k >> 5) & 1)) * 32 + m) * 8 + (k & 7);
+}
+
 constexpr uint32_t kPastBuffer = 0x80000000u;  // a buffer offset that reads as zero
 
 // Lane shape of the one-row (M = 1) tile, shared by every kernel that computes it so

@@ -123,7 +123,7 @@ struct ResidualOut {
   int32_t ld;
   int32_t pad;
 };
-constexpr int kNormMaxTiles = 64;
+constexpr int kNormMaxTiles = 128;
 constexpr int kNormSlots = IMQ_MAX_ROWS * kNormMaxTiles / 4;  // (row, four partials) pairs
 
 // One b128 of the partials of pair p = (row p % 32, partials 4 (p / 32) ..): the offset to
@@ -1699,9 +1699,12 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   const uint32_t sb_bytes = (uint32_t)N * (uint32_t)G * 2u;
   const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.s, sb_bytes);
   const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(P.b, sb_bytes);
+  // x as rows, or in the tile layout (ldx == 0: group g's piece t at 4096 g + 1024 t)
+  const bool xt = P.ldx == 0;  // uniform
   const __amdgpu_buffer_rsrc_t xrs =
-      buffer_rsrc(P.x, (uint32_t)(((int64_t)(M - 1) * P.ldx + K) * 2));
-  const uint32_t xrow = j < M ? (uint32_t)j * (uint32_t)P.ldx * 2u + 64u * (uint32_t)kb : kPastBuffer;
+      buffer_rsrc(P.x, xt ? (uint32_t)K * 64u : (uint32_t)(((int64_t)(M - 1) * P.ldx + K) * 2));
+  const uint32_t xrow = j >= M ? kPastBuffer : xt ? 16u * (uint32_t)lane : (uint32_t)j * (uint32_t)P.ldx * 2u + 64u * (uint32_t)kb;
+  const uint32_t xgs = xt ? 4096u : 128u, xts = xt ? 1024u : 16u;
 
   // 0. the input norm's partial sums of squares, before every other load (the first wait
   //    below then covers them): NQ b128 per thread cover 32 rows x kNormMaxTiles partials
@@ -1754,9 +1757,9 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
   };
   auto load_x = [&](XG& xg, int gi) {
     const int g = g0 + gi;
-    const uint32_t off = g < gs1 ? xrow + 128u * (uint32_t)g : kPastBuffer;
+    const uint32_t off = g < gs1 ? xrow + xgs * (uint32_t)g : kPastBuffer;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xg.v[t] = load_b128(xrs, off + 16u * (uint32_t)t);
+    for (int t = 0; t < 4; ++t) xg.v[t] = load_b128(xrs, off + xts * (uint32_t)t);
   };
 
   XG xq[GMAX];
@@ -1886,7 +1889,8 @@ __global__ __launch_bounds__(64 * W) void qmv_dma_kernel(LaunchArgs a, DmaArgs d
       const float hn = hv[i] + bf16_bits_to_f32(f32_to_bf16_bits(y));
       if (n < N) {
         d.res.h[(size_t)m * d.res.ldh + n] = hn;
-        if (d.res.w) d.res.x[(size_t)m * d.res.ldx + n] = f32_to_bf16_bits(hn * wn);
+        if (d.res.w)
+          d.res.x[d.res.ldx == 0 ? (size_t)tile_elem(m, n) : (size_t)m * d.res.ldx + n] = f32_to_bf16_bits(hn * wn);
         sq[i] = hn * hn;
       }
     }
@@ -2024,8 +2028,9 @@ __global__ __launch_bounds__(64 * W) void qmv_pair_rows_kernel(LaunchArgs a, Nor
 
   const uint32_t wbytes = (uint32_t)N * (uint32_t)(K >> 1);
   const __amdgpu_buffer_rsrc_t wgr = buffer_rsrc(Pg.w, wbytes), wur = buffer_rsrc(Pu.w, wbytes);
+  const bool xt = Pg.ldx == 0;  // x in the tile layout (uniform)
   const __amdgpu_buffer_rsrc_t xrs =
-      buffer_rsrc(Pg.x, (uint32_t)(((int64_t)(M - 1) * Pg.ldx + K) * 2));
+      buffer_rsrc(Pg.x, xt ? (uint32_t)K * 64u : (uint32_t)(((int64_t)(M - 1) * Pg.ldx + K) * 2));
 
   // 0. the input norm's partial sums of squares, before every other load
   constexpr int NQ = (kNormSlots + 64 * W - 1) / (64 * W);
@@ -2053,12 +2058,13 @@ __global__ __launch_bounds__(64 * W) void qmv_pair_rows_kernel(LaunchArgs a, Nor
     bv[b] = *reinterpret_cast<const u32x2_t*>((up ? Pu.b : Pg.b) + o);
   }
   // 2. x: four groups of 64 bytes a lane
-  const uint32_t xrow = j < M ? (uint32_t)j * (uint32_t)Pg.ldx * 2u + 64u * (uint32_t)kb : kPastBuffer;
+  const uint32_t xrow = j >= M ? kPastBuffer : xt ? 16u * (uint32_t)lane : (uint32_t)j * (uint32_t)Pg.ldx * 2u + 64u * (uint32_t)kb;
+  const uint32_t xgs = xt ? 4096u : 128u, xts = xt ? 1024u : 16u;
   uint4 xq[4][4];
 #pragma unroll
   for (int gi = 0; gi < 4; ++gi)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xq[gi][t] = load_b128(xrs, xrow + 128u * (uint32_t)(g0 + gi) + 16u * (uint32_t)t);
+    for (int t = 0; t < 4; ++t) xq[gi][t] = load_b128(xrs, xrow + xgs * (uint32_t)(g0 + gi) + xts * (uint32_t)t);
   // 3. weights: octet o = slots [8 o, 8 o + 8) x this wavefront's 128 bytes of each, to
   //    byte (o % 4) * 1024 + 16 lane of the wavefront's chunk of block o / 4 (octets past
   //    the slots or the rows read zeros, no traffic)
@@ -2175,7 +2181,187 @@ __global__ __launch_bounds__(64 * W) void qmv_pair_rows_kernel(LaunchArgs a, Nor
     const float sc = norm_in ? norm_row_inv(ni, nsum, m) : 1.0f;
     const float g0v = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? gs * sc : gs));
     const float u0v = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? us * sc : us));
-    act[(size_t)m * Pg.ldy + n] = f32_to_bf16_bits(g0v / (1.0f + expf(-g0v)) * u0v);
+    act[Pg.ldy == 0 ? (size_t)tile_elem(m, n) : (size_t)m * Pg.ldy + n] =
+        f32_to_bf16_bits(g0v / (1.0f + expf(-g0v)) * u0v);
+  }
+}
+
+// -------------- one projection over bands of 32 rows and the whole K (the residual form)
+//
+// The o and down projections of the batched decode step with their residual epilogue, and
+// no K-ranges: workgroup i owns weight rows [32 i, 32 i + 32) (one MFMA block) over the whole
+// K with 16 wavefronts, wavefront w owning a run of whole 4-group chunks (the C = K / 256
+// chunks dealt as evenly as they go, at most three each: K <= 9728), so no partial leaves
+// the workgroup and no second launch adds planes.  A wavefront issues its scales and biases,
+// its chunks' weights (by the LDS path: 32 rows x 128 bytes, chunk j of every wavefront in
+// LDS array j), then x for its first rb::kXAhead groups; each computed group issues x for
+// the group rb::kXAhead ahead, so the x stream (the whole of x per workgroup, from L2) runs
+// under the arithmetic.  x in the tile layout (ldx == 0) reads as contiguous 1 KB pieces,
+// rows as in qmv_dma_kernel otherwise.  Per group: four bf16 MFMAs, acc += 16 s P, and per
+// pair of groups the bias MFMA, as in qmv_dma_kernel.  The wavefronts' accumulators add in
+// K order through LDS; thread (m, n) then writes h += bf16(y), x' = bf16(h * w) and the
+// band's sum of squares of row m's new h (ssq[m * ld + band]).
+namespace rb {
+constexpr int kWaves = 16;
+constexpr int kChunk = 4096;                       // a chunk's weights: 32 rows x 128 bytes
+constexpr int kMaxChunks = 38;                     // K <= 9728
+constexpr int kThird = kMaxChunks - 2 * kWaves;    // wavefronts with a third chunk
+constexpr int kXAhead = 2;                         // groups of x in flight
+// s_waitcnt vmcnt(n) for the n the unrolled loop folds to (0, 4 or 8; else vmcnt(0))
+__device__ __forceinline__ void wait_younger(int n) {
+  switch (n) {
+    case 8: __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(8)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(4)); break;
+    default: __builtin_amdgcn_s_waitcnt(dm::vmcnt_imm(0)); break;
+  }
+}
+}  // namespace rb
+
+template <int NI>
+__device__ __forceinline__ void rowband_wave(const Problem& P, int M, int r0, int c0, int wave, int lane,
+                                             char* const (&arr)[3], f32x16_t& acc) {
+  const int N = P.N, K = P.K, G = K >> 6;
+  const int j = lane & 31, kb = lane >> 5;
+  const bool tiled = P.ldx == 0;  // uniform
+  const int nr = r0 + j < N ? r0 + j : N - 1;  // this lane's weight row (clamped)
+  // scales and biases of row nr, four groups per chunk, straight into registers
+  u32x2_t sv[NI > 0 ? NI : 1], bv[NI > 0 ? NI : 1];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const size_t o = (size_t)nr * G + 4 * (c0 + i);
+    sv[i] = *reinterpret_cast<const u32x2_t*>(P.s + o);
+    bv[i] = *reinterpret_cast<const u32x2_t*>(P.b + o);
+  }
+  // the chunks' weights: instruction q of chunk i = rows 8q .. 8q + 7 x 128 bytes
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(P.w, (uint32_t)N * (uint32_t)(K >> 1));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = 8 * q + (lane >> 3);
+      const int c = (lane & 7) ^ dm::swz(r);
+      const uint32_t off = r0 + r < N ? (uint32_t)(r0 + r) * (uint32_t)(K >> 1) + 32u * (uint32_t)(4 * (c0 + i) + (c >> 1)) +
+                                            16u * (uint32_t)(c & 1)
+                                      : kPastBuffer;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wrs, (__attribute__((address_space(3))) void*)(arr[i] + wave * rb::kChunk + q * 1024), 16, off, 0, 0, kNt);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  // x: lane (m, kb)'s 64 bytes of group g (rows m >= M: zeros, no traffic)
+  const __amdgpu_buffer_rsrc_t xrs =
+      buffer_rsrc(P.x, tiled ? (uint32_t)K * 64u : (uint32_t)(((int64_t)(M - 1) * P.ldx + K) * 2));
+  const bool xin = j < M;
+  const uint32_t xbase = tiled ? 16u * (uint32_t)lane : (uint32_t)j * (uint32_t)P.ldx * 2u + 64u * (uint32_t)kb;
+  constexpr int NG = 4 * NI;  // this wavefront's groups
+  uint4 xq[NG > 0 ? NG : 1][4];
+  auto load_x = [&](int s) {
+    const uint32_t g = (uint32_t)(4 * c0 + s);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      xq[s][t] = load_b128(xrs, xin ? xbase + (tiled ? (g * 4u + t) * 1024u : 128u * g + 16u * t) : kPastBuffer);
+  };
+#pragma unroll
+  for (int s = 0; s < rb::kXAhead && s < NG; ++s) load_x(s);
+  const uint32_t one = in_vgpr(kNibOne);
+  const f32x16_t zero = {};
+  float sum_even = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NG; ++s) {
+    const int i = s >> 2, gi = s & 3;
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + rb::kXAhead < NG) load_x(s + rb::kXAhead);
+    __builtin_amdgcn_sched_barrier(0);
+    // x of group s has landed, and with it every weight load (issued before it): only the
+    // x loads of the groups after s may be in flight
+    rb::wait_younger(4 * (s + rb::kXAhead < NG ? rb::kXAhead : NG - 1 - s));
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8_t xa[4];
+    float half = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      xa[t] = as_bf16x8(pair_order(xq[s][t]));
+      half = dot2(xq[s][t].x, one, half);
+      half = dot2(xq[s][t].y, one, half);
+      half = dot2(xq[s][t].z, one, half);
+      half = dot2(xq[s][t].w, one, half);
+    }
+    const float gsum = add_xor32(half);
+    const int c = 2 * gi + kb;
+    const uint4 wv = *reinterpret_cast<const uint4*>(arr[i] + wave * rb::kChunk + (j >> 3) * 1024 +
+                                                     16 * (8 * (j & 7) + (c ^ dm::swz(j))));
+    f32x16_t p = zero;
+    p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[0], unpack16(wv.x, one), p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[1], unpack16(wv.y, one), p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[2], unpack16(wv.z, one), p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[3], unpack16(wv.w, one), p, 0, 0, 0);
+    const uint32_t sw = sv[i][gi >> 1];
+    const float s16 = 16.0f * __uint_as_float((gi & 1) ? (sw & 0xffff0000u) : (sw << 16));
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = fmaf(s16, p[e], acc[e]);
+    if (gi & 1) {
+      // the pair's offset term: A = the rows' sums (lanes kb = 0 / 1: the pair's first /
+      // second group), B = b - 16 s of the same groups per weight row
+      const uint32_t bw = bv[i][gi >> 1];
+      const uint32_t sk = kb ? (sw & 0xffff0000u) : (sw << 16);
+      const uint32_t bk = kb ? (bw & 0xffff0000u) : (bw << 16);
+      const float cg = fmaf(-16.0f, __uint_as_float(sk), __uint_as_float(bk));
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kb ? gsum : sum_even, cg, acc, 0, 0, 0);
+    }
+    sum_even = gsum;
+  }
+}
+
+__global__ __launch_bounds__(64 * rb::kWaves) void qmv_rowband_kernel(Problem P, int M, ResidualOut res) {
+  __shared__ __attribute__((aligned(16))) char arr0[rb::kWaves * rb::kChunk];
+  __shared__ __attribute__((aligned(16))) char arr1[rb::kWaves * rb::kChunk];
+  __shared__ __attribute__((aligned(16))) char arr2[rb::kThird * rb::kChunk];
+  const int N = P.N, C = P.K >> 8;
+  const int band = blockIdx.x, r0 = band * 32;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // this wavefront's chunks [c0, c0 + nc): C / 16 each, one more for the first C % 16
+  const int base = C / rb::kWaves, extra = C - base * rb::kWaves;
+  const int nc = base + (wave < extra ? 1 : 0);
+  const int c0 = wave * base + (wave < extra ? wave : extra);
+  char* const arr[3] = {arr0, arr1, arr2};
+  const f32x16_t zero = {};
+  f32x16_t acc = zero;
+  switch (nc) {  // uniform
+    case 1: rowband_wave<1>(P, M, r0, c0, wave, lane, arr, acc); break;
+    case 2: rowband_wave<2>(P, M, r0, c0, wave, lane, arr, acc); break;
+    case 3: rowband_wave<3>(P, M, r0, c0, wave, lane, arr, acc); break;
+    default: break;
+  }
+
+  // residual rows of this thread's output (m = tid / 32, column n = r0 + tid % 32), in
+  // flight with the reduction
+  const int m = tid >> 5, n = r0 + (tid & 31);
+  const bool mine = m < M && n < N;
+  const float hv = mine ? res.h[(size_t)m * res.ldh + n] : 0.0f;
+  const float wn = mine && res.w ? bf16_bits_to_f32(res.w[n]) : 0.0f;
+  // the accumulators through LDS: wavefront w's [e][lane] in its chunk-0 slot (its own
+  // weight reads are done: a wavefront's LDS accesses complete in order)
+  float* red = reinterpret_cast<float*>(arr0);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) red[wave * (rb::kChunk / 4) + e * 64 + lane] = acc[e];
+  __syncthreads();
+  const int at = (4 * (m >> 3) + (m & 3)) * 64 + (tid & 31) + 32 * ((m >> 2) & 1);
+  float y = 0.0f;
+#pragma unroll
+  for (int w = 0; w < rb::kWaves; ++w) y += red[w * (rb::kChunk / 4) + at];
+  float sq = 0.0f;
+  if (mine) {
+    const float hn = hv + bf16_bits_to_f32(f32_to_bf16_bits(y));
+    res.h[(size_t)m * res.ldh + n] = hn;
+    if (res.w) res.x[res.ldx == 0 ? (size_t)tile_elem(m, n) : (size_t)m * res.ldx + n] = f32_to_bf16_bits(hn * wn);
+    sq = hn * hn;
+  }
+  if (res.ssq) {
+    // row m's sum over the band's 32 columns: lanes 0-31 hold row 2w, 32-63 row 2w + 1
+    sq = row16_sum(sq);
+    const float lo = lane_value(sq, 0) + lane_value(sq, 16), hi = lane_value(sq, 32) + lane_value(sq, 48);
+    if ((lane & 31) == 0 && m < M) res.ssq[m * res.ld + band] = lane ? hi : lo;
   }
 }
 
@@ -2216,7 +2402,7 @@ __global__ __launch_bounds__(64 * kResRowsPerGroup) void residual_planes_kernel(
   float sq = 0.0f;
   if (in) {
     r.h[(size_t)m * r.ldh + n] = hn;
-    if (r.w) r.x[(size_t)m * r.ldx + n] = f32_to_bf16_bits(hn * wn);
+    if (r.w) r.x[r.ldx == 0 ? (size_t)tile_elem(m, n) : (size_t)m * r.ldx + n] = f32_to_bf16_bits(hn * wn);
     sq = hn * hn;
   }
   if (r.ssq) {
@@ -3640,6 +3826,23 @@ NormIn to_norm_in(const imq_norm_in* in) {
   return n;
 }
 
+// x' of a residual epilogue: rows ldx apart, or the tile layout (ldx == IMQ_LD_TILED, N a
+// multiple of 64); the row stride the kernels take (0: tiled).
+int32_t check_x_out(const imq_residual_out* out, int32_t M, int32_t N) {
+  if (!out->weight) return IMQ_OK;
+  if (!aligned(out->weight, 2) || !out->x || !aligned(out->x, 2))
+    return fail(IMQ_EINVAL, "norm weight and x' must be non-null and 2-byte aligned");
+  if (out->ldx == IMQ_LD_TILED) {
+    if (N % 64 != 0 || M > IMQ_MAX_ROWS) return fail(IMQ_EINVAL, "a tiled x' needs N a multiple of 64");
+    return IMQ_OK;
+  }
+  if (M > 1 && out->ldx < N) return fail(IMQ_EINVAL, "x' ldx must be >= N");
+  return IMQ_OK;
+}
+int64_t x_out_ld(const imq_residual_out* out, int32_t M, int32_t N) {
+  return out->ldx == IMQ_LD_TILED ? 0 : M > 1 ? out->ldx : N;
+}
+
 // Validates a fused-norm call into `a`, the plan `pl` and the device arguments.
 int32_t build_norm(LaunchArgs& a, DmaPlan* pl, NormIn* nin, ResidualOut* res,
                    const imq_problem* problems, int32_t count, int32_t M, int32_t group_size,
@@ -3649,7 +3852,15 @@ int32_t build_norm(LaunchArgs& a, DmaPlan* pl, NormIn* nin, ResidualOut* res,
   if (count < 1 || count > IMQ_MAX_PROBLEMS) return fail(IMQ_EINVAL, "count must be 1..IMQ_MAX_PROBLEMS");
   if (out && count != 1) return fail(IMQ_EINVAL, "a residual epilogue takes one problem");
   imq_problem probs[IMQ_MAX_PROBLEMS];
-  for (int i = 0; i < count; ++i) probs[i] = problems[i];
+  bool xt[IMQ_MAX_PROBLEMS] = {};
+  for (int i = 0; i < count; ++i) {
+    probs[i] = problems[i];
+    if (probs[i].ldx == IMQ_LD_TILED) {  // the tile layout: validated as K-element rows
+      if (probs[i].K % 64 != 0) return fail(IMQ_EINVAL, "a tiled x needs K a multiple of 64");
+      xt[i] = true;
+      probs[i].ldx = probs[i].K;
+    }
+  }
   if (out) {  // y is not written: validate the rows against the residual rows instead
     if (!out->h || !aligned(out->h, 4)) return fail(IMQ_EINVAL, "residual h must be non-null and 4-byte aligned");
     if (M > 1 && out->ldh < probs[0].N) return fail(IMQ_EINVAL, "residual ldh must be >= N");
@@ -3658,6 +3869,8 @@ int32_t build_norm(LaunchArgs& a, DmaPlan* pl, NormIn* nin, ResidualOut* res,
   }
   int32_t code = build_grouped(a, probs, count, M, group_size, bits, IMQ_BF16);
   if (code != IMQ_OK) return code;
+  for (int i = 0; i < count; ++i)
+    if (xt[i]) a.p[i].ldx = 0;
   memset(nin, 0, sizeof(*nin));
   memset(res, 0, sizeof(*res));
   if (in) {
@@ -3666,15 +3879,10 @@ int32_t build_norm(LaunchArgs& a, DmaPlan* pl, NormIn* nin, ResidualOut* res,
   }
   if (out) {
     const int N = probs[0].N, tiles = (N + 63) / 64;
-    if (out->weight) {
-      if (!aligned(out->weight, 2) || !out->x || !aligned(out->x, 2))
-        return fail(IMQ_EINVAL, "norm weight and x' must be non-null and 2-byte aligned");
-      if (M > 1 && out->ldx < N) return fail(IMQ_EINVAL, "x' ldx must be >= N");
-    }
+    if ((code = check_x_out(out, M, N)) != IMQ_OK) return code;
     if (out->ssq && (!aligned(out->ssq, 4) || out->ld < tiles || out->ld % 4))
       return fail(IMQ_EINVAL, "residual ssq must be 4-byte aligned with ld >= ceil(N / 64), a multiple of 4");
-    *res = ResidualOut{out->h, M > 1 ? out->ldh : N, out->weight, out->x, M > 1 ? out->ldx : N,
-                       out->ssq, out->ld, 0};
+    *res = ResidualOut{out->h, M > 1 ? out->ldh : N, out->weight, out->x, x_out_ld(out, M, N), out->ssq, out->ld, 0};
   }
   *dev = current_device(&code);
   if (!*dev) return code;
@@ -3747,7 +3955,11 @@ int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint1
   if (code != IMQ_OK) return code;
   if ((code = check_weights(w_gate, s_gate, b_gate)) != IMQ_OK) return code;
   if ((code = check_weights(w_up, s_up, b_up)) != IMQ_OK) return code;
-  if ((code = check_rows(x, ldx, act, ld_act, M, N, K, IMQ_BF16)) != IMQ_OK) return code;
+  // the norm form takes x and act in the tile layout too (row stride IMQ_LD_TILED)
+  const bool xt = in && ldx == IMQ_LD_TILED, at = in && ld_act == IMQ_LD_TILED;
+  if ((xt && K % 64 != 0) || (at && N % 64 != 0))
+    return fail(IMQ_EINVAL, "the tile layout needs K (x) or N (act) a multiple of 64");
+  if ((code = check_rows(x, xt ? K : ldx, act, at ? N : ld_act, M, N, K, IMQ_BF16)) != IMQ_OK) return code;
   if (in && (code = check_norm_in(in)) != IMQ_OK) return code;
   // without the folded norm the launch keeps the bits of the grouped launch and silu_mul,
   // whose plans take the few-row VALU kernel below 5 rows
@@ -3760,16 +3972,19 @@ int32_t gate_up_silu(const uint32_t* w_gate, const uint16_t* s_gate, const uint1
   if (!dev) return code;
   LaunchArgs a;
   memset(&a, 0, sizeof(a));
-  a.p[0] = Problem{w_gate, s_gate, b_gate, x, act, ldx, ld_act, N, K, 0, 0, 0, 0};
-  a.p[1] = Problem{w_up, s_up, b_up, x, nullptr, ldx, ld_act, N, K, 0, 0, 0, 0};
+  const int64_t lx = xt ? 0 : M > 1 ? ldx : K, la = at ? 0 : M > 1 ? ld_act : N;
+  a.p[0] = Problem{w_gate, s_gate, b_gate, x, act, lx, la, N, K, 0, 0, 0, 0};
+  a.p[1] = Problem{w_up, s_up, b_up, x, nullptr, lx, la, N, K, 0, 0, 0, 0};
   a.count = 2;
   a.M = M;
   PairRowsPlan rp;
-  if (in && IMQ_PAIR_ROWS && plan_pair_rows(M, N, K, ldx, x, dev->cu_count, &rp)) {
+  if (in && IMQ_PAIR_ROWS && plan_pair_rows(M, N, K, lx, x, dev->cu_count, &rp)) {
     const hipError_t e = launch_pair_rows(a, to_norm_in(in), rp, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("gate/up launch failed: ") + hipGetErrorString(e));
     return ok();
   }
+  if (xt || at)
+    return fail(IMQ_EUNSUPPORTED, "the tile layout takes the row-band gate/up kernel: K of 4, 8, 10 or 12 times 256");
   PairPlan pl = plan_pair(N, K, dev->cu_count);
   if (pl.parts > 1 && (!workspace || workspace_bytes < pl.bytes)) pl = PairPlan{(N + 31) / 32, 0, 1, 0};
   if (pl.parts > 1 && !aligned(workspace, 16)) return fail(IMQ_EINVAL, "workspace must be 16-byte aligned");
@@ -3825,6 +4040,42 @@ int32_t imq_qmv_norm(const imq_problem* problems, int32_t count, int32_t M, int3
   return ok();
 }
 
+int32_t imq_qmv_residual_bands(const imq_problem* problem, int32_t M, int32_t group_size, int32_t bits,
+                               const imq_residual_out* out, void* stream) {
+  if (!problem) return fail(IMQ_EINVAL, "problem must be non-null");
+  if (!out) return fail(IMQ_EINVAL, "out must be non-null");
+  const imq_problem& p = *problem;
+  int32_t code = check_format(p.N, p.K, group_size, bits);
+  if (code != IMQ_OK) return code;
+  if ((code = check_weights(p.w, p.scales, p.biases)) != IMQ_OK) return code;
+  if (M < 1 || M > IMQ_MAX_ROWS) return fail(IMQ_EINVAL, "M must be 1..32");
+  if (!p.x) return fail(IMQ_EINVAL, "x must be non-null");
+  const bool tiled = p.ldx == IMQ_LD_TILED;
+  if (!tiled && (p.ldx < p.K || p.ldx % 8 != 0 || !aligned(p.x, 16)))
+    return fail(IMQ_EINVAL, "x rows must be 16-byte aligned, ldx >= K and a multiple of 8 (or IMQ_LD_TILED)");
+  if (tiled && !aligned(p.x, 16)) return fail(IMQ_EINVAL, "a tiled x must be 16-byte aligned");
+  if (p.K % 256 != 0 || p.K / 256 > rb::kMaxChunks)
+    return fail(IMQ_EUNSUPPORTED, "the row-band projection takes K a multiple of 256, at most 9728");
+  const int64_t xbytes = tiled ? (int64_t)p.K * 64 : ((int64_t)(M - 1) * p.ldx + p.K) * 2;
+  if ((int64_t)p.N * (p.K / 2) >= ((int64_t)1 << 31) || xbytes >= ((int64_t)1 << 31))
+    return fail(IMQ_EUNSUPPORTED, "a weight or activation of 2 GiB or more exceeds the kernel's offsets");
+  const int N = p.N, bands = (N + 31) / 32;
+  if (!out->h || !aligned(out->h, 4)) return fail(IMQ_EINVAL, "residual h must be non-null and 4-byte aligned");
+  if (M > 1 && out->ldh < N) return fail(IMQ_EINVAL, "residual ldh must be >= N");
+  if ((code = check_x_out(out, M, N)) != IMQ_OK) return code;
+  if (out->ssq && (!aligned(out->ssq, 4) || out->ld < bands || out->ld % 4))
+    return fail(IMQ_EINVAL, "residual ssq must be 4-byte aligned with ld >= ceil(N / 32), a multiple of 4");
+  if (!current_device(&code)) return code;
+  const Problem P{p.w, p.scales, p.biases, p.x, nullptr, tiled ? 0 : p.ldx, 0, N, p.K, 0, 0, 0, 0};
+  const ResidualOut r{out->h, M > 1 ? out->ldh : N, out->weight, out->x, x_out_ld(out, M, N), out->ssq,
+                      out->ld, 0};
+  hipLaunchKernelGGL(qmv_rowband_kernel, dim3(bands), dim3(64 * rb::kWaves), 0, static_cast<hipStream_t>(stream),
+                     P, M, r);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("row-band launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
 int32_t imq_residual_planes(const float* planes, int32_t nplanes, int32_t M, int32_t N,
                             const imq_residual_out* out, void* stream) {
   if (!planes || !aligned(planes, 4)) return fail(IMQ_EINVAL, "planes must be non-null and 4-byte aligned");
@@ -3836,16 +4087,12 @@ int32_t imq_residual_planes(const float* planes, int32_t nplanes, int32_t M, int
   if (!out->h || !aligned(out->h, 4)) return fail(IMQ_EINVAL, "residual h must be non-null and 4-byte aligned");
   if (M > 1 && out->ldh < N) return fail(IMQ_EINVAL, "residual ldh must be >= N");
   const int tiles = (N + 63) / 64;
-  if (out->weight) {
-    if (!aligned(out->weight, 2) || !out->x || !aligned(out->x, 2))
-      return fail(IMQ_EINVAL, "norm weight and x' must be non-null and 2-byte aligned");
-    if (M > 1 && out->ldx < N) return fail(IMQ_EINVAL, "x' ldx must be >= N");
-  }
+  int32_t code = check_x_out(out, M, N);
+  if (code != IMQ_OK) return code;
   if (out->ssq && (!aligned(out->ssq, 4) || out->ld < tiles || out->ld % 4))
     return fail(IMQ_EINVAL, "residual ssq must be 4-byte aligned with ld >= ceil(N / 64), a multiple of 4");
-  int32_t code;
   if (!current_device(&code)) return code;
-  const ResidualOut r{out->h, M > 1 ? out->ldh : N, out->weight, out->x, M > 1 ? out->ldx : N, out->ssq,
+  const ResidualOut r{out->h, M > 1 ? out->ldh : N, out->weight, out->x, x_out_ld(out, M, N), out->ssq,
                       out->ld, 0};
   const dim3 grid(tiles, (M + kResRowsPerGroup - 1) / kResRowsPerGroup), block(64 * kResRowsPerGroup);
   const hipStream_t st = static_cast<hipStream_t>(stream);

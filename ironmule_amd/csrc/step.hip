@@ -112,7 +112,8 @@ struct Stage {
   float* part;
   float* ml;
   uint32_t* combine;  // one counter per (request, KV head)
-  int32_t Hq, Hkv, capacity, num_slots, max_len, splits, cps, pad3;
+  int32_t Hq, Hkv, capacity, num_slots, max_len, splits, cps;
+  int32_t out_tiled;  // 1: the attention output in the 32-row tile layout (else rows Hq * 128 apart)
   // q, k and v as fp32 output planes of a split projection instead (staged launches only):
   // problem i (q, k, v), plane s, request b at qkv + i * qkv_pstride + (s * qkv_rows + b) * N_i
   const float* qkv;
@@ -774,15 +775,19 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
   __syncthreads();
 
   uint16_t* out = S.attn_out;
-  const uint32_t out_bytes = (uint32_t)(b + 1) * Hq * kD * 2u;
+  const uint32_t out_bytes = S.out_tiled ? 64u * (uint32_t)Hq * kD : (uint32_t)(b + 1) * Hq * kD * 2u;
+  // byte offset of the output pair (request b, head hd, dimensions 2 lane, 2 lane + 1)
+  auto out_at = [&](int hd) {
+    return S.out_tiled ? tile_elem((uint32_t)b, (uint32_t)(hd * kD + 2 * lane)) * 2u
+                       : (uint32_t)((b * Hq + hd) * kD + 2 * lane) * 2u;
+  };
   if (first >= last) {
     if (used == 0 && s == 0) {  // nothing to attend to: zeros
 #pragma unroll
       for (int r = 0; r < kRounds; ++r) {
         const int g = wave + W * r;
         if (g < G)
-          store_b32_sc1(buffer_rsrc(out, out_bytes),
-                        (uint32_t)((b * Hq + kvh * G + g) * kD + 2 * lane) * 2u, 0u);
+          store_b32_sc1(buffer_rsrc(out, out_bytes), out_at(kvh * G + g), 0u);
       }
     }
     return true;
@@ -951,7 +956,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
       if (g < G) {
         const float lx = Ls[r] + 0.0f;
         const uint32_t o = (uint32_t)to_bf((a0[r] + 0.0f) / lx) | ((uint32_t)to_bf((a1[r] + 0.0f) / lx) << 16);
-        store_b32_sc1(buffer_rsrc(out, out_bytes), (uint32_t)((b * Hq + kvh * G + g) * kD + 2 * lane) * 2u, o);
+        store_b32_sc1(buffer_rsrc(out, out_bytes), out_at(kvh * G + g), o);
       }
     }
     return true;
@@ -1018,7 +1023,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
           }
         }
         const uint32_t o = (uint32_t)to_bf(c0 / Lx) | ((uint32_t)to_bf(c1 / Lx) << 16);
-        store_b32_sc1(buffer_rsrc(out, out_bytes), (uint32_t)((b * Hq + hh) * kD + 2 * lane) * 2u, o);
+        store_b32_sc1(buffer_rsrc(out, out_bytes), out_at(hh), o);
         continue;
       }
       float Mx = -INFINITY;
@@ -1054,7 +1059,7 @@ __device__ __forceinline__ bool attention_task(SRef S, int task, const StepArgs&
         }
       }
       const uint32_t o = (uint32_t)to_bf(c0 / Lx) | ((uint32_t)to_bf(c1 / Lx) << 16);
-      store_b32_sc1(buffer_rsrc(out, out_bytes), (uint32_t)((b * Hq + hh) * kD + 2 * lane) * 2u, o);
+      store_b32_sc1(buffer_rsrc(out, out_bytes), out_at(hh), o);
     }
   }
   return true;
@@ -1351,7 +1356,8 @@ int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             const int32_t* positions, const int32_t* slots, uint16_t* k_pool,
                             uint16_t* v_pool, uint16_t* out, int32_t B, int32_t Hq, int32_t Hkv,
                             int32_t capacity, int32_t num_slots, int32_t max_len, float theta,
-                            float eps, float* workspace, uint32_t* counters, void* stream) {
+                            float eps, float* workspace, uint32_t* counters, void* stream,
+                            bool out_tiled = false) {
   if ((planes ? false : (!q || !k || !v)) || !q_norm || !k_norm || !positions || !slots || !k_pool ||
       !v_pool || !out || !workspace || !counters)
     return fail(IMQ_EINVAL, "null pointer");
@@ -1396,6 +1402,7 @@ int32_t attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t* v,
   A.k_pool = k_pool;
   A.v_pool = v_pool;
   A.attn_out = out;
+  A.out_tiled = out_tiled ? 1 : 0;
   A.positions = positions;
   A.slots = slots;
   A.part = workspace;
@@ -1464,13 +1471,17 @@ int32_t imq_attention_fused(const uint16_t* q, const uint16_t* k, const uint16_t
 int32_t imq_attention_fused_planes(const float* planes, int64_t pstride, int32_t nplanes,
                                    const uint16_t* q_norm, const uint16_t* k_norm,
                                    const int32_t* positions, const int32_t* slots, uint16_t* k_pool,
-                                   uint16_t* v_pool, uint16_t* out, int32_t B, int32_t Hq, int32_t Hkv,
-                                   int32_t capacity, int32_t num_slots, int32_t max_len, float theta,
-                                   float eps, float* workspace, uint32_t* counters, void* stream) {
+                                   uint16_t* v_pool, uint16_t* out, int64_t ld_out, int32_t B, int32_t Hq,
+                                   int32_t Hkv, int32_t capacity, int32_t num_slots, int32_t max_len,
+                                   float theta, float eps, float* workspace, uint32_t* counters, void* stream) {
   if (!planes) return fail(IMQ_EINVAL, "planes must be non-null");
+  if (ld_out != IMQ_LD_TILED && ld_out != (int64_t)Hq * kD)
+    return fail(IMQ_EINVAL, "ld_out must be Hq * 128 (rows) or IMQ_LD_TILED");
+  if (ld_out == IMQ_LD_TILED && (B > 32 || !aligned(out, 4)))
+    return fail(IMQ_EINVAL, "a tiled attention output takes at most 32 requests, 4-byte aligned");
   return attention_fused(nullptr, nullptr, nullptr, planes, pstride, nplanes, q_norm, k_norm, positions,
                          slots, k_pool, v_pool, out, B, Hq, Hkv, capacity, num_slots, max_len, theta, eps,
-                         workspace, counters, stream);
+                         workspace, counters, stream, ld_out == IMQ_LD_TILED);
 }
 
 int32_t imq_qmv_program_create(const imq_qmv_stage* stages, int32_t count, imq_program** out) {

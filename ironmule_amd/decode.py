@@ -154,6 +154,13 @@ class DecodeState:
         # the o and down projections' K-range planes (both hidden wide), added into h by
         # their own epilogue launch
         self.res_planes = _native.ResidualPlanes(batch, c.hidden, device)
+        # the activations the batched step's launches hand to one another, in the 32-row
+        # tile layout (the MFMA kernels read them as contiguous 1 KB pieces): x' for q/k/v
+        # and gate/up, the attention output for o, SiLU * up for down
+        rows = _native.MAX_ROWS
+        self.x_t = torch.zeros(rows * c.hidden, **bf)
+        self.attn_t = torch.zeros(rows * c.heads * c.head_dim, **bf)
+        self.act_t = torch.zeros(rows * c.intermediate, **bf)
         self.workspace = torch.empty(_native.attention_workspace(batch, c.heads, self.max_len),
                                      dtype=torch.float32, device=device)
         self.attn_counters = torch.zeros(batch * c.kv_heads, dtype=torch.int32, device=device)
@@ -212,10 +219,34 @@ def decode_step(weights: DecoderWeights, state: DecodeState, stream=None) -> tor
     return s.logits
 
 
-def _residual_projection(weight, x, state: DecodeState, next_norm, x_out, stats_out, stream) -> None:
-    """h += bf16(x @ W.T), x_out = bf16(h * next_norm) and its per-tile sums of squares: as
-    K-range planes and an epilogue launch when the projection splits, else in one launch."""
+# Hidden sizes whose gate/up launch takes the row-band kernel (K / 256 wavefronts of 4, 8,
+# 10 or 12): the batched step then hands its activations on in the 32-row tile layout.
+TILED_GATE_UP_K = (1024, 2048, 2560, 3072)
+
+# The widest K the row-band projection (a workgroup per 32 weight rows over the whole K)
+# takes in the decode step: its x stream, the whole of x per workgroup, runs at about 70
+# GB/s per CU, which beats the K-range planes and their epilogue launch at o's K = 4096
+# (9.2 against 12.1 us at batch 32) but not at down's 9728 (18.0 against 14.7).
+RESIDUAL_BANDS_MAX_K = 4096
+
+
+def _residual_projection(weight, x, state: DecodeState, next_norm, x_out, stats_out, stream,
+                         tiled: bool = False) -> None:
+    """h += bf16(x @ W.T), x_out = bf16(h * next_norm) and the per-row partial sums of
+    squares of the new h: over bands of 32 rows and the whole K up to RESIDUAL_BANDS_MAX_K,
+    else as K-range planes and an epilogue launch when the projection splits, else in one
+    launch.  With `tiled` x and x_out are 32-row tile layout buffers."""
     n, s = _native, state
+    k = int(weight[0].shape[1]) * 8
+    if k % 256 == 0 and k <= RESIDUAL_BANDS_MAX_K:
+        n.qmv_residual_bands(weight, x, s.batch, s.h, next_norm=next_norm, x_out=x_out, stats_out=stats_out,
+                             tiled=tiled, tiled_out=tiled, stream=stream)
+        return
+    if tiled:  # K-range planes read the tiled x, the epilogue writes x' tiled
+        n.qmv_residual_planes(weight, x, s.res_planes, stream=stream, tiled=True)
+        n.residual_planes(s.res_planes, s.h, next_norm=next_norm, x_out=x_out, stats_out=stats_out,
+                          stream=stream, tiled_out=True)
+        return
     if 2 <= n.residual_split_planes(weight, x) <= s.res_planes.max_planes:
         n.qmv_residual_planes(weight, x, s.res_planes, stream=stream)
         n.residual_planes(s.res_planes, s.h, next_norm=next_norm, x_out=x_out, stats_out=stats_out,
@@ -253,18 +284,21 @@ def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream
     n = _native
     n.embed(*weights.embed, s.tokens, s.h, stream=stream)
     n.rmsnorm_prescale(s.h, weights.layers[0]["input_norm"], s.x, s.stats_in, stream=stream)
+    t = c.hidden in TILED_GATE_UP_K  # the activations between launches in the tile layout
+    xn, attn, act = (s.x_t, s.attn_t, s.act_t) if t else (s.x, s.attn, s.act)
     for i, layer in enumerate(weights.layers):
-        n.qmv_norm_planes([layer["q"], layer["k"], layer["v"]], s.x, s.qkv_planes,
-                          norm_in=s.stats_in, eps=c.eps, stream=stream)
+        # the first layer's x' comes from the prescale as rows
+        n.qmv_norm_planes([layer["q"], layer["k"], layer["v"]], s.x if i == 0 else xn, s.qkv_planes,
+                          norm_in=s.stats_in, eps=c.eps, stream=stream, tiled=t and i > 0)
         n.attention_fused_planes(s.qkv_planes, layer["q_norm"], layer["k_norm"], s.positions,
-                                 s.slot_ids, s.k_pool[i], s.v_pool[i], s.attn, s.max_len,
-                                 c.theta, c.eps, s.workspace, s.attn_counters, stream=stream)
-        _residual_projection(layer["o"], s.attn, s, layer["post_norm"], s.x, s.stats_post, stream)
-        n.gate_up_silu_norm(layer["gate"], layer["up"], s.x, s.act, s.stats_post, c.eps,
-                            stream=stream)
+                                 s.slot_ids, s.k_pool[i], s.v_pool[i], attn, s.max_len,
+                                 c.theta, c.eps, s.workspace, s.attn_counters, stream=stream, tiled=t)
+        _residual_projection(layer["o"], attn, s, layer["post_norm"], xn, s.stats_post, stream, tiled=t)
+        n.gate_up_silu_norm(layer["gate"], layer["up"], xn, act, s.stats_post, c.eps,
+                            stream=stream, rows=s.batch, tiled_x=t, tiled_out=t)
         last = i + 1 == len(weights.layers)
-        _residual_projection(layer["down"], s.act, s, None if last else weights.layers[i + 1]["input_norm"],
-                             None if last else s.x, None if last else s.stats_in, stream)
+        _residual_projection(layer["down"], act, s, None if last else weights.layers[i + 1]["input_norm"],
+                             None if last else xn, None if last else s.stats_in, stream, tiled=t)
     n.add_rmsnorm(s.h, weights.norm, s.x, c.eps, stream=stream)
     n.qmv(*weights.embed, s.x, out=s.logits, stream=stream)
     return s.logits

@@ -11,11 +11,11 @@ producer writes x' = bf16(h * w) and partial sums of squares, the consumer scale
   the decode shapes (q/k/v, o and down at 5 and 32 rows) and for the gate/up launch against
   silu_mul of the halved grouped outputs.
 * input norm with random partials: within the oracle's bf16 bar of inv * (x' W^T), inv from
-  the float64 sum (plus 2^-18 relative for the fp32 sum of up to 64 partials).
+  the float64 sum (plus 2^-18 relative for the fp32 sum of up to 128 partials).
 * residual epilogue: h_new = h + bf16(y) bit-exact with y the plain projection's output, x' =
   bf16(h_new * w) bit-exact, the per-tile sums of squares within fp32 rounding; h only
   without a weight; a small forced plan (K = 512, 8 rows, whole-K tiles) against the oracle.
-* refusals: a residual epilogue over two weights, partial counts outside 1..64, ld not a
+* refusals: a residual epilogue over two weights, partial counts outside 1..128, ld not a
   multiple of 4.
 """
 
@@ -274,7 +274,7 @@ def test_refusals(native, oracle):
     h = torch.zeros((8, 512), device="cuda")
     with pytest.raises(ValueError):
         native.qmv_norm(weights, x, residual=h)
-    for tiles, ld in ((0, 4), (65, 68), (5, 6)):
+    for tiles, ld in ((0, 4), (129, 132), (5, 6)):
         st = native.NormStats(8, 512, "cuda")
         nin = NormIn(st.ssq.data_ptr(), tiles, ld, 512, 1e-6)
         probs = (Problem * 1)()
