@@ -2174,11 +2174,13 @@ __global__ __launch_bounds__(64 * W) void qmv_pair_rows_kernel(LaunchArgs a, Nor
     for (int w = 0; w < W; ++w) v += red[w * (pr::kChunk / 4) + at];
     return v;
   };
+  // row m's 1/rms in lane m of every wavefront (the pair sums in order), fetched per output
+  const float inv_lane = norm_in && lane < 32 ? norm_row_inv(ni, nsum, lane) : 1.0f;
   for (int idx = tid; idx < 32 * R; idx += 64 * W) {
     const int m = idx / R, nl = idx - m * R, n = r0 + nl;
+    const float sc = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * m, __float_as_int(inv_lane)));
     if (m >= M || n >= N) continue;
     const float gs = slot_sum(nl, m), us = slot_sum(R + nl, m);
-    const float sc = norm_in ? norm_row_inv(ni, nsum, m) : 1.0f;
     const float g0v = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? gs * sc : gs));
     const float u0v = bf16_bits_to_f32(f32_to_bf16_bits(norm_in ? us * sc : us));
     act[Pg.ldy == 0 ? (size_t)tile_elem(m, n) : (size_t)m * Pg.ldy + n] =
