@@ -404,10 +404,13 @@ def _epilogue_launches(weights, batch: int) -> int:
     import torch
 
     from ironmule_amd import _native
+    from ironmule_amd.decode import RESIDUAL_BANDS_MAX_K
     layer = weights.layers[0]
     count = 0
     c = weights.config
     for name, k in (("o", c.heads * c.head_dim), ("down", c.intermediate)):
+        if k % 256 == 0 and k <= RESIDUAL_BANDS_MAX_K:
+            continue  # over bands of rows and the whole K: one launch
         x = torch.empty((batch, k), dtype=torch.bfloat16, device=layer[name][0].device)
         if 2 <= _native.residual_split_planes(layer[name], x) <= _native.RESIDUAL_MAX_PLANES:
             count += 1
@@ -627,7 +630,7 @@ def copy_calibration(torch, device) -> None:
 
 
 def _short(name: str) -> str:
-    for marker in ("stream_chain_kernel", "stream_kernel", "qmv_stage_kernel", "attention_stage_kernel",
+    for marker in ("qmv_pair_rows_kernel", "qmv_rowband_kernel", "stream_chain_kernel", "stream_kernel", "qmv_stage_kernel", "attention_stage_kernel",
                    "step_kernel", "reset_kernel", "qmv_gather_kernel", "qmv_m1c_kernel", "qmv_m1_kernel", "qmv_rows_kernel",
                    "qmv_mma_staged_kernel", "qmv_mma_kernel", "qmv_dma_kernel", "qmv_band_kernel", "xprep_kernel",
                    "qmv_xs_kernel", "qmv_mr_kernel", "clear_words_kernel",
