@@ -173,7 +173,9 @@ IMQ_API int32_t imq_qmv_norm_splits(const imq_problem* problems, int32_t count, 
  * The problems' y are not written (may be NULL).  Same limits as imq_qmv_norm; no workspace.
  * Replaces the same reference calls as imq_qmv_norm (the q/k/v projections of the decode
  * step, ironmule/dense_plan.py:348-353), for a reader that adds the planes itself
- * (imq_attention_fused_planes, ironmule_decode.h).
+ * (imq_attention_fused_planes, ironmule_decode.h).  With x in the tile layout (every
+ * problem's ldx == IMQ_LD_TILED, at most three problems of one K <= 4096) each problem is
+ * one plane from bands of 32 weight rows over the whole K (*splits = 1).
  */
 IMQ_API int32_t imq_qmv_norm_planes(const imq_problem* problems, int32_t count, int32_t M,
                                     int32_t group_size, int32_t bits, const imq_norm_in* in,

@@ -2314,14 +2314,47 @@ __device__ __forceinline__ void rowband_wave(const Problem& P, int M, int r0, in
   }
 }
 
-__global__ __launch_bounds__(64 * rb::kWaves) void qmv_rowband_kernel(Problem P, int M, ResidualOut res) {
+// The launch: up to rb::kMaxProblems projections of one x (the same K), bands [band0[i],
+// band0[i + 1]) of the grid for problem i; either the residual epilogue (one problem, res.h
+// set) or an fp32 output plane per problem, planes + i * pstride + m * N_i + n, scaled by
+// row m's 1/rms when the input norm is folded in (ni.ssq set).
+struct RowbandArgs {
+  Problem p[3];
+  int32_t band0[4];
+  int32_t count, M;
+  NormIn ni;
+  ResidualOut res;
+  float* planes;
+  int64_t pstride;
+};
+
+__global__ __launch_bounds__(64 * rb::kWaves) void qmv_rowband_kernel(RowbandArgs A) {
   __shared__ __attribute__((aligned(16))) char arr0[rb::kWaves * rb::kChunk];
   __shared__ __attribute__((aligned(16))) char arr1[rb::kWaves * rb::kChunk];
   __shared__ __attribute__((aligned(16))) char arr2[rb::kThird * rb::kChunk];
+  __shared__ float nsum[kNormMaxTiles / 4][32];  // input norm: pair sums [j][row]
+  const int M = A.M;
+  // the problem of this band (uniform), its fields selected from static loads of all three
+  // (an indexed load would wait for the band test before fetching them)
+  const int bx = blockIdx.x;
+  const int pi = A.count > 1 && bx >= A.band0[1] ? (A.count > 2 && bx >= A.band0[2] ? 2 : 1) : 0;
+  const Problem P = pi == 0 ? A.p[0] : pi == 1 ? A.p[1] : A.p[2];
   const int N = P.N, C = P.K >> 8;
-  const int band = blockIdx.x, r0 = band * 32;
+  const int band = blockIdx.x - A.band0[pi], r0 = band * 32;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the input norm's partial sums of squares, before every other load
+  constexpr int NQ = (kNormSlots + 64 * rb::kWaves - 1) / (64 * rb::kWaves);
+  const bool norm_in = A.ni.ssq != nullptr;  // uniform
+  uint4 nq[NQ];
+  if (norm_in) {
+    const __amdgpu_buffer_rsrc_t qrs = buffer_rsrc(A.ni.ssq, (uint32_t)(M * A.ni.ld * 4));
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      const int p = tid + 64 * rb::kWaves * r;
+      nq[r] = load_b128(qrs, p < kNormSlots ? norm_pair_offset(A.ni, M, p) : kPastBuffer);
+    }
+  }
   // this wavefront's chunks [c0, c0 + nc): C / 16 each, one more for the first C % 16
   const int base = C / rb::kWaves, extra = C - base * rb::kWaves;
   const int nc = base + (wave < extra ? 1 : 0);
@@ -2336,22 +2369,38 @@ __global__ __launch_bounds__(64 * rb::kWaves) void qmv_rowband_kernel(Problem P,
     default: break;
   }
 
-  // residual rows of this thread's output (m = tid / 32, column n = r0 + tid % 32), in
+  // this thread's output: row m = tid / 32, column n = r0 + tid % 32; the residual rows in
   // flight with the reduction
+  const ResidualOut& res = A.res;
+  const bool plane = res.h == nullptr;  // uniform
   const int m = tid >> 5, n = r0 + (tid & 31);
   const bool mine = m < M && n < N;
-  const float hv = mine ? res.h[(size_t)m * res.ldh + n] : 0.0f;
-  const float wn = mine && res.w ? bf16_bits_to_f32(res.w[n]) : 0.0f;
+  const float hv = mine && !plane ? res.h[(size_t)m * res.ldh + n] : 0.0f;
+  const float wn = mine && !plane && res.w ? bf16_bits_to_f32(res.w[n]) : 0.0f;
   // the accumulators through LDS: wavefront w's [e][lane] in its chunk-0 slot (its own
   // weight reads are done: a wavefront's LDS accesses complete in order)
   float* red = reinterpret_cast<float*>(arr0);
 #pragma unroll
   for (int e = 0; e < 16; ++e) red[wave * (rb::kChunk / 4) + e * 64 + lane] = acc[e];
+  if (norm_in) {  // the input norm's pair sums, published by the barrier below
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      const int p = tid + 64 * rb::kWaves * r;
+      if (p < kNormSlots) nsum[p >> 5][p & 31] = norm_pair_sum(A.ni, p, nq[r]);
+    }
+  }
   __syncthreads();
   const int at = (4 * (m >> 3) + (m & 3)) * 64 + (tid & 31) + 32 * ((m >> 2) & 1);
   float y = 0.0f;
 #pragma unroll
   for (int w = 0; w < rb::kWaves; ++w) y += red[w * (rb::kChunk / 4) + at];
+  if (plane) {
+    // row m's 1/rms in lane m of every wavefront (the pair sums in order), fetched per output
+    const float inv_lane = norm_in && lane < 32 ? norm_row_inv(A.ni, nsum, lane) : 1.0f;
+    const float inv = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * m, __float_as_int(inv_lane)));
+    if (mine) A.planes[pi * A.pstride + (int64_t)m * N + n] = norm_in ? y * inv : y;
+    return;
+  }
   float sq = 0.0f;
   if (mine) {
     const float hn = hv + bf16_bits_to_f32(f32_to_bf16_bits(y));
@@ -3828,6 +3877,23 @@ NormIn to_norm_in(const imq_norm_in* in) {
   return n;
 }
 
+// imq_qmv_norm_planes over the row-band kernel (one plane per problem) instead of K-range
+// planes: x in the tile layout, at most three problems of one K, K a multiple of 256 and at
+// most IMQ_ROWBAND_PLANES_MAX_K (the q/k/v projections of the batched decode step: 7.0
+// against 9.1 us at K = 2560 and 32 rows).
+#ifndef IMQ_ROWBAND_PLANES_MAX_K
+#define IMQ_ROWBAND_PLANES_MAX_K 4096
+#endif
+bool rowband_planes(const imq_problem* problems, int32_t count) {
+  if (count < 1 || count > 3) return false;
+  for (int i = 0; i < count; ++i) {
+    const imq_problem& q = problems[i];
+    if (q.ldx != IMQ_LD_TILED || q.K != problems[0].K || q.K % 256 != 0 || q.K > IMQ_ROWBAND_PLANES_MAX_K)
+      return false;
+  }
+  return true;
+}
+
 // x' of a residual epilogue: rows ldx apart, or the tile layout (ldx == IMQ_LD_TILED, N a
 // multiple of 64); the row stride the kernels take (0: tiled).
 int32_t check_x_out(const imq_residual_out* out, int32_t M, int32_t N) {
@@ -4068,11 +4134,14 @@ int32_t imq_qmv_residual_bands(const imq_problem* problem, int32_t M, int32_t gr
   if (out->ssq && (!aligned(out->ssq, 4) || out->ld < bands || out->ld % 4))
     return fail(IMQ_EINVAL, "residual ssq must be 4-byte aligned with ld >= ceil(N / 32), a multiple of 4");
   if (!current_device(&code)) return code;
-  const Problem P{p.w, p.scales, p.biases, p.x, nullptr, tiled ? 0 : p.ldx, 0, N, p.K, 0, 0, 0, 0};
-  const ResidualOut r{out->h, M > 1 ? out->ldh : N, out->weight, out->x, x_out_ld(out, M, N), out->ssq,
-                      out->ld, 0};
-  hipLaunchKernelGGL(qmv_rowband_kernel, dim3(bands), dim3(64 * rb::kWaves), 0, static_cast<hipStream_t>(stream),
-                     P, M, r);
+  RowbandArgs A;
+  memset(&A, 0, sizeof(A));
+  A.p[0] = Problem{p.w, p.scales, p.biases, p.x, nullptr, tiled ? 0 : p.ldx, 0, N, p.K, 0, 0, 0, 0};
+  A.band0[1] = bands;
+  A.count = 1;
+  A.M = M;
+  A.res = ResidualOut{out->h, M > 1 ? out->ldh : N, out->weight, out->x, x_out_ld(out, M, N), out->ssq, out->ld, 0};
+  hipLaunchKernelGGL(qmv_rowband_kernel, dim3(bands), dim3(64 * rb::kWaves), 0, static_cast<hipStream_t>(stream), A);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("row-band launch failed: ") + hipGetErrorString(e));
   return ok();
@@ -4111,6 +4180,7 @@ int32_t imq_residual_planes(const float* planes, int32_t nplanes, int32_t M, int
 
 int32_t imq_qmv_norm_splits(const imq_problem* problems, int32_t count, int32_t M) {
   if (!problems || count < 1 || count > IMQ_MAX_PROBLEMS || M < 1 || M > IMQ_MAX_ROWS) return 0;
+  if (rowband_planes(problems, count)) return 1;
   int32_t code;
   const DeviceInfo* dev = current_device(&code);
   if (!dev) return 0;
@@ -4154,6 +4224,25 @@ int32_t imq_qmv_norm_planes(const imq_problem* problems, int32_t count, int32_t 
   if (pstride < need) return fail(IMQ_EINVAL, "pstride must hold every plane of the widest problem (" +
                                                   std::to_string(need) + " floats)");
   if (((int64_t)count * pstride) * 4 >= ((int64_t)1 << 31)) return fail(IMQ_EUNSUPPORTED, "planes of 2 GiB or more");
+  if (rowband_planes(problems, count)) {  // one plane per problem from the row-band kernel
+    RowbandArgs A;
+    memset(&A, 0, sizeof(A));
+    for (int i = 0; i < count; ++i) {
+      A.p[i] = a.p[i];
+      A.band0[i + 1] = A.band0[i] + (a.p[i].N + 31) / 32;
+    }
+    A.count = count;
+    A.M = M;
+    A.ni = nin;
+    A.planes = planes;
+    A.pstride = pstride;
+    *splits = 1;
+    hipLaunchKernelGGL(qmv_rowband_kernel, dim3(A.band0[count]), dim3(64 * rb::kWaves), 0,
+                       static_cast<hipStream_t>(stream), A);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("row-band launch failed: ") + hipGetErrorString(e));
+    return ok();
+  }
   *splits = pl.splits;
   const hipError_t e = launch_dma(a, pl, nullptr, static_cast<hipStream_t>(stream), &nin, &res, planes, pstride);
   if (e != hipSuccess) return fail(IMQ_ELAUNCH, std::string("fused-norm qmv launch failed: ") + hipGetErrorString(e));

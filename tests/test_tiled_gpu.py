@@ -2,9 +2,11 @@
 producer's tiled output is tile_rows of its output as rows, and each consumer gives the same
 bits from a tiled x as from x in rows, through the C ABI.
 
-* q/k/v planes (imq_qmv_norm_planes) and the o/down K-range planes (imq_qmv_norm_planes, one
-  weight) from a tiled x; the residual epilogue (imq_residual_planes) and the row-band
-  projection (imq_qmv_residual_bands) writing x' tiled;
+* q/k/v (imq_qmv_norm_planes) from a tiled x take the row-band kernel, one plane per
+  projection: against the oracle's bar of inv * (x' W^T) like the K-range planes from rows,
+  and the same bits on a second call; down's K-range planes (K = 9728, past the row-band
+  range) from a tiled x give the bits of rows; the residual epilogue (imq_residual_planes)
+  and the row-band projection (imq_qmv_residual_bands) writing x' tiled;
 * the gate/up launch (imq_qmv_gate_up_silu_norm) reading x and writing SiLU * up tiled;
 * the planes attention (imq_attention_fused_planes) writing its output tiled.
 At 32, 8 and 3 rows (rows past M are neither read nor written: the buffers start as 7.0)."""
@@ -16,7 +18,7 @@ import pytest
 import torch
 
 from tests.conftest import gpu_available
-from tests.gpu_util import announce, to_device
+from tests.gpu_util import announce, bf16_bits, to_device
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
@@ -56,10 +58,25 @@ def test_tiled_producers_and_consumers(native, oracle, m):
     a, b = native.QkvPlanes(m, 32, 8, "cuda"), native.QkvPlanes(m, 32, 8, "cuda")
     ca = native.qmv_norm_planes(weights, x, a, norm_in=st)
     cb = native.qmv_norm_planes(weights, xt, b, norm_in=st, tiled=True)
+    again = native.QkvPlanes(m, 32, 8, "cuda")
+    native.qmv_norm_planes(weights, xt, again, norm_in=st, tiled=True)
     torch.cuda.synchronize()
-    assert ca == cb
+    # rows: K-range planes of the direct-to-LDS kernel; tiled: one plane per projection from
+    # the row-band kernel.  Each against the oracle's bar of inv * (x' W^T).
+    assert ca >= 1 and cb == 1
+    ssq = st.ssq[:, :40].double().cpu().numpy().sum(axis=1)
+    inv = 1.0 / np.sqrt(ssq / 2560 + 1e-6)
     for i in range(3):
-        assert torch.equal(a.view(i), b.view(i)), i
+        ref, mag = oracle.qmv_f64(probs[i].w, probs[i].s, probs[i].b, probs[0].x)
+        for pl, cnt in ((a, ca), (b, cb)):
+            v = pl.view(i)
+            tot = v[0].clone()
+            for s_ in range(1, cnt):
+                tot = tot + v[s_]
+            got = tot.to(torch.bfloat16)
+            chk = oracle.check_bf16(bf16_bits(got), ref * inv[:, None], mag * inv[:, None] + 4.0 * np.abs(ref * inv[:, None]) * 2.0 ** -18)
+            assert chk.ok, (i, cnt, chk.detail)
+        assert torch.equal(b.view(i), again.view(i)), i
     # attention on the planes, output as rows and tiled
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -90,7 +107,7 @@ def test_tiled_producers_and_consumers(native, oracle, m):
     res = []
     for tiled in (False, True):
         pl = native.ResidualPlanes(m, 2560, "cuda")
-        native.qmv_residual_planes(wo, outs[1] if tiled else xo, pl, tiled=tiled)
+        native.qmv_residual_planes(wo, xo, pl)  # K-range planes from rows (tiled: one row-band plane)
         h = h0.clone()
         xp = torch.full((32 * 2560,) if tiled else (m, 2560), 7.0, dtype=torch.bfloat16, device="cuda")
         sto = native.NormStats(m, 2560, "cuda")
