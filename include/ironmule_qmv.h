@@ -134,7 +134,7 @@ typedef struct imq_residual_out {
   int64_t ldh;
   const uint16_t* weight;  /* (N) bf16 weight of the next RMSNorm; NULL: update h only */
   uint16_t* x;             /* (M, N) bf16 x' = bf16(h * weight), rows ldx apart */
-  int64_t ldx;
+  int64_t ldx;             /* or IMQ_LD_TILED: x' in the 32-row tile layout (N % 64 == 0) */
   float* ssq;              /* NULL, or (M, ld): ssq[m * ld + t] = sum of h[m][n]^2 over
                             * the 64 columns n of tile t, t < ceil(N / 64) */
   int32_t ld;              /* a multiple of 4, >= ceil(N / 64) */
@@ -232,12 +232,15 @@ IMQ_API size_t imq_qmv_gate_up_silu_norm_workspace(int32_t M, int32_t N, int32_t
  *   act[m][n] = bf16(silu(g) * u),  g = bf16(inv_m * sum_k x'[m][k] W_gate[n][k]),
  *                                   u = bf16(inv_m * sum_k x'[m][k] W_up[n][k]).
  * Same shapes and limits as imq_qmv_gate_up_silu, except that any M from 1 to 32 is taken
- * (the decode step folds its norms from 3 rows).  With a workspace of
- * imq_qmv_gate_up_silu_norm_workspace bytes (zero-filled before its first use and left
- * ready by every call; calls sharing one must not overlap) the last round's tiles are cut
- * into K-parts whose sums are added in part order; with none (NULL, 0 bytes) every tile is
- * whole.  Replaces the post-attention RMSNorm, the fused gate/up launch and the SwiGLU,
- * ironmule/dense_plan.py:359-360 and ironmule/fast.py:186-215.
+ * (the decode step folds its norms from 3 rows).  K of 4, 8, 10 or 12 times 256 runs one
+ * workgroup per CU over bands of 8-row units of both weights and the whole K (no
+ * workspace; x and act may then be in the tile layout, ldx / ld_act == IMQ_LD_TILED).
+ * Otherwise, with a workspace of imq_qmv_gate_up_silu_norm_workspace bytes (zero-filled
+ * before its first use and left ready by every call; calls sharing one must not overlap)
+ * the last round's 32-row tiles are cut into K-parts whose sums are added in part order;
+ * with none (NULL, 0 bytes) every tile is whole.  Replaces the post-attention RMSNorm, the
+ * fused gate/up launch and the SwiGLU, ironmule/dense_plan.py:359-360 and
+ * ironmule/fast.py:186-215.
  */
 IMQ_API int32_t imq_qmv_gate_up_silu_norm(const uint32_t* w_gate, const uint16_t* s_gate,
                 const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up,
