@@ -257,29 +257,33 @@ def _residual_projection(weight, x, state: DecodeState, next_norm, x_out, stats_
 
 
 def _decode_step_fused_norms(weights: DecoderWeights, state: DecodeState, stream=None) -> torch.Tensor:
-    """decode_step with every RMSNorm but the last folded into the launches around it, five
+    """decode_step with every RMSNorm but the last folded into the launches around it, six
     launches per layer:
 
         x' = bf16(h * w_in), stats                 imq_rmsnorm_prescale (first layer only)
         per layer:
             q, k, v = inv * (x' @ W.T)             imq_qmv_norm_planes (norm_in: the stats;
-                                                   the K-ranges' partials as output planes)
+                                                   bands of 32 rows over the whole K, one
+                                                   fp32 plane per projection; the first
+                                                   layer's from x' as rows: K-range planes)
             attention                              imq_attention_fused_planes (adds the
                                                    planes as it reads q, k and v)
-            h += o @ Wo.T; x' = bf16(h * w_post)   imq_qmv_norm_planes + imq_residual_planes
-                                                   (the K-ranges as planes, then the residual
+            h += o @ Wo.T; x' = bf16(h * w_post)   imq_qmv_residual_bands (bands of 32 rows
+                                                   over the whole K with the residual add, x'
+                                                   and per-band sums of squares)
+            act = silu(inv * g) * (inv * u)        imq_qmv_gate_up_silu_norm (bands of rows
+                                                   of both weights, one workgroup per CU)
+            h += act @ Wd.T; x' = bf16(h * w_in')  imq_qmv_norm_planes + imq_residual_planes
+                                                   (K-range planes, then the residual
                                                    epilogue: h, x' and the per-tile sums of
-                                                   squares)
-            act = silu(inv * g) * (inv * u)        imq_qmv_gate_up_silu_norm
-            h += act @ Wd.T; x' = bf16(h * w_in')  as for o (the last layer updates h only)
+                                                   squares; the last layer updates h only)
         logits = rms_norm(h) @ E.T                 imq_add_rmsnorm, imq_qmv
 
     inv is each row's 1 / rms(h), so inv * (x' W^T) is rms_norm(h) W^T up to the place of one
-    bf16 rounding (x' is rounded before the scaling instead of after it).  The o and down
-    projections and their epilogue are two launches when the projection splits K into 2 to
-    16 ranges (the split launch's counter and reload round trips, and an epilogue run by one
-    workgroup per 64 columns, cost more than a launch), else one (imq_qmv_norm with the
-    epilogue); both forms give the same bits."""
+    bf16 rounding (x' is rounded before the scaling instead of after it).  Where the hidden
+    size takes the row-band gate/up kernel (TILED_GATE_UP_K), the launches hand x', the
+    attention output and act to one another in the 32-row tile layout (IMQ_LD_TILED), which
+    the batched kernels read as contiguous 1 KB pieces; otherwise as rows."""
     c, s = weights.config, state
     n = _native
     n.embed(*weights.embed, s.tokens, s.h, stream=stream)
