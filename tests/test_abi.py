@@ -98,6 +98,31 @@ def test_residual_planes_refusals(lib, over):
     assert code in (_native.IMQ_EINVAL, _native.IMQ_EUNSUPPORTED), (over, code)
 
 
+def _residual_bands(lib, **over):
+    args = dict(w=1 << 20, s=1 << 21, b=1 << 22, x=1 << 23, ldx=4096, N=2560, K=4096, M=32, gs=64, bits=4,
+                h=1 << 24, ldh=2560, weight=1 << 25, xo=1 << 26, ldxo=2560, ssq=1 << 27, ld=80)
+    args.update(over)
+    prob = _native.Problem(args["w"], args["s"], args["b"], args["x"], args["ldx"], None, 0, args["N"], args["K"])
+    out = _native.ResidualOut(args["h"], args["ldh"], args["weight"], args["xo"], args["ldxo"],
+                              args["ssq"], args["ld"])
+    return lib.imq_qmv_residual_bands(ctypes.byref(prob), args["M"], args["gs"], args["bits"],
+                                      ctypes.byref(out), None)
+
+
+@pytest.mark.parametrize("over", [
+    {"M": 0}, {"M": 33}, {"x": 0}, {"x": (1 << 23) + 8}, {"ldx": 4000}, {"ldx": 4100}, {"K": 4160},
+    {"K": 9984, "ldx": 9984}, {"gs": 32}, {"bits": 8}, {"h": 0}, {"ldh": 100}, {"xo": 0}, {"ldxo": 100},
+    {"ldxo": _native.LD_TILED, "N": 2528}, {"ld": 40}, {"ld": 82}, {"w": 0},
+])
+def test_residual_bands_refusals(lib, over):
+    """imq_qmv_residual_bands refuses malformed calls before it looks for a device: rows out
+    of 1..32, x misaligned or ldx short or not a multiple of 8, K past 9728 or not a
+    multiple of 256, another format, h or x' missing or short, a tiled x' of N not a
+    multiple of 64, ssq ld short of the 80 bands or not a multiple of 4."""
+    code = _residual_bands(lib, **over)
+    assert code in (_native.IMQ_EINVAL, _native.IMQ_EUNSUPPORTED), (over, code)
+
+
 def test_python_side_validates_before_the_abi():
     import torch
     w = torch.zeros((8, 8), dtype=torch.int32)
